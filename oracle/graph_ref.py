@@ -1,0 +1,310 @@
+"""CPU oracle for the conv/GEMM hot path — TEST INFRASTRUCTURE ONLY.
+
+Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may
+import this module, and only as the checker; the product never routes through
+it.
+
+A float64 numpy restatement of what the reference engine computes for an
+`.engine` graph on the YOLOv8 path.  The reference keeps activations NHWC and
+remaps ONNX axes by heuristics (PDEFA1.0/src/core/session_parts/*.inc); the
+results it realises for the traced YOLOv8 pattern are the ONNX operator
+semantics, which is what this module evaluates in NCHW:
+
+  Conv      session_ops_nn.inc:2-65 -> ops::conv2d (conv2d.cpp:484-651);
+            output size (H + 2p - ((k-1)d + 1)) / s + 1 (conv2d.cpp:442-446);
+            fused activation codes 1 relu, 2 leaky, 3 sigmoid, 4 tanh, 5 silu
+            (session_fusion.inc:33-107, conv2d.hpp:16-24)
+  MaxPool   session_ops_nn.inc:267-347 -> pooling.cpp:35-101 (padding never wins)
+  Resize    session_ops_shape.inc:96-202: nearest, target = in * scale
+            (+0.5 truncation), source index floor(out * in/out)
+  Concat    session_ops_shape.inc:66-93
+  Slice     session_ops_shape.inc:754-889 (clamped starts/ends, steps)
+  Reshape   session_ops_shape.inc:512-726 (0 copies a dim, -1 infers)
+  Transpose session_ops_shape.inc:946-1096
+  Softmax   session_ops_math.inc:223-318 (max-subtracted exp, / sum)
+  Add/Sub/Mul/Div  session_ops_math.inc:4-220 (numpy broadcasting)
+  Sigmoid   activation_avx2.cpp:110-121 (1 / (1 + e^-x))
+
+Pins (tests/test_oracle.py): the compiled reference (oracle/_ref) on the same
+`.engine` files and inputs; closed-form conv known answers from
+PDEFA1.0/examples/test_conv2d.cpp:13-148; brute-force direct loops on tiny
+shapes; silu(1) = 0.7311 (pdefa/tests/test_ops_extra.py:26-30).
+"""
+from __future__ import annotations
+
+import numpy as np
+
+from pdefa_amd.engine_format import EngineModel, OP_NAME
+
+
+def conv2d(x, w, b=None, stride=(1, 1), pad=(0, 0), dil=(1, 1), act=0, slope=0.01):
+    """NCHW conv, float64 accumulation; w is [Cout, Cin, KH, KW]."""
+    x = np.asarray(x, np.float64)
+    w = np.asarray(w, np.float64)
+    n, c, h, wd = x.shape
+    co, ci, kh, kw = w.shape
+    if ci != c:
+        raise ValueError(f"conv: input has {c} channels, weight expects {ci}")
+    sh, sw = stride
+    ph, pw = pad
+    dh, dw = dil
+    ho = (h + 2 * ph - ((kh - 1) * dh + 1)) // sh + 1
+    wo = (wd + 2 * pw - ((kw - 1) * dw + 1)) // sw + 1
+    xp = np.pad(x, ((0, 0), (0, 0), (ph, ph), (pw, pw)))
+    wm = w.reshape(co, ci * kh * kw).T
+    out = np.empty((n, co, ho, wo), np.float64)
+    for i in range(n):
+        cols = np.empty((ci, kh, kw, ho, wo), np.float64)
+        for a in range(kh):
+            for bb in range(kw):
+                y0, x0 = a * dh, bb * dw
+                cols[:, a, bb] = xp[i, :, y0:y0 + sh * (ho - 1) + 1:sh, x0:x0 + sw * (wo - 1) + 1:sw]
+        cols = cols.reshape(ci * kh * kw, ho * wo).T
+        out[i] = (cols @ wm).T.reshape(co, ho, wo)
+    if b is not None:
+        out += np.asarray(b, np.float64)[None, :, None, None]
+    return activation(out, act, slope)
+
+
+def activation(x, act, slope=0.01):
+    if act == 0:
+        return x
+    if act == 1:
+        return np.maximum(x, 0)
+    if act == 2:
+        return np.where(x > 0, x, x * slope)
+    if act == 3:
+        return 1.0 / (1.0 + np.exp(-x))
+    if act == 4:
+        return np.tanh(x)
+    if act == 5:
+        return x / (1.0 + np.exp(-x))
+    raise ValueError(f"activation code {act}")
+
+
+def silu_winograd_compat(x):
+    """The SiLU the reference applies in its Winograd epilogue, restated in
+    float32 (PDEFA1.0/src/kernels/simd/avx2/conv2d_winograd.cpp:81-101).
+
+    exp(-x) is formed as 2^n * P(f) with n = round(-x * log2 e) and
+    f = -x * log2 e - n, where P is the degree-6 polynomial
+    1 + f/2 + c4 f^2 + ... evaluated in f's log2 units; the result differs from
+    the true SiLU by up to ~2% of |x|.  Inputs beyond the +/-88.37626 clamp
+    return x (large positive) or 0 (large negative)."""
+    x = np.asarray(x, np.float32)
+    f32 = np.float32
+    neg = -x
+    fx = neg * f32(1.44269504088896341)
+    n = np.where(fx >= 0, np.floor(fx + f32(0.5)), np.ceil(fx - f32(0.5))).astype(np.float32)
+    f = (fx - n).astype(np.float32)
+    p = np.full_like(f, f32(1.9875691500e-4))
+    for c in (1.3981999507e-3, 8.3334519073e-3, 4.1665795894e-2, 1.6666665459e-1,
+              5.0000001201e-1, 1.0):
+        p = (p * f + f32(c)).astype(np.float32)
+    e = np.clip(n, -127, 128).astype(np.int64) + 127
+    scale = np.ldexp(np.float32(1.0), (e - 127).astype(np.int32)).astype(np.float32)
+    with np.errstate(over="ignore", invalid="ignore"):
+        y = (x / (f32(1.0) + p * scale)).astype(np.float32)
+    y = np.where(neg < f32(-88.37626), x, y)
+    y = np.where(neg > f32(88.37626), f32(0.0), y)
+    return y
+
+
+def winograd_path(cin, kh, kw, stride, dil, groups):
+    """True when the reference conv dispatcher routes a conv to its Winograd
+    kernel (PDEFA1.0/src/ops/conv2d.cpp:602-631): 3x3, stride 1, dilation 1,
+    groups 1, and 16 < Cin <= 512 (Cin <= 16 goes to the direct kernel)."""
+    return (kh == 3 and kw == 3 and tuple(stride) == (1, 1) and tuple(dil) == (1, 1)
+            and groups == 1 and 16 < cin <= 512)
+
+
+def conv2d_direct(x, w, b=None, stride=(1, 1), pad=(0, 0)):
+    """Brute-force seven-loop conv (pins conv2d on tiny shapes)."""
+    n, c, h, wd = x.shape
+    co, ci, kh, kw = w.shape
+    ho = (h + 2 * pad[0] - kh) // stride[0] + 1
+    wo = (wd + 2 * pad[1] - kw) // stride[1] + 1
+    out = np.zeros((n, co, ho, wo), np.float64)
+    for i in range(n):
+        for o in range(co):
+            for y in range(ho):
+                for xx in range(wo):
+                    s = 0.0 if b is None else float(b[o])
+                    for k in range(ci):
+                        for a in range(kh):
+                            for bb in range(kw):
+                                iy = y * stride[0] - pad[0] + a
+                                ix = xx * stride[1] - pad[1] + bb
+                                if 0 <= iy < h and 0 <= ix < wd:
+                                    s += float(x[i, k, iy, ix]) * float(w[o, k, a, bb])
+                    out[i, o, y, xx] = s
+    return out
+
+
+def maxpool2d(x, k, s, p):
+    n, c, h, w = x.shape
+    ho = (h + 2 * p[0] - k[0]) // s[0] + 1
+    wo = (w + 2 * p[1] - k[1]) // s[1] + 1
+    xp = np.pad(x, ((0, 0), (0, 0), (p[0], p[0]), (p[1], p[1])), constant_values=-np.inf)
+    out = np.full((n, c, ho, wo), -np.inf, x.dtype)
+    for a in range(k[0]):
+        for b in range(k[1]):
+            out = np.maximum(out, xp[:, :, a:a + s[0] * (ho - 1) + 1:s[0],
+                                     b:b + s[1] * (wo - 1) + 1:s[1]])
+    return out
+
+
+def resize_nearest(x, scales):
+    n, c, h, w = x.shape
+    sh, sw = float(scales[2]), float(scales[3])
+    ho = int(np.float32(h) * np.float32(sh) + np.float32(0.5))
+    wo = int(np.float32(w) * np.float32(sw) + np.float32(0.5))
+    ry = np.float32(h) / np.float32(ho)
+    rx = np.float32(w) / np.float32(wo)
+    iy = np.minimum((np.arange(ho, dtype=np.float32) * ry).astype(np.int64), h - 1)
+    ix = np.minimum((np.arange(wo, dtype=np.float32) * rx).astype(np.int64), w - 1)
+    return x[:, :, iy][:, :, :, ix]
+
+
+def softmax(x, axis):
+    m = np.max(x, axis=axis, keepdims=True)
+    e = np.exp(x - m)
+    return e / np.sum(e, axis=axis, keepdims=True)
+
+
+def _ints(t):
+    return [int(v) for v in np.asarray(t).reshape(-1)]
+
+
+def slice_(x, starts, ends, axes=None, steps=None):
+    idx = [slice(None)] * x.ndim
+    axes = list(range(len(starts))) if axes is None else axes
+    steps = [1] * len(starts) if steps is None else steps
+    for s, e, a, st in zip(starts, ends, axes, steps):
+        if a < 0:
+            a += x.ndim
+        d = x.shape[a]
+        s = s + d if s < 0 else s
+        e = e + d if e < 0 else e
+        s = min(max(s, 0), d)
+        e = min(max(e, 0), d)
+        idx[a] = slice(s, max(e, s), st)
+    return x[tuple(idx)]
+
+
+def reshape(x, shape):
+    shape = list(shape)
+    for i, s in enumerate(shape):
+        if s == 0:
+            shape[i] = x.shape[i]
+    return x.reshape(shape)
+
+
+def _consumers(model, ref):
+    return [n for n in model.nodes if ref in n.inputs] + \
+        [None for o in model.graph_outputs if o == ref]
+
+
+def _silu_nodes(model, conv):
+    """(sigmoid, mul) node names when conv's output feeds exactly a Sigmoid and
+    a Mul(conv, sigmoid), the pattern session_fusion.inc:33-81 fuses."""
+    out = conv.outputs[0]
+    cons = _consumers(model, out)
+    if len(cons) != 2 or None in cons:
+        return None
+    sig = next((n for n in cons if n.op_name == "Sigmoid" and n.inputs == [out]), None)
+    if sig is None or len(_consumers(model, sig.outputs[0])) != 1:
+        return None
+    mul = next((n for n in cons if n.op_name == "Mul" and sorted(n.inputs) ==
+                sorted([out, sig.outputs[0]])), None)
+    if mul is None:
+        return None
+    return {sig.name, mul.name}
+
+
+def _silu_consumer(model, conv):
+    names = _silu_nodes(model, conv)
+    if names is None:
+        return None
+    mul = next(n for n in model.nodes if n.name in names and n.op_name == "Mul")
+    return mul.outputs[0]
+
+
+def run_graph(model: EngineModel, inputs, dtype=np.float64, compat_silu=True):
+    """Evaluates the graph on `inputs` (list of NCHW arrays); returns outputs
+    as float32 arrays in graph_outputs order.  compat_silu=False evaluates the
+    true SiLU everywhere."""
+    inter = {}
+    skip = set()
+
+    def get(ref):
+        if ref <= -1000:
+            return model.weights[-1000 - ref].astype(dtype)
+        if ref < 0:
+            return np.asarray(inputs[-1 - ref], dtype)
+        return inter[ref]
+
+    for node in model.nodes:
+        if node.name in skip:
+            continue
+        op = OP_NAME.get(node.op)
+        ins = node.inputs
+        p = node.params
+        if op == "Conv":
+            b = get(ins[2]) if len(ins) > 2 else None
+            if int(p.get("groups", 1)) not in (0, 1):
+                raise NotImplementedError("grouped conv")
+            x, w = get(ins[0]), get(ins[1])
+            stride, dil = (p["stride_h"], p["stride_w"]), (p["dil_h"], p["dil_w"])
+            y = conv2d(x, w, b, stride, (p["pad_h"], p["pad_w"]), dil)
+            # Conv -> Sigmoid -> Mul is fused into the conv by the reference
+            # session (session_fusion.inc:33-81); on Winograd layers the fused
+            # SiLU is the compat form above.
+            silu = _silu_consumer(model, node)
+            if silu is not None:
+                if compat_silu and winograd_path(x.shape[1], w.shape[2], w.shape[3],
+                                                 stride, dil, 1):
+                    y = silu_winograd_compat(y.astype(np.float32)).astype(dtype)
+                else:
+                    y = y / (1.0 + np.exp(-y))
+                inter[node.outputs[0]] = y
+                inter[silu] = y
+                skip.update(_silu_nodes(model, node))
+                continue
+        elif op == "Sigmoid":
+            y = 1.0 / (1.0 + np.exp(-get(ins[0])))
+        elif op in ("Add", "Sub", "Mul", "Div"):
+            a, b = get(ins[0]), get(ins[1])
+            y = {"Add": np.add, "Sub": np.subtract, "Mul": np.multiply,
+                 "Div": np.divide}[op](a, b)
+        elif op == "MaxPool":
+            y = maxpool2d(get(ins[0]), (p["kernel_h"], p["kernel_w"]),
+                          (p["stride_h"], p["stride_w"]), (p["pad_h"], p["pad_w"]))
+        elif op == "Resize":
+            scales = None
+            for r in ins[1:]:
+                t = get(r)
+                if t.size == 4:
+                    scales = t.reshape(-1)
+                    break
+            if scales is None:
+                raise NotImplementedError("Resize without a 4-element scales input")
+            y = resize_nearest(get(ins[0]), scales)
+        elif op == "Concat":
+            y = np.concatenate([get(r) for r in ins], axis=int(p["axis"]))
+        elif op == "Slice":
+            axes = _ints(get(ins[3])) if len(ins) > 3 else None
+            steps = _ints(get(ins[4])) if len(ins) > 4 else None
+            y = slice_(get(ins[0]), _ints(get(ins[1])), _ints(get(ins[2])), axes, steps)
+        elif op == "Reshape":
+            y = reshape(get(ins[0]), _ints(get(ins[1])))
+        elif op == "Transpose":
+            y = np.transpose(get(ins[0]), _ints(get(ins[1])))
+        elif op == "Softmax":
+            y = softmax(get(ins[0]), int(p["axis"]))
+        elif op in ("Input", "Output"):
+            continue
+        else:
+            raise NotImplementedError(f"oracle: op {node.op} ({op}) in node {node.name}")
+        inter[node.outputs[0]] = y
+    return [inter[o].astype(np.float32) for o in model.graph_outputs]

@@ -1,0 +1,332 @@
+"""Seeded synthetic models in the `.engine` format.
+
+The YOLOv8 graph emitted here follows the node pattern of an Ultralytics
+static ONNX export (opset 18, BN folded into the conv bias) after the
+reference converter's rewrites (pdefa/tools/onnx_to_engine.py:200-268 turns
+Split into Slice nodes with constant starts/ends/axes; :580-590 appends the
+Transpose perm as a weight; constants become F32 weights):
+
+  Conv block      Conv(k, s, p=k//2, bias) -> Sigmoid -> Mul
+  C2f             Conv1x1 -> Slice x2 -> [Conv3x3 -> Conv3x3 (+ Add)] x n
+                  -> Concat(axis 1) -> Conv1x1
+  SPPF            Conv1x1 -> MaxPool(k5 s1 p2) x3 -> Concat -> Conv1x1
+  FPN/PAN         Resize(scales [1,1,2,2], nearest) -> Concat
+  Detect level    cv2: Conv3x3 -> Conv3x3 -> Conv1x1(64)
+                  cv3: Conv3x3 -> Conv3x3 -> Conv1x1(nc)
+                  -> Concat(axis 1) -> Reshape [1, 64+nc, -1]
+  head            Concat(axis 2) -> Slice(64 | nc)
+                  box: Reshape [1,4,16,A] -> Transpose [0,2,1,3] -> Softmax(1)
+                       -> Conv1x1(16->1, w = arange(16)) -> Reshape [1,4,A]
+                       -> Slice(2 | 2) -> anchors - lt, anchors + rb
+                       -> (x1y1 + x2y2) / 2, x2y2 - x1y1 -> Concat -> Mul(strides)
+                  cls: Sigmoid
+                  out: Concat(axis 1) -> [1, 4+nc, A]
+
+Architecture constants follow the public YOLOv8 model definition: backbone
+Conv(64,3,2) Conv(128,3,2) C2f(128)x3 Conv(256,3,2) C2f(256)x6 Conv(512,3,2)
+C2f(512)x6 Conv(1024,3,2) C2f(1024)x3 SPPF(1024); head Upsample Concat(P4)
+C2f(512)x3 Upsample Concat(P3) C2f(256)x3 Conv(256,3,2) Concat C2f(512)x3
+Conv(512,3,2) Concat C2f(1024)x3 Detect; widths scaled by the width multiple
+and capped at max_channels, repeats by the depth multiple.
+"""
+from __future__ import annotations
+
+import math
+from typing import List, Optional, Tuple
+
+import numpy as np
+
+from .engine_format import OP, EngineModel, Node, TensorInfo, write_engine
+
+SCALES = {
+    # depth multiple, width multiple, max channels
+    "n": (0.33, 0.25, 1024),
+    "s": (0.33, 0.50, 1024),
+    "m": (0.67, 0.75, 768),
+    "l": (1.00, 1.00, 512),
+    "x": (1.00, 1.25, 512),
+}
+
+
+class GraphBuilder:
+    """Emits engine nodes the way the reference converter numbers them:
+    weights as -1000-w, the graph input as -1, intermediates from 0 upward."""
+
+    def __init__(self) -> None:
+        self.weights: List[np.ndarray] = []
+        self.wnames: List[str] = []
+        self.nodes: List[Node] = []
+        self.n_inter = 0
+
+    def const(self, name: str, arr) -> int:
+        self.weights.append(np.ascontiguousarray(np.asarray(arr, dtype=np.float32)))
+        self.wnames.append(name)
+        return -1000 - (len(self.weights) - 1)
+
+    def node(self, op: str, name: str, inputs: List[int], n_out: int = 1, **params):
+        outs = list(range(self.n_inter, self.n_inter + n_out))
+        self.n_inter += n_out
+        self.nodes.append(Node(OP[op], name, list(inputs), outs, params))
+        return outs[0] if n_out == 1 else outs
+
+    def model(self, in_shape, out_shape, outputs: List[int]) -> EngineModel:
+        return EngineModel(self.weights, self.wnames, self.nodes, [-1], outputs,
+                           [TensorInfo("images", list(in_shape))],
+                           [TensorInfo("output0", list(out_shape))])
+
+
+def make_divisible(x: float, d: int = 8) -> int:
+    return int(math.ceil(x / d) * d)
+
+
+def kaiming_uniform(rng: np.random.Generator, shape) -> np.ndarray:
+    fan_in = int(np.prod(shape[1:]))
+    bound = math.sqrt(6.0 / fan_in)
+    return rng.uniform(-bound, bound, size=shape).astype(np.float32)
+
+
+class _Yolo:
+    def __init__(self, b: GraphBuilder, rng: np.random.Generator, cls_bias: float):
+        self.b, self.rng, self.cls_bias = b, rng, cls_bias
+
+    def conv_raw(self, x, cin, cout, k, s, name, bias_value=None):
+        w = kaiming_uniform(self.rng, (cout, cin, k, k))
+        if bias_value is None:
+            bias = self.rng.uniform(-0.1, 0.1, size=cout).astype(np.float32)
+        else:
+            bias = np.full(cout, bias_value, np.float32)
+        wi = self.b.const(f"{name}.weight", w)
+        bi = self.b.const(f"{name}.bias", bias)
+        p = k // 2
+        return self.b.node("Conv", f"/{name}/Conv", [x, wi, bi], stride_h=s, stride_w=s,
+                           pad_h=p, pad_w=p, dil_h=1, dil_w=1, groups=1)
+
+    def conv(self, x, cin, cout, k, s, name):
+        y = self.conv_raw(x, cin, cout, k, s, f"{name}/conv")
+        sg = self.b.node("Sigmoid", f"/{name}/act/Sigmoid", [y])
+        return self.b.node("Mul", f"/{name}/act/Mul", [y, sg])
+
+    def slice(self, x, start, end, axis, name):
+        s = self.b.const(f"{name}_start::const", [start])
+        e = self.b.const(f"{name}_end::const", [end])
+        a = self.b.const(f"{name}_axes::const", [axis])
+        return self.b.node("Slice", name, [x, s, e, a])
+
+    def c2f(self, x, cin, cout, n, shortcut, name):
+        c = int(cout * 0.5)
+        y = self.conv(x, cin, 2 * c, 1, 1, f"{name}/cv1")
+        parts = [self.slice(y, 0, c, 1, f"/{name}/Split_slice_0"),
+                 self.slice(y, c, 2 * c, 1, f"/{name}/Split_slice_1")]
+        for i in range(n):
+            h = self.conv(parts[-1], c, c, 3, 1, f"{name}/m.{i}/cv1")
+            h = self.conv(h, c, c, 3, 1, f"{name}/m.{i}/cv2")
+            if shortcut:
+                h = self.b.node("Add", f"/{name}/m.{i}/add", [parts[-1], h])
+            parts.append(h)
+        cat = self.b.node("Concat", f"/{name}/Concat", parts, axis=1)
+        return self.conv(cat, (2 + n) * c, cout, 1, 1, f"{name}/cv2")
+
+    def sppf(self, x, cin, cout, name):
+        c_ = cin // 2
+        y = self.conv(x, cin, c_, 1, 1, f"{name}/cv1")
+        ys = [y]
+        for i in range(3):
+            ys.append(self.b.node("MaxPool", f"/{name}/m/MaxPool_{i}", [ys[-1]], kernel_h=5,
+                                  kernel_w=5, stride_h=1, stride_w=1, pad_h=2, pad_w=2))
+        cat = self.b.node("Concat", f"/{name}/Concat", ys, axis=1)
+        return self.conv(cat, 4 * c_, cout, 1, 1, f"{name}/cv2")
+
+    def upsample(self, x, name):
+        sc = self.b.const(f"{name}/scales::const", [1.0, 1.0, 2.0, 2.0])
+        return self.b.node("Resize", f"/{name}/Resize", [x, sc])
+
+
+def build_yolov8(scale: str = "n", seed: int = 0, nc: int = 80, imgsz: int = 640,
+                 cls_bias: float = -4.0) -> EngineModel:
+    """YOLOv8{scale} detection graph with seeded random weights (BN folded)."""
+    depth, width, max_ch = SCALES[scale]
+    ch = lambda c: make_divisible(min(c, max_ch) * width, 8)
+    rep = lambda n: max(round(n * depth), 1)
+    rng = np.random.default_rng(seed)
+    b = GraphBuilder()
+    y = _Yolo(b, rng, cls_bias)
+    x = -1
+    c0, c1, c2, c3, c4 = ch(64), ch(128), ch(256), ch(512), ch(1024)
+    x = y.conv(x, 3, c0, 3, 2, "model.0")
+    x = y.conv(x, c0, c1, 3, 2, "model.1")
+    x = y.c2f(x, c1, c1, rep(3), True, "model.2")
+    x = y.conv(x, c1, c2, 3, 2, "model.3")
+    p3 = y.c2f(x, c2, c2, rep(6), True, "model.4")
+    x = y.conv(p3, c2, c3, 3, 2, "model.5")
+    p4 = y.c2f(x, c3, c3, rep(6), True, "model.6")
+    x = y.conv(p4, c3, c4, 3, 2, "model.7")
+    x = y.c2f(x, c4, c4, rep(3), True, "model.8")
+    p5 = y.sppf(x, c4, c4, "model.9")
+    x = y.upsample(p5, "model.10")
+    x = b.node("Concat", "/model.11/Concat", [x, p4], axis=1)
+    h12 = y.c2f(x, c4 + c3, c3, rep(3), False, "model.12")
+    x = y.upsample(h12, "model.13")
+    x = b.node("Concat", "/model.14/Concat", [x, p3], axis=1)
+    h15 = y.c2f(x, c3 + c2, c2, rep(3), False, "model.15")
+    x = y.conv(h15, c2, c2, 3, 2, "model.16")
+    x = b.node("Concat", "/model.17/Concat", [x, h12], axis=1)
+    h18 = y.c2f(x, c2 + c3, c3, rep(3), False, "model.18")
+    x = y.conv(h18, c3, c3, 3, 2, "model.19")
+    x = b.node("Concat", "/model.20/Concat", [x, p5], axis=1)
+    h21 = y.c2f(x, c3 + c4, c4, rep(3), False, "model.21")
+
+    # Detect head (reg_max 16)
+    feats = [(h15, c2, 8), (h18, c3, 16), (h21, c4, 32)]
+    reg = 16
+    no = nc + 4 * reg
+    cb = max(16, c2 // 4, 4 * reg)
+    cc = max(c2, min(nc, 100))
+    flat = []
+    anchors, strides = [], []
+    for i, (f, cin, s) in enumerate(feats):
+        n = f"model.22"
+        a = y.conv(f, cin, cb, 3, 1, f"{n}/cv2.{i}/cv2.{i}.0")
+        a = y.conv(a, cb, cb, 3, 1, f"{n}/cv2.{i}/cv2.{i}.1")
+        a = y.conv_raw(a, cb, 4 * reg, 1, 1, f"{n}/cv2.{i}/cv2.{i}.2", bias_value=1.0)
+        c = y.conv(f, cin, cc, 3, 1, f"{n}/cv3.{i}/cv3.{i}.0")
+        c = y.conv(c, cc, cc, 3, 1, f"{n}/cv3.{i}/cv3.{i}.1")
+        c = y.conv_raw(c, cc, nc, 1, 1, f"{n}/cv3.{i}/cv3.{i}.2", bias_value=cls_bias)
+        cat = b.node("Concat", f"/{n}/Concat_{i}", [a, c], axis=1)
+        shp = b.const(f"/{n}/Reshape_{i}/shape::const", [1, no, -1])
+        flat.append(b.node("Reshape", f"/{n}/Reshape_{i}", [cat, shp]))
+        hw = imgsz // s
+        sx = np.arange(hw, dtype=np.float32) + 0.5
+        gy, gx = np.meshgrid(sx, sx, indexing="ij")
+        anchors.append(np.stack([gx.ravel(), gy.ravel()], 0))
+        strides.append(np.full(hw * hw, s, np.float32))
+    n_anchor = sum(a.shape[1] for a in anchors)
+    xcat = b.node("Concat", "/model.22/Concat_3", flat, axis=2)
+    box = y.slice(xcat, 0, 4 * reg, 1, "/model.22/Split_slice_0")
+    cls = y.slice(xcat, 4 * reg, no, 1, "/model.22/Split_slice_1")
+    shp = b.const("/model.22/dfl/Reshape/shape::const", [1, 4, reg, n_anchor])
+    t = b.node("Reshape", "/model.22/dfl/Reshape", [box, shp])
+    perm = b.const("/model.22/dfl/Transpose::perm", [0, 2, 1, 3])
+    t = b.node("Transpose", "/model.22/dfl/Transpose", [t, perm])
+    t = b.node("Softmax", "/model.22/dfl/Softmax", [t], axis=1)
+    dflw = b.const("model.22.dfl.conv.weight",
+                   np.arange(reg, dtype=np.float32).reshape(1, reg, 1, 1))
+    t = b.node("Conv", "/model.22/dfl/conv/Conv", [t, dflw], stride_h=1, stride_w=1,
+               pad_h=0, pad_w=0, dil_h=1, dil_w=1, groups=1)
+    shp = b.const("/model.22/dfl/Reshape_1/shape::const", [1, 4, n_anchor])
+    dist = b.node("Reshape", "/model.22/dfl/Reshape_1", [t, shp])
+    lt = y.slice(dist, 0, 2, 1, "/model.22/Split_1_slice_0")
+    rb = y.slice(dist, 2, 4, 1, "/model.22/Split_1_slice_1")
+    anc = b.const("/model.22/anchors::const", np.concatenate(anchors, 1)[None])
+    x1y1 = b.node("Sub", "/model.22/Sub", [anc, lt])
+    x2y2 = b.node("Add", "/model.22/Add", [anc, rb])
+    ssum = b.node("Add", "/model.22/Add_1", [x1y1, x2y2])
+    two = b.const("/model.22/Constant_two::const", np.array(2.0, np.float32))
+    cxy = b.node("Div", "/model.22/Div", [ssum, two])
+    wh = b.node("Sub", "/model.22/Sub_1", [x2y2, x1y1])
+    dbox = b.node("Concat", "/model.22/Concat_4", [cxy, wh], axis=1)
+    strd = b.const("/model.22/strides::const", np.concatenate(strides)[None])
+    dbox = b.node("Mul", "/model.22/Mul_2", [dbox, strd])
+    sig = b.node("Sigmoid", "/model.22/Sigmoid", [cls])
+    out = b.node("Concat", "/model.22/Concat_5", [dbox, sig], axis=1)
+    return b.model([1, 3, imgsz, imgsz], [1, 4 + nc, n_anchor], [out])
+
+
+def build_single_conv(cin: int, cout: int, k: int, stride: int, hw: int, seed: int = 7,
+                      silu: bool = True) -> Tuple[EngineModel, np.ndarray]:
+    """One Conv2d(k, stride, pad k//2) + bias (+ SiLU as Sigmoid*Mul) graph.
+
+    Returns the model and its seeded input x ~ U[0,1) of shape [1,cin,hw,hw].
+    Seed stream: x, then W (Kaiming-uniform, bound sqrt(6/fan_in)), then
+    b ~ U[-0.1, 0.1]."""
+    rng = np.random.default_rng(seed)
+    x = rng.random((1, cin, hw, hw), dtype=np.float32)
+    w = kaiming_uniform(rng, (cout, cin, k, k))
+    bias = rng.uniform(-0.1, 0.1, size=cout).astype(np.float32)
+    b = GraphBuilder()
+    wi, bi = b.const("conv.weight", w), b.const("conv.bias", bias)
+    p = k // 2
+    y = b.node("Conv", "/conv/Conv", [-1, wi, bi], stride_h=stride, stride_w=stride,
+               pad_h=p, pad_w=p, dil_h=1, dil_w=1, groups=1)
+    if silu:
+        sg = b.node("Sigmoid", "/act/Sigmoid", [y])
+        y = b.node("Mul", "/act/Mul", [y, sg])
+    ho = (hw + 2 * p - k) // stride + 1
+    return b.model([1, cin, hw, hw], [1, cout, ho, ho], [y]), x
+
+
+# Source image sizes for the batch-8 workload: aspect cycle 16:9, 4:3, 1:1.
+ASPECT_SIZES = [(1280, 720), (1024, 768), (800, 800)]
+
+
+def synth_image(seed: int, w: int = 1280, h: int = 720) -> np.ndarray:
+    """A synthetic RGB8 image, pixels ~ U[0, 255], shape [h, w, 3] uint8."""
+    rng = np.random.default_rng(seed)
+    return rng.integers(0, 256, size=(h, w, 3), dtype=np.uint8)
+
+
+def letterbox(img: np.ndarray, target_w: int = 640, target_h: int = 640,
+              scale: float = 1.0 / 255.0, pad_value: float = 114.0 / 255.0):
+    """Bilinear letterbox to an NCHW float32 [1,3,th,tw] tensor.
+
+    Restates imageloader/src/preprocess.cpp:15-144: ratio = min(tw/w, th/h),
+    scaled size = clamp(round(src*ratio), 1, target), centred pads (integer
+    halves), sample positions s = d * (1/ratio) truncated to int, x0/y0
+    clamped to src-2, bilinear weights with the scale folded into the row
+    weights, and the pad value written raw (not scaled).
+    Returns (tensor, meta dict)."""
+    h, w = img.shape[:2]
+    ch = 1 if img.ndim == 2 else img.shape[2]
+    if img.ndim == 2:
+        img = img[:, :, None]
+    ratio = np.float32(min(np.float32(target_w) / np.float32(w),
+                           np.float32(target_h) / np.float32(h)))
+    # std::round rounds halves away from zero (numpy's round is half-to-even)
+    sw = int(np.clip(int(np.floor(np.float32(w) * ratio + np.float32(0.5))), 1, target_w))
+    sh = int(np.clip(int(np.floor(np.float32(h) * ratio + np.float32(0.5))), 1, target_h))
+    px, py = (target_w - sw) // 2, (target_h - sh) // 2
+    out = np.full((3, target_h, target_w), np.float32(pad_value), np.float32)
+    inv = np.float32(1.0) / ratio
+    sx = np.arange(sw, dtype=np.float32) * inv
+    x0 = sx.astype(np.int64)
+    if w > 1:
+        x0 = np.minimum(x0, w - 2)
+    x1 = np.where(x0 + 1 < w, x0 + 1, x0)
+    fx = (sx - x0.astype(np.float32)).astype(np.float32)
+    sy = np.arange(sh, dtype=np.float32) * inv
+    y0 = sy.astype(np.int64)
+    if h > 1:
+        y0 = np.minimum(y0, h - 2)
+    y1 = np.where(y0 + 1 < h, y0 + 1, y0)
+    fy = (sy - y0.astype(np.float32)).astype(np.float32)
+    ns = np.float32(scale)
+    wy0 = ((np.float32(1) - fy) * ns)[:, None]
+    wy1 = (fy * ns)[:, None]
+    w0 = (np.float32(1) - fx)[None, :]
+    w1 = fx[None, :]
+    src = img.astype(np.float32)
+    chans = [0, 0, 0] if ch == 1 else [0, 1, 2]
+    for c in range(3):
+        p = src[:, :, chans[c]]
+        r0 = p[y0][:, x0] * w0 + p[y0][:, x1] * w1
+        r1 = p[y1][:, x0] * w0 + p[y1][:, x1] * w1
+        out[c, py:py + sh, px:px + sw] = r0 * wy0 + r1 * wy1
+    meta = dict(target_w=target_w, target_h=target_h, orig_w=w, orig_h=h, pad_x=px,
+                pad_y=py, scaled_w=sw, scaled_h=sh, ratio=float(ratio))
+    return out[None], meta
+
+
+def yolo_inputs(batch: int, imgsz: int = 640) -> Tuple[np.ndarray, list]:
+    """Letterboxed synthetic inputs: image i has seed i and the i-th size of the
+    16:9 / 4:3 / 1:1 cycle; pad 114/255, scale 1/255."""
+    xs, metas = [], []
+    for i in range(batch):
+        w, h = ASPECT_SIZES[i % len(ASPECT_SIZES)]
+        t, m = letterbox(synth_image(i, w, h), imgsz, imgsz)
+        xs.append(t)
+        metas.append(m)
+    return np.concatenate(xs, 0), metas
+
+
+def save(model: EngineModel, path: str) -> str:
+    write_engine(path, model)
+    return path
