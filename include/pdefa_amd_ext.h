@@ -1,0 +1,37 @@
+/* pdefa_amd_ext.h — entry points of libpdefa_native.so with no counterpart in
+ * the reference.  They serve benchmarking and testing of the device program;
+ * the drop-in ABI (engine_c_api.h, pdefa_c_api.h) does not depend on them.
+ */
+#ifndef PDEFA_AMD_EXT_H
+#define PDEFA_AMD_EXT_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#include "engine_c_api.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Re-runs the session's prepared device program `iters` times on the input
+ * already resident in HBM (uploaded by the last engine_session_run), with no
+ * host copies; *out_ms = elapsed device time from HIP events on the session's
+ * stream.  Requires one completed engine_session_run. */
+PDEFA_EXPORT EngineStatus pdefa_amd_session_replay(EngineSession* sess, int32_t iters, double* out_ms);
+
+/* Text dump of the session's current device program (one line per kernel). */
+PDEFA_EXPORT EngineStatus pdefa_amd_session_plan(const EngineSession* sess, char* buf, size_t cap, size_t* out_len);
+
+/* Plans `m` for inputs of the given shape without touching a GPU and returns
+ * the program text (planner tests on hosts without a device). */
+PDEFA_EXPORT EngineStatus pdefa_amd_plan_model(const EngineModel* m, const int64_t* shape, int32_t ndim, char* buf,
+                                               size_t cap, size_t* out_len);
+
+/* "<name> (<gcnArch>)" of HIP device 0, or "none". */
+PDEFA_EXPORT const char* pdefa_amd_device_name(void);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* PDEFA_AMD_EXT_H */

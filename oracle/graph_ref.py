@@ -110,6 +110,36 @@ def silu_winograd_compat(x):
     return y
 
 
+def _silu_form_with_n(x, n):
+    f32 = np.float32
+    fx = (-x) * f32(1.44269504088896341)
+    f = (fx - n).astype(np.float32)
+    p = np.full_like(f, f32(1.9875691500e-4))
+    for c in (1.3981999507e-3, 8.3334519073e-3, 4.1665795894e-2, 1.6666665459e-1,
+              5.0000001201e-1, 1.0):
+        p = (p * f + f32(c)).astype(np.float32)
+    scale = np.ldexp(np.float32(1.0), np.clip(n, -127, 128).astype(np.int32)).astype(np.float32)
+    with np.errstate(over="ignore", invalid="ignore"):
+        return (x / (f32(1.0) + p * scale)).astype(np.float32)
+
+
+def silu_winograd_compat_branches(x, tol=2e-6):
+    """Both sides of the compat SiLU's jumps.
+
+    The form is discontinuous where -x log2 e crosses a half-integer (n
+    switches while P(f) does not wrap continuously), jumping by ~2% of |x|.
+    For inputs within `tol` (relative) of such a point a 1-ulp change in the
+    conv result selects the other side, so a checker accepts either value
+    there.  Returns (y_low_n, y_high_n, unstable_mask)."""
+    x = np.asarray(x, np.float32)
+    fx = ((-x) * np.float32(1.44269504088896341)).astype(np.float64)
+    lo = np.floor(fx)
+    unstable = np.abs(fx - lo - 0.5) <= tol * np.maximum(1.0, np.abs(fx))
+    y_lo = _silu_form_with_n(x, lo.astype(np.float32))
+    y_hi = _silu_form_with_n(x, (lo + 1).astype(np.float32))
+    return y_lo, y_hi, unstable
+
+
 def winograd_path(cin, kh, kw, stride, dil, groups):
     """True when the reference conv dispatcher routes a conv to its Winograd
     kernel (PDEFA1.0/src/ops/conv2d.cpp:602-631): 3x3, stride 1, dilation 1,

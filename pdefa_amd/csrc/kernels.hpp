@@ -1,0 +1,135 @@
+// Launch interface between the host runtime and the HIP kernels (gfx950).
+// Everything here is plain structs of device pointers, sizes and strides; the
+// launchers check the shapes they are given before launching.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+namespace pdefa {
+namespace k {
+
+constexpr int kMaxRank = 6;
+
+// A strided view of fp32 device memory.  dims/str are in elements; the view's
+// element (i0..i{r-1}) lives at ptr[sum i_d * str_d].  Strides may be 0
+// (broadcast) on inputs.
+struct View {
+    float* ptr = nullptr;
+    int32_t rank = 0;
+    int64_t dims[kMaxRank] = {0, 0, 0, 0, 0, 0};
+    int64_t str[kMaxRank] = {0, 0, 0, 0, 0, 0};
+};
+
+// Fused epilogue activation codes.  1-5 follow the reference's
+// Conv2dConfig::FusedActivation numbering (PDEFA1.0/include/engine/ops/conv2d.hpp:16-24);
+// 6 is the SiLU form the reference's Winograd epilogue evaluates
+// (PDEFA1.0/src/kernels/simd/avx2/conv2d_winograd.cpp:81-101).
+enum Act : int32_t {
+    kActNone = 0,
+    kActRelu = 1,
+    kActLeaky = 2,
+    kActSigmoid = 3,
+    kActTanh = 4,
+    kActSilu = 5,
+    kActSiluWinogradForm = 6,
+};
+
+// Implicit-GEMM convolution tile configurations (BM x BN output tile, 4 waves).
+enum ConvTile : int32_t {
+    kTile128x32 = 0,
+    kTile128x64 = 1,
+    kTile128x128 = 2,
+    kTile64x64 = 3,
+    kTile64x128 = 4,
+    kNumConvTiles = 5,
+};
+constexpr int kConvBK = 16;
+int conv_tile_bm(int tile);
+int conv_tile_bn(int tile);
+
+// NHWC implicit GEMM: M = N*Ho*Wo, Ncol = Cout, K = KH*KW*Cin with k ordered
+// (kh, kw, ci).  Input/output/residual are channels-last views (channel stride
+// 1) described by their n/h/w strides.  Weights are pre-packed as
+// [Cout_pad/BN][K_pad/BK][BN][BK]; bias is padded to Cout_pad.
+struct ConvArgs {
+    const float* x = nullptr;
+    int64_t x_sn = 0, x_sh = 0, x_sw = 0;
+    int32_t N = 0, H = 0, W = 0, Cin = 0;
+    float* y = nullptr;
+    int64_t y_sn = 0, y_sh = 0, y_sw = 0;
+    int32_t Ho = 0, Wo = 0, Cout = 0;
+    const float* res = nullptr;  // optional residual added after the activation
+    int64_t r_sn = 0, r_sh = 0, r_sw = 0;
+    const float* wpk = nullptr;
+    const float* bias = nullptr;
+    int32_t KH = 1, KW = 1, sh = 1, sw = 1, ph = 0, pw = 0, dh = 1, dw = 1;
+    int32_t K = 0;        // KH*KW*Cin
+    int32_t ktiles = 0;   // ceil(K / BK)
+    int32_t act = 0;
+    float slope = 0.01f;
+    // split-K: splits > 1 writes raw partial sums to ws[split][M][Cout] and a
+    // reduce kernel applies bias/activation/residual.
+    float* ws = nullptr;
+    int32_t splits = 1;
+    int32_t kt_per_split = 0;
+};
+
+// Host-side checks + launch.  vec selects 16-byte input loads (requires
+// Cin % 4 == 0 and 16-byte aligned pixel rows).
+void launch_conv_mfma(const ConvArgs& a, int tile, bool vec, hipStream_t s);
+
+// Generic direct convolution over arbitrary strided NCHW-logical views
+// (any layout; one thread per output element).
+struct ConvDirectArgs {
+    View x;    // logical [N, Cin, H, W]
+    View y;    // logical [N, Cout, Ho, Wo]
+    View res;  // optional, same logical shape as y (ptr == nullptr if absent)
+    const float* w = nullptr;  // [Cout, Cin, KH, KW] contiguous
+    const float* bias = nullptr;
+    int32_t KH = 1, KW = 1, sh = 1, sw = 1, ph = 0, pw = 0, dh = 1, dw = 1;
+    int32_t act = 0;
+    float slope = 0.01f;
+};
+void launch_conv_direct(const ConvDirectArgs& a, hipStream_t s);
+
+// Elementwise over out's logical shape; a/b are broadcast views of the same rank.
+enum EltOp : int32_t {
+    kEltCopy = 0,
+    kEltAdd = 1,
+    kEltSub = 2,
+    kEltMul = 3,
+    kEltDiv = 4,
+    kEltSigmoid = 5,
+    kEltRelu = 6,
+    kEltTanh = 7,
+    kEltLeaky = 8,
+    kEltSilu = 9,
+};
+void launch_eltwise(int op, const View& out, const View& a, const View& b, float alpha,
+                    hipStream_t s);
+
+// Max pooling over logical [N, C, H, W] views (padding never wins).
+void launch_maxpool(const View& out, const View& in, int kh, int kw, int sh, int sw, int ph,
+                    int pw, hipStream_t s);
+
+// Nearest resize over logical [N, C, H, W] views: src = min(floor(dst * in/out), in-1)
+// with the ratio computed in fp32 as the reference does.
+void launch_resize_nearest(const View& out, const View& in, hipStream_t s);
+
+// Softmax along `axis` of the logical shape.
+void launch_softmax(const View& out, const View& in, int axis, hipStream_t s);
+
+// Packs conv weights [Cout, Cin, KH, KW] (device, contiguous) into the
+// [Cout_pad/BN][K_pad/BK][BN][BK] layout with k = (kh*KW + kw)*Cin + ci.
+void launch_pack_conv_weights(float* dst, const float* w, int Cout, int Cin, int KH, int KW,
+                              int bn, hipStream_t s);
+// Packs a row-major B[K, N] matrix the same way (a 1x1 conv with Cin = K).
+void launch_pack_gemm_b(float* dst, const float* b, int K, int N, int bn, hipStream_t s);
+
+// Bytes of packed weights for a given tile width.
+int64_t packed_weight_elems(int Cout, int K, int bn);
+
+}  // namespace k
+}  // namespace pdefa

@@ -1,0 +1,50 @@
+// Device-side activation functions shared by the conv epilogues and the
+// elementwise kernels.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+#include "../kernels.hpp"
+
+namespace pdefa {
+namespace k {
+
+// The SiLU form of the reference's Winograd epilogue
+// (PDEFA1.0/src/kernels/simd/avx2/conv2d_winograd.cpp:81-101): e^-x is formed
+// as 2^n * P(f) with n = round(-x log2 e), f the remainder in log2 units and P
+// the polynomial below.  The reference applies it on 3x3/s1 layers with
+// 16 < Cin <= 512, and its outputs are matched only with the same function.
+__device__ __forceinline__ float silu_winograd_form(float x) {
+    const float neg_x = -x;
+    if (neg_x < -88.37626f) return x;
+    if (neg_x > 88.37626f) return 0.0f;
+    const float fx = neg_x * 1.44269504088896341f;
+    const float n = roundf(fx);
+    const float f = fx - n;
+    float p = 1.9875691500e-4f;
+    p = p * f + 1.3981999507e-3f;
+    p = p * f + 8.3334519073e-3f;
+    p = p * f + 4.1665795894e-2f;
+    p = p * f + 1.6666665459e-1f;
+    p = p * f + 5.0000001201e-1f;
+    p = p * f + 1.0f;
+    const int32_t e = (static_cast<int32_t>(n) + 127) << 23;
+    return x / (1.0f + p * __int_as_float(e));
+}
+
+__device__ __forceinline__ float apply_act(float v, int act, float slope) {
+    switch (act) {
+        case kActRelu: return v > 0.0f ? v : 0.0f;
+        case kActLeaky: return v > 0.0f ? v : v * slope;
+        case kActSigmoid: return 1.0f / (1.0f + expf(-v));
+        case kActTanh: return tanhf(v);
+        case kActSilu: return v / (1.0f + expf(-v));
+        case kActSiluWinogradForm: return silu_winograd_form(v);
+        default: return v;
+    }
+}
+
+}  // namespace k
+}  // namespace pdefa

@@ -1,0 +1,319 @@
+// pdefa_* C ABI (image / letterbox / box mapping) plus the pdefa_amd_*
+// extensions used by the benchmark and the tests.  Image decoding is not part
+// of the GPU hot path: binary PPM/PGM are read here; PNG/JPEG are reported as
+// unsupported.
+#include <algorithm>
+#include <cmath>
+#include <cstdio>
+#include <cstring>
+#include <fstream>
+#include <memory>
+#include <string>
+#include <vector>
+
+#include "../../include/pdefa_amd_ext.h"
+#include "../../include/pdefa_c_api.h"
+#include "api_internal.hpp"
+
+using pdefa::HostTensor;
+using pdefa::api::clear_error;
+using pdefa::api::guarded;
+using pdefa::api::set_error;
+
+struct PdefaImage {
+    int32_t width = 0, height = 0, channels = 0;
+    std::vector<uint8_t> pixels;  // row-major, interleaved
+};
+
+namespace {
+
+bool read_token(std::istream& in, std::string& tok) {
+    tok.clear();
+    char c;
+    while (in.get(c)) {
+        if (c == '#') {
+            std::string skip;
+            std::getline(in, skip);
+            continue;
+        }
+        if (std::isspace(static_cast<unsigned char>(c))) {
+            if (!tok.empty()) return true;
+            continue;
+        }
+        tok.push_back(c);
+    }
+    return !tok.empty();
+}
+
+// Binary PPM (P6, RGB8) and PGM (P5, GRAY8), maxval <= 255.
+std::unique_ptr<PdefaImage> load_pnm(const std::string& path, std::string* why) {
+    std::ifstream in(path, std::ios::binary);
+    if (!in) {
+        *why = "cannot open image file";
+        return nullptr;
+    }
+    std::string magic, w, h, mx;
+    if (!read_token(in, magic) || (magic != "P6" && magic != "P5")) {
+        *why = "unsupported image format (binary PPM/PGM only; PNG/JPEG decoding is not built in)";
+        return nullptr;
+    }
+    if (!read_token(in, w) || !read_token(in, h) || !read_token(in, mx)) {
+        *why = "truncated PNM header";
+        return nullptr;
+    }
+    auto img = std::make_unique<PdefaImage>();
+    img->width = std::atoi(w.c_str());
+    img->height = std::atoi(h.c_str());
+    img->channels = magic == "P6" ? 3 : 1;
+    if (img->width <= 0 || img->height <= 0 || std::atoi(mx.c_str()) > 255) {
+        *why = "unsupported PNM dimensions or depth";
+        return nullptr;
+    }
+    img->pixels.resize(static_cast<size_t>(img->width) * img->height * img->channels);
+    in.read(reinterpret_cast<char*>(img->pixels.data()), static_cast<std::streamsize>(img->pixels.size()));
+    if (static_cast<size_t>(in.gcount()) != img->pixels.size()) {
+        *why = "truncated PNM pixel data";
+        return nullptr;
+    }
+    return img;
+}
+
+// Letterbox restated from imageloader/src/preprocess.cpp:15-144: ratio =
+// min(tw/w, th/h); scaled = clamp(round(src*ratio), 1, target); centred
+// integer pads; source x = dx/ratio truncated, x0 clamped to w-2; bilinear
+// with the scale folded into the row weights; pad value written raw; NCHW.
+void letterbox(const PdefaImage& img, int tw, int th, float scale, float pad, float* out, PdefaPreprocessMeta* m) {
+    const int sw_src = img.width, sh_src = img.height, ch = img.channels;
+    const float ratio = std::min(static_cast<float>(tw) / sw_src, static_cast<float>(th) / sh_src);
+    const int sw = std::clamp(static_cast<int>(std::round(sw_src * ratio)), 1, tw);
+    const int sh = std::clamp(static_cast<int>(std::round(sh_src * ratio)), 1, th);
+    const int px = (tw - sw) / 2, py = (th - sh) / 2;
+    const size_t plane = static_cast<size_t>(tw) * th;
+    std::fill(out, out + 3 * plane, pad);
+    const float inv = 1.0f / ratio;
+    std::vector<int> x0v(sw), x1v(sw);
+    std::vector<float> fxv(sw);
+    for (int dx = 0; dx < sw; ++dx) {
+        const float sx = dx * inv;
+        int x0 = static_cast<int>(sx);
+        if (x0 > sw_src - 2 && sw_src > 1) x0 = sw_src - 2;
+        x0v[dx] = x0;
+        x1v[dx] = x0 + 1 < sw_src ? x0 + 1 : x0;
+        fxv[dx] = sx - x0;
+    }
+    const uint8_t* src = img.pixels.data();
+    for (int dy = 0; dy < sh; ++dy) {
+        const float sy = dy * inv;
+        int y0 = static_cast<int>(sy);
+        if (y0 > sh_src - 2 && sh_src > 1) y0 = sh_src - 2;
+        const int y1 = y0 + 1 < sh_src ? y0 + 1 : y0;
+        const float fy = sy - y0;
+        const float wy0 = (1.0f - fy) * scale, wy1 = fy * scale;
+        const uint8_t* r0 = src + static_cast<size_t>(y0) * sw_src * ch;
+        const uint8_t* r1 = src + static_cast<size_t>(y1) * sw_src * ch;
+        const size_t row = static_cast<size_t>(dy + py) * tw + px;
+        for (int dx = 0; dx < sw; ++dx) {
+            const int a = x0v[dx], b = x1v[dx];
+            const float w1 = fxv[dx], w0 = 1.0f - w1;
+            for (int c = 0; c < 3; ++c) {
+                const int sc = ch == 1 ? 0 : c;
+                const float v = (r0[a * ch + sc] * w0 + r0[b * ch + sc] * w1) * wy0 +
+                                (r1[a * ch + sc] * w0 + r1[b * ch + sc] * w1) * wy1;
+                out[c * plane + row + dx] = v;
+            }
+        }
+    }
+    if (m) {
+        m->target_w = tw;
+        m->target_h = th;
+        m->orig_w = sw_src;
+        m->orig_h = sh_src;
+        m->pad_x = px;
+        m->pad_y = py;
+        m->scaled_w = sw;
+        m->scaled_h = sh;
+        m->ratio = ratio;
+    }
+}
+
+EngineStatus letterbox_tensor(const PdefaImage& img, int tw, int th, float scale, float pad, EngineTensor** out,
+                              PdefaPreprocessMeta* meta) {
+    if (tw <= 0 || th <= 0) {
+        set_error("target size must be positive");
+        return ENGINE_ERR_INVALID_ARG;
+    }
+    const int64_t shape[4] = {1, 3, th, tw};
+    HostTensor t = HostTensor::empty(shape, 4, pdefa::kF32);
+    letterbox(img, tw, th, scale, pad, t.f32(), meta);
+    *out = pdefa::api::wrap(std::move(t));
+    return ENGINE_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+PDEFA_EXPORT const char* pdefa_version(void) { return engine_version(); }
+PDEFA_EXPORT const char* pdefa_last_error(void) { return pdefa::api::last_error(); }
+
+PDEFA_EXPORT PdefaImage* pdefa_image_load(const char* path) {
+    if (!path) {
+        set_error("path null");
+        return nullptr;
+    }
+    clear_error();
+    try {
+        std::string why;
+        auto img = load_pnm(path, &why);
+        if (!img) set_error(why);
+        return img.release();
+    } catch (const std::exception& e) {
+        set_error(e.what());
+        return nullptr;
+    }
+}
+
+PDEFA_EXPORT void pdefa_image_free(PdefaImage* img) { delete img; }
+PDEFA_EXPORT int32_t pdefa_image_width(const PdefaImage* img) { return img ? img->width : 0; }
+PDEFA_EXPORT int32_t pdefa_image_height(const PdefaImage* img) { return img ? img->height : 0; }
+PDEFA_EXPORT int32_t pdefa_image_channels(const PdefaImage* img) { return img ? img->channels : 0; }
+PDEFA_EXPORT int32_t pdefa_image_format(const PdefaImage* img) {
+    if (!img) return -1;
+    return img->channels == 1 ? PDEFA_PIXFMT_GRAY8 : (img->channels == 4 ? PDEFA_PIXFMT_RGBA8 : PDEFA_PIXFMT_RGB8);
+}
+PDEFA_EXPORT const uint8_t* pdefa_image_pixels(const PdefaImage* img, size_t* out_bytes) {
+    if (!img) return nullptr;
+    if (out_bytes) *out_bytes = img->pixels.size();
+    return img->pixels.data();
+}
+
+PDEFA_EXPORT EngineStatus pdefa_preprocess_letterbox(const PdefaImage* img, const PdefaPreprocessConfig* cfg,
+                                                     EngineTensor** out_tensor, PdefaPreprocessMeta* out_meta) {
+    if (!img || !cfg || !out_tensor) {
+        set_error("null arg");
+        return ENGINE_ERR_NULL_PTR;
+    }
+    *out_tensor = nullptr;
+    return guarded([&] {
+        clear_error();
+        return letterbox_tensor(*img, cfg->target_w, cfg->target_h, cfg->scale, cfg->pad_value, out_tensor, out_meta);
+    });
+}
+
+PDEFA_EXPORT EngineStatus pdefa_prepare_for_engine(const char* path, int32_t target_w, int32_t target_h, float scale,
+                                                   float pad_value, EngineTensor** out_tensor,
+                                                   PdefaPreprocessMeta* out_meta) {
+    if (!path || !out_tensor) {
+        set_error("null arg");
+        return ENGINE_ERR_NULL_PTR;
+    }
+    *out_tensor = nullptr;
+    return guarded([&] {
+        clear_error();
+        std::string why;
+        auto img = load_pnm(path, &why);
+        if (!img) {
+            set_error("prepare_for_engine failed: " + why);
+            return ENGINE_ERR_RUNTIME;
+        }
+        return letterbox_tensor(*img, target_w, target_h, scale, pad_value, out_tensor, out_meta);
+    });
+}
+
+PDEFA_EXPORT EngineStatus pdefa_load_image_as_tensor(const char* image_path, int32_t target_w, int32_t target_h,
+                                                     EngineTensor** out_tensor) {
+    return pdefa_prepare_for_engine(image_path, target_w, target_h, 1.0f / 255.0f, 0.0f, out_tensor, nullptr);
+}
+
+// imageloader/src/engine_api.cpp:59-90
+PDEFA_EXPORT EngineStatus pdefa_map_box_to_original(const float* in_box, const PdefaPreprocessMeta* meta, float* out_box) {
+    if (!in_box || !meta || !out_box) {
+        set_error("null arg");
+        return ENGINE_ERR_NULL_PTR;
+    }
+    auto mx = [&](float x) {
+        float v = (x - static_cast<float>(meta->pad_x)) / meta->ratio;
+        return v < 0.f ? 0.f : (v > static_cast<float>(meta->orig_w) ? static_cast<float>(meta->orig_w) : v);
+    };
+    auto my = [&](float y) {
+        float v = (y - static_cast<float>(meta->pad_y)) / meta->ratio;
+        return v < 0.f ? 0.f : (v > static_cast<float>(meta->orig_h) ? static_cast<float>(meta->orig_h) : v);
+    };
+    const float b[4] = {mx(in_box[0]), my(in_box[1]), mx(in_box[2]), my(in_box[3])};
+    std::memcpy(out_box, b, sizeof(b));
+    return ENGINE_OK;
+}
+
+PDEFA_EXPORT EngineStatus pdefa_map_point_to_original(float* x, float* y, const PdefaPreprocessMeta* meta) {
+    if (!x || !y || !meta) {
+        set_error("null arg");
+        return ENGINE_ERR_NULL_PTR;
+    }
+    *x = (*x - static_cast<float>(meta->pad_x)) / meta->ratio;
+    *y = (*y - static_cast<float>(meta->pad_y)) / meta->ratio;
+    if (*x < 0.f) *x = 0.f;
+    if (*y < 0.f) *y = 0.f;
+    if (*x > static_cast<float>(meta->orig_w)) *x = static_cast<float>(meta->orig_w);
+    if (*y > static_cast<float>(meta->orig_h)) *y = static_cast<float>(meta->orig_h);
+    return ENGINE_OK;
+}
+
+// ------------------------------------------------------------ extensions
+
+PDEFA_EXPORT EngineStatus pdefa_amd_session_replay(EngineSession* sess, int32_t iters, double* out_ms) {
+    if (!sess || sess->magic != kMagicSession) return ENGINE_ERR_INVALID_HANDLE;
+    if (!out_ms) return ENGINE_ERR_NULL_PTR;
+    if (iters <= 0) return ENGINE_ERR_INVALID_ARG;
+    return guarded([&] {
+        clear_error();
+        *out_ms = sess->inner->replay(iters);
+        return ENGINE_OK;
+    });
+}
+
+PDEFA_EXPORT EngineStatus pdefa_amd_session_plan(const EngineSession* sess, char* buf, size_t cap, size_t* out_len) {
+    if (!sess || sess->magic != kMagicSession) return ENGINE_ERR_INVALID_HANDLE;
+    return guarded([&] {
+        const std::string s = sess->inner->plan_text();
+        if (out_len) *out_len = s.size();
+        if (buf && cap) {
+            const size_t n = std::min(cap - 1, s.size());
+            std::memcpy(buf, s.data(), n);
+            buf[n] = '\0';
+        }
+        return ENGINE_OK;
+    });
+}
+
+PDEFA_EXPORT EngineStatus pdefa_amd_plan_model(const EngineModel* m, const int64_t* shape, int32_t ndim, char* buf,
+                                               size_t cap, size_t* out_len) {
+    if (!m || m->magic != kMagicModel) return ENGINE_ERR_INVALID_HANDLE;
+    if (!shape || ndim <= 0 || ndim > 6) return ENGINE_ERR_INVALID_ARG;
+    return guarded([&] {
+        clear_error();
+        std::vector<std::vector<int64_t>> dims(static_cast<size_t>(m->inner->num_inputs()),
+                                               std::vector<int64_t>(shape, shape + ndim));
+        pdefa::PlanOptions opt;
+        const pdefa::Plan p = pdefa::build_plan(*m->inner, dims, opt);
+        const std::string s = pdefa::describe_plan(*m->inner, p);
+        if (out_len) *out_len = s.size();
+        if (buf && cap) {
+            const size_t n = std::min(cap - 1, s.size());
+            std::memcpy(buf, s.data(), n);
+            buf[n] = '\0';
+        }
+        return ENGINE_OK;
+    });
+}
+
+PDEFA_EXPORT const char* pdefa_amd_device_name(void) {
+    static std::string name = [] {
+        if (!pdefa::device_available()) return std::string("none");
+        hipDeviceProp_t p;
+        if (hipGetDeviceProperties(&p, 0) != hipSuccess) return std::string("unknown");
+        return std::string(p.name) + " (" + p.gcnArchName + ")";
+    }();
+    return name.c_str();
+}
+
+}  // extern "C"

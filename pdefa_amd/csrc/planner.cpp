@@ -1,0 +1,1077 @@
+#include "planner.hpp"
+
+#include <algorithm>
+#include <cmath>
+#include <cstring>
+#include <map>
+#include <sstream>
+#include <stdexcept>
+#include <unordered_map>
+
+namespace pdefa {
+
+int conv_pack_bn(int cout) { return cout <= 32 ? 32 : (cout <= 64 ? 64 : 128); }
+
+namespace {
+
+using Dims = std::vector<int64_t>;
+
+[[noreturn]] void fail(const Model& m, int node, const std::string& msg) {
+    std::string where = node >= 0 && node < static_cast<int>(m.nodes.size())
+                            ? " (node " + std::to_string(node) + " '" + m.nodes[node].name + "' " +
+                                  op_name(m.nodes[node].op) + ")"
+                            : "";
+    throw std::runtime_error("plan: " + msg + where);
+}
+
+int64_t prod(const Dims& d) {
+    int64_t n = 1;
+    for (auto v : d) n *= v;
+    return n;
+}
+
+// ---------------------------------------------------------------- views ----
+VRef make_view(int32_t buf, int64_t off, const Dims& dims, const int64_t* str) {
+    VRef v;
+    v.buf = buf;
+    v.off = off;
+    v.rank = static_cast<int32_t>(dims.size());
+    for (int d = 0; d < v.rank; ++d) {
+        v.dims[d] = dims[d];
+        v.str[d] = str[d];
+    }
+    return v;
+}
+
+VRef contiguous_view(int32_t buf, const Dims& dims) {
+    int64_t str[k::kMaxRank];
+    int64_t s = 1;
+    for (int d = static_cast<int>(dims.size()) - 1; d >= 0; --d) {
+        str[d] = s;
+        s *= dims[d];
+    }
+    return make_view(buf, 0, dims, str);
+}
+
+// Channels-last: logical dim 1 gets stride 1, the others keep their order.
+VRef channels_last_view(int32_t buf, const Dims& dims) {
+    const int r = static_cast<int>(dims.size());
+    if (r < 3) return contiguous_view(buf, dims);
+    int64_t str[k::kMaxRank];
+    str[1] = 1;
+    int64_t s = dims[1];
+    for (int d = r - 1; d >= 2; --d) {
+        str[d] = s;
+        s *= dims[d];
+    }
+    str[0] = s;
+    return make_view(buf, 0, dims, str);
+}
+
+Dims dims_of(const VRef& v) { return Dims(v.dims, v.dims + v.rank); }
+
+bool views_equal(const VRef& a, const VRef& b) {
+    if (a.buf != b.buf || a.aux != b.aux || a.off != b.off || a.rank != b.rank) return false;
+    for (int d = 0; d < a.rank; ++d) {
+        if (a.dims[d] != b.dims[d]) return false;
+        if (a.dims[d] != 1 && a.str[d] != b.str[d]) return false;
+    }
+    return true;
+}
+
+VRef slice_view(VRef v, int axis, int64_t start, int64_t len, int64_t step = 1) {
+    v.off += start * v.str[axis];
+    v.dims[axis] = len;
+    v.str[axis] *= step;
+    return v;
+}
+
+VRef permute_view(const VRef& v, const std::vector<int32_t>& perm) {
+    VRef o = v;
+    for (int d = 0; d < v.rank; ++d) {
+        o.dims[d] = v.dims[perm[d]];
+        o.str[d] = v.str[perm[d]];
+    }
+    return o;
+}
+
+// Re-expresses view `v` with logical shape `nd` without moving data, when the
+// strides allow it (the no-copy reshape rule: each group of old dims that is
+// merged must be mutually contiguous).
+bool reshape_view(const VRef& v, const Dims& nd, VRef* out) {
+    if (nd.size() > static_cast<size_t>(k::kMaxRank)) return false;
+    int64_t od[k::kMaxRank], os[k::kMaxRank];
+    int orank = 0;
+    for (int d = 0; d < v.rank; ++d)
+        if (v.dims[d] != 1) {
+            od[orank] = v.dims[d];
+            os[orank++] = v.str[d];
+        }
+    int64_t ndd[k::kMaxRank], ns[k::kMaxRank];
+    int map[k::kMaxRank];
+    int nr = 0;
+    for (size_t d = 0; d < nd.size(); ++d)
+        if (nd[d] != 1) {
+            map[nr] = static_cast<int>(d);
+            ndd[nr++] = nd[d];
+        }
+    int64_t on = 1, nn = 1;
+    for (int i = 0; i < orank; ++i) on *= od[i];
+    for (int i = 0; i < nr; ++i) nn *= ndd[i];
+    if (on != nn) return false;
+    int oi = 0, oj = 1, ni = 0, nj = 1;
+    while (ni < nr && oi < orank) {
+        int64_t np = ndd[ni], op = od[oi];
+        while (np != op) {
+            if (np < op) {
+                if (nj >= nr) return false;
+                np *= ndd[nj++];
+            } else {
+                if (oj >= orank) return false;
+                op *= od[oj++];
+            }
+        }
+        for (int ok = oi; ok < oj - 1; ++ok)
+            if (os[ok] != od[ok + 1] * os[ok + 1]) return false;
+        ns[nj - 1] = os[oj - 1];
+        for (int nk = nj - 1; nk > ni; --nk) ns[nk - 1] = ns[nk] * ndd[nk];
+        ni = nj++;
+        oi = oj++;
+    }
+    VRef o = v;
+    o.rank = static_cast<int32_t>(nd.size());
+    for (size_t d = 0; d < nd.size(); ++d) {
+        o.dims[d] = nd[d];
+        o.str[d] = 0;
+    }
+    for (int i = 0; i < nr; ++i) o.str[map[i]] = ns[i];
+    *out = o;
+    return true;
+}
+
+// Broadcasts view `a` to `dims` (numpy rules, trailing alignment).
+VRef broadcast_view(const VRef& a, const Dims& dims) {
+    VRef o;
+    o.buf = a.buf;
+    o.aux = a.aux;
+    o.off = a.off;
+    o.rank = static_cast<int32_t>(dims.size());
+    const int pad = o.rank - a.rank;
+    for (int d = 0; d < o.rank; ++d) {
+        o.dims[d] = dims[d];
+        const int s = d - pad;
+        if (s < 0 || a.dims[s] == 1)
+            o.str[d] = 0;
+        else
+            o.str[d] = a.str[s];
+    }
+    return o;
+}
+
+// ------------------------------------------------------------ graph ops ----
+enum class EK { Conv, Elt, MaxPool, Resize, Softmax, Concat, Slice, Reshape, Transpose };
+
+struct EOp {
+    EK k = EK::Elt;
+    int node = -1;
+    std::vector<int32_t> in;
+    int32_t out = 0;
+    int act = 0;
+    float slope = 0.01f;
+    int32_t res = INT32_MIN;  // residual ref (conv)
+    int elt = 0;
+    float alpha = 0.0f;
+    // resolved at shape inference
+    int axis = 0;
+    std::vector<int64_t> sl_start, sl_step;  // per dim (slice)
+    std::vector<int32_t> perm;                // transpose
+    Dims target;                              // reshape
+    // concat slots (reverse pass) and which inputs need copies
+    std::vector<VRef> slots;
+    std::vector<bool> copy;
+};
+
+struct Val {
+    bool known = false;
+    Dims dims;
+    bool has_view = false;
+    VRef view;
+    int producer = -1;
+    bool is_output = false;
+    bool is_input = false;
+    int input_index = -1;
+    bool is_weight = false;
+    int weight_index = -1;
+    std::vector<int> consumers;  // eop indices
+    int nhwc_copy_buf = -1;      // graph input converted to channels-last for convs
+    VRef nhwc_view;
+};
+
+class Planner {
+   public:
+    Planner(const Model& m, const std::vector<Dims>& in_dims, const PlanOptions& opt)
+        : m_(m), in_dims_(in_dims), opt_(opt) {}
+
+    Plan run() {
+        if (in_dims_.size() != m_.graph_inputs.size())
+            throw std::runtime_error("plan: expected " + std::to_string(m_.graph_inputs.size()) + " inputs");
+        build_eops();
+        infer_shapes();
+        fuse_residuals();
+        assign_storage();
+        emit();
+        allocate();
+        return std::move(plan_);
+    }
+
+   private:
+    const Model& m_;
+    std::vector<Dims> in_dims_;
+    PlanOptions opt_;
+    std::vector<EOp> eops_;
+    std::map<int32_t, Val> vals_;
+    Plan plan_;
+
+    Val& val(int32_t ref) {
+        auto it = vals_.find(ref);
+        if (it != vals_.end()) return it->second;
+        Val& v = vals_[ref];
+        if (ref <= -1000) {
+            const int w = -1000 - ref;
+            if (w < 0 || w >= static_cast<int>(m_.weights.size())) throw std::runtime_error("plan: bad weight ref");
+            v.is_weight = true;
+            v.weight_index = w;
+            v.known = true;
+            const HostTensor& t = m_.weights[w];
+            v.dims.assign(t.dims, t.dims + t.rank);
+            v.has_view = true;
+            v.view = contiguous_view(kBufWeight, v.dims);
+            v.view.aux = w;
+        } else if (ref < 0) {
+            v.is_input = true;
+            v.input_index = -1 - ref;
+        }
+        return v;
+    }
+
+    const HostTensor& weight_tensor(int32_t ref, int node) {
+        if (ref > -1000) fail(m_, node, "expected a constant input");
+        return m_.weights[-1000 - ref];
+    }
+
+    std::vector<int64_t> const_ints(int32_t ref, int node) {
+        const HostTensor& t = weight_tensor(ref, node);
+        std::vector<int64_t> v(static_cast<size_t>(t.numel()));
+        // F32 constants are truncated toward zero, as get_tensor_int does
+        // (session_helpers.inc:156-170).
+        for (size_t i = 0; i < v.size(); ++i) v[i] = static_cast<int64_t>(t.f32()[i]);
+        return v;
+    }
+
+    int new_buf(int64_t elems) {
+        Buffer b;
+        b.elems = std::max<int64_t>(elems, 1);
+        plan_.bufs.push_back(b);
+        return static_cast<int>(plan_.bufs.size()) - 1;
+    }
+
+    // ---- 1. fused op list ------------------------------------------------
+    void build_eops() {
+        const auto& nodes = m_.nodes;
+        std::unordered_map<int32_t, int> n_cons;  // node-level consumer counts
+        for (const auto& n : nodes)
+            for (int32_t r : n.inputs) n_cons[r]++;
+        for (int32_t r : m_.graph_outputs) n_cons[r]++;
+        std::vector<bool> absorbed(nodes.size(), false);
+
+        for (size_t i = 0; i < nodes.size(); ++i) {
+            if (absorbed[i]) continue;
+            const Node& n = nodes[i];
+            EOp e;
+            e.node = static_cast<int>(i);
+            e.in = n.inputs;
+            if (n.outputs.empty()) {
+                if (n.op == kOpInput || n.op == kOpOutput) continue;
+                fail(m_, e.node, "node without outputs");
+            }
+            e.out = n.outputs[0];
+            switch (n.op) {
+                case kOpInput:
+                case kOpOutput:
+                    continue;
+                case kOpConv: {
+                    e.k = EK::Conv;
+                    if (n.inputs.size() < 2) fail(m_, e.node, "conv needs input and weight");
+                    e.act = n.params.fused_activation;
+                    e.slope = n.params.leaky_slope;
+                    const int32_t co = n.outputs[0];
+                    const int cons = n_cons[co];
+                    bool fused = false;
+                    if (cons == 2 && e.act == 0) {
+                        // Conv -> {Sigmoid, Mul(conv, sigmoid)}: SiLU (session_fusion.inc:33-81)
+                        int sig = -1, mul = -1;
+                        for (size_t j = i + 1; j < nodes.size(); ++j) {
+                            const Node& s = nodes[j];
+                            if (s.op == kOpSigmoid && s.inputs.size() == 1 && s.inputs[0] == co && !s.outputs.empty()) {
+                                if (n_cons[s.outputs[0]] == 1) sig = static_cast<int>(j);
+                                break;
+                            }
+                        }
+                        if (sig >= 0) {
+                            const int32_t so = nodes[sig].outputs[0];
+                            for (size_t j = i + 1; j < nodes.size(); ++j) {
+                                const Node& u = nodes[j];
+                                if (u.op == kOpMul && u.inputs.size() == 2 && !u.outputs.empty() &&
+                                    ((u.inputs[0] == co && u.inputs[1] == so) || (u.inputs[1] == co && u.inputs[0] == so))) {
+                                    mul = static_cast<int>(j);
+                                    break;
+                                }
+                            }
+                        }
+                        if (sig >= 0 && mul >= 0) {
+                            e.act = k::kActSilu;
+                            e.out = nodes[mul].outputs[0];
+                            absorbed[sig] = absorbed[mul] = true;
+                            fused = true;
+                        }
+                    }
+                    if (!fused && cons == 1 && e.act == 0) {
+                        // single-consumer ReLU / LeakyReLU / Sigmoid / Tanh (session_fusion.inc:85-107)
+                        for (size_t j = i + 1; j < nodes.size(); ++j) {
+                            const Node& s = nodes[j];
+                            if (s.inputs.size() == 1 && s.inputs[0] == co && !s.outputs.empty()) {
+                                int a = 0;
+                                if (s.op == kOpRelu) a = k::kActRelu;
+                                else if (s.op == kOpLeaky) a = k::kActLeaky;
+                                else if (s.op == kOpSigmoid) a = k::kActSigmoid;
+                                else if (s.op == kOpTanh) a = k::kActTanh;
+                                if (a) {
+                                    e.act = a;
+                                    if (a == k::kActLeaky) e.slope = s.params.leaky_slope;
+                                    e.out = s.outputs[0];
+                                    absorbed[j] = true;
+                                }
+                                break;
+                            }
+                        }
+                    }
+                    break;
+                }
+                case kOpSigmoid: e.k = EK::Elt; e.elt = k::kEltSigmoid; break;
+                case kOpRelu: e.k = EK::Elt; e.elt = k::kEltRelu; break;
+                case kOpTanh: e.k = EK::Elt; e.elt = k::kEltTanh; break;
+                case kOpSilu: e.k = EK::Elt; e.elt = k::kEltSilu; break;
+                case kOpLeaky: e.k = EK::Elt; e.elt = k::kEltLeaky; e.alpha = n.params.leaky_slope; break;
+                case kOpAdd: e.k = EK::Elt; e.elt = k::kEltAdd; break;
+                case kOpSub: e.k = EK::Elt; e.elt = k::kEltSub; break;
+                case kOpMul: e.k = EK::Elt; e.elt = k::kEltMul; break;
+                case kOpDiv: e.k = EK::Elt; e.elt = k::kEltDiv; break;
+                case kOpMaxPool:
+                    if (n.params.kernel_h <= 0 || n.params.kernel_w <= 0) fail(m_, e.node, "global max pool unsupported");
+                    e.k = EK::MaxPool;
+                    break;
+                case kOpResize:
+                case kOpUpsample:
+                    if (n.params.upsample_mode != 0) fail(m_, e.node, "only nearest resize is supported");
+                    e.k = EK::Resize;
+                    break;
+                case kOpSoftmax: e.k = EK::Softmax; break;
+                case kOpConcat: e.k = EK::Concat; break;
+                case kOpSlice: e.k = EK::Slice; break;
+                case kOpReshape: e.k = EK::Reshape; break;
+                case kOpTranspose: e.k = EK::Transpose; break;
+                default:
+                    fail(m_, e.node, "op not supported by the device executor");
+            }
+            if (e.k == EK::Elt) {
+                const bool binary = e.elt == k::kEltAdd || e.elt == k::kEltSub || e.elt == k::kEltMul || e.elt == k::kEltDiv;
+                if (binary && e.in.size() < 2) fail(m_, e.node, "binary op needs two inputs");
+                if (!binary) e.in.resize(1);
+            }
+            eops_.push_back(std::move(e));
+        }
+        for (size_t i = 0; i < eops_.size(); ++i) {
+            for (int32_t r : eops_[i].in) val(r).consumers.push_back(static_cast<int>(i));
+            Val& o = val(eops_[i].out);
+            if (o.producer >= 0) fail(m_, eops_[i].node, "tensor produced twice");
+            o.producer = static_cast<int>(i);
+        }
+        for (int32_t r : m_.graph_outputs) val(r).is_output = true;
+        for (size_t i = 0; i < m_.graph_inputs.size(); ++i) {
+            Val& v = val(m_.graph_inputs[i]);
+            v.is_input = true;
+            v.input_index = static_cast<int>(i);
+            v.known = true;
+            v.dims = in_dims_[i];
+        }
+    }
+
+    // ---- 2. shapes (ONNX semantics) --------------------------------------
+    const Dims& dims(int32_t r, int node) {
+        Val& v = val(r);
+        if (!v.known) fail(m_, node, "input tensor " + std::to_string(r) + " is not available");
+        return v.dims;
+    }
+
+    void infer_shapes() {
+        const int64_t batch = in_dims_.empty() || in_dims_[0].empty() ? 1 : in_dims_[0][0];
+        for (auto& e : eops_) {
+            const Node& n = m_.nodes[e.node];
+            const OpParams& p = n.params;
+            Dims out;
+            switch (e.k) {
+                case EK::Conv: {
+                    const Dims x = dims(e.in[0], e.node);
+                    const Dims w = dims(e.in[1], e.node);
+                    if (x.size() != 4 || w.size() != 4) fail(m_, e.node, "conv expects rank-4 input and weight");
+                    if (p.groups > 1) fail(m_, e.node, "grouped conv unsupported");
+                    if (x[1] != w[1]) fail(m_, e.node, "conv channel mismatch");
+                    if (!val(e.in[1]).is_weight) fail(m_, e.node, "conv weight must be a constant");
+                    if (e.in.size() > 2 && !val(e.in[2]).is_weight) fail(m_, e.node, "conv bias must be a constant");
+                    const int64_t ho = (x[2] + 2 * p.pad_h - ((w[2] - 1) * p.dil_h + 1)) / p.stride_h + 1;
+                    const int64_t wo = (x[3] + 2 * p.pad_w - ((w[3] - 1) * p.dil_w + 1)) / p.stride_w + 1;
+                    if (ho <= 0 || wo <= 0) fail(m_, e.node, "empty conv output");
+                    out = {x[0], w[0], ho, wo};
+                    break;
+                }
+                case EK::Elt: {
+                    const Dims a = dims(e.in[0], e.node);
+                    if (e.in.size() == 1) {
+                        out = a;
+                        break;
+                    }
+                    const Dims b = dims(e.in[1], e.node);
+                    const size_t r = std::max(a.size(), b.size());
+                    out.assign(r, 1);
+                    for (size_t d = 0; d < r; ++d) {
+                        const int64_t da = d < r - a.size() ? 1 : a[d - (r - a.size())];
+                        const int64_t db = d < r - b.size() ? 1 : b[d - (r - b.size())];
+                        if (da != db && da != 1 && db != 1) fail(m_, e.node, "broadcast mismatch");
+                        out[d] = std::max(da, db);
+                    }
+                    break;
+                }
+                case EK::MaxPool: {
+                    const Dims x = dims(e.in[0], e.node);
+                    if (x.size() != 4) fail(m_, e.node, "max pool expects rank 4");
+                    const int64_t ho = (x[2] + 2 * p.pad_h - p.kernel_h) / p.stride_h + 1;
+                    const int64_t wo = (x[3] + 2 * p.pad_w - p.kernel_w) / p.stride_w + 1;
+                    out = {x[0], x[1], ho, wo};
+                    break;
+                }
+                case EK::Resize: {
+                    // Target size: params, then a 4- or 2-element scales/sizes input, then 2x
+                    // (session_ops_shape.inc:110-163).
+                    const Dims x = dims(e.in[0], e.node);
+                    if (x.size() != 4) fail(m_, e.node, "resize expects rank 4");
+                    int64_t H = 0, W = 0;
+                    if (n.op == kOpUpsample) {
+                        H = x[2] * p.scale_h;
+                        W = x[3] * p.scale_w;
+                    } else {
+                        H = p.target_h;
+                        W = p.target_w;
+                        if ((H <= 0 || W <= 0) && p.scale_h > 1 && p.scale_w > 1) {
+                            H = x[2] * p.scale_h;
+                            W = x[3] * p.scale_w;
+                        }
+                        if (H <= 0 || W <= 0) {
+                            for (size_t j = 1; j < e.in.size() && j < 4; ++j) {
+                                if (!val(e.in[j]).is_weight) continue;
+                                const HostTensor& t = weight_tensor(e.in[j], e.node);
+                                if (t.numel() == 4 || t.numel() == 2) {
+                                    const int o = t.numel() == 4 ? 2 : 0;
+                                    const float s0 = t.f32()[o], s1 = t.f32()[o + 1];
+                                    if (s0 > 8.0f && s1 > 8.0f) {
+                                        H = static_cast<int64_t>(s0 + 0.5f);
+                                        W = static_cast<int64_t>(s1 + 0.5f);
+                                    } else {
+                                        H = static_cast<int64_t>(static_cast<float>(x[2]) * s0 + 0.5f);
+                                        W = static_cast<int64_t>(static_cast<float>(x[3]) * s1 + 0.5f);
+                                    }
+                                    break;
+                                }
+                            }
+                        }
+                        if (H <= 0 || W <= 0) {
+                            H = x[2] * 2;
+                            W = x[3] * 2;
+                        }
+                    }
+                    out = {x[0], x[1], H, W};
+                    break;
+                }
+                case EK::Softmax: {
+                    out = dims(e.in[0], e.node);
+                    int ax = p.axis < 0 ? p.axis + static_cast<int>(out.size()) : p.axis;
+                    if (ax < 0 || ax >= static_cast<int>(out.size())) fail(m_, e.node, "softmax axis out of range");
+                    e.axis = ax;
+                    break;
+                }
+                case EK::Concat: {
+                    const Dims a = dims(e.in[0], e.node);
+                    int ax = p.axis < 0 ? p.axis + static_cast<int>(a.size()) : p.axis;
+                    if (ax < 0 || ax >= static_cast<int>(a.size())) fail(m_, e.node, "concat axis out of range");
+                    e.axis = ax;
+                    out = a;
+                    out[ax] = 0;
+                    for (int32_t r : e.in) {
+                        const Dims b = dims(r, e.node);
+                        if (b.size() != a.size()) fail(m_, e.node, "concat rank mismatch");
+                        for (size_t d = 0; d < a.size(); ++d)
+                            if (static_cast<int>(d) != ax && b[d] != a[d]) fail(m_, e.node, "concat shape mismatch");
+                        out[ax] += b[ax];
+                    }
+                    break;
+                }
+                case EK::Slice: {
+                    const Dims x = dims(e.in[0], e.node);
+                    if (e.in.size() < 3) fail(m_, e.node, "slice needs starts and ends");
+                    const auto starts = const_ints(e.in[1], e.node);
+                    const auto ends = const_ints(e.in[2], e.node);
+                    std::vector<int64_t> axes, steps;
+                    if (e.in.size() > 3) axes = const_ints(e.in[3], e.node);
+                    if (e.in.size() > 4) steps = const_ints(e.in[4], e.node);
+                    out = x;
+                    e.sl_start.assign(x.size(), 0);
+                    e.sl_step.assign(x.size(), 1);
+                    for (size_t j = 0; j < starts.size(); ++j) {
+                        int64_t ax = axes.empty() ? static_cast<int64_t>(j) : axes[j];
+                        if (ax < 0) ax += static_cast<int64_t>(x.size());
+                        if (ax < 0 || ax >= static_cast<int64_t>(x.size())) fail(m_, e.node, "slice axis out of range");
+                        const int64_t st = steps.empty() ? 1 : steps[j];
+                        if (st <= 0) fail(m_, e.node, "only positive slice steps are supported");
+                        const int64_t d = x[ax];
+                        int64_t s = starts[j], en = ends[j];
+                        if (s < 0) s += d;
+                        if (en < 0) en += d;
+                        s = std::min(std::max<int64_t>(s, 0), d);
+                        en = std::min(std::max<int64_t>(en, 0), d);
+                        if (en < s) en = s;
+                        e.sl_start[ax] = s;
+                        e.sl_step[ax] = st;
+                        out[ax] = (en - s + st - 1) / st;
+                    }
+                    break;
+                }
+                case EK::Reshape: {
+                    const Dims x = dims(e.in[0], e.node);
+                    if (e.in.size() < 2) fail(m_, e.node, "reshape needs a shape input");
+                    auto t = const_ints(e.in[1], e.node);
+                    // The graph was exported for batch 1: a leading 1 follows the run's batch.
+                    if (!t.empty() && t[0] == 1 && !x.empty() && x[0] == batch && batch > 1) t[0] = batch;
+                    int neg = -1;
+                    int64_t known = 1;
+                    for (size_t d = 0; d < t.size(); ++d) {
+                        if (t[d] == 0) t[d] = d < x.size() ? x[d] : 1;
+                        if (t[d] == -1) neg = static_cast<int>(d);
+                        else known *= t[d];
+                    }
+                    if (neg >= 0) t[neg] = known > 0 ? prod(x) / known : 0;
+                    if (prod(t) != prod(x)) fail(m_, e.node, "reshape element count mismatch");
+                    e.target = t;
+                    out = t;
+                    break;
+                }
+                case EK::Transpose: {
+                    const Dims x = dims(e.in[0], e.node);
+                    if (e.in.size() < 2) fail(m_, e.node, "transpose needs a perm input");
+                    const auto pv = const_ints(e.in[1], e.node);
+                    if (pv.size() != x.size()) fail(m_, e.node, "perm rank mismatch");
+                    e.perm.clear();
+                    out.clear();
+                    for (auto q : pv) {
+                        const int64_t a = q < 0 ? q + static_cast<int64_t>(x.size()) : q;
+                        if (a < 0 || a >= static_cast<int64_t>(x.size())) fail(m_, e.node, "bad perm");
+                        e.perm.push_back(static_cast<int32_t>(a));
+                        out.push_back(x[a]);
+                    }
+                    break;
+                }
+            }
+            if (out.size() > static_cast<size_t>(k::kMaxRank)) fail(m_, e.node, "rank > 6 unsupported");
+            Val& o = val(e.out);
+            o.known = true;
+            o.dims = out;
+        }
+        for (int32_t r : m_.graph_outputs)
+            if (!val(r).known) throw std::runtime_error("plan: graph output " + std::to_string(r) + " is never produced");
+    }
+
+    // ---- 3. residual Add -> conv epilogue --------------------------------
+    void fuse_residuals() {
+        for (size_t i = 0; i < eops_.size(); ++i) {
+            EOp& c = eops_[i];
+            if (c.k != EK::Conv || c.res != INT32_MIN) continue;
+            Val& o = val(c.out);
+            if (o.is_output || o.consumers.size() != 1) continue;
+            EOp& a = eops_[o.consumers[0]];
+            if (a.k != EK::Elt || a.elt != k::kEltAdd || a.in.size() != 2) continue;
+            const int32_t other = a.in[0] == c.out ? a.in[1] : a.in[0];
+            if (other == c.out) continue;
+            Val& r = val(other);
+            if (r.is_weight || !r.known || r.dims != o.dims) continue;
+            if (!r.is_input && !(r.producer >= 0 && r.producer < static_cast<int>(i))) continue;
+            // conv now produces the Add's output; the Add disappears.
+            c.res = other;
+            r.consumers.erase(std::remove(r.consumers.begin(), r.consumers.end(), o.consumers[0]), r.consumers.end());
+            r.consumers.push_back(static_cast<int>(i));
+            const int32_t new_out = a.out;
+            Val& no = val(new_out);
+            no.producer = static_cast<int>(i);
+            o.consumers.clear();
+            o.producer = -1;
+            c.out = new_out;
+            a.k = EK::Elt;
+            a.elt = -1;  // dead
+        }
+        eops_.erase(std::remove_if(eops_.begin(), eops_.end(), [](const EOp& e) { return e.k == EK::Elt && e.elt == -1; }),
+                    eops_.end());
+        // re-number producers/consumers after the erase
+        for (auto& kv : vals_) {
+            kv.second.producer = -1;
+            kv.second.consumers.clear();
+        }
+        for (size_t i = 0; i < eops_.size(); ++i) {
+            for (int32_t r : eops_[i].in) val(r).consumers.push_back(static_cast<int>(i));
+            val(eops_[i].out).producer = static_cast<int>(i);
+        }
+    }
+
+    // ---- 4. storage: reverse pass with concat placement ------------------
+    bool view_kind(EK k) const { return k == EK::Slice || k == EK::Reshape || k == EK::Transpose; }
+
+    void assign_fresh(Val& v, bool contiguous) {
+        const int b = new_buf(prod(v.dims));
+        v.view = contiguous ? contiguous_view(b, v.dims) : channels_last_view(b, v.dims);
+        v.has_view = true;
+    }
+
+    // Can tensor `t` end up exactly at view `P` (a slot of concat `ce`) without a copy?
+    bool try_place(int32_t t, const VRef& P, const EOp& ce, const VRef& S) {
+        Val& v = val(t);
+        if (v.is_weight) return false;
+        if (v.has_view) return views_equal(v.view, P);
+        if (v.is_input || v.is_output || v.producer < 0) return false;
+        EOp& p = eops_[v.producer];
+        switch (p.k) {
+            case EK::Conv:
+                if (P.rank == 4 && P.str[1] != 1) return false;
+                break;
+            case EK::Elt:
+            case EK::MaxPool:
+            case EK::Resize:
+            case EK::Softmax:
+            case EK::Concat:
+                break;
+            case EK::Reshape: {
+                VRef q;
+                if (!reshape_view(P, val(p.in[0]).dims, &q)) return false;
+                if (!try_place(p.in[0], q, ce, S)) return false;
+                break;
+            }
+            case EK::Transpose: {
+                std::vector<int32_t> inv(p.perm.size());
+                for (size_t d = 0; d < p.perm.size(); ++d) inv[p.perm[d]] = static_cast<int32_t>(d);
+                if (!try_place(p.in[0], permute_view(P, inv), ce, S)) return false;
+                break;
+            }
+            case EK::Slice: {
+                // Only a single-axis, step-1 slice along the concat axis can be undone.
+                const Dims& ud = val(p.in[0]).dims;
+                int ax = -1;
+                for (size_t d = 0; d < ud.size(); ++d) {
+                    if (p.sl_step[d] != 1) return false;
+                    if (p.sl_start[d] != 0 || ud[d] != v.dims[d]) {
+                        if (ax >= 0) return false;
+                        ax = static_cast<int>(d);
+                    }
+                }
+                if (ax < 0 || ax != ce.axis) return false;
+                // P must be a slot of S along the concat axis.
+                if (P.rank != S.rank || P.buf != S.buf) return false;
+                for (int d = 0; d < S.rank; ++d) {
+                    if (P.str[d] != S.str[d]) return false;
+                    if (d != ax && P.dims[d] != S.dims[d]) return false;
+                }
+                // The slot's position inside S along the axis:
+                const int64_t pos = (P.off - S.off) / std::max<int64_t>(1, S.str[ax]);
+                const int64_t base = pos - p.sl_start[ax];
+                if (base < 0 || base + ud[ax] > S.dims[ax]) return false;
+                // Every other input of `ce` overlapping [base, base + ud[ax]) must be a
+                // slice of the same tensor sitting at its matching position.
+                int64_t off = 0;
+                for (size_t j = 0; j < ce.in.size(); ++j) {
+                    const int64_t len = val(ce.in[j]).dims[ce.axis];
+                    const bool overlap = off < base + ud[ax] && off + len > base;
+                    if (overlap && ce.in[j] != t) {
+                        Val& oj = val(ce.in[j]);
+                        if (oj.producer < 0) return false;
+                        const EOp& pj = eops_[oj.producer];
+                        if (pj.k != EK::Slice || pj.in[0] != p.in[0] || off != base + pj.sl_start[ax]) return false;
+                    }
+                    off += len;
+                }
+                VRef q = P;
+                q.off -= p.sl_start[ax] * P.str[ax];
+                q.dims[ax] = ud[ax];
+                if (!try_place(p.in[0], q, ce, S)) return false;
+                break;
+            }
+        }
+        v.view = P;
+        v.has_view = true;
+        return true;
+    }
+
+    void assign_storage() {
+        for (int i = static_cast<int>(eops_.size()) - 1; i >= 0; --i) {
+            EOp& e = eops_[i];
+            Val& o = val(e.out);
+            if (!o.has_view) {
+                if (view_kind(e.k)) {
+                    if (o.is_output) assign_fresh(o, true);  // materialised by a copy
+                } else {
+                    // A conv writes channels-last even for a graph output; the
+                    // output is then copied to its contiguous buffer.
+                    assign_fresh(o, o.is_output && e.k != EK::Conv);
+                }
+            }
+            if (e.k == EK::Concat) {
+                const VRef S = o.view;
+                int64_t off = 0;
+                e.slots.clear();
+                e.copy.clear();
+                for (int32_t t : e.in) {
+                    const int64_t len = val(t).dims[e.axis];
+                    const VRef P = slice_view(S, e.axis, off, len);
+                    e.slots.push_back(P);
+                    e.copy.push_back(!try_place(t, P, e, S));
+                    off += len;
+                }
+            }
+        }
+    }
+
+    // ---- 5. steps ---------------------------------------------------------
+    VRef input_view(int32_t r) {
+        Val& v = val(r);
+        if (v.is_input && !v.has_view) {
+            const int b = new_buf(prod(v.dims));
+            plan_.input_bufs[v.input_index] = b;
+            v.view = contiguous_view(b, v.dims);
+            v.has_view = true;
+        }
+        if (!v.has_view) throw std::runtime_error("plan: tensor " + std::to_string(r) + " has no storage");
+        return v.view;
+    }
+
+    void emit_copy(int node, const VRef& dst, const VRef& src) {
+        Step s;
+        s.kind = StepKind::Elt;
+        s.node = node;
+        s.elt = k::kEltCopy;
+        s.out = dst;
+        s.a = src;
+        s.b = src;
+        plan_.steps.push_back(s);
+        plan_.n_copies++;
+    }
+
+    // Channels-last copy of a graph input, made once, for conv consumers.
+    VRef conv_input_view(int32_t r, int node) {
+        VRef x = input_view(r);
+        Val& v = val(r);
+        if (x.rank == 4 && x.str[1] != 1 && v.is_input) {
+            if (v.nhwc_copy_buf < 0) {
+                v.nhwc_copy_buf = new_buf(prod(v.dims));
+                v.nhwc_view = channels_last_view(v.nhwc_copy_buf, v.dims);
+                emit_copy(node, v.nhwc_view, x);
+                plan_.n_copies--;  // the layout change of the input is expected
+            }
+            return v.nhwc_view;
+        }
+        return x;
+    }
+
+    void emit_conv(const EOp& e) {
+        const Node& n = m_.nodes[e.node];
+        const OpParams& p = n.params;
+        const Dims& wd = val(e.in[1]).dims;
+        const VRef x = conv_input_view(e.in[0], e.node);
+        const VRef y = val(e.out).view;
+        Step s;
+        s.node = e.node;
+        s.out = y;
+        s.a = x;
+        s.KH = static_cast<int32_t>(wd[2]);
+        s.KW = static_cast<int32_t>(wd[3]);
+        s.sh = static_cast<int32_t>(p.stride_h);
+        s.sw = static_cast<int32_t>(p.stride_w);
+        s.ph = static_cast<int32_t>(p.pad_h);
+        s.pw = static_cast<int32_t>(p.pad_w);
+        s.dh = static_cast<int32_t>(p.dil_h);
+        s.dw = static_cast<int32_t>(p.dil_w);
+        const int64_t cin = wd[1], cout = wd[0];
+        s.act = e.act;
+        s.slope = e.slope;
+        // The reference routes 3x3/s1/d1 convs with 16 < Cin <= 512 to its Winograd
+        // kernel (conv2d.cpp:602-631), whose fused SiLU is the polynomial form.
+        const bool winograd = s.KH == 3 && s.KW == 3 && s.sh == 1 && s.sw == 1 && s.dh == 1 && s.dw == 1 && cin > 16 &&
+                              cin <= 512;
+        if (s.act == k::kActSilu && winograd && opt_.winograd_form_silu) s.act = k::kActSiluWinogradForm;
+        if (e.res != INT32_MIN) {
+            s.has_res = true;
+            s.res = input_view(e.res);
+        }
+        const bool cl = x.str[1] == 1 && y.str[1] == 1 && (!s.has_res || s.res.str[1] == 1);
+        if (cl && cout >= 8) {
+            s.kind = StepKind::ConvMfma;
+            s.vec = cin % 4 == 0 && x.off % 4 == 0 && x.str[0] % 4 == 0 && x.str[2] % 4 == 0 && x.str[3] % 4 == 0;
+            const int bn = conv_pack_bn(static_cast<int>(cout));
+            const int64_t M = y.dims[0] * y.dims[2] * y.dims[3];
+            const int64_t nt = (cout + bn - 1) / bn;
+            if (bn == 32) {
+                s.tile = k::kTile128x32;
+            } else {
+                const bool big = ((M + 127) / 128) * nt >= 256;
+                s.tile = bn == 64 ? (big ? k::kTile128x64 : k::kTile64x64) : (big ? k::kTile128x128 : k::kTile64x128);
+            }
+            const int bm = k::conv_tile_bm(s.tile);
+            const int64_t K = cin * s.KH * s.KW;
+            const int ktiles = static_cast<int>((K + k::kConvBK - 1) / k::kConvBK);
+            const int64_t wgs = ((M + bm - 1) / bm) * nt;
+            int splits = 1;
+            if (opt_.split_k && wgs < 128 && ktiles >= 32) {
+                splits = static_cast<int>(std::min<int64_t>({16, ktiles / 16, (256 + wgs - 1) / wgs}));
+                splits = std::max(splits, 1);
+            }
+            s.kt_per_split = (ktiles + splits - 1) / splits;
+            s.splits = (ktiles + s.kt_per_split - 1) / s.kt_per_split;
+            if (s.splits > 1) s.ws_buf = new_buf(static_cast<int64_t>(s.splits) * M * cout);
+        } else {
+            s.kind = StepKind::ConvDirect;
+        }
+        plan_.steps.push_back(s);
+    }
+
+    void emit() {
+        plan_.input_dims = in_dims_;
+        plan_.input_bufs.assign(m_.graph_inputs.size(), -1);
+        for (int32_t r : m_.graph_inputs) input_view(r);
+        for (auto& e : eops_) {
+            Val& o = val(e.out);
+            switch (e.k) {
+                case EK::Conv:
+                    emit_conv(e);
+                    break;
+                case EK::Elt: {
+                    Step s;
+                    s.kind = StepKind::Elt;
+                    s.node = e.node;
+                    s.elt = e.elt;
+                    s.alpha = e.alpha;
+                    s.out = o.view;
+                    s.a = broadcast_view(input_view(e.in[0]), o.dims);
+                    s.b = e.in.size() > 1 ? broadcast_view(input_view(e.in[1]), o.dims) : s.a;
+                    plan_.steps.push_back(s);
+                    break;
+                }
+                case EK::MaxPool: {
+                    const OpParams& p = m_.nodes[e.node].params;
+                    Step s;
+                    s.kind = StepKind::MaxPool;
+                    s.node = e.node;
+                    s.out = o.view;
+                    s.a = input_view(e.in[0]);
+                    s.KH = static_cast<int32_t>(p.kernel_h);
+                    s.KW = static_cast<int32_t>(p.kernel_w);
+                    s.sh = static_cast<int32_t>(p.stride_h);
+                    s.sw = static_cast<int32_t>(p.stride_w);
+                    s.ph = static_cast<int32_t>(p.pad_h);
+                    s.pw = static_cast<int32_t>(p.pad_w);
+                    plan_.steps.push_back(s);
+                    break;
+                }
+                case EK::Resize: {
+                    Step s;
+                    s.kind = StepKind::Resize;
+                    s.node = e.node;
+                    s.out = o.view;
+                    s.a = input_view(e.in[0]);
+                    plan_.steps.push_back(s);
+                    break;
+                }
+                case EK::Softmax: {
+                    Step s;
+                    s.kind = StepKind::Softmax;
+                    s.node = e.node;
+                    s.out = o.view;
+                    s.a = input_view(e.in[0]);
+                    s.axis = e.axis;
+                    plan_.steps.push_back(s);
+                    break;
+                }
+                case EK::Concat:
+                    for (size_t j = 0; j < e.in.size(); ++j)
+                        if (e.copy[j]) emit_copy(e.node, e.slots[j], input_view(e.in[j]));
+                    break;
+                case EK::Slice:
+                case EK::Reshape:
+                case EK::Transpose: {
+                    VRef src = input_view(e.in[0]);
+                    VRef f;
+                    if (e.k == EK::Slice) {
+                        f = src;
+                        for (int d = 0; d < f.rank; ++d) f = slice_view(f, d, e.sl_start[d], o.dims[d], e.sl_step[d]);
+                    } else if (e.k == EK::Transpose) {
+                        f = permute_view(src, e.perm);
+                    } else if (!reshape_view(src, e.target, &f)) {
+                        // materialise in logical order, then the reshape is a view
+                        const Dims sd = dims_of(src);
+                        const int b = new_buf(prod(sd));
+                        const VRef tmp = contiguous_view(b, sd);
+                        emit_copy(e.node, tmp, src);
+                        if (!reshape_view(tmp, e.target, &f)) fail(m_, e.node, "reshape failed");
+                    }
+                    if (o.has_view) {
+                        if (!views_equal(f, o.view)) emit_copy(e.node, o.view, f);
+                    } else {
+                        o.view = f;
+                        o.has_view = true;
+                    }
+                    break;
+                }
+            }
+        }
+        for (int32_t r : m_.graph_outputs) {
+            Val& v = val(r);
+            VRef ov = v.view;
+            // graph outputs must be contiguous in logical order for the host copy
+            const VRef want = contiguous_view(ov.buf, v.dims);
+            if (ov.off != 0 || !views_equal(ov, want)) {
+                const int b = new_buf(prod(v.dims));
+                const VRef dst = contiguous_view(b, v.dims);
+                emit_copy(-1, dst, ov);
+                ov = dst;
+            }
+            plan_.outputs.push_back(ov);
+            plan_.output_dims.push_back(v.dims);
+        }
+    }
+
+    // ---- 6. liveness + arena ----------------------------------------------
+    void touch(const VRef& v, int step) {
+        if (v.buf < 0) return;
+        Buffer& b = plan_.bufs[v.buf];
+        b.first = std::min(b.first, step);
+        b.last = std::max(b.last, step);
+    }
+
+    void allocate() {
+        const int n = static_cast<int>(plan_.steps.size());
+        for (int i = 0; i < n; ++i) {
+            const Step& s = plan_.steps[i];
+            touch(s.out, i);
+            touch(s.a, i);
+            if (s.kind == StepKind::Elt) touch(s.b, i);
+            if (s.has_res) touch(s.res, i);
+            if (s.ws_buf >= 0) {
+                plan_.bufs[s.ws_buf].first = std::min(plan_.bufs[s.ws_buf].first, i);
+                plan_.bufs[s.ws_buf].last = std::max(plan_.bufs[s.ws_buf].last, i);
+            }
+        }
+        for (int b : plan_.input_bufs) {
+            plan_.bufs[b].first = -1;
+            plan_.bufs[b].last = std::max(plan_.bufs[b].last, -1);
+        }
+        for (const VRef& o : plan_.outputs) {
+            plan_.bufs[o.buf].first = std::min(plan_.bufs[o.buf].first, n);
+            plan_.bufs[o.buf].last = n;
+        }
+        // Greedy by size: each buffer takes the lowest 256-byte aligned offset that
+        // does not overlap a live-range-overlapping buffer already placed.
+        std::vector<int> order(plan_.bufs.size());
+        for (size_t i = 0; i < order.size(); ++i) order[i] = static_cast<int>(i);
+        std::sort(order.begin(), order.end(), [&](int a, int b) {
+            if (plan_.bufs[a].elems != plan_.bufs[b].elems) return plan_.bufs[a].elems > plan_.bufs[b].elems;
+            return a < b;
+        });
+        constexpr int64_t kAlign = 64;  // floats
+        std::vector<int> placed;
+        int64_t top = 0;
+        for (int id : order) {
+            Buffer& b = plan_.bufs[id];
+            if (b.last < b.first) {  // never used
+                b.first = b.last = 0;
+            }
+            std::vector<std::pair<int64_t, int64_t>> busy;
+            for (int q : placed) {
+                const Buffer& o = plan_.bufs[q];
+                if (o.first <= b.last && b.first <= o.last) busy.push_back({o.offset, o.offset + o.elems});
+            }
+            std::sort(busy.begin(), busy.end());
+            int64_t off = 0;
+            for (auto& iv : busy) {
+                if (off + b.elems <= iv.first) break;
+                off = std::max(off, (iv.second + kAlign - 1) / kAlign * kAlign);
+            }
+            b.offset = off;
+            top = std::max(top, off + (b.elems + kAlign - 1) / kAlign * kAlign);
+            placed.push_back(id);
+        }
+        plan_.arena_elems = top;
+    }
+};
+
+const char* step_kind_name(StepKind k) {
+    switch (k) {
+        case StepKind::ConvMfma: return "conv_mfma";
+        case StepKind::ConvDirect: return "conv_direct";
+        case StepKind::Elt: return "eltwise";
+        case StepKind::MaxPool: return "maxpool";
+        case StepKind::Resize: return "resize";
+        case StepKind::Softmax: return "softmax";
+    }
+    return "?";
+}
+
+std::string fmt_view(const VRef& v) {
+    std::ostringstream os;
+    os << "b" << v.buf << "+" << v.off << "[";
+    for (int d = 0; d < v.rank; ++d) os << (d ? "," : "") << v.dims[d];
+    os << "]s[";
+    for (int d = 0; d < v.rank; ++d) os << (d ? "," : "") << v.str[d];
+    os << "]";
+    return os.str();
+}
+
+}  // namespace
+
+Plan build_plan(const Model& m, const std::vector<std::vector<int64_t>>& input_dims, const PlanOptions& opt) {
+    Planner p(m, input_dims, opt);
+    return p.run();
+}
+
+std::string describe_plan(const Model& m, const Plan& p) {
+    std::ostringstream os;
+    os << "steps=" << p.steps.size() << " bufs=" << p.bufs.size() << " arena_bytes=" << p.arena_elems * 4
+       << " copies=" << p.n_copies << "\n";
+    for (size_t i = 0; i < p.steps.size(); ++i) {
+        const Step& s = p.steps[i];
+        os << i << " " << step_kind_name(s.kind);
+        if (s.kind == StepKind::Elt) os << "(" << s.elt << ")";
+        if (s.kind == StepKind::ConvMfma)
+            os << "(tile=" << s.tile << ",vec=" << s.vec << ",splits=" << s.splits << ",act=" << s.act << ")";
+        if (s.kind == StepKind::ConvDirect) os << "(act=" << s.act << ")";
+        os << " node=" << s.node;
+        if (s.node >= 0) os << " '" << m.nodes[s.node].name << "'";
+        os << " out=" << fmt_view(s.out) << " a=" << fmt_view(s.a);
+        if (s.kind == StepKind::Elt && s.elt >= k::kEltAdd && s.elt <= k::kEltDiv) os << " b=" << fmt_view(s.b);
+        if (s.has_res) os << " res=" << fmt_view(s.res);
+        os << "\n";
+    }
+    return os.str();
+}
+
+}  // namespace pdefa

@@ -1,0 +1,89 @@
+// Lowers an `.engine` graph to a fixed device program for one input shape.
+//
+// Semantics are the ONNX operator semantics the reference session realises on
+// the YOLOv8 path (PDEFA1.0/src/core/session.cpp:181-425 and
+// session_parts/*.inc); layout is the planner's own: every rank-3/4
+// intermediate is channels-last in one HBM arena, Slice/Reshape/Transpose are
+// strided views, Concat inputs are written by their producers straight into
+// the concat buffer, Conv -> Sigmoid -> Mul becomes the conv's SiLU epilogue
+// (the fusion of session_fusion.inc:33-107) and a C2f residual Add becomes a
+// conv epilogue add.
+#pragma once
+
+#include <climits>
+#include <cstdint>
+#include <string>
+#include <vector>
+
+#include "kernels.hpp"
+#include "model.hpp"
+
+namespace pdefa {
+
+constexpr int32_t kBufWeight = -2;  // VRef::buf for a model weight (aux = weight index)
+
+// A strided view of a planned buffer (or of a model weight).
+struct VRef {
+    int32_t buf = -1;
+    int32_t aux = 0;
+    int64_t off = 0;
+    int32_t rank = 0;
+    int64_t dims[k::kMaxRank] = {0, 0, 0, 0, 0, 0};
+    int64_t str[k::kMaxRank] = {0, 0, 0, 0, 0, 0};
+};
+
+enum class StepKind : int32_t { ConvMfma, ConvDirect, Elt, MaxPool, Resize, Softmax };
+
+struct Step {
+    StepKind kind = StepKind::Elt;
+    int32_t node = -1;  // graph node the step implements (first of a fused group)
+    VRef out, a, b, res;
+    bool has_res = false;
+    // conv
+    int32_t act = 0;
+    float slope = 0.01f;
+    int32_t KH = 1, KW = 1, sh = 1, sw = 1, ph = 0, pw = 0, dh = 1, dw = 1;
+    int32_t tile = 0;
+    bool vec = false;
+    int32_t splits = 1, kt_per_split = 0;
+    int32_t ws_buf = -1;
+    // eltwise
+    int32_t elt = 0;
+    float alpha = 0.0f;
+    // softmax
+    int32_t axis = 0;
+};
+
+struct Buffer {
+    int64_t elems = 0;
+    int32_t first = INT32_MAX;
+    int32_t last = -1;
+    int64_t offset = 0;  // elements from the arena base
+};
+
+struct Plan {
+    std::vector<std::vector<int64_t>> input_dims;
+    std::vector<int32_t> input_bufs;          // contiguous NCHW staging, one per graph input
+    std::vector<VRef> outputs;                // contiguous views, graph_outputs order
+    std::vector<std::vector<int64_t>> output_dims;
+    std::vector<Step> steps;
+    std::vector<Buffer> bufs;
+    int64_t arena_elems = 0;
+    int32_t n_copies = 0;                     // materialising copies the planner could not avoid
+};
+
+// Tile width the packed weights of a conv with `cout` outputs use.
+int conv_pack_bn(int cout);
+
+struct PlanOptions {
+    bool split_k = true;
+    bool winograd_form_silu = true;  // match the reference's Winograd-layer SiLU
+};
+
+// Throws std::runtime_error naming the node for an unsupported op or pattern.
+Plan build_plan(const Model& m, const std::vector<std::vector<int64_t>>& input_dims, const PlanOptions& opt);
+
+// Human-readable dump (one line per step) for tests and debugging.
+std::string describe_plan(const Model& m, const Plan& p);
+
+}  // namespace pdefa

@@ -1,0 +1,589 @@
+#include "runtime.hpp"
+
+#include <algorithm>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <mutex>
+#include <sstream>
+
+namespace pdefa {
+
+void hip_check(hipError_t e, const char* expr, const char* file, int line) {
+    if (e == hipSuccess) return;
+    std::ostringstream os;
+    os << "HIP error " << hipGetErrorName(e) << " (" << hipGetErrorString(e) << ") at " << expr << " [" << file << ":"
+       << line << "]";
+    throw HipError(e, os.str());
+}
+
+bool device_available() {
+    static int cached = -1;
+    if (cached < 0) {
+        int n = 0;
+        cached = (hipGetDeviceCount(&n) == hipSuccess && n > 0) ? 1 : 0;
+    }
+    return cached == 1;
+}
+
+namespace {
+
+bool env_flag(const char* name, bool dflt) {
+    const char* v = std::getenv(name);
+    if (!v || !*v) return dflt;
+    return !(v[0] == '0' || v[0] == 'n' || v[0] == 'N' || v[0] == 'f' || v[0] == 'F');
+}
+
+constexpr size_t kAlignFloats = 64;
+size_t align_up(size_t n) { return (n + kAlignFloats - 1) / kAlignFloats * kAlignFloats; }
+
+}  // namespace
+
+DeviceModel::~DeviceModel() {
+    if (blob) (void)hipFree(blob);
+}
+
+std::shared_ptr<DeviceModel> upload_model(const Model& m) {
+    auto dm = std::make_shared<DeviceModel>();
+    PDEFA_HIP(hipGetDevice(&dm->device));
+    std::vector<size_t> woff(m.weights.size());
+    size_t total = 0;
+    for (size_t i = 0; i < m.weights.size(); ++i) {
+        woff[i] = total;
+        total += align_up(static_cast<size_t>(std::max<int64_t>(1, m.weights[i].numel())));
+    }
+    struct PackPlan {
+        size_t node, wpk_off, bias_off;
+        int cout, cin, kh, kw, bn, w, b;
+    };
+    std::vector<PackPlan> pp;
+    for (size_t i = 0; i < m.nodes.size(); ++i) {
+        const Node& n = m.nodes[i];
+        if (n.op != kOpConv || n.inputs.size() < 2 || n.inputs[1] > -1000) continue;
+        const int w = -1000 - n.inputs[1];
+        if (w >= static_cast<int>(m.weights.size()) || m.weights[w].rank != 4) continue;
+        const HostTensor& wt = m.weights[w];
+        PackPlan p{};
+        p.node = i;
+        p.cout = static_cast<int>(wt.dims[0]);
+        p.cin = static_cast<int>(wt.dims[1]);
+        p.kh = static_cast<int>(wt.dims[2]);
+        p.kw = static_cast<int>(wt.dims[3]);
+        p.bn = conv_pack_bn(p.cout);
+        p.w = w;
+        p.b = (n.inputs.size() > 2 && n.inputs[2] <= -1000) ? -1000 - n.inputs[2] : -1;
+        if (p.b >= 0 && m.weights[p.b].numel() < p.cout) p.b = -1;
+        p.wpk_off = total;
+        total += align_up(static_cast<size_t>(k::packed_weight_elems(p.cout, p.kh * p.kw * p.cin, p.bn)));
+        p.bias_off = total;
+        total += align_up(static_cast<size_t>((p.cout + p.bn - 1) / p.bn * p.bn));
+        pp.push_back(p);
+    }
+    total = std::max<size_t>(total, kAlignFloats);
+    // Host image of the blob: raw weights + zeroed pack/bias regions (biases filled in).
+    std::vector<float> host(total, 0.0f);
+    for (size_t i = 0; i < m.weights.size(); ++i)
+        if (m.weights[i].nbytes) std::memcpy(host.data() + woff[i], m.weights[i].data, m.weights[i].nbytes);
+    for (const auto& p : pp)
+        if (p.b >= 0) std::memcpy(host.data() + p.bias_off, m.weights[p.b].data, sizeof(float) * p.cout);
+    dm->blob_bytes = total * sizeof(float);
+    PDEFA_HIP(hipMalloc(&dm->blob, dm->blob_bytes));
+    PDEFA_HIP(hipMemcpy(dm->blob, host.data(), dm->blob_bytes, hipMemcpyHostToDevice));
+    dm->wptr.resize(m.weights.size());
+    for (size_t i = 0; i < m.weights.size(); ++i) dm->wptr[i] = dm->blob + woff[i];
+    dm->packs.resize(m.nodes.size());
+    hipStream_t s;
+    PDEFA_HIP(hipStreamCreateWithFlags(&s, hipStreamNonBlocking));
+    try {
+        for (const auto& p : pp) {
+            DeviceModel::Pack& pk = dm->packs[p.node];
+            pk.wpk = dm->blob + p.wpk_off;
+            pk.bias = dm->blob + p.bias_off;
+            pk.bn = p.bn;
+            k::launch_pack_conv_weights(pk.wpk, dm->wptr[p.w], p.cout, p.cin, p.kh, p.kw, p.bn, s);
+            PDEFA_HIP(hipGetLastError());
+        }
+        PDEFA_HIP(hipStreamSynchronize(s));
+    } catch (...) {
+        (void)hipStreamDestroy(s);
+        throw;
+    }
+    PDEFA_HIP(hipStreamDestroy(s));
+    return dm;
+}
+
+std::shared_ptr<DeviceModel> device_model(Model& m) {
+    std::lock_guard<std::mutex> g(m.device_mu);
+    if (!m.device) m.device = upload_model(m);
+    return m.device;
+}
+
+// ------------------------------------------------------------------ Session
+
+Session::Session(Model& m) : model_(&m) {
+    inputs_.assign(static_cast<size_t>(m.num_inputs()), nullptr);
+    use_graph_ = env_flag("PDEFA_HIP_GRAPH", true);
+    opts_.split_k = env_flag("PDEFA_SPLITK", true);
+    const char* silu = std::getenv("PDEFA_SILU");
+    opts_.winograd_form_silu = !(silu && std::strcmp(silu, "exact") == 0);
+}
+
+Session::~Session() {
+    try {
+        release_prepared();
+    } catch (...) {
+    }
+    if (stream_) (void)hipStreamDestroy(stream_);
+}
+
+void Session::set_input(int32_t idx, const HostTensor* t) {
+    if (idx < 0 || idx >= static_cast<int32_t>(inputs_.size())) return;  // ignored, as the reference does
+    inputs_[idx] = t;
+}
+
+const HostTensor* Session::output(int32_t idx) const {
+    if (!prep_ || idx < 0 || idx >= static_cast<int32_t>(prep_->outputs.size())) return nullptr;
+    if (runs == 0) return nullptr;
+    return &prep_->outputs[idx];
+}
+
+void Session::release_prepared() {
+    if (!prep_) return;
+    if (stream_) (void)hipStreamSynchronize(stream_);
+    if (prep_->exec) (void)hipGraphExecDestroy(prep_->exec);
+    if (prep_->graph) (void)hipGraphDestroy(prep_->graph);
+    if (prep_->arena) (void)hipFree(prep_->arena);
+    for (float* h : prep_->host_out)
+        if (h) (void)hipHostFree(h);
+    prep_.reset();
+}
+
+namespace {
+
+int64_t view_extent_check(const VRef& r, int64_t limit, const char* what, int step) {
+    int64_t lo = r.off, hi = r.off;
+    for (int d = 0; d < r.rank; ++d) {
+        if (r.dims[d] <= 0) return 0;
+        const int64_t span = (r.dims[d] - 1) * r.str[d];
+        if (span >= 0) hi += span;
+        else lo += span;
+    }
+    if (lo < 0 || hi >= limit) {
+        std::ostringstream os;
+        os << "plan view out of bounds (" << what << ", step " << step << "): [" << lo << ", " << hi << "] vs " << limit;
+        throw std::runtime_error(os.str());
+    }
+    return hi;
+}
+
+std::string step_label(const Model& m, const Step& s, int idx) {
+    std::ostringstream os;
+    if (s.node >= 0) {
+        const Node& n = m.nodes[s.node];
+        os << "node_" << s.node << "_op" << n.op << " '" << n.name << "' [";
+    } else {
+        os << "step_" << idx << "_copy 'output' [";
+    }
+    for (int d = 0; d < s.out.rank; ++d) os << (d ? "," : "") << s.out.dims[d];
+    os << "]";
+    return os.str();
+}
+
+}  // namespace
+
+void Session::prepare(const std::vector<std::vector<int64_t>>& dims) {
+    release_prepared();
+    auto p = std::make_unique<Prepared>();
+    p->plan = build_plan(*model_, dims, opts_);
+    const Plan& plan = p->plan;
+    PDEFA_HIP(hipMalloc(&p->arena, static_cast<size_t>(std::max<int64_t>(plan.arena_elems, 64)) * sizeof(float)));
+    prep_ = std::move(p);  // owned from here so a throw below releases it
+
+    auto V = [&](const VRef& r, const char* what, int step) -> k::View {
+        k::View v;
+        int64_t limit;
+        float* base;
+        if (r.buf == kBufWeight) {
+            base = dev_->wptr.at(r.aux);
+            limit = std::max<int64_t>(1, model_->weights.at(r.aux).numel());
+        } else {
+            const Buffer& b = plan.bufs.at(r.buf);
+            base = prep_->arena + b.offset;
+            limit = b.elems;
+        }
+        view_extent_check(r, limit, what, step);
+        v.ptr = base + r.off;
+        v.rank = r.rank;
+        for (int d = 0; d < r.rank; ++d) {
+            v.dims[d] = r.dims[d];
+            v.str[d] = r.str[d];
+        }
+        return v;
+    };
+
+    for (size_t i = 0; i < plan.steps.size(); ++i) {
+        const Step& s = plan.steps[i];
+        const int si = static_cast<int>(i);
+        Launch l;
+        l.kind = s.kind;
+        l.label = step_label(*model_, s, si);
+        switch (s.kind) {
+            case StepKind::ConvMfma: {
+                const Node& n = model_->nodes.at(s.node);
+                const DeviceModel::Pack& pk = dev_->packs.at(s.node);
+                if (!pk.wpk) throw std::runtime_error("conv weights were not packed: " + n.name);
+                if (pk.bn != k::conv_tile_bn(s.tile)) throw std::runtime_error("pack width does not match tile");
+                const k::View x = V(s.a, "conv x", si), y = V(s.out, "conv y", si);
+                if (x.str[1] != 1 || y.str[1] != 1) throw std::runtime_error("conv_mfma needs channels-last views");
+                k::ConvArgs& c = l.conv;
+                c.x = x.ptr;
+                c.N = static_cast<int32_t>(x.dims[0]);
+                c.Cin = static_cast<int32_t>(x.dims[1]);
+                c.H = static_cast<int32_t>(x.dims[2]);
+                c.W = static_cast<int32_t>(x.dims[3]);
+                c.x_sn = x.str[0];
+                c.x_sh = x.str[2];
+                c.x_sw = x.str[3];
+                c.y = y.ptr;
+                c.Cout = static_cast<int32_t>(y.dims[1]);
+                c.Ho = static_cast<int32_t>(y.dims[2]);
+                c.Wo = static_cast<int32_t>(y.dims[3]);
+                c.y_sn = y.str[0];
+                c.y_sh = y.str[2];
+                c.y_sw = y.str[3];
+                if (s.has_res) {
+                    const k::View r = V(s.res, "conv res", si);
+                    if (r.str[1] != 1) throw std::runtime_error("conv residual must be channels-last");
+                    c.res = r.ptr;
+                    c.r_sn = r.str[0];
+                    c.r_sh = r.str[2];
+                    c.r_sw = r.str[3];
+                }
+                const HostTensor& wt = model_->weights.at(-1000 - n.inputs[1]);
+                if (wt.dims[0] != c.Cout || wt.dims[1] != c.Cin) throw std::runtime_error("conv weight shape mismatch");
+                c.wpk = pk.wpk;
+                c.bias = pk.bias;
+                c.KH = s.KH;
+                c.KW = s.KW;
+                c.sh = s.sh;
+                c.sw = s.sw;
+                c.ph = s.ph;
+                c.pw = s.pw;
+                c.dh = s.dh;
+                c.dw = s.dw;
+                c.K = c.KH * c.KW * c.Cin;
+                c.ktiles = (c.K + k::kConvBK - 1) / k::kConvBK;
+                c.act = s.act;
+                c.slope = s.slope;
+                c.splits = s.splits;
+                c.kt_per_split = s.kt_per_split;
+                if (s.splits > 1) {
+                    const Buffer& wb = plan.bufs.at(s.ws_buf);
+                    const int64_t need = static_cast<int64_t>(s.splits) * c.N * c.Ho * c.Wo * c.Cout;
+                    if (wb.elems < need) throw std::runtime_error("split-K workspace too small");
+                    c.ws = prep_->arena + wb.offset;
+                }
+                // output extent must match the conv arithmetic
+                if ((c.H + 2 * c.ph - ((c.KH - 1) * c.dh + 1)) / c.sh + 1 != c.Ho ||
+                    (c.W + 2 * c.pw - ((c.KW - 1) * c.dw + 1)) / c.sw + 1 != c.Wo)
+                    throw std::runtime_error("conv output size mismatch");
+                l.tile = s.tile;
+                l.vec = s.vec;
+                break;
+            }
+            case StepKind::ConvDirect: {
+                const Node& n = model_->nodes.at(s.node);
+                k::ConvDirectArgs& d = l.direct;
+                d.x = V(s.a, "conv x", si);
+                d.y = V(s.out, "conv y", si);
+                if (s.has_res) d.res = V(s.res, "conv res", si);
+                const int w = -1000 - n.inputs[1];
+                d.w = dev_->wptr.at(w);
+                const HostTensor& wt = model_->weights.at(w);
+                if (wt.dims[0] != d.y.dims[1] || wt.dims[1] != d.x.dims[1]) throw std::runtime_error("conv weight shape mismatch");
+                if (n.inputs.size() > 2 && n.inputs[2] <= -1000) {
+                    const int b = -1000 - n.inputs[2];
+                    if (model_->weights.at(b).numel() < d.y.dims[1]) throw std::runtime_error("conv bias too short");
+                    d.bias = dev_->wptr.at(b);
+                }
+                d.KH = s.KH;
+                d.KW = s.KW;
+                d.sh = s.sh;
+                d.sw = s.sw;
+                d.ph = s.ph;
+                d.pw = s.pw;
+                d.dh = s.dh;
+                d.dw = s.dw;
+                d.act = s.act;
+                d.slope = s.slope;
+                break;
+            }
+            case StepKind::Elt:
+                l.out = V(s.out, "elt out", si);
+                l.a = V(s.a, "elt a", si);
+                l.b = V(s.b, "elt b", si);
+                l.elt = s.elt;
+                l.alpha = s.alpha;
+                break;
+            case StepKind::MaxPool:
+            case StepKind::Resize:
+            case StepKind::Softmax:
+                l.out = V(s.out, "out", si);
+                l.a = V(s.a, "in", si);
+                l.kh = s.KH;
+                l.kw = s.KW;
+                l.sh = s.sh;
+                l.sw = s.sw;
+                l.ph = s.ph;
+                l.pw = s.pw;
+                l.axis = s.axis;
+                break;
+        }
+        prep_->launches.push_back(std::move(l));
+    }
+    for (int32_t b : plan.input_bufs)
+        if (b < 0) throw std::runtime_error("graph input has no staging buffer");
+    for (size_t i = 0; i < plan.outputs.size(); ++i) {
+        const VRef& o = plan.outputs[i];
+        int64_t n = 1;
+        for (auto d : plan.output_dims[i]) n *= d;
+        view_extent_check(o, plan.bufs.at(o.buf).elems, "output", -1);
+        float* h = nullptr;
+        PDEFA_HIP(hipHostMalloc(reinterpret_cast<void**>(&h), static_cast<size_t>(std::max<int64_t>(n, 1)) * sizeof(float),
+                                hipHostMallocDefault));
+        prep_->host_out.push_back(h);
+        HostTensor t;
+        t.dtype = kF32;
+        t.rank = static_cast<int32_t>(plan.output_dims[i].size());
+        for (int d = 0; d < t.rank; ++d) t.dims[d] = plan.output_dims[i][d];
+        t.data = h;
+        t.nbytes = static_cast<size_t>(n) * sizeof(float);
+        t.owns = false;
+        prep_->outputs.push_back(std::move(t));
+    }
+}
+
+void Session::launch_one(const Launch& l, hipStream_t s) {
+    switch (l.kind) {
+        case StepKind::ConvMfma: k::launch_conv_mfma(l.conv, l.tile, l.vec, s); break;
+        case StepKind::ConvDirect: k::launch_conv_direct(l.direct, s); break;
+        case StepKind::Elt: k::launch_eltwise(l.elt, l.out, l.a, l.b, l.alpha, s); break;
+        case StepKind::MaxPool: k::launch_maxpool(l.out, l.a, l.kh, l.kw, l.sh, l.sw, l.ph, l.pw, s); break;
+        case StepKind::Resize: k::launch_resize_nearest(l.out, l.a, s); break;
+        case StepKind::Softmax: k::launch_softmax(l.out, l.a, l.axis, s); break;
+    }
+}
+
+void Session::launch_all(hipStream_t s) {
+    for (const Launch& l : prep_->launches) launch_one(l, s);
+}
+
+void Session::upload_inputs() {
+    const Plan& plan = prep_->plan;
+    for (size_t i = 0; i < inputs_.size(); ++i) {
+        const HostTensor* t = inputs_[i];
+        float* dst = prep_->arena + plan.bufs.at(plan.input_bufs[i]).offset;
+        PDEFA_HIP(hipMemcpyAsync(dst, t->data, t->nbytes, hipMemcpyHostToDevice, stream_));
+    }
+}
+
+void Session::download_outputs() {
+    const Plan& plan = prep_->plan;
+    for (size_t i = 0; i < plan.outputs.size(); ++i) {
+        const float* src = prep_->arena + plan.bufs.at(plan.outputs[i].buf).offset + plan.outputs[i].off;
+        PDEFA_HIP(hipMemcpyAsync(prep_->host_out[i], src, prep_->outputs[i].nbytes, hipMemcpyDeviceToHost, stream_));
+    }
+}
+
+void Session::run() {
+    const auto t0 = std::chrono::high_resolution_clock::now();
+    if (!device_available()) throw std::runtime_error("no HIP device available for the session");
+    std::vector<std::vector<int64_t>> dims;
+    for (size_t i = 0; i < inputs_.size(); ++i) {
+        const HostTensor* t = inputs_[i];
+        if (!t) throw std::runtime_error("input " + std::to_string(i) + " is not set");
+        if (t->dtype != kF32) throw std::runtime_error("input " + std::to_string(i) + " must be F32");
+        dims.emplace_back(t->dims, t->dims + t->rank);
+    }
+    if (!dev_) dev_ = device_model(*model_);
+    if (!stream_) PDEFA_HIP(hipStreamCreateWithFlags(&stream_, hipStreamNonBlocking));
+    if (!prep_ || prep_->plan.input_dims != dims) prepare(dims);
+    upload_inputs();
+    const bool per_step = prof_fn_ != nullptr || std::getenv("ENGINE_PROFILE_CSV") != nullptr;
+    if (per_step) {
+        std::vector<double> ms;
+        std::vector<std::string> labels;
+        time_steps(ms, labels);
+        if (prof_fn_)
+            for (size_t i = 0; i < ms.size(); ++i) prof_fn_(labels[i].c_str(), ms[i], prof_user_);
+        if (const char* path = std::getenv("ENGINE_PROFILE_CSV")) {
+            if (std::FILE* f = std::fopen(path, "a")) {
+                for (size_t i = 0; i < ms.size(); ++i) std::fprintf(f, "%zu,\"%s\",%.6f\n", i, labels[i].c_str(), ms[i]);
+                std::fclose(f);
+            }
+        }
+    } else if (use_graph_) {
+        if (!prep_->exec) {
+            PDEFA_HIP(hipStreamBeginCapture(stream_, hipStreamCaptureModeThreadLocal));
+            try {
+                launch_all(stream_);
+            } catch (...) {
+                hipGraph_t g = nullptr;
+                (void)hipStreamEndCapture(stream_, &g);
+                if (g) (void)hipGraphDestroy(g);
+                throw;
+            }
+            PDEFA_HIP(hipStreamEndCapture(stream_, &prep_->graph));
+            PDEFA_HIP(hipGraphInstantiate(&prep_->exec, prep_->graph, nullptr, nullptr, 0));
+        }
+        PDEFA_HIP(hipGraphLaunch(prep_->exec, stream_));
+    } else {
+        launch_all(stream_);
+        PDEFA_HIP(hipGetLastError());
+    }
+    download_outputs();
+    PDEFA_HIP(hipStreamSynchronize(stream_));
+    const auto t1 = std::chrono::high_resolution_clock::now();
+    last_run_ms = std::chrono::duration<double, std::milli>(t1 - t0).count();
+    ++runs;
+}
+
+double Session::replay(int32_t iters) {
+    if (!prep_ || runs == 0) throw std::runtime_error("replay needs a completed run");
+    hipEvent_t a, b;
+    PDEFA_HIP(hipEventCreate(&a));
+    PDEFA_HIP(hipEventCreate(&b));
+    PDEFA_HIP(hipEventRecord(a, stream_));
+    for (int32_t i = 0; i < iters; ++i) {
+        if (prep_->exec)
+            PDEFA_HIP(hipGraphLaunch(prep_->exec, stream_));
+        else
+            launch_all(stream_);
+    }
+    PDEFA_HIP(hipEventRecord(b, stream_));
+    PDEFA_HIP(hipEventSynchronize(b));
+    float ms = 0.0f;
+    PDEFA_HIP(hipEventElapsedTime(&ms, a, b));
+    (void)hipEventDestroy(a);
+    (void)hipEventDestroy(b);
+    return ms;
+}
+
+void Session::time_steps(std::vector<double>& ms, std::vector<std::string>& labels) {
+    const size_t n = prep_->launches.size();
+    std::vector<hipEvent_t> ev(n + 1);
+    for (auto& e : ev) PDEFA_HIP(hipEventCreate(&e));
+    PDEFA_HIP(hipEventRecord(ev[0], stream_));
+    for (size_t i = 0; i < n; ++i) {
+        launch_one(prep_->launches[i], stream_);
+        PDEFA_HIP(hipEventRecord(ev[i + 1], stream_));
+    }
+    PDEFA_HIP(hipEventSynchronize(ev[n]));
+    ms.assign(n, 0.0);
+    labels.clear();
+    for (size_t i = 0; i < n; ++i) {
+        float t = 0.0f;
+        PDEFA_HIP(hipEventElapsedTime(&t, ev[i], ev[i + 1]));
+        ms[i] = t;
+        labels.push_back(prep_->launches[i].label);
+    }
+    for (auto& e : ev) (void)hipEventDestroy(e);
+}
+
+std::string Session::plan_text() const { return prep_ ? describe_plan(*model_, prep_->plan) : std::string(); }
+
+// ------------------------------------------------------------- ops_matmul
+
+namespace {
+
+struct MatmulScratch {
+    std::mutex mu;
+    hipStream_t stream = nullptr;
+    float* buf = nullptr;
+    size_t cap = 0;  // floats
+    ~MatmulScratch() {
+        if (buf) (void)hipFree(buf);
+        if (stream) (void)hipStreamDestroy(stream);
+    }
+};
+
+MatmulScratch& matmul_scratch() {
+    static MatmulScratch s;
+    return s;
+}
+
+}  // namespace
+
+void device_matmul(const float* A, const float* B, float* C, int64_t M, int64_t K, int64_t N) {
+    if (!device_available()) throw std::runtime_error("no HIP device available for ops_matmul");
+    if (M <= 0 || K <= 0 || N <= 0) return;
+    if (M >= (int64_t{1} << 31) || K >= (int64_t{1} << 30) || N >= (int64_t{1} << 30))
+        throw std::runtime_error("ops_matmul: shape too large");
+    MatmulScratch& sc = matmul_scratch();
+    std::lock_guard<std::mutex> g(sc.mu);
+    if (!sc.stream) PDEFA_HIP(hipStreamCreateWithFlags(&sc.stream, hipStreamNonBlocking));
+    const int bn = conv_pack_bn(static_cast<int>(N));
+    const size_t nA = align_up(static_cast<size_t>(M * K));
+    const size_t nB = align_up(static_cast<size_t>(K * N));
+    const size_t nP = align_up(static_cast<size_t>(k::packed_weight_elems(static_cast<int>(N), static_cast<int>(K), bn)));
+    const size_t nBias = align_up(static_cast<size_t>((N + bn - 1) / bn * bn));
+    const size_t nC = align_up(static_cast<size_t>(M * N));
+    // split-K for small grids
+    const int tile = bn == 32 ? k::kTile128x32 : (bn == 64 ? k::kTile64x64 : k::kTile64x128);
+    const int bm = k::conv_tile_bm(tile);
+    const int ktiles = static_cast<int>((K + k::kConvBK - 1) / k::kConvBK);
+    const int64_t wgs = ((M + bm - 1) / bm) * ((N + bn - 1) / bn);
+    int splits = 1;
+    if (wgs < 128 && ktiles >= 32) splits = static_cast<int>(std::min<int64_t>({16, ktiles / 16, (256 + wgs - 1) / wgs}));
+    splits = std::max(splits, 1);
+    const int kps = (ktiles + splits - 1) / splits;
+    splits = (ktiles + kps - 1) / kps;
+    const size_t nW = splits > 1 ? align_up(static_cast<size_t>(splits) * M * N) : 0;
+    const size_t need = nA + nB + nP + nBias + nC + nW;
+    if (need > sc.cap) {
+        if (sc.buf) PDEFA_HIP(hipFree(sc.buf));
+        sc.buf = nullptr;
+        sc.cap = 0;
+        PDEFA_HIP(hipMalloc(&sc.buf, need * sizeof(float)));
+        sc.cap = need;
+    }
+    float* dA = sc.buf;
+    float* dB = dA + nA;
+    float* dP = dB + nB;
+    float* dBias = dP + nP;
+    float* dC = dBias + nBias;
+    float* dW = dC + nC;
+    PDEFA_HIP(hipMemcpyAsync(dA, A, sizeof(float) * M * K, hipMemcpyHostToDevice, sc.stream));
+    PDEFA_HIP(hipMemcpyAsync(dB, B, sizeof(float) * K * N, hipMemcpyHostToDevice, sc.stream));
+    PDEFA_HIP(hipMemsetAsync(dBias, 0, nBias * sizeof(float), sc.stream));
+    k::launch_pack_gemm_b(dP, dB, static_cast<int>(K), static_cast<int>(N), bn, sc.stream);
+    k::ConvArgs c;
+    c.x = dA;
+    c.N = 1;
+    c.H = static_cast<int32_t>(M);
+    c.W = 1;
+    c.Cin = static_cast<int32_t>(K);
+    c.x_sn = M * K;
+    c.x_sh = K;
+    c.x_sw = K;
+    c.y = dC;
+    c.Ho = static_cast<int32_t>(M);
+    c.Wo = 1;
+    c.Cout = static_cast<int32_t>(N);
+    c.y_sn = M * N;
+    c.y_sh = N;
+    c.y_sw = N;
+    c.wpk = dP;
+    c.bias = dBias;
+    c.K = static_cast<int32_t>(K);
+    c.ktiles = ktiles;
+    c.splits = splits;
+    c.kt_per_split = kps;
+    c.ws = splits > 1 ? dW : nullptr;
+    k::launch_conv_mfma(c, tile, K % 4 == 0, sc.stream);
+    PDEFA_HIP(hipGetLastError());
+    PDEFA_HIP(hipMemcpyAsync(C, dC, sizeof(float) * M * N, hipMemcpyDeviceToHost, sc.stream));
+    PDEFA_HIP(hipStreamSynchronize(sc.stream));
+}
+
+}  // namespace pdefa

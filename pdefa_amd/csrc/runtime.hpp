@@ -1,0 +1,126 @@
+// Device runtime: model weights resident in HBM (uploaded once, conv weights
+// pre-packed for the MFMA kernel) and the per-session executor that runs a
+// planned program on its own HIP stream, captured once as a hipGraph and
+// replayed on every run.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <chrono>
+#include <cstdint>
+#include <memory>
+#include <stdexcept>
+#include <string>
+#include <vector>
+
+#include "host_tensor.hpp"
+#include "kernels.hpp"
+#include "model.hpp"
+#include "planner.hpp"
+
+namespace pdefa {
+
+struct HipError : std::runtime_error {
+    hipError_t code;
+    HipError(hipError_t c, const std::string& what) : std::runtime_error(what), code(c) {}
+};
+
+void hip_check(hipError_t e, const char* expr, const char* file, int line);
+#define PDEFA_HIP(expr) ::pdefa::hip_check((expr), #expr, __FILE__, __LINE__)
+
+// True when a HIP device is present (counts devices without creating a context).
+bool device_available();
+
+struct DeviceModel {
+    int device = 0;
+    float* blob = nullptr;  // one allocation: raw weights, packed conv weights, padded biases
+    size_t blob_bytes = 0;
+    std::vector<float*> wptr;  // raw weight i
+    struct Pack {
+        float* wpk = nullptr;
+        float* bias = nullptr;  // padded to the pack width, zeros when the conv has no bias
+        int bn = 0;
+    };
+    std::vector<Pack> packs;  // by node index (empty for non-conv nodes)
+    ~DeviceModel();
+};
+
+// Uploads and packs on the current device (throws on HIP errors).
+std::shared_ptr<DeviceModel> upload_model(const Model& m);
+std::shared_ptr<DeviceModel> device_model(Model& m);  // lazily, once per model
+
+class Session {
+   public:
+    using ProfileFn = void (*)(const char*, double, void*);
+
+    explicit Session(Model& m);
+    ~Session();
+    Session(const Session&) = delete;
+    Session& operator=(const Session&) = delete;
+
+    int32_t num_inputs() const { return model_->num_inputs(); }
+    int32_t num_outputs() const { return model_->num_outputs(); }
+    void set_input(int32_t idx, const HostTensor* t);
+    void run();  // throws
+    const HostTensor* output(int32_t idx) const;
+
+    // Re-runs the prepared program `iters` times on the input already in HBM
+    // (no host copies); returns the elapsed device time in ms (HIP events).
+    double replay(int32_t iters);
+    // Runs each step once with HIP events around it; fills per-step ms.
+    void time_steps(std::vector<double>& ms, std::vector<std::string>& labels);
+
+    void set_profile(ProfileFn fn, void* user) {
+        prof_fn_ = fn;
+        prof_user_ = user;
+    }
+    double last_run_ms = 0.0;
+    uint64_t runs = 0;
+    std::string plan_text() const;
+    const Plan* plan() const { return prep_ ? &prep_->plan : nullptr; }
+
+   private:
+    struct Launch {
+        StepKind kind;
+        k::ConvArgs conv;
+        int tile = 0;
+        bool vec = false;
+        k::ConvDirectArgs direct;
+        k::View out, a, b;
+        int elt = 0;
+        float alpha = 0.0f;
+        int kh = 0, kw = 0, sh = 1, sw = 1, ph = 0, pw = 0, axis = 0;
+        std::string label;
+    };
+    struct Prepared {
+        Plan plan;
+        float* arena = nullptr;
+        std::vector<Launch> launches;
+        hipGraph_t graph = nullptr;
+        hipGraphExec_t exec = nullptr;
+        std::vector<float*> host_out;  // pinned
+        std::vector<HostTensor> outputs;
+    };
+
+    void prepare(const std::vector<std::vector<int64_t>>& dims);
+    void release_prepared();
+    void launch_all(hipStream_t s);
+    void launch_one(const Launch& l, hipStream_t s);
+    void upload_inputs();
+    void download_outputs();
+
+    Model* model_;
+    std::shared_ptr<DeviceModel> dev_;
+    hipStream_t stream_ = nullptr;
+    std::vector<const HostTensor*> inputs_;
+    std::unique_ptr<Prepared> prep_;
+    ProfileFn prof_fn_ = nullptr;
+    void* prof_user_ = nullptr;
+    bool use_graph_ = true;
+    PlanOptions opts_;
+};
+
+// C = A[M,K] @ B[K,N] on the device (the ops_matmul path); host pointers.
+void device_matmul(const float* A, const float* B, float* C, int64_t M, int64_t K, int64_t N);
+
+}  // namespace pdefa

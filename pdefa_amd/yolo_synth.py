@@ -89,8 +89,8 @@ class _Yolo:
     def __init__(self, b: GraphBuilder, rng: np.random.Generator, cls_bias: float):
         self.b, self.rng, self.cls_bias = b, rng, cls_bias
 
-    def conv_raw(self, x, cin, cout, k, s, name, bias_value=None):
-        w = kaiming_uniform(self.rng, (cout, cin, k, k))
+    def conv_raw(self, x, cin, cout, k, s, name, bias_value=None, gain=1.0):
+        w = kaiming_uniform(self.rng, (cout, cin, k, k)) * np.float32(gain)
         if bias_value is None:
             bias = self.rng.uniform(-0.1, 0.1, size=cout).astype(np.float32)
         else:
@@ -142,8 +142,13 @@ class _Yolo:
 
 
 def build_yolov8(scale: str = "n", seed: int = 0, nc: int = 80, imgsz: int = 640,
-                 cls_bias: float = -4.0) -> EngineModel:
-    """YOLOv8{scale} detection graph with seeded random weights (BN folded)."""
+                 cls_bias: float = -6.0, cls_gain: float = 30.0) -> EngineModel:
+    """YOLOv8{scale} detection graph with seeded random weights (BN folded).
+
+    The class head's last conv has its Kaiming weights scaled by cls_gain and
+    a constant bias cls_bias, so that a random-weight model still yields on
+    the order of a hundred candidates above 0.25 on a synthetic image (the
+    unscaled head scores every anchor near sigmoid(cls_bias))."""
     depth, width, max_ch = SCALES[scale]
     ch = lambda c: make_divisible(min(c, max_ch) * width, 8)
     rep = lambda n: max(round(n * depth), 1)
@@ -190,7 +195,7 @@ def build_yolov8(scale: str = "n", seed: int = 0, nc: int = 80, imgsz: int = 640
         a = y.conv_raw(a, cb, 4 * reg, 1, 1, f"{n}/cv2.{i}/cv2.{i}.2", bias_value=1.0)
         c = y.conv(f, cin, cc, 3, 1, f"{n}/cv3.{i}/cv3.{i}.0")
         c = y.conv(c, cc, cc, 3, 1, f"{n}/cv3.{i}/cv3.{i}.1")
-        c = y.conv_raw(c, cc, nc, 1, 1, f"{n}/cv3.{i}/cv3.{i}.2", bias_value=cls_bias)
+        c = y.conv_raw(c, cc, nc, 1, 1, f"{n}/cv3.{i}/cv3.{i}.2", bias_value=cls_bias, gain=cls_gain)
         cat = b.node("Concat", f"/{n}/Concat_{i}", [a, c], axis=1)
         shp = b.const(f"/{n}/Reshape_{i}/shape::const", [1, no, -1])
         flat.append(b.node("Reshape", f"/{n}/Reshape_{i}", [cat, shp]))
