@@ -20,6 +20,14 @@ extern "C" {
  * stream.  Requires one completed engine_session_run. */
 PDEFA_EXPORT EngineStatus pdefa_amd_session_replay(EngineSession* sess, int32_t iters, double* out_ms);
 
+/* Average device time of each step of the prepared program over `iters`
+ * step-by-step replays (HIP events between launches on the session stream).
+ * Per step: ms[i], kind[i] (0 conv_mfma, 1 conv_direct, 2 eltwise,
+ * 3 maxpool, 4 resize, 5 softmax) and flops[i] (2*N*Cout*Cin*KH*KW*Ho*Wo for
+ * convs, else 0).  *n = number of steps; at most `cap` entries are written. */
+PDEFA_EXPORT EngineStatus pdefa_amd_session_step_times(EngineSession* sess, int32_t iters, double* ms, int32_t* kind,
+                                                       int64_t* flops, int32_t cap, int32_t* n);
+
 /* Text dump of the session's current device program (one line per kernel). */
 PDEFA_EXPORT EngineStatus pdefa_amd_session_plan(const EngineSession* sess, char* buf, size_t cap, size_t* out_len);
 

@@ -102,7 +102,8 @@ def silu_winograd_compat(x):
               5.0000001201e-1, 1.0):
         p = (p * f + f32(c)).astype(np.float32)
     e = np.clip(n, -127, 128).astype(np.int64) + 127
-    scale = np.ldexp(np.float32(1.0), (e - 127).astype(np.int32)).astype(np.float32)
+    with np.errstate(over="ignore"):  # n = 128 gives the exponent pattern of +inf, as in the reference
+        scale = np.ldexp(np.float32(1.0), (e - 127).astype(np.int32)).astype(np.float32)
     with np.errstate(over="ignore", invalid="ignore"):
         y = (x / (f32(1.0) + p * scale)).astype(np.float32)
     y = np.where(neg < f32(-88.37626), x, y)

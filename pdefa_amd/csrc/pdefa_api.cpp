@@ -271,6 +271,26 @@ PDEFA_EXPORT EngineStatus pdefa_amd_session_replay(EngineSession* sess, int32_t 
     });
 }
 
+PDEFA_EXPORT EngineStatus pdefa_amd_session_step_times(EngineSession* sess, int32_t iters, double* ms, int32_t* kind,
+                                                       int64_t* flops, int32_t cap, int32_t* n) {
+    if (!sess || sess->magic != kMagicSession) return ENGINE_ERR_INVALID_HANDLE;
+    if (!n || iters <= 0) return ENGINE_ERR_INVALID_ARG;
+    return guarded([&] {
+        clear_error();
+        std::vector<double> m;
+        std::vector<int32_t> k;
+        std::vector<int64_t> f;
+        sess->inner->step_stats(iters, m, k, f);
+        *n = static_cast<int32_t>(m.size());
+        for (int32_t i = 0; i < *n && i < cap; ++i) {
+            if (ms) ms[i] = m[i];
+            if (kind) kind[i] = k[i];
+            if (flops) flops[i] = f[i];
+        }
+        return ENGINE_OK;
+    });
+}
+
 PDEFA_EXPORT EngineStatus pdefa_amd_session_plan(const EngineSession* sess, char* buf, size_t cap, size_t* out_len) {
     if (!sess || sess->magic != kMagicSession) return ENGINE_ERR_INVALID_HANDLE;
     return guarded([&] {

@@ -490,6 +490,32 @@ void Session::time_steps(std::vector<double>& ms, std::vector<std::string>& labe
     for (auto& e : ev) (void)hipEventDestroy(e);
 }
 
+void Session::step_stats(int32_t iters, std::vector<double>& ms, std::vector<int32_t>& kind,
+                         std::vector<int64_t>& flops) {
+    if (!prep_ || runs == 0) throw std::runtime_error("step_stats needs a completed run");
+    const size_t n = prep_->launches.size();
+    ms.assign(n, 0.0);
+    std::vector<double> one;
+    std::vector<std::string> labels;
+    for (int32_t it = 0; it < iters; ++it) {
+        time_steps(one, labels);
+        for (size_t i = 0; i < n; ++i) ms[i] += one[i] / iters;
+    }
+    kind.resize(n);
+    flops.assign(n, 0);
+    for (size_t i = 0; i < n; ++i) {
+        const Launch& l = prep_->launches[i];
+        kind[i] = static_cast<int32_t>(l.kind);
+        if (l.kind == StepKind::ConvMfma) {
+            const k::ConvArgs& c = l.conv;
+            flops[i] = 2LL * c.N * c.Cout * c.Cin * c.KH * c.KW * static_cast<int64_t>(c.Ho) * c.Wo;
+        } else if (l.kind == StepKind::ConvDirect) {
+            const k::ConvDirectArgs& d = l.direct;
+            flops[i] = 2LL * d.y.dims[0] * d.y.dims[1] * d.x.dims[1] * d.KH * d.KW * d.y.dims[2] * d.y.dims[3];
+        }
+    }
+}
+
 std::string Session::plan_text() const { return prep_ ? describe_plan(*model_, prep_->plan) : std::string(); }
 
 // ------------------------------------------------------------- ops_matmul

@@ -69,6 +69,10 @@ class Session {
     double replay(int32_t iters);
     // Runs each step once with HIP events around it; fills per-step ms.
     void time_steps(std::vector<double>& ms, std::vector<std::string>& labels);
+    // Average per-step device time over `iters` step-by-step replays, with the
+    // step kind and its algorithmic flops (2*N*Cout*Cin*KH*KW*Ho*Wo for convs).
+    void step_stats(int32_t iters, std::vector<double>& ms, std::vector<int32_t>& kind,
+                    std::vector<int64_t>& flops);
 
     void set_profile(ProfileFn fn, void* user) {
         prof_fn_ = fn;

@@ -65,6 +65,8 @@ def lib() -> C.CDLL:
             "engine_ops_matmul": (C.c_int, [vp, vp, vp]),
             "pdefa_amd_session_replay": (C.c_int, [vp, i32, C.POINTER(C.c_double)]),
             "pdefa_amd_session_plan": (C.c_int, [vp, C.c_char_p, sz, C.POINTER(sz)]),
+            "pdefa_amd_session_step_times": (C.c_int, [vp, i32, C.POINTER(C.c_double), C.POINTER(i32),
+                                                       C.POINTER(i64), i32, C.POINTER(i32)]),
             "pdefa_amd_plan_model": (C.c_int, [vp, C.POINTER(i64), i32, C.c_char_p, sz, C.POINTER(sz)]),
             "pdefa_amd_device_name": (C.c_char_p, []),
         }
@@ -144,6 +146,18 @@ class Engine:
         ms = C.c_double()
         check(lib().pdefa_amd_session_replay(self.sess, iters, C.byref(ms)), "pdefa_amd_session_replay")
         return ms.value
+
+    def step_times(self, iters: int):
+        """(ms, kind, flops) arrays: per-step average device time over `iters`."""
+        cap = 4096
+        ms = (C.c_double * cap)()
+        kind = (C.c_int32 * cap)()
+        flops = (C.c_int64 * cap)()
+        n = C.c_int32()
+        check(lib().pdefa_amd_session_step_times(self.sess, iters, ms, kind, flops, cap, C.byref(n)),
+              "pdefa_amd_session_step_times")
+        k = min(n.value, cap)
+        return (np.array(ms[:k]), np.array(kind[:k]), np.array(flops[:k], dtype=np.int64))
 
     def plan(self) -> str:
         buf = C.create_string_buffer(1 << 20)

@@ -163,3 +163,48 @@ def test_graph_and_eager_agree(tmp_path, monkeypatch):
     monkeypatch.setenv("PDEFA_HIP_GRAPH", "0")
     b = run_engine(path, x)[0]
     assert np.array_equal(a, b)
+
+
+# ---- against the golden vectors written from the compiled reference engine
+
+def _golden(name):
+    import json
+    here = os.path.dirname(os.path.abspath(__file__))
+    with open(os.path.join(here, "golden", name + ".json")) as f:
+        return json.load(f)
+
+
+def _check_golden_samples(arr, g):
+    flat = arr.reshape(-1).astype(np.float64)
+    idx = np.asarray(g["samples"]["index"])
+    want = np.asarray(g["samples"]["value"])
+    bad = np.abs(flat[idx] - want) > ATOL + RTOL * np.abs(want)
+    assert not bad.any(), f"{int(bad.sum())} golden samples out of tolerance"
+    means = arr.reshape(arr.shape[0], arr.shape[1], -1).astype(np.float64).mean(axis=(0, 2))
+    np.testing.assert_allclose(means, g["channel_means"], atol=ATOL, rtol=RTOL)
+
+
+@pytest.mark.parametrize("name,args", [("conv3x3_s2_64_160", (64, 64, 3, 2, 160)),
+                                       ("conv1x1_128_64_160", (128, 64, 1, 1, 160))])
+def test_conv_vs_reference_golden(tmp_path, name, args):
+    g = _golden(name)
+    model, x = ys.build_single_conv(*args, seed=7)
+    path = str(tmp_path / "c.engine")
+    ys.save(model, path)
+    _check_golden_samples(run_engine(path, x)[0], g)
+
+
+def test_yolov8n_batch_vs_reference_golden(yolov8n):
+    """b3 stacked run; each image against the reference's output and detections."""
+    _, path = yolov8n
+    x, metas = ys.yolo_inputs(3)
+    out = run_engine(path, x)[0]
+    for i in range(3):
+        g = _golden(f"yolov8n_640_img{i}")
+        _check_golden_samples(out[i:i + 1], g)
+        dets = decode_yolo(out[i:i + 1], metas[i], with_anchor=True)
+        gd = g["detections"]
+        assert [(d["anchor"], d["cls"]) for d in dets] == [(d["anchor"], d["cls"]) for d in gd]
+        for a, b in zip(dets, gd):
+            for k in ("x1", "y1", "x2", "y2", "conf"):
+                assert abs(a[k] - b[k]) <= ATOL + RTOL * abs(b[k]), (i, k, a, b)

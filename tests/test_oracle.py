@@ -1,0 +1,269 @@
+"""Pins the CPU oracle (oracle/graph_ref.py, oracle/decode_ref.py) before it is
+trusted as the checker of the GPU path.
+
+- golden vectors written from the compiled reference engine (tests/golden/);
+- the compiled reference itself (oracle/_ref) on fresh cases, when built;
+- closed-form convolution answers of PDEFA1.0/examples/test_conv2d.cpp:13-148;
+- brute-force direct loops on tiny shapes (catches index/transpose mistakes);
+- ONNX-semantics identities for pooling, resize, softmax, slice, reshape;
+- letterbox known answers (imageloader/tests/test_preprocess.cpp:27-130).
+"""
+import json
+import math
+import os
+
+import numpy as np
+import pytest
+
+from oracle import decode_ref, graph_ref, ref_lib
+from pdefa_amd import postprocess, yolo_synth as ys
+
+GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+TOL = dict(atol=1e-3, rtol=1e-3)
+
+
+def golden(name):
+    with open(os.path.join(GOLDEN, name + ".json")) as f:
+        return json.load(f)
+
+
+def check_samples(arr, g, atol=1e-3, rtol=1e-3):
+    flat = arr.reshape(-1)
+    idx = np.asarray(g["samples"]["index"])
+    np.testing.assert_allclose(flat[idx], np.asarray(g["samples"]["value"]), atol=atol, rtol=rtol)
+    means = arr.reshape(arr.shape[0], arr.shape[1], -1).astype(np.float64).mean(axis=(0, 2))
+    np.testing.assert_allclose(means, np.asarray(g["channel_means"]), atol=atol, rtol=rtol)
+
+
+# ---------------------------------------------------------------- conv KATs
+
+def test_conv_kat_all_ones():
+    y = graph_ref.conv2d(np.ones((1, 1, 5, 5)), np.ones((1, 1, 3, 3)), np.zeros(1))
+    assert y.shape == (1, 1, 3, 3) and np.all(y == 9.0)
+
+
+def test_conv_kat_varied():
+    x = np.arange(1, 10, dtype=np.float64).reshape(1, 1, 3, 3)
+    y = graph_ref.conv2d(x, np.ones((1, 1, 2, 2)), np.zeros(1))
+    assert y.reshape(-1).tolist() == [12.0, 16.0, 24.0, 28.0]
+
+
+def test_conv_kat_stride_pad():
+    y = graph_ref.conv2d(np.ones((1, 1, 4, 4)), np.ones((1, 1, 3, 3)), np.zeros(1), stride=(2, 2), pad=(1, 1))
+    assert y.reshape(-1).tolist() == [4.0, 6.0, 6.0, 9.0]
+
+
+def test_conv_kat_fused_relu():
+    y = graph_ref.conv2d(-np.ones((1, 1, 3, 3)), np.ones((1, 1, 2, 2)), np.zeros(1), act=1)
+    assert np.all(y == 0.0)
+
+
+@pytest.mark.parametrize("shape", [(1, 3, 7, 6, 4, 3, 1, 1), (2, 5, 9, 9, 3, 3, 2, 1), (1, 4, 8, 5, 6, 1, 1, 0),
+                                   (1, 2, 6, 7, 2, 5, 3, 2)])
+def test_conv_matches_brute_force(shape):
+    n, ci, h, w, co, k, s, p = shape
+    rng = np.random.default_rng(sum(shape))
+    x = rng.standard_normal((n, ci, h, w))
+    wt = rng.standard_normal((co, ci, k, k))
+    b = rng.standard_normal(co)
+    np.testing.assert_allclose(graph_ref.conv2d(x, wt, b, (s, s), (p, p)),
+                               graph_ref.conv2d_direct(x, wt, b, (s, s), (p, p)), rtol=1e-12, atol=1e-12)
+
+
+def test_silu_known_values():
+    assert abs(graph_ref.activation(np.array([1.0]), 5)[0] - 0.7311) < 1e-3
+    assert graph_ref.activation(np.array([0.0]), 5)[0] == 0.0
+
+
+def test_winograd_form_silu_shape():
+    # a faithful SiLU near 0 and for large |x|, ~2% off in between, with jumps
+    x = np.linspace(-20, 20, 4001, dtype=np.float32)
+    y = graph_ref.silu_winograd_compat(x)
+    exact = x / (1 + np.exp(-x.astype(np.float64)))
+    assert np.max(np.abs(y - exact)) < 0.05 * np.max(np.abs(x)) + 1e-3
+    assert np.max(np.abs(y - exact)) > 1e-3  # not the exact function
+    assert graph_ref.silu_winograd_compat(np.array([100.0], np.float32))[0] == 100.0
+    assert graph_ref.silu_winograd_compat(np.array([-100.0], np.float32))[0] == 0.0
+
+
+def test_winograd_dispatch_rule():
+    assert graph_ref.winograd_path(64, 3, 3, (1, 1), (1, 1), 1)
+    assert not graph_ref.winograd_path(16, 3, 3, (1, 1), (1, 1), 1)   # direct kernel
+    assert not graph_ref.winograd_path(576, 3, 3, (1, 1), (1, 1), 1)  # Cin > 512
+    assert not graph_ref.winograd_path(64, 3, 3, (2, 2), (1, 1), 1)
+    assert not graph_ref.winograd_path(64, 1, 1, (1, 1), (1, 1), 1)
+
+
+# ------------------------------------------------------- other op semantics
+
+def test_maxpool_sppf_equivalence():
+    rng = np.random.default_rng(1)
+    x = rng.standard_normal((1, 3, 11, 9))
+    p5 = graph_ref.maxpool2d(x, (5, 5), (1, 1), (2, 2))
+    p9 = graph_ref.maxpool2d(x, (9, 9), (1, 1), (4, 4))
+    np.testing.assert_array_equal(graph_ref.maxpool2d(p5, (5, 5), (1, 1), (2, 2)), p9)
+    # brute force
+    ref = np.empty_like(p5)
+    for i in range(11):
+        for j in range(9):
+            ref[..., i, j] = x[..., max(i - 2, 0):i + 3, max(j - 2, 0):j + 3].max(axis=(-1, -2))
+    np.testing.assert_array_equal(p5, ref)
+
+
+def test_resize_nearest_2x():
+    x = np.arange(6, dtype=np.float32).reshape(1, 1, 2, 3)
+    y = graph_ref.resize_nearest(x, [1, 1, 2, 2])
+    np.testing.assert_array_equal(y, x.repeat(2, 2).repeat(2, 3))
+
+
+def test_softmax_and_slice():
+    x = np.random.default_rng(0).standard_normal((2, 16, 3))
+    s = graph_ref.softmax(x, 1)
+    np.testing.assert_allclose(s.sum(1), 1.0, rtol=1e-12)
+    y = graph_ref.slice_(x, [2], [2 ** 31 - 1], [1])
+    assert y.shape == (2, 14, 3)
+    assert graph_ref.reshape(x, [0, -1]).shape == (2, 48)
+
+
+# ------------------------------------------------------- golden vectors
+
+@pytest.mark.parametrize("name,args", [("conv3x3_s1_64_160", (64, 64, 3, 1, 160)),
+                                       ("conv3x3_s2_64_160", (64, 64, 3, 2, 160)),
+                                       ("conv1x1_128_64_160", (128, 64, 1, 1, 160))])
+def test_oracle_single_conv_vs_golden(name, args):
+    g = golden(name)
+    model, x = ys.build_single_conv(*args, seed=7)
+    import hashlib
+    assert hashlib.sha256(x.tobytes()).hexdigest() == g["input_sha256"]
+    out = graph_ref.run_graph(model, [x])[0]
+    assert list(out.shape) == g["shape"]
+    check_samples(out, g, atol=2e-5, rtol=2e-5)
+
+
+@pytest.fixture(scope="module")
+def yolov8n_model():
+    return ys.build_yolov8("n", seed=0)
+
+
+@pytest.mark.parametrize("img", [0, 1, 2])
+def test_oracle_yolov8n_vs_golden(yolov8n_model, img):
+    g = golden(f"yolov8n_640_img{img}")
+    x, metas = ys.yolo_inputs(img + 1)
+    x = x[img:img + 1]
+    import hashlib
+    assert hashlib.sha256(x.tobytes()).hexdigest() == g["input_sha256"]
+    out = graph_ref.run_graph(yolov8n_model, [x])[0]
+    assert list(out.shape) == g["shape"]
+    check_samples(out, g)
+    dets = decode_ref.decode(out.tolist(), metas[img])
+    gd = g["detections"]
+    assert [(d["anchor"], d["cls"]) for d in dets] == [(d["anchor"], d["cls"]) for d in gd]
+    for a, b in zip(dets, gd):
+        for k in ("x1", "y1", "x2", "y2", "conf"):
+            assert math.isclose(a[k], b[k], rel_tol=1e-3, abs_tol=1e-3)
+
+
+def test_sgemm_golden():
+    g = golden("sgemm_512")
+    rng = np.random.default_rng(42)
+    a = rng.standard_normal((512, 512), dtype=np.float32)
+    b = rng.standard_normal((512, 512), dtype=np.float32)
+    c = a.astype(np.float64) @ b.astype(np.float64)
+    idx = np.asarray(g["samples"]["index"])
+    np.testing.assert_allclose(c.reshape(-1)[idx], g["samples"]["value"], atol=1e-3, rtol=1e-4)
+    np.testing.assert_allclose(c.sum(1), g["row_sums"], atol=1e-2, rtol=1e-4)
+    np.testing.assert_allclose(np.eye(4) @ np.arange(16.0).reshape(4, 4), np.arange(16.0).reshape(4, 4))
+
+
+# ------------------------------------------------------- letterbox
+
+def test_letterbox_known_answers():
+    img = np.full((4, 4, 3), 128, np.uint8)
+    t, m = ys.letterbox(img, 8, 8, 1 / 255, 0.0)
+    assert t.shape == (1, 3, 8, 8) and (m["pad_x"], m["pad_y"], m["scaled_w"], m["scaled_h"]) == (0, 0, 8, 8)
+    assert abs(t[0, 0, 0, 0] - 128 / 255) < 0.01
+    img = np.full((50, 100, 3), 200, np.uint8)
+    t, m = ys.letterbox(img, 100, 100, 1 / 255, 0.0)
+    assert (m["scaled_w"], m["scaled_h"], m["pad_x"], m["pad_y"]) == (100, 50, 0, 25)
+    assert abs(t.reshape(-1)[50]) < 1e-3 and abs(t.reshape(-1)[50 * 100 + 50] - 200 / 255) < 0.02
+    g = np.full((4, 4), 100, np.uint8)
+    t, _ = ys.letterbox(g, 4, 4, 1 / 255, 0.0)
+    assert np.allclose(t[0, 0], t[0, 1]) and np.allclose(t[0, 0], t[0, 2])
+    assert abs(t[0, 0, 0, 0] - 100 / 255) < 0.01
+
+
+def test_letterbox_vs_golden():
+    g = golden("letterbox_1280x720")
+    img = ys.synth_image(0, 1280, 720)
+    t, m = ys.letterbox(img, 640, 640, 1 / 255, 114 / 255)
+    for k in ("pad_x", "pad_y", "scaled_w", "scaled_h"):
+        assert m[k] == g["meta"][k]
+    idx = np.asarray(g["samples"]["index"])
+    np.testing.assert_allclose(t.reshape(-1)[idx], g["samples"]["value"], atol=1e-6)
+
+
+# ------------------------------------------------------- decode / NMS
+
+def test_decode_zeros_is_empty():
+    assert postprocess.decode_yolo(np.zeros((1, 84, 8400), np.float32)) == []
+    assert decode_ref.decode(np.zeros((1, 84, 8400), np.float32).tolist()) == []
+
+
+def test_decode_matches_restatement():
+    rng = np.random.default_rng(5)
+    out = np.zeros((1, 84, 500), np.float32)
+    out[0, :2] = rng.uniform(0, 640, (2, 500))
+    out[0, 2:4] = rng.uniform(5, 80, (2, 500))
+    out[0, 4:] = rng.uniform(0, 0.3, (80, 500))
+    out[0, 4 + 7, :40] = 0.9  # duplicated classes -> suppression
+    meta = {"ratio": 0.5, "pad_x": 0, "pad_y": 140, "orig_w": 1280, "orig_h": 720}
+    a = postprocess.decode_yolo(out, meta, with_anchor=True)
+    b = decode_ref.decode(out.tolist(), meta)
+    assert len(a) > 5 and a == b
+
+
+# ------------------------------------------------------- compiled reference
+
+needs_ref = pytest.mark.skipif(not ref_lib.available(), reason="oracle/_ref not built (make -C oracle)")
+
+
+@needs_ref
+@pytest.mark.parametrize("cin,cout,k,s,hw", [(64, 64, 3, 1, 40), (32, 48, 3, 2, 33), (128, 64, 1, 1, 24),
+                                             (16, 16, 3, 1, 20), (3, 16, 3, 2, 32), (600, 40, 3, 1, 6)])
+def test_oracle_vs_compiled_reference_conv(tmp_path, cin, cout, k, s, hw):
+    model, x = ys.build_single_conv(cin, cout, k, s, hw, seed=cin + hw)
+    path = str(tmp_path / "c.engine")
+    ys.save(model, path)
+    r = ref_lib.RefSession(path).run(x)[0]
+    o = graph_ref.run_graph(model, [x])[0]
+    np.testing.assert_allclose(o, r, atol=2e-5, rtol=2e-5)
+
+
+@needs_ref
+def test_oracle_vs_compiled_reference_yolov8n_small(tmp_path):
+    model = ys.build_yolov8("n", seed=3, imgsz=160)
+    path = str(tmp_path / "y.engine")
+    ys.save(model, path)
+    x, _ = ys.yolo_inputs(2, imgsz=160)
+    r = ref_lib.RefSession(path).run(x[1:2])[0]
+    o = graph_ref.run_graph(model, [x[1:2]])[0]
+    np.testing.assert_allclose(o, r, **TOL)
+
+
+@needs_ref
+def test_oracle_vs_compiled_reference_letterbox():
+    for (w, h) in [(1280, 720), (1024, 768), (800, 800), (37, 91)]:
+        img = ys.synth_image(w + h, w, h)
+        a, ma = ys.letterbox(img, 640, 640, 1 / 255, 114 / 255)
+        b, mb = ref_lib.letterbox(img, 640, 640, 1 / 255, 114 / 255)
+        for k in ("pad_x", "pad_y", "scaled_w", "scaled_h"):
+            assert ma[k] == mb[k]
+        np.testing.assert_allclose(a, b, atol=1e-6)
+
+
+@needs_ref
+def test_compiled_reference_matmul():
+    rng = np.random.default_rng(2)
+    a = rng.standard_normal((70, 130), dtype=np.float32)
+    b = rng.standard_normal((130, 45), dtype=np.float32)
+    np.testing.assert_allclose(ref_lib.matmul(a, b), a.astype(np.float64) @ b, atol=1e-4, rtol=1e-4)
