@@ -36,7 +36,8 @@ enum Act : int32_t {
     kActSiluWinogradForm = 6,
 };
 
-// Implicit-GEMM convolution tile configurations (BM x BN output tile, 4 waves).
+// Implicit-GEMM convolution tile configurations (BM x BN output tile, 4 waves,
+// K advanced kConvBK at a time).
 enum ConvTile : int32_t {
     kTile128x32 = 0,
     kTile128x64 = 1,
@@ -45,7 +46,7 @@ enum ConvTile : int32_t {
     kTile64x128 = 4,
     kNumConvTiles = 5,
 };
-constexpr int kConvBK = 16;
+constexpr int kConvBK = 32;
 int conv_tile_bm(int tile);
 int conv_tile_bn(int tile);
 
@@ -70,7 +71,7 @@ struct ConvArgs {
     int32_t act = 0;
     float slope = 0.01f;
     // split-K: splits > 1 writes raw partial sums to ws[split][M][Cout] and a
-    // reduce kernel applies bias/activation/residual.
+    // reduce kernel sums them in split order and applies bias/activation/residual.
     float* ws = nullptr;
     int32_t splits = 1;
     int32_t kt_per_split = 0;
@@ -80,13 +81,16 @@ struct ConvArgs {
 // Cin % 4 == 0 and 16-byte aligned pixel rows).
 void launch_conv_mfma(const ConvArgs& a, int tile, bool vec, hipStream_t s);
 
-// Generic direct convolution over arbitrary strided NCHW-logical views
-// (any layout; one thread per output element).
+// Direct convolution over arbitrary strided NCHW-logical views (any layout),
+// for layers the implicit GEMM does not take: tiny Cin (the 3-channel stem,
+// read straight from the NCHW input) or tiny Cout.  One lane computes one
+// output pixel for kDirectCB output channels.
+constexpr int kDirectCB = 16;
 struct ConvDirectArgs {
     View x;    // logical [N, Cin, H, W]
     View y;    // logical [N, Cout, Ho, Wo]
     View res;  // optional, same logical shape as y (ptr == nullptr if absent)
-    const float* w = nullptr;  // [Cout, Cin, KH, KW] contiguous
+    const float* wpk = nullptr;  // [ceil(Cout/kDirectCB)][Cin*KH*KW][kDirectCB], k = (ci, kh, kw)
     const float* bias = nullptr;
     int32_t KH = 1, KW = 1, sh = 1, sw = 1, ph = 0, pw = 0, dh = 1, dw = 1;
     int32_t act = 0;
@@ -128,8 +132,12 @@ void launch_pack_conv_weights(float* dst, const float* w, int Cout, int Cin, int
 // Packs a row-major B[K, N] matrix the same way (a 1x1 conv with Cin = K).
 void launch_pack_gemm_b(float* dst, const float* b, int K, int N, int bn, hipStream_t s);
 
-// Bytes of packed weights for a given tile width.
+// Elements of packed weights for a given tile width.
 int64_t packed_weight_elems(int Cout, int K, int bn);
+// Elements of direct-conv packed weights.
+inline int64_t direct_packed_elems(int Cout, int K) {
+    return static_cast<int64_t>((Cout + kDirectCB - 1) / kDirectCB) * K * kDirectCB;
+}
 
 }  // namespace k
 }  // namespace pdefa

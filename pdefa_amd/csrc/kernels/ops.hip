@@ -35,13 +35,48 @@ int64_t numel(const View& v) {
 
 }  // namespace
 
-__global__ __launch_bounds__(256) void eltwise_kernel(int op, View out, View a, View b, float alpha, int64_t total) {
-    for (int64_t i = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; i < total;
-         i += static_cast<int64_t>(gridDim.x) * blockDim.x) {
-        int64_t rem = i, oo = 0, ao = 0, bo = 0;
+// Views with every offset inside int32 take the int32 instantiations (the
+// index decomposition is most of the work of these kernels).
+template <typename I>
+struct IView {
+    float* ptr;
+    int32_t rank;
+    I dims[kMaxRank];
+    I str[kMaxRank];
+};
+
+template <typename I>
+IView<I> iview(const View& v) {
+    IView<I> r{};
+    r.ptr = v.ptr;
+    r.rank = v.rank;
+    for (int d = 0; d < kMaxRank; ++d) {
+        r.dims[d] = static_cast<I>(v.dims[d]);
+        r.str[d] = static_cast<I>(v.str[d]);
+    }
+    return r;
+}
+
+// True when every element offset of the view (and its element count) fits in int32.
+bool fits_i32(const View& v) {
+    int64_t ext = 0, n = 1;
+    for (int d = 0; d < v.rank; ++d) {
+        if (v.dims[d] <= 0) return true;
+        ext += (v.dims[d] - 1) * (v.str[d] < 0 ? -v.str[d] : v.str[d]);
+        n *= v.dims[d];
+    }
+    return ext < (int64_t{1} << 31) && n < (int64_t{1} << 31);
+}
+
+template <typename I>
+__global__ __launch_bounds__(256) void eltwise_kernel(int op, IView<I> out, IView<I> a, IView<I> b, float alpha,
+                                                      I total) {
+    for (I i = blockIdx.x * static_cast<I>(blockDim.x) + threadIdx.x; i < total;
+         i += static_cast<I>(gridDim.x) * blockDim.x) {
+        I rem = i, oo = 0, ao = 0, bo = 0;
         for (int d = out.rank - 1; d >= 0; --d) {
-            const int64_t n = out.dims[d];
-            const int64_t idx = rem % n;
+            const I n = out.dims[d];
+            const I idx = rem % n;
             rem /= n;
             oo += idx * out.str[d];
             ao += idx * a.str[d];
@@ -73,29 +108,34 @@ void launch_eltwise(int op, const View& out, const View& a, const View& b, float
     if (a.rank != out.rank || (binary && b.rank != out.rank)) throw std::runtime_error("eltwise: rank mismatch");
     const int64_t total = numel(out);
     if (total == 0) return;
-    hipLaunchKernelGGL(eltwise_kernel, dim3(grid_for(total)), dim3(256), 0, s, op, out, a, binary ? b : a, alpha,
-                       total);
+    const View& bb = binary ? b : a;
+    if (fits_i32(out) && fits_i32(a) && fits_i32(bb))
+        hipLaunchKernelGGL(eltwise_kernel<int32_t>, dim3(grid_for(total)), dim3(256), 0, s, op, iview<int32_t>(out),
+                           iview<int32_t>(a), iview<int32_t>(bb), alpha, static_cast<int32_t>(total));
+    else
+        hipLaunchKernelGGL(eltwise_kernel<int64_t>, dim3(grid_for(total)), dim3(256), 0, s, op, iview<int64_t>(out),
+                           iview<int64_t>(a), iview<int64_t>(bb), alpha, total);
 }
 
-__global__ __launch_bounds__(256) void maxpool_kernel(View out, View in, int kh, int kw, int sh, int sw, int ph,
-                                                      int pw, int64_t total) {
-    const int64_t N = out.dims[0], C = out.dims[1], Ho = out.dims[2], Wo = out.dims[3];
-    const int64_t H = in.dims[2], W = in.dims[3];
-    for (int64_t i = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; i < total;
-         i += static_cast<int64_t>(gridDim.x) * blockDim.x) {
-        int64_t t = i;
-        const int64_t c = t % C; t /= C;
-        const int64_t wo = t % Wo; t /= Wo;
-        const int64_t ho = t % Ho;
-        const int64_t n = t / Ho;
-        (void)N;
+template <typename I>
+__global__ __launch_bounds__(256) void maxpool_kernel(IView<I> out, IView<I> in, int kh, int kw, int sh, int sw, int ph,
+                                                      int pw, I total) {
+    const I C = out.dims[1], Ho = out.dims[2], Wo = out.dims[3];
+    const I H = in.dims[2], W = in.dims[3];
+    for (I i = blockIdx.x * static_cast<I>(blockDim.x) + threadIdx.x; i < total;
+         i += static_cast<I>(gridDim.x) * blockDim.x) {
+        I t = i;
+        const I c = t % C; t /= C;
+        const I wo = t % Wo; t /= Wo;
+        const I ho = t % Ho;
+        const I n = t / Ho;
         const float* base = in.ptr + n * in.str[0] + c * in.str[1];
         float m = -3.402823466e+38f;
         for (int a = 0; a < kh; ++a) {
-            const int64_t hi = ho * sh - ph + a;
+            const I hi = ho * sh - ph + a;
             if (hi < 0 || hi >= H) continue;
             for (int b = 0; b < kw; ++b) {
-                const int64_t wi = wo * sw - pw + b;
+                const I wi = wo * sw - pw + b;
                 if (wi < 0 || wi >= W) continue;
                 const float v = base[hi * in.str[2] + wi * in.str[3]];
                 m = v > m ? v : m;
@@ -112,21 +152,27 @@ void launch_maxpool(const View& out, const View& in, int kh, int kw, int sh, int
     if (out.dims[0] != in.dims[0] || out.dims[1] != in.dims[1]) throw std::runtime_error("maxpool: N/C mismatch");
     const int64_t total = numel(out);
     if (total == 0) return;
-    hipLaunchKernelGGL(maxpool_kernel, dim3(grid_for(total)), dim3(256), 0, s, out, in, kh, kw, sh, sw, ph, pw, total);
+    if (fits_i32(out) && fits_i32(in))
+        hipLaunchKernelGGL(maxpool_kernel<int32_t>, dim3(grid_for(total)), dim3(256), 0, s, iview<int32_t>(out),
+                           iview<int32_t>(in), kh, kw, sh, sw, ph, pw, static_cast<int32_t>(total));
+    else
+        hipLaunchKernelGGL(maxpool_kernel<int64_t>, dim3(grid_for(total)), dim3(256), 0, s, iview<int64_t>(out),
+                           iview<int64_t>(in), kh, kw, sh, sw, ph, pw, total);
 }
 
-__global__ __launch_bounds__(256) void resize_nearest_kernel(View out, View in, float ry, float rx, int64_t total) {
-    const int64_t C = out.dims[1], Ho = out.dims[2], Wo = out.dims[3];
-    const int64_t H = in.dims[2], W = in.dims[3];
-    for (int64_t i = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; i < total;
-         i += static_cast<int64_t>(gridDim.x) * blockDim.x) {
-        int64_t t = i;
-        const int64_t c = t % C; t /= C;
-        const int64_t wo = t % Wo; t /= Wo;
-        const int64_t ho = t % Ho;
-        const int64_t n = t / Ho;
-        int64_t hi = static_cast<int64_t>(static_cast<float>(ho) * ry);
-        int64_t wi = static_cast<int64_t>(static_cast<float>(wo) * rx);
+template <typename I>
+__global__ __launch_bounds__(256) void resize_nearest_kernel(IView<I> out, IView<I> in, float ry, float rx, I total) {
+    const I C = out.dims[1], Ho = out.dims[2], Wo = out.dims[3];
+    const I H = in.dims[2], W = in.dims[3];
+    for (I i = blockIdx.x * static_cast<I>(blockDim.x) + threadIdx.x; i < total;
+         i += static_cast<I>(gridDim.x) * blockDim.x) {
+        I t = i;
+        const I c = t % C; t /= C;
+        const I wo = t % Wo; t /= Wo;
+        const I ho = t % Ho;
+        const I n = t / Ho;
+        I hi = static_cast<I>(static_cast<float>(ho) * ry);
+        I wi = static_cast<I>(static_cast<float>(wo) * rx);
         hi = hi < H - 1 ? hi : H - 1;
         wi = wi < W - 1 ? wi : W - 1;
         out.ptr[n * out.str[0] + c * out.str[1] + ho * out.str[2] + wo * out.str[3]] =
@@ -143,35 +189,79 @@ void launch_resize_nearest(const View& out, const View& in, hipStream_t s) {
     const float rx = static_cast<float>(in.dims[3]) / static_cast<float>(out.dims[3]);
     const int64_t total = numel(out);
     if (total == 0) return;
-    hipLaunchKernelGGL(resize_nearest_kernel, dim3(grid_for(total)), dim3(256), 0, s, out, in, ry, rx, total);
+    if (fits_i32(out) && fits_i32(in))
+        hipLaunchKernelGGL(resize_nearest_kernel<int32_t>, dim3(grid_for(total)), dim3(256), 0, s, iview<int32_t>(out),
+                           iview<int32_t>(in), ry, rx, static_cast<int32_t>(total));
+    else
+        hipLaunchKernelGGL(resize_nearest_kernel<int64_t>, dim3(grid_for(total)), dim3(256), 0, s, iview<int64_t>(out),
+                           iview<int64_t>(in), ry, rx, total);
 }
 
-__global__ __launch_bounds__(256) void softmax_kernel(View out, View in, int axis, int64_t rows) {
-    const int64_t L = in.dims[axis];
-    for (int64_t r = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; r < rows;
-         r += static_cast<int64_t>(gridDim.x) * blockDim.x) {
-        int64_t rem = r, io = 0, oo = 0;
+template <typename I>
+__global__ __launch_bounds__(256) void softmax_kernel(IView<I> out, IView<I> in, int axis, I rows) {
+    const I L = in.dims[axis];
+    for (I r = blockIdx.x * static_cast<I>(blockDim.x) + threadIdx.x; r < rows;
+         r += static_cast<I>(gridDim.x) * blockDim.x) {
+        I rem = r, io = 0, oo = 0;
         for (int d = in.rank - 1; d >= 0; --d) {
             if (d == axis) continue;
-            const int64_t idx = rem % in.dims[d];
+            const I idx = rem % in.dims[d];
             rem /= in.dims[d];
             io += idx * in.str[d];
             oo += idx * out.str[d];
         }
-        const int64_t is = in.str[axis], os = out.str[axis];
+        const I is = in.str[axis], os = out.str[axis];
         float mx = -1e30f;
-        for (int64_t j = 0; j < L; ++j) {
+        for (I j = 0; j < L; ++j) {
             const float v = in.ptr[io + j * is];
             mx = v > mx ? v : mx;
         }
         float sum = 0.0f;
-        for (int64_t j = 0; j < L; ++j) {
+        for (I j = 0; j < L; ++j) {
             const float e = expf(in.ptr[io + j * is] - mx);
             out.ptr[oo + j * os] = e;
             sum += e;
         }
         const float inv = sum > 0.0f ? 1.0f / sum : 0.0f;
-        for (int64_t j = 0; j < L; ++j) out.ptr[oo + j * os] *= inv;
+        for (I j = 0; j < L; ++j) out.ptr[oo + j * os] *= inv;
+    }
+}
+
+// Softmax over a contiguous axis of L = 4*Q elements (Q <= 16), one row per
+// lane held in registers: 16-byte loads and stores, int32 row decomposition.
+// Same arithmetic as the generic kernel (max, exp(x - max), sum, * 1/sum).
+template <int Q>
+__global__ __launch_bounds__(256) void softmax_vec_kernel(IView<int32_t> out, IView<int32_t> in, int axis,
+                                                          int32_t rows) {
+    typedef float f4 __attribute__((ext_vector_type(4)));
+    for (int32_t r = blockIdx.x * 256 + threadIdx.x; r < rows; r += gridDim.x * 256) {
+        int32_t rem = r, io = 0, oo = 0;
+        for (int d = in.rank - 1; d >= 0; --d) {
+            if (d == axis) continue;
+            const int32_t idx = rem % in.dims[d];
+            rem /= in.dims[d];
+            io += idx * in.str[d];
+            oo += idx * out.str[d];
+        }
+        f4 v[Q];
+#pragma unroll
+        for (int q = 0; q < Q; ++q) v[q] = *reinterpret_cast<const f4*>(in.ptr + io + 4 * q);
+        float mx = -1e30f;
+#pragma unroll
+        for (int q = 0; q < Q; ++q)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) mx = v[q][e] > mx ? v[q][e] : mx;
+        float sum = 0.0f;
+#pragma unroll
+        for (int q = 0; q < Q; ++q)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                v[q][e] = expf(v[q][e] - mx);
+                sum += v[q][e];
+            }
+        const float inv = sum > 0.0f ? 1.0f / sum : 0.0f;
+#pragma unroll
+        for (int q = 0; q < Q; ++q) *reinterpret_cast<f4*>(out.ptr + oo + 4 * q) = v[q] * inv;
     }
 }
 
@@ -179,51 +269,108 @@ void launch_softmax(const View& out, const View& in, int axis, hipStream_t s) {
     check_view(out, "softmax out");
     check_view(in, "softmax in");
     if (out.rank != in.rank || axis < 0 || axis >= in.rank) throw std::runtime_error("softmax: bad axis/rank");
-    const int64_t rows = numel(in) / std::max<int64_t>(1, in.dims[axis]);
+    const int64_t L = in.dims[axis];
+    const int64_t rows = numel(in) / std::max<int64_t>(1, L);
     if (rows == 0) return;
-    hipLaunchKernelGGL(softmax_kernel, dim3(grid_for(rows)), dim3(256), 0, s, out, in, axis, rows);
+    const bool i32 = fits_i32(out) && fits_i32(in);
+    bool vec = i32 && in.str[axis] == 1 && out.str[axis] == 1 && L % 4 == 0 && L >= 4 && L <= 64 &&
+               (reinterpret_cast<uintptr_t>(in.ptr) & 15) == 0 && (reinterpret_cast<uintptr_t>(out.ptr) & 15) == 0;
+    for (int d = 0; d < in.rank && vec; ++d)
+        if (d != axis && (in.str[d] % 4 != 0 || out.str[d] % 4 != 0)) vec = false;
+    const unsigned g = grid_for(rows);
+    if (vec) {
+        const IView<int32_t> o = iview<int32_t>(out), x = iview<int32_t>(in);
+        const int32_t r = static_cast<int32_t>(rows);
+        switch (L / 4) {
+            case 1: hipLaunchKernelGGL(softmax_vec_kernel<1>, dim3(g), dim3(256), 0, s, o, x, axis, r); return;
+            case 2: hipLaunchKernelGGL(softmax_vec_kernel<2>, dim3(g), dim3(256), 0, s, o, x, axis, r); return;
+            case 4: hipLaunchKernelGGL(softmax_vec_kernel<4>, dim3(g), dim3(256), 0, s, o, x, axis, r); return;
+            case 8: hipLaunchKernelGGL(softmax_vec_kernel<8>, dim3(g), dim3(256), 0, s, o, x, axis, r); return;
+            case 16: hipLaunchKernelGGL(softmax_vec_kernel<16>, dim3(g), dim3(256), 0, s, o, x, axis, r); return;
+            default: break;
+        }
+    }
+    if (i32)
+        hipLaunchKernelGGL(softmax_kernel<int32_t>, dim3(g), dim3(256), 0, s, iview<int32_t>(out), iview<int32_t>(in),
+                           axis, static_cast<int32_t>(rows));
+    else
+        hipLaunchKernelGGL(softmax_kernel<int64_t>, dim3(g), dim3(256), 0, s, iview<int64_t>(out), iview<int64_t>(in),
+                           axis, rows);
 }
 
-__global__ __launch_bounds__(256) void conv_direct_kernel(ConvDirectArgs a, int64_t total) {
-    const int64_t Co = a.y.dims[1], Ho = a.y.dims[2], Wo = a.y.dims[3];
-    const int64_t Ci = a.x.dims[1], H = a.x.dims[2], W = a.x.dims[3];
-    for (int64_t i = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; i < total;
-         i += static_cast<int64_t>(gridDim.x) * blockDim.x) {
-        int64_t t = i;
-        const int64_t co = t % Co; t /= Co;
-        const int64_t wo = t % Wo; t /= Wo;
-        const int64_t ho = t % Ho;
-        const int64_t n = t / Ho;
-        float acc = 0.0f;
-        const float* xb = a.x.ptr + n * a.x.str[0];
-        const float* wb = a.w + co * Ci * a.KH * a.KW;
-        for (int64_t c = 0; c < Ci; ++c) {
-            for (int kh = 0; kh < a.KH; ++kh) {
-                const int64_t hi = ho * a.sh - a.ph + kh * a.dh;
-                if (hi < 0 || hi >= H) continue;
-                for (int kw = 0; kw < a.KW; ++kw) {
-                    const int64_t wi = wo * a.sw - a.pw + kw * a.dw;
-                    if (wi < 0 || wi >= W) continue;
-                    acc += xb[c * a.x.str[1] + hi * a.x.str[2] + wi * a.x.str[3]] *
-                           wb[(c * a.KH + kh) * a.KW + kw];
-                }
+// Direct convolution, one output pixel x kDirectCB output channels per lane.
+// Weights are pre-packed [ceil(Cout/CB)][Cin*KH*KW][CB] so the CB weights of
+// one (ci, kh, kw) are one contiguous, wave-uniform 64-byte read; each input
+// value loaded feeds CB FMAs.  Index math is int32 within one image.
+__global__ __launch_bounds__(256) void conv_direct_kernel(ConvDirectArgs a, int P) {
+    constexpr int CB = kDirectCB;
+    const int p = blockIdx.x * 256 + threadIdx.x;
+    const int cob = blockIdx.y;
+    const int Co = static_cast<int>(a.y.dims[1]), Ho = static_cast<int>(a.y.dims[2]), Wo = static_cast<int>(a.y.dims[3]);
+    const int Ci = static_cast<int>(a.x.dims[1]), H = static_cast<int>(a.x.dims[2]), W = static_cast<int>(a.x.dims[3]);
+    const int K = Ci * a.KH * a.KW;
+    const float* wb = a.wpk + static_cast<int64_t>(cob) * K * CB;
+    if (p >= P) return;
+    const int HoWo = Ho * Wo;
+    const int n = p / HoWo;
+    const int rem = p - n * HoWo;
+    const int ho = rem / Wo;
+    const int wo = rem - ho * Wo;
+    const float* xb = a.x.ptr + static_cast<int64_t>(n) * a.x.str[0];
+    const int xsc = static_cast<int>(a.x.str[1]), xsh = static_cast<int>(a.x.str[2]), xsw = static_cast<int>(a.x.str[3]);
+    const int hi0 = ho * a.sh - a.ph, wi0 = wo * a.sw - a.pw;
+    float acc[CB];
+#pragma unroll
+    for (int j = 0; j < CB; ++j) acc[j] = 0.0f;
+    const float* wk = wb;
+    for (int c = 0; c < Ci; ++c) {
+        for (int kh = 0; kh < a.KH; ++kh) {
+            const int hi = hi0 + kh * a.dh;
+            const bool hok = static_cast<unsigned>(hi) < static_cast<unsigned>(H);
+            for (int kw = 0; kw < a.KW; ++kw, wk += CB) {
+                const int wi = wi0 + kw * a.dw;
+                const bool ok = hok && static_cast<unsigned>(wi) < static_cast<unsigned>(W);
+                const float xv = ok ? xb[c * xsc + hi * xsh + wi * xsw] : 0.0f;
+#pragma unroll
+                for (int j = 0; j < CB; ++j) acc[j] += xv * wk[j];
             }
         }
-        if (a.bias) acc += a.bias[co];
-        float v = apply_act(acc, a.act, a.slope);
-        if (a.res.ptr) v += a.res.ptr[n * a.res.str[0] + co * a.res.str[1] + ho * a.res.str[2] + wo * a.res.str[3]];
-        a.y.ptr[n * a.y.str[0] + co * a.y.str[1] + ho * a.y.str[2] + wo * a.y.str[3]] = v;
+    }
+    const int64_t yo = static_cast<int64_t>(n) * a.y.str[0] + static_cast<int64_t>(ho) * a.y.str[2] +
+                       static_cast<int64_t>(wo) * a.y.str[3];
+    const int64_t ro = a.res.ptr ? static_cast<int64_t>(n) * a.res.str[0] + static_cast<int64_t>(ho) * a.res.str[2] +
+                                       static_cast<int64_t>(wo) * a.res.str[3]
+                                 : 0;
+#pragma unroll
+    for (int j = 0; j < CB; ++j) {
+        const int co = cob * CB + j;
+        if (co < Co) {
+            float v = apply_act(acc[j] + (a.bias ? a.bias[co] : 0.0f), a.act, a.slope);
+            if (a.res.ptr) v += a.res.ptr[ro + co * a.res.str[1]];
+            a.y.ptr[yo + co * a.y.str[1]] = v;
+        }
     }
 }
 
 void launch_conv_direct(const ConvDirectArgs& a, hipStream_t s) {
     check_view(a.x, "conv_direct x");
     check_view(a.y, "conv_direct y");
-    if (!a.w) throw std::runtime_error("conv_direct: null weights");
+    if (!a.wpk) throw std::runtime_error("conv_direct: null weights");
     if (a.x.rank != 4 || a.y.rank != 4) throw std::runtime_error("conv_direct: rank 4 views expected");
-    const int64_t total = numel(a.y);
-    if (total == 0) return;
-    hipLaunchKernelGGL(conv_direct_kernel, dim3(grid_for(total)), dim3(256), 0, s, a, total);
+    if (a.res.ptr && a.res.rank != 4) throw std::runtime_error("conv_direct: rank 4 residual expected");
+    const int64_t P = a.y.dims[0] * a.y.dims[2] * a.y.dims[3];
+    if (P == 0 || a.y.dims[1] == 0) return;
+    auto extent = [](const View& v) {
+        int64_t e = 1;
+        for (int d = 1; d < 4; ++d) e += (v.dims[d] - 1) * std::abs(v.str[d]);
+        return e;
+    };
+    if (P >= (int64_t{1} << 31) || extent(a.x) >= (int64_t{1} << 31) ||
+        a.x.dims[1] * a.KH * a.KW * kDirectCB >= (int64_t{1} << 31))
+        throw std::runtime_error("conv_direct: shape exceeds int32 indexing");
+    const dim3 grid(static_cast<unsigned>((P + 255) / 256),
+                    static_cast<unsigned>((a.y.dims[1] + kDirectCB - 1) / kDirectCB));
+    hipLaunchKernelGGL(conv_direct_kernel, grid, dim3(256), 0, s, a, static_cast<int>(P));
 }
 
 }  // namespace k

@@ -798,7 +798,10 @@ class Planner {
         const Node& n = m_.nodes[e.node];
         const OpParams& p = n.params;
         const Dims& wd = val(e.in[1]).dims;
-        const VRef x = conv_input_view(e.in[0], e.node);
+        // Tiny-Cin layers (the 3-channel stem) and tiny-Cout layers go to the
+        // direct kernel, which reads any layout (no channels-last input copy).
+        const bool small = wd[0] < 8 || (wd[1] % 4 != 0 && wd[1] * wd[2] * wd[3] <= 64);
+        const VRef x = small ? input_view(e.in[0]) : conv_input_view(e.in[0], e.node);
         const VRef y = val(e.out).view;
         Step s;
         s.node = e.node;
@@ -825,7 +828,7 @@ class Planner {
             s.res = input_view(e.res);
         }
         const bool cl = x.str[1] == 1 && y.str[1] == 1 && (!s.has_res || s.res.str[1] == 1);
-        if (cl && cout >= 8) {
+        if (cl && !small) {
             s.kind = StepKind::ConvMfma;
             s.vec = cin % 4 == 0 && x.off % 4 == 0 && x.str[0] % 4 == 0 && x.str[2] % 4 == 0 && x.str[3] % 4 == 0;
             const int bn = conv_pack_bn(static_cast<int>(cout));
@@ -841,9 +844,11 @@ class Planner {
             const int64_t K = cin * s.KH * s.KW;
             const int ktiles = static_cast<int>((K + k::kConvBK - 1) / k::kConvBK);
             const int64_t wgs = ((M + bm - 1) / bm) * nt;
+            // Split K when the grid cannot fill the 256 CUs, keeping >= 3 K-tiles
+            // per split and aiming at ~384 workgroups.
             int splits = 1;
-            if (opt_.split_k && wgs < 128 && ktiles >= 32) {
-                splits = static_cast<int>(std::min<int64_t>({16, ktiles / 16, (256 + wgs - 1) / wgs}));
+            if (opt_.split_k && wgs < 256 && ktiles >= 6) {
+                splits = static_cast<int>(std::min<int64_t>({32, ktiles / 3, (384 + wgs - 1) / wgs}));
                 splits = std::max(splits, 1);
             }
             s.kt_per_split = (ktiles + splits - 1) / splits;

@@ -53,7 +53,7 @@ std::shared_ptr<DeviceModel> upload_model(const Model& m) {
         total += align_up(static_cast<size_t>(std::max<int64_t>(1, m.weights[i].numel())));
     }
     struct PackPlan {
-        size_t node, wpk_off, bias_off;
+        size_t node, wpk_off, bias_off, dpk_off;
         int cout, cin, kh, kw, bn, w, b;
     };
     std::vector<PackPlan> pp;
@@ -77,6 +77,8 @@ std::shared_ptr<DeviceModel> upload_model(const Model& m) {
         total += align_up(static_cast<size_t>(k::packed_weight_elems(p.cout, p.kh * p.kw * p.cin, p.bn)));
         p.bias_off = total;
         total += align_up(static_cast<size_t>((p.cout + p.bn - 1) / p.bn * p.bn));
+        p.dpk_off = total;
+        total += align_up(static_cast<size_t>(k::direct_packed_elems(p.cout, p.kh * p.kw * p.cin)));
         pp.push_back(p);
     }
     total = std::max<size_t>(total, kAlignFloats);
@@ -84,8 +86,17 @@ std::shared_ptr<DeviceModel> upload_model(const Model& m) {
     std::vector<float> host(total, 0.0f);
     for (size_t i = 0; i < m.weights.size(); ++i)
         if (m.weights[i].nbytes) std::memcpy(host.data() + woff[i], m.weights[i].data, m.weights[i].nbytes);
-    for (const auto& p : pp)
+    for (const auto& p : pp) {
         if (p.b >= 0) std::memcpy(host.data() + p.bias_off, m.weights[p.b].data, sizeof(float) * p.cout);
+        // direct-conv layout [co / CB][k][co % CB], k = (ci, kh, kw); padding stays zero
+        const int K = p.cin * p.kh * p.kw;
+        const float* src = static_cast<const float*>(m.weights[p.w].data);
+        float* dst = host.data() + p.dpk_off;
+        for (int co = 0; co < p.cout; ++co)
+            for (int kk = 0; kk < K; ++kk)
+                dst[(static_cast<size_t>(co / k::kDirectCB) * K + kk) * k::kDirectCB + co % k::kDirectCB] =
+                    src[static_cast<size_t>(co) * K + kk];
+    }
     dm->blob_bytes = total * sizeof(float);
     PDEFA_HIP(hipMalloc(&dm->blob, dm->blob_bytes));
     PDEFA_HIP(hipMemcpy(dm->blob, host.data(), dm->blob_bytes, hipMemcpyHostToDevice));
@@ -100,6 +111,7 @@ std::shared_ptr<DeviceModel> upload_model(const Model& m) {
             pk.wpk = dm->blob + p.wpk_off;
             pk.bias = dm->blob + p.bias_off;
             pk.bn = p.bn;
+            pk.dpk = dm->blob + p.dpk_off;
             k::launch_pack_conv_weights(pk.wpk, dm->wptr[p.w], p.cout, p.cin, p.kh, p.kw, p.bn, s);
             PDEFA_HIP(hipGetLastError());
         }
@@ -298,14 +310,12 @@ void Session::prepare(const std::vector<std::vector<int64_t>>& dims) {
                 d.y = V(s.out, "conv y", si);
                 if (s.has_res) d.res = V(s.res, "conv res", si);
                 const int w = -1000 - n.inputs[1];
-                d.w = dev_->wptr.at(w);
                 const HostTensor& wt = model_->weights.at(w);
                 if (wt.dims[0] != d.y.dims[1] || wt.dims[1] != d.x.dims[1]) throw std::runtime_error("conv weight shape mismatch");
-                if (n.inputs.size() > 2 && n.inputs[2] <= -1000) {
-                    const int b = -1000 - n.inputs[2];
-                    if (model_->weights.at(b).numel() < d.y.dims[1]) throw std::runtime_error("conv bias too short");
-                    d.bias = dev_->wptr.at(b);
-                }
+                const DeviceModel::Pack& pk = dev_->packs.at(s.node);
+                if (!pk.dpk || !pk.bias) throw std::runtime_error("conv weights not packed");
+                d.wpk = pk.dpk;
+                d.bias = pk.bias;
                 d.KH = s.KH;
                 d.KW = s.KW;
                 d.sh = s.sh;
