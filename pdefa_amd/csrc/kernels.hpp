@@ -36,24 +36,37 @@ enum Act : int32_t {
     kActSiluWinogradForm = 6,
 };
 
-// Implicit-GEMM convolution tile configurations (BM x BN output tile, 4 waves,
-// K advanced kConvBK at a time).
-enum ConvTile : int32_t {
-    kTile128x32 = 0,
-    kTile128x64 = 1,
-    kTile128x128 = 2,
-    kTile64x64 = 3,
-    kTile64x128 = 4,
-    kNumConvTiles = 5,
+// Implicit-GEMM convolution tile configurations.  A workgroup is 4 waves and
+// computes a BM x BN output tile; each wave owns a WM x WN sub-tile of 32x32
+// MFMA blocks and one of KG interleaved K slices.  KG > 1 splits K across the
+// waves of one workgroup (partial tiles summed through LDS in slice order),
+// which multiplies the workgroup count of small layers without any
+// cross-workgroup traffic.
+struct ConvTileShape {
+    int bm, bn, wm, wn, kg;
 };
+enum ConvTile : int32_t {
+    kTile128x128 = 0,   // 2x2 waves of 64x64
+    kTile128x64 = 1,    // 2x2 waves of 64x32
+    kTile64x128 = 2,    // 2x2 waves of 32x64
+    kTile64x64 = 3,     // 2x2 waves of 32x32
+    kTile128x32 = 4,    // 4x1 waves of 32x32
+    kTile64x32K2 = 5,   // 2x1 waves of 32x32, K split in 2
+    kTile32x64K2 = 6,   // 1x2 waves of 32x32, K split in 2
+    kTile32x32K4 = 7,   // 1 wave tile of 32x32, K split in 4
+    kNumConvTiles = 8,
+};
+ConvTileShape conv_tile_shape(int tile);
+const char* conv_tile_name(int tile);
+
+// Packed conv weights: [ceil(Cout/32)][ceil(K/32)][32 co][32 k] with
+// k = (kh*KW + kw)*Cin + ci, zero padded.  32-wide blocks serve every tile.
 constexpr int kConvBK = 32;
-int conv_tile_bm(int tile);
-int conv_tile_bn(int tile);
+constexpr int kConvBN = 32;
 
 // NHWC implicit GEMM: M = N*Ho*Wo, Ncol = Cout, K = KH*KW*Cin with k ordered
 // (kh, kw, ci).  Input/output/residual are channels-last views (channel stride
-// 1) described by their n/h/w strides.  Weights are pre-packed as
-// [Cout_pad/BN][K_pad/BK][BN][BK]; bias is padded to Cout_pad.
+// 1) described by their n/h/w strides.
 struct ConvArgs {
     const float* x = nullptr;
     int64_t x_sn = 0, x_sh = 0, x_sw = 0;
@@ -64,18 +77,27 @@ struct ConvArgs {
     const float* res = nullptr;  // optional residual added after the activation
     int64_t r_sn = 0, r_sh = 0, r_sw = 0;
     const float* wpk = nullptr;
-    const float* bias = nullptr;
+    const float* bias = nullptr;  // >= Cout floats
     int32_t KH = 1, KW = 1, sh = 1, sw = 1, ph = 0, pw = 0, dh = 1, dw = 1;
     int32_t K = 0;        // KH*KW*Cin
-    int32_t ktiles = 0;   // ceil(K / BK)
+    int32_t ktiles = 0;   // ceil(K / 32): 32-wide K blocks of the packed weights
     int32_t act = 0;
     float slope = 0.01f;
-    // split-K: splits > 1 writes raw partial sums to ws[split][M][Cout] and a
-    // reduce kernel sums them in split order and applies bias/activation/residual.
+    // split-K across workgroups: splits > 1 writes raw partial sums to
+    // ws[split][M][Cout] (split z covers K blocks [z*kt_per_split, ...)) and a
+    // reduce kernel sums them in split order, then applies the epilogue.
     float* ws = nullptr;
     int32_t splits = 1;
-    int32_t kt_per_split = 0;
+    int32_t kt_per_split = 0;  // multiple of the tile's KG
 };
+
+// Tile and split-K choice for an implicit GEMM of this shape on the 256 CUs.
+struct ConvLaunchShape {
+    int tile = kTile64x64;
+    int splits = 1;
+    int kt_per_split = 0;
+};
+ConvLaunchShape conv_select(int64_t M, int Cout, int K, bool allow_split);
 
 // Host-side checks + launch.  vec selects 16-byte input loads (requires
 // Cin % 4 == 0 and 16-byte aligned pixel rows).
@@ -125,15 +147,14 @@ void launch_resize_nearest(const View& out, const View& in, hipStream_t s);
 // Softmax along `axis` of the logical shape.
 void launch_softmax(const View& out, const View& in, int axis, hipStream_t s);
 
-// Packs conv weights [Cout, Cin, KH, KW] (device, contiguous) into the
-// [Cout_pad/BN][K_pad/BK][BN][BK] layout with k = (kh*KW + kw)*Cin + ci.
-void launch_pack_conv_weights(float* dst, const float* w, int Cout, int Cin, int KH, int KW,
-                              int bn, hipStream_t s);
+// Packs conv weights [Cout, Cin, KH, KW] (device, contiguous) into the packed
+// layout above.
+void launch_pack_conv_weights(float* dst, const float* w, int Cout, int Cin, int KH, int KW, hipStream_t s);
 // Packs a row-major B[K, N] matrix the same way (a 1x1 conv with Cin = K).
-void launch_pack_gemm_b(float* dst, const float* b, int K, int N, int bn, hipStream_t s);
+void launch_pack_gemm_b(float* dst, const float* b, int K, int N, hipStream_t s);
 
-// Elements of packed weights for a given tile width.
-int64_t packed_weight_elems(int Cout, int K, int bn);
+// Elements of packed weights.
+int64_t packed_weight_elems(int Cout, int K);
 // Elements of direct-conv packed weights.
 inline int64_t direct_packed_elems(int Cout, int K) {
     return static_cast<int64_t>((Cout + kDirectCB - 1) / kDirectCB) * K * kDirectCB;

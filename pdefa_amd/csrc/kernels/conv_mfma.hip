@@ -3,20 +3,28 @@
 // GEMM view of an NHWC convolution: C[m, co] = sum_k A[m, k] * B[k, co] with
 // m = (n, ho, wo), k = (kh, kw, ci) and A gathered on the fly from the input
 // (no im2col buffer).  One workgroup = 4 waves (256 lanes) computes a BM x BN
-// output tile; each wave owns a (BM/WAVES_M) x (BN/WAVES_N) sub-tile made of
-// 32x32 MFMA blocks.
+// output tile.  Each wave owns a WM x WN sub-tile of 32x32 MFMA blocks and one
+// of KG K slices: a pipeline step advances K by BKT = 32*KG, slice g of the
+// step (32 k wide) feeding the waves of group g.  With KG > 1 the slices'
+// partial tiles are summed through LDS in slice order at the end.
 //
-// K advances BK = 32 at a time.  Global loads run two K-tiles ahead of the
-// MFMAs (two register stages) into two LDS stages whose rows are padded to 36
-// floats; each lane feeds four MFMA steps from one 16-byte LDS read: lane half
-// h supplies k = 8q + 4h + j for step (q, j), the same k for A and B, which
-// covers the 32 k of a tile exactly once.
+// Global loads run two steps ahead of the MFMAs (two register stages) into two
+// LDS stages whose rows are padded to 36 floats; each lane feeds four MFMA
+// steps from one 16-byte LDS read: lane half h supplies k = 8q + 4h + j for
+// step (q, j), the same k for A and B, which covers the 32 k of a slice once.
+// Loads are issued unconditionally (out-of-range A rows read the tensor base,
+// out-of-range K blocks and N rows re-read the last valid block) and the
+// in-range mask is applied when a stage is written to LDS, so the loads of the
+// newest step stay in flight while the previous stage is stored.
 //
-// Split-K (small-M deep layers): each split writes its partial tile to a
-// workspace and a reduce kernel sums the partials in split order (so the result
-// does not depend on scheduling) and applies the epilogue.  An in-kernel
-// "last split reduces" fixup was measured slower: on this multi-XCD part the
-// device-scope release/acquire it needs writes back and invalidates the L2.
+// Workgroups are dispatched round-robin over the 8 XCDs, each with its own L2;
+// the tile index is remapped so that every XCD works through a contiguous
+// range of tiles (neighbouring output rows share input rows and all tiles of
+// one N block share weights).
+//
+// Split-K across workgroups (layers whose tile grid cannot fill the chip even
+// with KG = 4): each split writes its partial tile to a workspace and a reduce
+// kernel sums the partials in split order and applies the epilogue.
 //
 // Epilogue: + bias, activation, + optional residual (the C2f bottleneck add),
 // stored through the output view's strides so the result can land directly in
@@ -24,6 +32,8 @@
 #include "../kernels.hpp"
 #include "act.hpp"
 
+#include <algorithm>
+#include <cmath>
 #include <mutex>
 #include <stdexcept>
 #include <string>
@@ -37,52 +47,72 @@ typedef float floatx16 __attribute__((ext_vector_type(16)));
 
 namespace {
 
-constexpr int BK = kConvBK;         // 32
-constexpr int CHUNKS = BK / 4;      // float4 chunks per tile row
+constexpr int BK = kConvBK;         // 32: K per slice and per packed block
 constexpr int LDS_STRIDE = BK + 4;  // floats; 16-byte aligned rows, conflict-free float4 reads
+constexpr int kXcds = 8;
 
-template <int BM, int BN>
+template <int BM, int BN, int KG>
 constexpr size_t lds_bytes() {
-    return sizeof(float) * 2 * (BM + BN) * LDS_STRIDE;
+    return sizeof(float) * 2 * KG * (BM + BN) * LDS_STRIDE;
 }
 
 }  // namespace
 
-template <int BM, int BN, int WAVES_M, bool VEC>
+template <int BM, int BN, int WM, int WN, int KG, bool VEC>
 __global__ __launch_bounds__(256) void conv_mfma_kernel(ConvArgs a) {
-    constexpr int WAVES_N = 4 / WAVES_M;
-    constexpr int WM = BM / WAVES_M;
-    constexpr int WN = BN / WAVES_N;
+    constexpr int WAVES_M = BM / WM;
+    constexpr int WAVES_N = BN / WN;
+    static_assert(WAVES_M * WAVES_N * KG == 4, "4 waves per workgroup");
     constexpr int TM = WM / 32;
     constexpr int TN = WN / 32;
-    constexpr int ROW_STEP = 256 / CHUNKS;   // rows covered by one pass of 256 lanes
-    constexpr int A_ROWS = BM / ROW_STEP;    // A float4 loads per lane per tile
-    constexpr int B_LOADS = (BN * CHUNKS + 255) / 256;
-    static_assert(TM >= 1 && TN >= 1 && WM % 32 == 0 && WN % 32 == 0, "tile");
-    static_assert(BM % ROW_STEP == 0, "BM");
+    constexpr int BKT = BK * KG;            // K per pipeline step
+    constexpr int CH = BKT / 4;             // float4 chunks per tile row per step
+    constexpr int ROW_STEP = 256 / CH;      // rows covered by one pass of 256 lanes
+    constexpr int A_ROWS = BM / ROW_STEP;   // A float4 loads per lane per step
+    constexpr int B_ROWS = BN / ROW_STEP;   // B float4 loads per lane per step
+    static_assert(WM % 32 == 0 && WN % 32 == 0 && BM % ROW_STEP == 0 && BN % ROW_STEP == 0, "tile");
+    static_assert(A_ROWS <= 32, "mask bits");
 
     extern __shared__ __attribute__((aligned(16))) float smem[];
-    float* As[2] = {smem, smem + BM * LDS_STRIDE};
-    float* Bs[2] = {smem + 2 * BM * LDS_STRIDE, smem + 2 * BM * LDS_STRIDE + BN * LDS_STRIDE};
+    // stage st, slice g: A tile at smem + (st*KG + g)*BM*LDS_STRIDE, B tiles after all A tiles
+    auto As = [&](int st, int g) { return smem + (st * KG + g) * BM * LDS_STRIDE; };
+    auto Bs = [&](int st, int g) { return smem + 2 * KG * BM * LDS_STRIDE + (st * KG + g) * BN * LDS_STRIDE; };
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = tid >> 6;
-    const int wave_m = wave % WAVES_M;
-    const int wave_n = wave / WAVES_M;
+    const int wg = wave % KG;
+    const int wave_m = (wave / KG) % WAVES_M;
+    const int wave_n = (wave / KG) / WAVES_M;
     const int HoWo = a.Ho * a.Wo;
     const int M = a.N * HoWo;
-    const int m0 = blockIdx.x * BM;
-    const int ntile = blockIdx.y;
-    const int n0 = ntile * BN;
-    const int kt_begin = blockIdx.z * a.kt_per_split;
-    const int kt_end = min(a.ktiles, kt_begin + a.kt_per_split);
+
+    // XCD-aware tile order: dispatch slot `lin` runs on XCD lin % 8; give each
+    // XCD a contiguous range of (m-tile fastest) tile indices.
+    const int gx = gridDim.x, gxy = gridDim.x * gridDim.y;
+    const int total = gxy * gridDim.z;
+    const int lin = blockIdx.x + gx * blockIdx.y + gxy * blockIdx.z;
+    const int q = total / kXcds, rmd = total % kXcds, xcd = lin % kXcds;
+    const int tile_id = xcd * q + min(xcd, rmd) + lin / kXcds;
+    const int bz = tile_id / gxy;
+    const int bxy = tile_id - bz * gxy;
+    const int by = bxy / gx;
+    const int bx = bxy - by * gx;
+
+    const int m0 = bx * BM;
+    const int n0 = by * BN;
+    const int kb_begin = bz * a.kt_per_split;  // first K block of this split
+    const int kb_end = min(a.ktiles, kb_begin + a.kt_per_split);
+    const int nk = (kb_end - kb_begin + KG - 1) / KG;  // pipeline steps
     const int taps = a.KH * a.KW;
 
-    // ---- A loader: this lane loads float4 chunk `chunk` of rows r0 + ROW_STEP*i.
+    // ---- loaders: this lane loads float4 chunk `chunk` (slice chunk / 8) of
+    // rows r0 + ROW_STEP*i of the A tile and of the B tile.
     // Offsets within one image fit in int32 (checked by the launcher).
-    const int chunk = tid % CHUNKS;
-    const int r0 = tid / CHUNKS;
+    const int chunk = tid % CH;
+    const int r0 = tid / CH;
+    const int cg = chunk / 8;  // slice of this chunk
+    const int cc = chunk % 8;  // chunk within the slice
     int row_hi0[A_ROWS];
     int row_wi0[A_ROWS];
     int row_off0[A_ROWS];
@@ -103,28 +133,33 @@ __global__ __launch_bounds__(256) void conv_mfma_kernel(ConvArgs a) {
         row_off0[r] = row_hi0[r] * xsh + row_wi0[r] * xsw;
         row_base[r] = a.x + static_cast<int64_t>(n) * a.x_sn;
     }
-    // (tap, ci, kh, kw) of this lane's chunk in the next tile to load
+    // (tap, ci, kh, kw) of this lane's chunk in the next step to load
     int tap = 0, ci = 0, kh = 0, kw = 0;
     if (VEC) {
-        const int k0 = kt_begin * BK + chunk * 4;
+        const int k0 = kb_begin * BK + chunk * 4;
         tap = k0 / a.Cin;
         ci = k0 - tap * a.Cin;
         kh = tap / a.KW;
         kw = tap - kh * a.KW;
     }
-    const bool cin_ge_bk = a.Cin >= BK;  // then a tile advance wraps Cin at most once
+    const bool cin_ge_bkt = a.Cin >= BKT;  // then a step advance wraps Cin at most once
 
-    const float* wtile = a.wpk + static_cast<int64_t>(ntile) * a.ktiles * (BN * BK);
+    // B rows of this lane: packed block row of output channel n0 + r0 + ROW_STEP*i
+    // (clamped to the last packed block; such columns are never stored).
+    const int nblocks = (a.Cout + kConvBN - 1) / kConvBN;
+    const float* brow[B_ROWS];
+#pragma unroll
+    for (int i = 0; i < B_ROWS; ++i) {
+        const int co = n0 + r0 + ROW_STEP * i;
+        const int nb = min(co / kConvBN, nblocks - 1);
+        brow[i] = a.wpk + static_cast<int64_t>(nb) * a.ktiles * (kConvBN * BK) + (co % kConvBN) * BK + cc * 4;
+    }
 
-    // Register stages.  Loads are issued unconditionally (out-of-range A rows
-    // read the tensor base, tiles past the end re-read the last tile) and the
-    // in-range mask is applied when the stage is written to LDS, so the loads
-    // of the newest tile stay in flight while the previous stage is stored.
     floatx4 areg[2][A_ROWS];
-    floatx4 breg[2][B_LOADS];
+    floatx4 breg[2][B_ROWS];
     unsigned amask[2] = {0u, 0u};
 
-    auto load_tile = [&](int kt, floatx4* ar, floatx4* br, unsigned& mask) {
+    auto load_step = [&](int kb0, floatx4* ar, floatx4* br, unsigned& mask) {
         unsigned mk = 0;
         if (VEC) {
             const int dy = kh * a.dh, dx = kw * a.dw;
@@ -140,9 +175,9 @@ __global__ __launch_bounds__(256) void conv_mfma_kernel(ConvArgs a) {
                 ar[r] = *reinterpret_cast<const floatx4*>(p);
                 mk |= static_cast<unsigned>(ok) << r;
             }
-            // advance this lane's chunk to the next tile's k
-            ci += BK;
-            if (cin_ge_bk) {
+            // advance this lane's chunk to the next step's k
+            ci += BKT;
+            if (cin_ge_bkt) {
                 const bool wrap = ci >= a.Cin;
                 ci = wrap ? ci - a.Cin : ci;
                 tap += wrap;
@@ -151,23 +186,20 @@ __global__ __launch_bounds__(256) void conv_mfma_kernel(ConvArgs a) {
                 kw = row ? 0 : kw;
                 kh += row;
             } else {
-#pragma unroll
-                for (int w = 0; w < BK / 4; ++w) {
-                    const bool wrap = ci >= a.Cin;
-                    ci = wrap ? ci - a.Cin : ci;
-                    tap += wrap;
-                    kw += wrap;
-                    const bool row = kw == a.KW;
-                    kw = row ? 0 : kw;
-                    kh += row;
-                }
+                const int w = ci / a.Cin;
+                ci -= w * a.Cin;
+                tap += w;
+                kw += w;
+                const int rw = kw / a.KW;
+                kw -= rw * a.KW;
+                kh += rw;
             }
         } else {
 #pragma unroll
             for (int r = 0; r < A_ROWS; ++r) {
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
-                    const int kk = kt * BK + chunk * 4 + e;
+                    const int kk = kb0 * BK + chunk * 4 + e;
                     float v = 0.0f;
                     if (row_ok[r] && kk < a.K) {
                         const int t = kk / a.Cin;
@@ -187,27 +219,22 @@ __global__ __launch_bounds__(256) void conv_mfma_kernel(ConvArgs a) {
             mk = ~0u;
         }
         mask = mk;
-        const float* bt = wtile + static_cast<int64_t>(min(kt, kt_end - 1)) * (BN * BK);
+        const int kb = min(kb0 + cg, a.ktiles - 1);
 #pragma unroll
-        for (int i = 0; i < B_LOADS; ++i) {
-            const int idx = tid + 256 * i;
-            if ((BN * CHUNKS) % 256 == 0 || idx < BN * CHUNKS) br[i] = *reinterpret_cast<const floatx4*>(bt + idx * 4);
-        }
+        for (int i = 0; i < B_ROWS; ++i)
+            br[i] = *reinterpret_cast<const floatx4*>(brow[i] + static_cast<int64_t>(kb) * (kConvBN * BK));
     };
-    auto store_tile = [&](int buf, const floatx4* ar, const floatx4* br, unsigned mask) {
-        float* A = As[buf];
-        float* B = Bs[buf];
+    auto store_step = [&](int st, const floatx4* ar, const floatx4* br, unsigned mask) {
+        float* A = As(st, cg);
+        float* B = Bs(st, cg);
         const floatx4 zero = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
         for (int r = 0; r < A_ROWS; ++r)
-            *reinterpret_cast<floatx4*>(&A[(r0 + ROW_STEP * r) * LDS_STRIDE + chunk * 4]) =
+            *reinterpret_cast<floatx4*>(&A[(r0 + ROW_STEP * r) * LDS_STRIDE + cc * 4]) =
                 ((mask >> r) & 1u) ? ar[r] : zero;
 #pragma unroll
-        for (int i = 0; i < B_LOADS; ++i) {
-            const int idx = tid + 256 * i;
-            if ((BN * CHUNKS) % 256 == 0 || idx < BN * CHUNKS)
-                *reinterpret_cast<floatx4*>(&B[(idx / CHUNKS) * LDS_STRIDE + (idx % CHUNKS) * 4]) = br[i];
-        }
+        for (int i = 0; i < B_ROWS; ++i)
+            *reinterpret_cast<floatx4*>(&B[(r0 + ROW_STEP * i) * LDS_STRIDE + cc * 4]) = br[i];
     };
 
     floatx16 acc[TM][TN];
@@ -220,20 +247,20 @@ __global__ __launch_bounds__(256) void conv_mfma_kernel(ConvArgs a) {
 
     const int half = lane >> 5;
     const int l32 = lane & 31;
-    auto compute_tile = [&](int buf) {
-        const float* Ab = As[buf];
-        const float* Bb = Bs[buf];
+    auto compute_step = [&](int st) {
+        const float* Ab = As(st, wg);
+        const float* Bb = Bs(st, wg);
 #pragma unroll
-        for (int q = 0; q < BK / 8; ++q) {
+        for (int qq = 0; qq < BK / 8; ++qq) {
             floatx4 av[TM], bv[TN];
 #pragma unroll
             for (int tm = 0; tm < TM; ++tm)
                 av[tm] = *reinterpret_cast<const floatx4*>(
-                    &Ab[(wave_m * WM + tm * 32 + l32) * LDS_STRIDE + q * 8 + half * 4]);
+                    &Ab[(wave_m * WM + tm * 32 + l32) * LDS_STRIDE + qq * 8 + half * 4]);
 #pragma unroll
             for (int tn = 0; tn < TN; ++tn)
                 bv[tn] = *reinterpret_cast<const floatx4*>(
-                    &Bb[(wave_n * WN + tn * 32 + l32) * LDS_STRIDE + q * 8 + half * 4]);
+                    &Bb[(wave_n * WN + tn * 32 + l32) * LDS_STRIDE + qq * 8 + half * 4]);
 #pragma unroll
             for (int j = 0; j < 4; ++j)
 #pragma unroll
@@ -244,20 +271,19 @@ __global__ __launch_bounds__(256) void conv_mfma_kernel(ConvArgs a) {
         }
     };
 
-    // ---- software pipeline: tile t is loaded at iteration t-2, stored to LDS
+    // ---- software pipeline: step t is loaded at iteration t-2, stored to LDS
     // at iteration t-1 and multiplied at iteration t.
-    const int nk = kt_end - kt_begin;
     if (nk > 0) {
-        load_tile(kt_begin, areg[0], breg[0], amask[0]);
-        load_tile(kt_begin + 1, areg[1], breg[1], amask[1]);
-        store_tile(0, areg[0], breg[0], amask[0]);
+        load_step(kb_begin, areg[0], breg[0], amask[0]);
+        load_step(kb_begin + KG, areg[1], breg[1], amask[1]);
+        store_step(0, areg[0], breg[0], amask[0]);
         __syncthreads();
     }
     auto iteration = [&](int it, auto stage) {
         constexpr int S = decltype(stage)::value;  // it % 2
-        load_tile(kt_begin + it + 2, areg[S], breg[S], amask[S]);
-        compute_tile(S);
-        if (it + 1 < nk) store_tile(S ^ 1, areg[S ^ 1], breg[S ^ 1], amask[S ^ 1]);
+        load_step(kb_begin + (it + 2) * KG, areg[S], breg[S], amask[S]);
+        compute_step(S);
+        if (it + 1 < nk) store_step(S ^ 1, areg[S ^ 1], breg[S ^ 1], amask[S ^ 1]);
         __syncthreads();
     };
     int it = 0;
@@ -267,51 +293,58 @@ __global__ __launch_bounds__(256) void conv_mfma_kernel(ConvArgs a) {
     }
     if (it < nk) iteration(it, std::integral_constant<int, 0>{});
 
-    // ---- split-K: publish the partial, the last arriving split reduces
-    if (a.splits > 1) {
+    // ---- output: tile element (row, col) -> split-K partial or epilogue
+    auto emit = [&](int row, int col, float v) {
+        const int m = m0 + row;
+        const int co = n0 + col;
+        if (m >= M || co >= a.Cout) return;
+        if (a.splits > 1) {
+            a.ws[(static_cast<int64_t>(bz) * M + m) * a.Cout + co] = v;
+            return;
+        }
+        const int n = m / HoWo;
+        const int rem = m - n * HoWo;
+        const int ho = rem / a.Wo;
+        const int wo = rem - ho * a.Wo;
+        float r = apply_act(v + a.bias[co], a.act, a.slope);
+        if (a.res)
+            r += a.res[static_cast<int64_t>(n) * a.r_sn + static_cast<int64_t>(ho) * a.r_sh +
+                       static_cast<int64_t>(wo) * a.r_sw + co];
+        a.y[static_cast<int64_t>(n) * a.y_sn + static_cast<int64_t>(ho) * a.y_sh + static_cast<int64_t>(wo) * a.y_sw +
+            co] = r;
+    };
+
+    // 32x32 block register e of lane l holds row 8*(e/4) + 4*(l/32) + e%4, column l%32.
+    if (KG == 1) {
 #pragma unroll
         for (int tm = 0; tm < TM; ++tm)
 #pragma unroll
-            for (int e = 0; e < 16; ++e) {
-                const int m = m0 + wave_m * WM + tm * 32 + (e >> 2) * 8 + half * 4 + (e & 3);
-                if (m >= M) continue;
-                float* wrow = a.ws + (static_cast<int64_t>(blockIdx.z) * M + m) * a.Cout;
+            for (int e = 0; e < 16; ++e)
+#pragma unroll
+                for (int tn = 0; tn < TN; ++tn)
+                    emit(wave_m * WM + tm * 32 + (e >> 2) * 8 + half * 4 + (e & 3), wave_n * WN + tn * 32 + l32,
+                         acc[tm][tn][e]);
+    } else {
+        // Slice partials -> LDS (the pipeline's last barrier has retired every
+        // LDS read of the stages), then every lane sums whole tile elements in
+        // slice order.
+        float* red = smem;  // [KG][BM][BN]
+#pragma unroll
+        for (int tm = 0; tm < TM; ++tm)
+#pragma unroll
+            for (int e = 0; e < 16; ++e)
 #pragma unroll
                 for (int tn = 0; tn < TN; ++tn) {
-                    const int col = n0 + wave_n * WN + tn * 32 + l32;
-                    if (col < a.Cout) wrow[col] = acc[tm][tn][e];
+                    const int row = wave_m * WM + tm * 32 + (e >> 2) * 8 + half * 4 + (e & 3);
+                    const int col = wave_n * WN + tn * 32 + l32;
+                    red[(wg * BM + row) * BN + col] = acc[tm][tn][e];
                 }
-            }
-        return;  // the reduce kernel finishes
-    }
-
-    // ---- epilogue.  32x32 block register e of lane l holds
-    // row 8*(e/4) + 4*(l/32) + e%4, column l%32.
+        __syncthreads();
+        for (int idx = tid; idx < BM * BN; idx += 256) {
+            float v = red[idx];
 #pragma unroll
-    for (int tm = 0; tm < TM; ++tm) {
-#pragma unroll
-        for (int e = 0; e < 16; ++e) {
-            const int row = wave_m * WM + tm * 32 + (e >> 2) * 8 + half * 4 + (e & 3);
-            const int m = m0 + row;
-            if (m >= M) continue;
-            const int n = m / HoWo;
-            const int rem = m - n * HoWo;
-            const int ho = rem / a.Wo;
-            const int wo = rem - ho * a.Wo;
-            float* yrow = a.y + static_cast<int64_t>(n) * a.y_sn + static_cast<int64_t>(ho) * a.y_sh +
-                          static_cast<int64_t>(wo) * a.y_sw;
-            const float* rrow = a.res ? a.res + static_cast<int64_t>(n) * a.r_sn + static_cast<int64_t>(ho) * a.r_sh +
-                                            static_cast<int64_t>(wo) * a.r_sw
-                                      : nullptr;
-#pragma unroll
-            for (int tn = 0; tn < TN; ++tn) {
-                const int col = n0 + wave_n * WN + tn * 32 + l32;
-                if (col < a.Cout) {
-                    float v = apply_act(acc[tm][tn][e] + a.bias[col], a.act, a.slope);
-                    if (rrow) v += rrow[col];
-                    yrow[col] = v;
-                }
-            }
+            for (int g = 1; g < KG; ++g) v += red[g * BM * BN + idx];
+            emit(idx / BN, idx % BN, v);
         }
     }
 }
@@ -336,64 +369,101 @@ __global__ __launch_bounds__(256) void conv_splitk_reduce(ConvArgs a) {
     }
 }
 
-int conv_tile_bm(int tile) {
-    switch (tile) {
-        case kTile128x32: case kTile128x64: case kTile128x128: return 128;
-        case kTile64x64: case kTile64x128: return 64;
-    }
-    return 0;
-}
-int conv_tile_bn(int tile) {
-    switch (tile) {
-        case kTile128x32: return 32;
-        case kTile128x64: case kTile64x64: return 64;
-        case kTile128x128: case kTile64x128: return 128;
-    }
-    return 0;
-}
-
-int64_t packed_weight_elems(int Cout, int K, int bn) {
-    const int64_t cout_pad = (Cout + bn - 1) / bn * bn;
-    const int64_t k_pad = (K + BK - 1) / BK * BK;
-    return cout_pad * k_pad;
-}
-
 namespace {
 
-template <int BM, int BN, int WAVES_M, bool VEC>
+constexpr ConvTileShape kShapes[kNumConvTiles] = {
+    {128, 128, 64, 64, 1}, {128, 64, 64, 32, 1}, {64, 128, 32, 64, 1}, {64, 64, 32, 32, 1},
+    {128, 32, 32, 32, 1},  {64, 32, 32, 32, 2},  {32, 64, 32, 32, 2},  {32, 32, 32, 32, 4},
+};
+constexpr const char* kNames[kNumConvTiles] = {"128x128", "128x64",  "64x128",  "64x64",
+                                               "128x32",  "64x32k2", "32x64k2", "32x32k4"};
+
+template <int BM, int BN, int WM, int WN, int KG, bool VEC>
 void launch_one(const ConvArgs& a, dim3 grid, hipStream_t s) {
-    constexpr size_t bytes = lds_bytes<BM, BN>();
+    constexpr size_t bytes = lds_bytes<BM, BN, KG>();
+    static_assert(bytes >= sizeof(float) * KG * BM * BN, "slice reduction fits in the stage buffers");
     static std::once_flag once;
     std::call_once(once, [] {
         if (bytes > 65536)
-            (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&conv_mfma_kernel<BM, BN, WAVES_M, VEC>),
+            (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&conv_mfma_kernel<BM, BN, WM, WN, KG, VEC>),
                                       hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(bytes));
     });
-    hipLaunchKernelGGL((conv_mfma_kernel<BM, BN, WAVES_M, VEC>), grid, dim3(256), bytes, s, a);
+    hipLaunchKernelGGL((conv_mfma_kernel<BM, BN, WM, WN, KG, VEC>), grid, dim3(256), bytes, s, a);
 }
 
-template <int BM, int BN, int WAVES_M>
+template <int BM, int BN, int WM, int WN, int KG>
 void launch_tile(const ConvArgs& a, bool vec, dim3 grid, hipStream_t s) {
     if (vec)
-        launch_one<BM, BN, WAVES_M, true>(a, grid, s);
+        launch_one<BM, BN, WM, WN, KG, true>(a, grid, s);
     else
-        launch_one<BM, BN, WAVES_M, false>(a, grid, s);
+        launch_one<BM, BN, WM, WN, KG, false>(a, grid, s);
 }
 
 void fail(const std::string& m) { throw std::runtime_error("conv_mfma: " + m); }
 
 }  // namespace
 
+ConvTileShape conv_tile_shape(int tile) {
+    if (tile < 0 || tile >= kNumConvTiles) return {0, 0, 0, 0, 0};
+    return kShapes[tile];
+}
+const char* conv_tile_name(int tile) { return tile >= 0 && tile < kNumConvTiles ? kNames[tile] : "?"; }
+
+int64_t packed_weight_elems(int Cout, int K) {
+    const int64_t cout_pad = (Cout + kConvBN - 1) / kConvBN * kConvBN;
+    const int64_t k_pad = (K + BK - 1) / BK * BK;
+    return cout_pad * k_pad;
+}
+
+// Cost model in CU cycles: one workgroup's MFMA time over its K range scaled
+// by how well its tile shape keeps the matrix cores fed, plus start-up and
+// per-step costs, times the number of workgroup rounds on the 256 CUs, plus a
+// fixed per-kernel cost and, for split-K, the reduce kernel.
+ConvLaunchShape conv_select(int64_t M, int Cout, int K, bool allow_split) {
+    constexpr double kCus = 256.0;
+    constexpr double kKernelCycles = 10000.0;  // launch + completion of one kernel
+    constexpr double kWgCycles = 1500.0;       // workgroup start-up (first loads)
+    constexpr double kStepCycles = 150.0;      // per pipeline step (barrier, LDS latency)
+    constexpr double kEff[kNumConvTiles] = {1.0, 0.92, 0.92, 0.85, 0.8, 0.75, 0.75, 0.7};
+    const int ktiles = (K + BK - 1) / BK;
+    ConvLaunchShape best;
+    double best_cost = 1e300;
+    for (int t = 0; t < kNumConvTiles; ++t) {
+        const ConvTileShape& sh = kShapes[t];
+        const int64_t wgs0 = ((M + sh.bm - 1) / sh.bm) * ((Cout + sh.bn - 1) / sh.bn);
+        const int steps_total = (ktiles + sh.kg - 1) / sh.kg;
+        const int max_splits = allow_split ? std::min(16, std::max(1, steps_total / 4)) : 1;
+        for (int sp = 1; sp <= max_splits; ++sp) {
+            const int steps = (steps_total + sp - 1) / sp;
+            const int splits = (steps_total + steps - 1) / steps;
+            if (splits != sp) continue;
+            const double flops_wg = 2.0 * sh.bm * sh.bn * static_cast<double>(steps) * sh.kg * BK;
+            const double wg_cycles = flops_wg / 256.0 / kEff[t] + kWgCycles + steps * kStepCycles;
+            const double rounds = std::ceil(static_cast<double>(wgs0 * splits) / kCus);
+            double cost = kKernelCycles + rounds * wg_cycles;
+            if (splits > 1) cost += kKernelCycles + static_cast<double>(splits) * M * Cout * 4.0 / 2048.0;
+            if (cost < best_cost * 0.999) {
+                best_cost = cost;
+                best.tile = t;
+                best.splits = splits;
+                best.kt_per_split = steps * sh.kg;
+            }
+        }
+    }
+    return best;
+}
+
 void launch_conv_mfma(const ConvArgs& a, int tile, bool vec, hipStream_t s) {
-    const int bm = conv_tile_bm(tile), bn = conv_tile_bn(tile);
-    if (bm == 0) fail("unknown tile");
+    const ConvTileShape sh = conv_tile_shape(tile);
+    if (sh.bm == 0) fail("unknown tile");
     if (!a.x || !a.y || !a.wpk || !a.bias) fail("null pointer");
     if (a.N <= 0 || a.H <= 0 || a.W <= 0 || a.Cin <= 0 || a.Ho <= 0 || a.Wo <= 0 || a.Cout <= 0) fail("empty shape");
     if (a.K != a.KH * a.KW * a.Cin) fail("K mismatch");
     if (a.ktiles != (a.K + BK - 1) / BK) fail("ktiles mismatch");
     const int64_t M = static_cast<int64_t>(a.N) * a.Ho * a.Wo;
     if (M * std::max(a.Cout, 1) >= (int64_t{1} << 31)) fail("M * Cout too large");
-    if (a.splits < 1 || a.kt_per_split < 1 || static_cast<int64_t>(a.splits) * a.kt_per_split < a.ktiles ||
+    if (a.splits < 1 || a.kt_per_split < 1 || a.kt_per_split % sh.kg != 0 ||
+        static_cast<int64_t>(a.splits) * a.kt_per_split < a.ktiles ||
         static_cast<int64_t>(a.splits - 1) * a.kt_per_split >= a.ktiles)
         fail("bad split");
     if (a.splits > 1 && !a.ws) fail("split-K without workspace");
@@ -405,14 +475,18 @@ void launch_conv_mfma(const ConvArgs& a, int tile, bool vec, hipStream_t s) {
         if ((reinterpret_cast<uintptr_t>(a.x) & 15) || (a.x_sn & 3) || (a.x_sh & 3) || (a.x_sw & 3))
             fail("vector loads need 16-byte aligned rows");
     }
-    const dim3 grid(static_cast<unsigned>((M + bm - 1) / bm), static_cast<unsigned>((a.Cout + bn - 1) / bn),
-                    static_cast<unsigned>(a.splits));
+    const int64_t gx = (M + sh.bm - 1) / sh.bm, gy = (a.Cout + sh.bn - 1) / sh.bn;
+    if (gx * gy * a.splits >= (int64_t{1} << 31) || gy > 65535 || a.splits > 65535) fail("grid too large");
+    const dim3 grid(static_cast<unsigned>(gx), static_cast<unsigned>(gy), static_cast<unsigned>(a.splits));
     switch (tile) {
-        case kTile128x32: launch_tile<128, 32, 4>(a, vec, grid, s); break;
-        case kTile128x64: launch_tile<128, 64, 2>(a, vec, grid, s); break;
-        case kTile128x128: launch_tile<128, 128, 2>(a, vec, grid, s); break;
-        case kTile64x64: launch_tile<64, 64, 2>(a, vec, grid, s); break;
-        case kTile64x128: launch_tile<64, 128, 2>(a, vec, grid, s); break;
+        case kTile128x128: launch_tile<128, 128, 64, 64, 1>(a, vec, grid, s); break;
+        case kTile128x64: launch_tile<128, 64, 64, 32, 1>(a, vec, grid, s); break;
+        case kTile64x128: launch_tile<64, 128, 32, 64, 1>(a, vec, grid, s); break;
+        case kTile64x64: launch_tile<64, 64, 32, 32, 1>(a, vec, grid, s); break;
+        case kTile128x32: launch_tile<128, 32, 32, 32, 1>(a, vec, grid, s); break;
+        case kTile64x32K2: launch_tile<64, 32, 32, 32, 2>(a, vec, grid, s); break;
+        case kTile32x64K2: launch_tile<32, 64, 32, 32, 2>(a, vec, grid, s); break;
+        case kTile32x32K4: launch_tile<32, 32, 32, 32, 4>(a, vec, grid, s); break;
     }
     if (a.splits > 1) {
         const int64_t total = M * a.Cout;
@@ -421,17 +495,17 @@ void launch_conv_mfma(const ConvArgs& a, int tile, bool vec, hipStream_t s) {
     }
 }
 
-__global__ void pack_conv_weights_kernel(float* dst, const float* w, int Cout, int Cin, int KH, int KW,
-                                         int bn, int ktiles, int64_t total) {
+__global__ void pack_conv_weights_kernel(float* dst, const float* w, int Cout, int Cin, int KH, int KW, int ktiles,
+                                         int64_t total) {
     for (int64_t i = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; i < total;
          i += static_cast<int64_t>(gridDim.x) * blockDim.x) {
         const int kk = static_cast<int>(i % BK);
         int64_t t = i / BK;
-        const int nn = static_cast<int>(t % bn);
-        t /= bn;
+        const int nn = static_cast<int>(t % kConvBN);
+        t /= kConvBN;
         const int kt = static_cast<int>(t % ktiles);
         const int nt = static_cast<int>(t / ktiles);
-        const int co = nt * bn + nn;
+        const int co = nt * kConvBN + nn;
         const int kidx = kt * BK + kk;
         const int K = KH * KW * Cin;
         float v = 0.0f;
@@ -446,36 +520,35 @@ __global__ void pack_conv_weights_kernel(float* dst, const float* w, int Cout, i
     }
 }
 
-__global__ void pack_gemm_b_kernel(float* dst, const float* b, int K, int N, int bn, int ktiles, int64_t total) {
+__global__ void pack_gemm_b_kernel(float* dst, const float* b, int K, int N, int ktiles, int64_t total) {
     for (int64_t i = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; i < total;
          i += static_cast<int64_t>(gridDim.x) * blockDim.x) {
         const int kk = static_cast<int>(i % BK);
         int64_t t = i / BK;
-        const int nn = static_cast<int>(t % bn);
-        t /= bn;
+        const int nn = static_cast<int>(t % kConvBN);
+        t /= kConvBN;
         const int kt = static_cast<int>(t % ktiles);
         const int nt = static_cast<int>(t / ktiles);
-        const int col = nt * bn + nn;
+        const int col = nt * kConvBN + nn;
         const int kidx = kt * BK + kk;
         dst[i] = (col < N && kidx < K) ? b[static_cast<int64_t>(kidx) * N + col] : 0.0f;
     }
 }
 
-void launch_pack_conv_weights(float* dst, const float* w, int Cout, int Cin, int KH, int KW, int bn,
-                              hipStream_t s) {
+void launch_pack_conv_weights(float* dst, const float* w, int Cout, int Cin, int KH, int KW, hipStream_t s) {
     const int K = KH * KW * Cin;
     const int ktiles = (K + BK - 1) / BK;
-    const int64_t total = packed_weight_elems(Cout, K, bn);
+    const int64_t total = packed_weight_elems(Cout, K);
     const unsigned blocks = static_cast<unsigned>(std::min<int64_t>((total + 255) / 256, 65535));
-    hipLaunchKernelGGL(pack_conv_weights_kernel, dim3(blocks), dim3(256), 0, s, dst, w, Cout, Cin, KH, KW, bn,
-                       ktiles, total);
+    hipLaunchKernelGGL(pack_conv_weights_kernel, dim3(blocks), dim3(256), 0, s, dst, w, Cout, Cin, KH, KW, ktiles,
+                       total);
 }
 
-void launch_pack_gemm_b(float* dst, const float* b, int K, int N, int bn, hipStream_t s) {
+void launch_pack_gemm_b(float* dst, const float* b, int K, int N, hipStream_t s) {
     const int ktiles = (K + BK - 1) / BK;
-    const int64_t total = packed_weight_elems(N, K, bn);
+    const int64_t total = packed_weight_elems(N, K);
     const unsigned blocks = static_cast<unsigned>(std::min<int64_t>((total + 255) / 256, 65535));
-    hipLaunchKernelGGL(pack_gemm_b_kernel, dim3(blocks), dim3(256), 0, s, dst, b, K, N, bn, ktiles, total);
+    hipLaunchKernelGGL(pack_gemm_b_kernel, dim3(blocks), dim3(256), 0, s, dst, b, K, N, ktiles, total);
 }
 
 }  // namespace k

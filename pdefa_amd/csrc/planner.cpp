@@ -10,8 +10,6 @@
 
 namespace pdefa {
 
-int conv_pack_bn(int cout) { return cout <= 32 ? 32 : (cout <= 64 ? 64 : 128); }
-
 namespace {
 
 using Dims = std::vector<int64_t>;
@@ -831,28 +829,21 @@ class Planner {
         if (cl && !small) {
             s.kind = StepKind::ConvMfma;
             s.vec = cin % 4 == 0 && x.off % 4 == 0 && x.str[0] % 4 == 0 && x.str[2] % 4 == 0 && x.str[3] % 4 == 0;
-            const int bn = conv_pack_bn(static_cast<int>(cout));
             const int64_t M = y.dims[0] * y.dims[2] * y.dims[3];
-            const int64_t nt = (cout + bn - 1) / bn;
-            if (bn == 32) {
-                s.tile = k::kTile128x32;
-            } else {
-                const bool big = ((M + 127) / 128) * nt >= 256;
-                s.tile = bn == 64 ? (big ? k::kTile128x64 : k::kTile64x64) : (big ? k::kTile128x128 : k::kTile64x128);
-            }
-            const int bm = k::conv_tile_bm(s.tile);
             const int64_t K = cin * s.KH * s.KW;
-            const int ktiles = static_cast<int>((K + k::kConvBK - 1) / k::kConvBK);
-            const int64_t wgs = ((M + bm - 1) / bm) * nt;
-            // Split K when the grid cannot fill the 256 CUs, keeping >= 3 K-tiles
-            // per split and aiming at ~384 workgroups.
-            int splits = 1;
-            if (opt_.split_k && wgs < 256 && ktiles >= 6) {
-                splits = static_cast<int>(std::min<int64_t>({32, ktiles / 3, (384 + wgs - 1) / wgs}));
-                splits = std::max(splits, 1);
+            k::ConvLaunchShape ls = k::conv_select(M, static_cast<int>(cout), static_cast<int>(K), opt_.split_k);
+            if (opt_.force_tile >= 0 && opt_.force_tile < k::kNumConvTiles) {
+                const int kg = k::conv_tile_shape(opt_.force_tile).kg;
+                const int steps_total = static_cast<int>((K + k::kConvBK - 1) / k::kConvBK + kg - 1) / kg;
+                const int want = std::max(1, std::min(opt_.force_splits, steps_total));
+                const int steps = (steps_total + want - 1) / want;
+                ls.tile = opt_.force_tile;
+                ls.splits = (steps_total + steps - 1) / steps;
+                ls.kt_per_split = steps * kg;
             }
-            s.kt_per_split = (ktiles + splits - 1) / splits;
-            s.splits = (ktiles + s.kt_per_split - 1) / s.kt_per_split;
+            s.tile = ls.tile;
+            s.splits = ls.splits;
+            s.kt_per_split = ls.kt_per_split;
             if (s.splits > 1) s.ws_buf = new_buf(static_cast<int64_t>(s.splits) * M * cout);
         } else {
             s.kind = StepKind::ConvDirect;
@@ -1067,7 +1058,7 @@ std::string describe_plan(const Model& m, const Plan& p) {
         os << i << " " << step_kind_name(s.kind);
         if (s.kind == StepKind::Elt) os << "(" << s.elt << ")";
         if (s.kind == StepKind::ConvMfma)
-            os << "(tile=" << s.tile << ",vec=" << s.vec << ",splits=" << s.splits << ",act=" << s.act << ")";
+            os << "(tile=" << k::conv_tile_name(s.tile) << ",vec=" << s.vec << ",splits=" << s.splits << ",act=" << s.act << ")";
         if (s.kind == StepKind::ConvDirect) os << "(act=" << s.act << ")";
         os << " node=" << s.node;
         if (s.node >= 0) os << " '" << m.nodes[s.node].name << "'";

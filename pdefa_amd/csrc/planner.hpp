@@ -72,11 +72,10 @@ struct Plan {
     int32_t n_copies = 0;                     // materialising copies the planner could not avoid
 };
 
-// Tile width the packed weights of a conv with `cout` outputs use.
-int conv_pack_bn(int cout);
-
 struct PlanOptions {
     bool split_k = true;
+    int force_tile = -1;   // >= 0: use this implicit-GEMM tile for every MFMA conv (tuning, tests)
+    int force_splits = 0;  // > 0 with force_tile: split-K across workgroups into this many splits
     bool winograd_form_silu = true;  // match the reference's Winograd-layer SiLU
 };
 

@@ -54,7 +54,7 @@ std::shared_ptr<DeviceModel> upload_model(const Model& m) {
     }
     struct PackPlan {
         size_t node, wpk_off, bias_off, dpk_off;
-        int cout, cin, kh, kw, bn, w, b;
+        int cout, cin, kh, kw, w, b;
     };
     std::vector<PackPlan> pp;
     for (size_t i = 0; i < m.nodes.size(); ++i) {
@@ -69,14 +69,13 @@ std::shared_ptr<DeviceModel> upload_model(const Model& m) {
         p.cin = static_cast<int>(wt.dims[1]);
         p.kh = static_cast<int>(wt.dims[2]);
         p.kw = static_cast<int>(wt.dims[3]);
-        p.bn = conv_pack_bn(p.cout);
         p.w = w;
         p.b = (n.inputs.size() > 2 && n.inputs[2] <= -1000) ? -1000 - n.inputs[2] : -1;
         if (p.b >= 0 && m.weights[p.b].numel() < p.cout) p.b = -1;
         p.wpk_off = total;
-        total += align_up(static_cast<size_t>(k::packed_weight_elems(p.cout, p.kh * p.kw * p.cin, p.bn)));
+        total += align_up(static_cast<size_t>(k::packed_weight_elems(p.cout, p.kh * p.kw * p.cin)));
         p.bias_off = total;
-        total += align_up(static_cast<size_t>((p.cout + p.bn - 1) / p.bn * p.bn));
+        total += align_up(static_cast<size_t>(p.cout));
         p.dpk_off = total;
         total += align_up(static_cast<size_t>(k::direct_packed_elems(p.cout, p.kh * p.kw * p.cin)));
         pp.push_back(p);
@@ -110,9 +109,8 @@ std::shared_ptr<DeviceModel> upload_model(const Model& m) {
             DeviceModel::Pack& pk = dm->packs[p.node];
             pk.wpk = dm->blob + p.wpk_off;
             pk.bias = dm->blob + p.bias_off;
-            pk.bn = p.bn;
             pk.dpk = dm->blob + p.dpk_off;
-            k::launch_pack_conv_weights(pk.wpk, dm->wptr[p.w], p.cout, p.cin, p.kh, p.kw, p.bn, s);
+            k::launch_pack_conv_weights(pk.wpk, dm->wptr[p.w], p.cout, p.cin, p.kh, p.kw, s);
             PDEFA_HIP(hipGetLastError());
         }
         PDEFA_HIP(hipStreamSynchronize(s));
@@ -136,6 +134,12 @@ Session::Session(Model& m) : model_(&m) {
     inputs_.assign(static_cast<size_t>(m.num_inputs()), nullptr);
     use_graph_ = env_flag("PDEFA_HIP_GRAPH", true);
     opts_.split_k = env_flag("PDEFA_SPLITK", true);
+    if (const char* t = std::getenv("PDEFA_CONV_TILE")) {
+        for (int i = 0; i < k::kNumConvTiles; ++i)
+            if (std::strcmp(t, k::conv_tile_name(i)) == 0) opts_.force_tile = i;
+        if (opts_.force_tile < 0) throw std::runtime_error(std::string("PDEFA_CONV_TILE: unknown tile ") + t);
+    }
+    if (const char* sp = std::getenv("PDEFA_CONV_SPLITS")) opts_.force_splits = std::atoi(sp);
     const char* silu = std::getenv("PDEFA_SILU");
     opts_.winograd_form_silu = !(silu && std::strcmp(silu, "exact") == 0);
 }
@@ -244,7 +248,6 @@ void Session::prepare(const std::vector<std::vector<int64_t>>& dims) {
                 const Node& n = model_->nodes.at(s.node);
                 const DeviceModel::Pack& pk = dev_->packs.at(s.node);
                 if (!pk.wpk) throw std::runtime_error("conv weights were not packed: " + n.name);
-                if (pk.bn != k::conv_tile_bn(s.tile)) throw std::runtime_error("pack width does not match tile");
                 const k::View x = V(s.a, "conv x", si), y = V(s.out, "conv y", si);
                 if (x.str[1] != 1 || y.str[1] != 1) throw std::runtime_error("conv_mfma needs channels-last views");
                 k::ConvArgs& c = l.conv;
@@ -558,22 +561,14 @@ void device_matmul(const float* A, const float* B, float* C, int64_t M, int64_t 
     MatmulScratch& sc = matmul_scratch();
     std::lock_guard<std::mutex> g(sc.mu);
     if (!sc.stream) PDEFA_HIP(hipStreamCreateWithFlags(&sc.stream, hipStreamNonBlocking));
-    const int bn = conv_pack_bn(static_cast<int>(N));
     const size_t nA = align_up(static_cast<size_t>(M * K));
     const size_t nB = align_up(static_cast<size_t>(K * N));
-    const size_t nP = align_up(static_cast<size_t>(k::packed_weight_elems(static_cast<int>(N), static_cast<int>(K), bn)));
-    const size_t nBias = align_up(static_cast<size_t>((N + bn - 1) / bn * bn));
+    const size_t nP = align_up(static_cast<size_t>(k::packed_weight_elems(static_cast<int>(N), static_cast<int>(K))));
+    const size_t nBias = align_up(static_cast<size_t>(N));
     const size_t nC = align_up(static_cast<size_t>(M * N));
-    // split-K for small grids
-    const int tile = bn == 32 ? k::kTile128x32 : (bn == 64 ? k::kTile64x64 : k::kTile64x128);
-    const int bm = k::conv_tile_bm(tile);
     const int ktiles = static_cast<int>((K + k::kConvBK - 1) / k::kConvBK);
-    const int64_t wgs = ((M + bm - 1) / bm) * ((N + bn - 1) / bn);
-    int splits = 1;
-    if (wgs < 128 && ktiles >= 32) splits = static_cast<int>(std::min<int64_t>({16, ktiles / 16, (256 + wgs - 1) / wgs}));
-    splits = std::max(splits, 1);
-    const int kps = (ktiles + splits - 1) / splits;
-    splits = (ktiles + kps - 1) / kps;
+    const k::ConvLaunchShape ls = k::conv_select(M, static_cast<int>(N), static_cast<int>(K), true);
+    const int tile = ls.tile, splits = ls.splits, kps = ls.kt_per_split;
     const size_t nW = splits > 1 ? align_up(static_cast<size_t>(splits) * M * N) : 0;
     const size_t need = nA + nB + nP + nBias + nC + nW;
     if (need > sc.cap) {
@@ -592,7 +587,7 @@ void device_matmul(const float* A, const float* B, float* C, int64_t M, int64_t 
     PDEFA_HIP(hipMemcpyAsync(dA, A, sizeof(float) * M * K, hipMemcpyHostToDevice, sc.stream));
     PDEFA_HIP(hipMemcpyAsync(dB, B, sizeof(float) * K * N, hipMemcpyHostToDevice, sc.stream));
     PDEFA_HIP(hipMemsetAsync(dBias, 0, nBias * sizeof(float), sc.stream));
-    k::launch_pack_gemm_b(dP, dB, static_cast<int>(K), static_cast<int>(N), bn, sc.stream);
+    k::launch_pack_gemm_b(dP, dB, static_cast<int>(K), static_cast<int>(N), sc.stream);
     k::ConvArgs c;
     c.x = dA;
     c.N = 1;

@@ -38,9 +38,8 @@ struct DeviceModel {
     std::vector<float*> wptr;  // raw weight i
     struct Pack {
         float* wpk = nullptr;
-        float* bias = nullptr;  // padded to the pack width, zeros when the conv has no bias
+        float* bias = nullptr;  // Cout floats, zeros when the conv has no bias
         float* dpk = nullptr;   // direct-conv layout (k::direct_packed_elems)
-        int bn = 0;
     };
     std::vector<Pack> packs;  // by node index (empty for non-conv nodes)
     ~DeviceModel();

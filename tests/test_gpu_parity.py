@@ -78,6 +78,37 @@ def test_single_conv(tmp_path, cin, cout, k, s, hw):
     assert err < 1e-4, err
 
 
+TILES = ["128x128", "128x64", "64x128", "64x64", "128x32", "64x32k2", "32x64k2", "32x32k4"]
+
+
+@pytest.mark.parametrize("tile", TILES)
+@pytest.mark.parametrize("splits", [1, 3])
+@pytest.mark.parametrize("cin,cout,k,s,hw", [(64, 64, 3, 1, 24), (48, 80, 3, 2, 31), (96, 40, 1, 1, 20)])
+def test_conv_every_tile(tmp_path, monkeypatch, tile, splits, cin, cout, k, s, hw):
+    """Each implicit-GEMM tile shape (and split-K across workgroups), forced,
+    against the oracle; exact SiLU so no compat-form branch points."""
+    print(f"[case] tile={tile} splits={splits} conv cin={cin} cout={cout} k={k} s={s} hw={hw}", flush=True)
+    monkeypatch.setenv("PDEFA_CONV_TILE", tile)
+    monkeypatch.setenv("PDEFA_CONV_SPLITS", str(splits))
+    monkeypatch.setenv("PDEFA_SILU", "exact")
+    model, x = ys.build_single_conv(cin, cout, k, s, hw, seed=11)
+    path = str(tmp_path / "conv.engine")
+    ys.save(model, path)
+    eng = native.Engine(path)
+    try:
+        got = eng.run(x)[0]
+        plan = eng.plan()
+    finally:
+        eng.close()
+    assert f"tile={tile}," in plan
+    kg = 4 if tile.endswith("k4") else (2 if tile.endswith("k2") else 1)
+    steps = -(-(-(-cin * k * k // 32)) // kg)
+    if splits > 1 and steps > 1:
+        assert "splits=1," not in plan
+    want = graph_ref.run_graph(model, [x], compat_silu=False)[0]
+    assert assert_close(got, want, "conv") < 1e-4
+
+
 def test_single_conv_no_act(tmp_path):
     model, x = ys.build_single_conv(64, 48, 3, 1, 30, seed=3, silu=False)
     path = str(tmp_path / "conv.engine")
