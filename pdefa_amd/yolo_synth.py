@@ -259,6 +259,24 @@ def build_single_conv(cin: int, cout: int, k: int, stride: int, hw: int, seed: i
     return b.model([1, cin, hw, hw], [1, cout, ho, ho], [y]), x
 
 
+def build_tiny(seed: int = 3) -> EngineModel:
+    """A small stand-in for the reference tests' tiny.engine (a 64x64
+    Conv -> AvgPool -> Linear to 4 outputs, pdefa/tests/README.md:13-39, not
+    shipped): one Conv(3 -> 4, 64x64 kernel, no padding) + bias over the
+    whole [1,3,64,64] image, i.e. a linear map to 4 values, then Reshape to
+    [1,4].  Same input/output shapes, built from ops on this path."""
+    rng = np.random.default_rng(seed)
+    w = kaiming_uniform(rng, (4, 3, 64, 64))
+    bias = rng.uniform(-0.1, 0.1, size=4).astype(np.float32)
+    b = GraphBuilder()
+    wi, bi = b.const("fc.weight", w), b.const("fc.bias", bias)
+    y = b.node("Conv", "/fc/Conv", [-1, wi, bi], stride_h=1, stride_w=1, pad_h=0, pad_w=0, dil_h=1, dil_w=1,
+               groups=1)
+    shp = b.const("/fc/Reshape/shape::const", [1, 4])
+    y = b.node("Reshape", "/fc/Reshape", [y, shp])
+    return b.model([1, 3, 64, 64], [1, 4], [y])
+
+
 # Source image sizes for the batch-8 workload: aspect cycle 16:9, 4:3, 1:1.
 ASPECT_SIZES = [(1280, 720), (1024, 768), (800, 800)]
 
