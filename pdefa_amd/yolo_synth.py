@@ -141,14 +141,22 @@ class _Yolo:
         return self.b.node("Resize", f"/{name}/Resize", [x, sc])
 
 
+# Class-head bias per scale: the spread of the random-weight class logits
+# grows with model width, so wider models need a lower bias for a few to a
+# hundred candidates above 0.25 on the synthetic images.
+CLS_BIAS = {"n": -6.0, "s": -6.0, "m": -7.75, "l": -7.75, "x": -7.75}
+
+
 def build_yolov8(scale: str = "n", seed: int = 0, nc: int = 80, imgsz: int = 640,
-                 cls_bias: float = -6.0, cls_gain: float = 30.0) -> EngineModel:
+                 cls_bias: Optional[float] = None, cls_gain: float = 30.0) -> EngineModel:
     """YOLOv8{scale} detection graph with seeded random weights (BN folded).
 
     The class head's last conv has its Kaiming weights scaled by cls_gain and
-    a constant bias cls_bias, so that a random-weight model still yields on
-    the order of a hundred candidates above 0.25 on a synthetic image (the
+    a constant bias cls_bias (default CLS_BIAS[scale]), so that a random-weight
+    model still yields candidates above 0.25 on a synthetic image (the
     unscaled head scores every anchor near sigmoid(cls_bias))."""
+    if cls_bias is None:
+        cls_bias = CLS_BIAS[scale]
     depth, width, max_ch = SCALES[scale]
     ch = lambda c: make_divisible(min(c, max_ch) * width, 8)
     rep = lambda n: max(round(n * depth), 1)

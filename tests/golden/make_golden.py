@@ -85,6 +85,8 @@ def main():
         out["yolov8n_640_img0"] = yolo_case(tmp, "n", 0, 0)
         out["yolov8n_640_img1"] = yolo_case(tmp, "n", 0, 1)
         out["yolov8n_640_img2"] = yolo_case(tmp, "n", 0, 2)
+        out["yolov8m_640_img0"] = yolo_case(tmp, "m", 1, 0)
+        out["yolov8m_640_img1"] = yolo_case(tmp, "m", 1, 1)
         rng = np.random.default_rng(42)
         a = rng.standard_normal((512, 512), dtype=np.float32)
         b = rng.standard_normal((512, 512), dtype=np.float32)

@@ -239,3 +239,31 @@ def test_yolov8n_batch_vs_reference_golden(yolov8n):
         for a, b in zip(dets, gd):
             for k in ("x1", "y1", "x2", "y2", "conf"):
                 assert abs(a[k] - b[k]) <= ATOL + RTOL * abs(b[k]), (i, k, a, b)
+
+
+def test_yolov8m_b16_vs_reference_golden(tmp_path):
+    """YOLOv8m (weight seed 1) at batch 16 in one batched program: images 0
+    and 1 against the reference's outputs and detections, three more
+    against single-image runs of the same session type."""
+    print("[case] yolov8m b16", flush=True)
+    path = str(tmp_path / "yolov8m.engine")
+    ys.save(ys.build_yolov8("m", seed=1), path)
+    x, metas = ys.yolo_inputs(16)
+    eng = native.Engine(path)
+    try:
+        out = eng.run(x)[0]
+        assert out.shape == (16, 84, 8400)
+        for i in range(2):
+            g = _golden(f"yolov8m_640_img{i}")
+            _check_golden_samples(out[i:i + 1], g)
+            dets = decode_yolo(out[i:i + 1], metas[i], with_anchor=True)
+            gd = g["detections"]
+            assert [(d["anchor"], d["cls"]) for d in dets] == [(d["anchor"], d["cls"]) for d in gd]
+            for a, b in zip(dets, gd):
+                for k in ("x1", "y1", "x2", "y2", "conf"):
+                    assert abs(a[k] - b[k]) <= ATOL + RTOL * abs(b[k]), (i, k, a, b)
+    finally:
+        eng.close()
+    for i in (2, 9, 15):
+        single = run_engine(path, x[i:i + 1])[0]
+        assert_close(out[i:i + 1], single, f"yolov8m b16 image {i} vs b1")
