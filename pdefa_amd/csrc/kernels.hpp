@@ -106,13 +106,14 @@ void launch_conv_mfma(const ConvArgs& a, int tile, bool vec, hipStream_t s);
 // Direct convolution over arbitrary strided NCHW-logical views (any layout),
 // for layers the implicit GEMM does not take: tiny Cin (the 3-channel stem,
 // read straight from the NCHW input) or tiny Cout.  One lane computes one
-// output pixel for kDirectCB output channels.
-constexpr int kDirectCB = 16;
+// output pixel for a block of direct_cb(Cout) output channels; the workgroup
+// writes its tile through LDS so that stores are coalesced along channels.
+inline int direct_cb(int Cout) { return Cout <= 16 ? 16 : (Cout <= 32 ? 32 : (Cout <= 48 ? 48 : 64)); }
 struct ConvDirectArgs {
     View x;    // logical [N, Cin, H, W]
     View y;    // logical [N, Cout, Ho, Wo]
     View res;  // optional, same logical shape as y (ptr == nullptr if absent)
-    const float* wpk = nullptr;  // [ceil(Cout/kDirectCB)][Cin*KH*KW][kDirectCB], k = (ci, kh, kw)
+    const float* wpk = nullptr;  // [ceil(Cout/CB)][Cin*KH*KW][CB], CB = direct_cb(Cout), k = (ci, kh, kw)
     const float* bias = nullptr;
     int32_t KH = 1, KW = 1, sh = 1, sw = 1, ph = 0, pw = 0, dh = 1, dw = 1;
     int32_t act = 0;
@@ -157,7 +158,8 @@ void launch_pack_gemm_b(float* dst, const float* b, int K, int N, hipStream_t s)
 int64_t packed_weight_elems(int Cout, int K);
 // Elements of direct-conv packed weights.
 inline int64_t direct_packed_elems(int Cout, int K) {
-    return static_cast<int64_t>((Cout + kDirectCB - 1) / kDirectCB) * K * kDirectCB;
+    const int cb = direct_cb(Cout);
+    return static_cast<int64_t>((Cout + cb - 1) / cb) * K * cb;
 }
 
 }  // namespace k

@@ -51,9 +51,15 @@ constexpr int BK = kConvBK;         // 32: K per slice and per packed block
 constexpr int LDS_STRIDE = BK + 4;  // floats; 16-byte aligned rows, conflict-free float4 reads
 constexpr int kXcds = 8;
 
+// Stage buffers (two stages of KG A and B slices), then the per-row output
+// offset table of the epilogue (two int64 per tile row).
+template <int BM, int BN, int KG>
+constexpr size_t lds_stage_bytes() {
+    return sizeof(float) * 2 * KG * (BM + BN) * LDS_STRIDE;
+}
 template <int BM, int BN, int KG>
 constexpr size_t lds_bytes() {
-    return sizeof(float) * 2 * KG * (BM + BN) * LDS_STRIDE;
+    return lds_stage_bytes<BM, BN, KG>() + 2 * sizeof(int64_t) * BM;
 }
 
 }  // namespace
@@ -105,6 +111,33 @@ __global__ __launch_bounds__(256) void conv_mfma_kernel(ConvArgs a) {
     const int kb_end = min(a.ktiles, kb_begin + a.kt_per_split);
     const int nk = (kb_end - kb_begin + KG - 1) / KG;  // pipeline steps
     const int taps = a.KH * a.KW;
+
+    // Epilogue row table: element offset of each tile row in the output (or in
+    // this split's partial slab) and in the residual; -1 past the last row.
+    // Built once here, read after the pipeline's barriers.
+    int64_t* s_yoff = reinterpret_cast<int64_t*>(reinterpret_cast<char*>(smem) + lds_stage_bytes<BM, BN, KG>());
+    int64_t* s_roff = s_yoff + BM;
+    if (tid < BM) {
+        const int m = m0 + tid;
+        int64_t yo = -1, ro = 0;
+        if (m < M) {
+            if (a.splits > 1) {
+                yo = (static_cast<int64_t>(bz) * M + m) * a.Cout;
+            } else {
+                const int n = m / HoWo;
+                const int rem = m - n * HoWo;
+                const int ho = rem / a.Wo;
+                const int wo = rem - ho * a.Wo;
+                yo = static_cast<int64_t>(n) * a.y_sn + static_cast<int64_t>(ho) * a.y_sh +
+                     static_cast<int64_t>(wo) * a.y_sw;
+                if (a.res)
+                    ro = static_cast<int64_t>(n) * a.r_sn + static_cast<int64_t>(ho) * a.r_sh +
+                         static_cast<int64_t>(wo) * a.r_sw;
+            }
+        }
+        s_yoff[tid] = yo;
+        s_roff[tid] = ro;
+    }
 
     // ---- loaders: this lane loads float4 chunk `chunk` (slice chunk / 8) of
     // rows r0 + ROW_STEP*i of the A tile and of the B tile.
@@ -272,80 +305,159 @@ __global__ __launch_bounds__(256) void conv_mfma_kernel(ConvArgs a) {
     };
 
     // ---- software pipeline: step t is loaded at iteration t-2, stored to LDS
-    // at iteration t-1 and multiplied at iteration t.
-    if (nk > 0) {
-        load_step(kb_begin, areg[0], breg[0], amask[0]);
-        load_step(kb_begin + KG, areg[1], breg[1], amask[1]);
-        store_step(0, areg[0], breg[0], amask[0]);
-        __syncthreads();
-    }
-    auto iteration = [&](int it, auto stage) {
+    // at iteration t-1 and multiplied at iteration t.  Iterations that load
+    // run in the (2x unrolled) main loop; the last two iterations load
+    // nothing, so no load is left in flight into the epilogue.
+    load_step(kb_begin, areg[0], breg[0], amask[0]);
+    if (nk > 1) load_step(kb_begin + KG, areg[1], breg[1], amask[1]);
+    store_step(0, areg[0], breg[0], amask[0]);
+    __syncthreads();
+    auto iteration = [&](int it, auto stage, auto load) {
         constexpr int S = decltype(stage)::value;  // it % 2
-        load_step(kb_begin + (it + 2) * KG, areg[S], breg[S], amask[S]);
+        if (decltype(load)::value) load_step(kb_begin + (it + 2) * KG, areg[S], breg[S], amask[S]);
         compute_step(S);
         if (it + 1 < nk) store_step(S ^ 1, areg[S ^ 1], breg[S ^ 1], amask[S ^ 1]);
         __syncthreads();
     };
+    using S0 = std::integral_constant<int, 0>;
+    using S1 = std::integral_constant<int, 1>;
+    using LD = std::true_type;
+    using NL = std::false_type;
     int it = 0;
-    for (; it + 1 < nk; it += 2) {
-        iteration(it, std::integral_constant<int, 0>{});
-        iteration(it + 1, std::integral_constant<int, 1>{});
+    for (; it + 3 < nk; it += 2) {
+        iteration(it, S0{}, LD{});
+        iteration(it + 1, S1{}, LD{});
     }
-    if (it < nk) iteration(it, std::integral_constant<int, 0>{});
-
-    // ---- output: tile element (row, col) -> split-K partial or epilogue
-    auto emit = [&](int row, int col, float v) {
-        const int m = m0 + row;
-        const int co = n0 + col;
-        if (m >= M || co >= a.Cout) return;
-        if (a.splits > 1) {
-            a.ws[(static_cast<int64_t>(bz) * M + m) * a.Cout + co] = v;
-            return;
-        }
-        const int n = m / HoWo;
-        const int rem = m - n * HoWo;
-        const int ho = rem / a.Wo;
-        const int wo = rem - ho * a.Wo;
-        float r = apply_act(v + a.bias[co], a.act, a.slope);
-        if (a.res)
-            r += a.res[static_cast<int64_t>(n) * a.r_sn + static_cast<int64_t>(ho) * a.r_sh +
-                       static_cast<int64_t>(wo) * a.r_sw + co];
-        a.y[static_cast<int64_t>(n) * a.y_sn + static_cast<int64_t>(ho) * a.y_sh + static_cast<int64_t>(wo) * a.y_sw +
-            co] = r;
-    };
-
-    // 32x32 block register e of lane l holds row 8*(e/4) + 4*(l/32) + e%4, column l%32.
-    if (KG == 1) {
-#pragma unroll
-        for (int tm = 0; tm < TM; ++tm)
-#pragma unroll
-            for (int e = 0; e < 16; ++e)
-#pragma unroll
-                for (int tn = 0; tn < TN; ++tn)
-                    emit(wave_m * WM + tm * 32 + (e >> 2) * 8 + half * 4 + (e & 3), wave_n * WN + tn * 32 + l32,
-                         acc[tm][tn][e]);
+    if (it + 2 < nk) iteration(it++, S0{}, LD{});
+    if ((it & 1) == 0) {
+        if (it < nk) iteration(it, S0{}, NL{});
+        if (it + 1 < nk) iteration(it + 1, S1{}, NL{});
     } else {
-        // Slice partials -> LDS (the pipeline's last barrier has retired every
-        // LDS read of the stages), then every lane sums whole tile elements in
-        // slice order.
-        float* red = smem;  // [KG][BM][BN]
+        if (it < nk) iteration(it, S1{}, NL{});
+        if (it + 1 < nk) iteration(it + 1, S0{}, NL{});
+    }
+
+    // ---- output.  The row table was written before the prologue barrier
+    // (every split has at least one step, checked by the launcher).  A tile
+    // element's raw sum becomes a split-K partial (splits > 1) or bias +
+    // activation + residual.  The activation, residual and partial choices are
+    // hoisted into template arguments so each lane's elements are straight-line
+    // code: all row offsets (LDS) first, then all residual loads, then all
+    // stores, every load or store of the tile in flight together.
+    auto epilogue = [&](auto act_c, auto res_c, auto part_c) {
+        constexpr int ACT = decltype(act_c)::value;
+        constexpr bool RES = decltype(res_c)::value;
+        constexpr bool PART = decltype(part_c)::value;
+        float* dst = PART ? a.ws : a.y;
+        if constexpr (KG == 1) {
+            // 32x32 block register e of lane l holds row 8*(e/4) + 4*(l/32) + e%4, column l%32.
+            int co[TN];
+            bool cok[TN];
+            float bias_v[TN];
 #pragma unroll
-        for (int tm = 0; tm < TM; ++tm)
+            for (int tn = 0; tn < TN; ++tn) {
+                co[tn] = n0 + wave_n * WN + tn * 32 + l32;
+                cok[tn] = co[tn] < a.Cout;
+                bias_v[tn] = (!PART && cok[tn]) ? a.bias[co[tn]] : 0.0f;
+            }
 #pragma unroll
-            for (int e = 0; e < 16; ++e)
+            for (int tm = 0; tm < TM; ++tm) {
+                int64_t yo[16], ro[16];
 #pragma unroll
-                for (int tn = 0; tn < TN; ++tn) {
+                for (int e = 0; e < 16; ++e) {
                     const int row = wave_m * WM + tm * 32 + (e >> 2) * 8 + half * 4 + (e & 3);
-                    const int col = wave_n * WN + tn * 32 + l32;
-                    red[(wg * BM + row) * BN + col] = acc[tm][tn][e];
+                    yo[e] = s_yoff[row];
+                    if (RES) ro[e] = s_roff[row];
                 }
-        __syncthreads();
-        for (int idx = tid; idx < BM * BN; idx += 256) {
-            float v = red[idx];
+                float rv[16][TN];
+                if constexpr (RES) {
 #pragma unroll
-            for (int g = 1; g < KG; ++g) v += red[g * BM * BN + idx];
-            emit(idx / BN, idx % BN, v);
+                    for (int e = 0; e < 16; ++e)
+#pragma unroll
+                        for (int tn = 0; tn < TN; ++tn) {
+                            const bool ok = yo[e] >= 0 && cok[tn];
+                            const float r = a.res[ok ? ro[e] + co[tn] : 0];
+                            rv[e][tn] = ok ? r : 0.0f;
+                        }
+                }
+#pragma unroll
+                for (int e = 0; e < 16; ++e)
+#pragma unroll
+                    for (int tn = 0; tn < TN; ++tn) {
+                        float v = acc[tm][tn][e];
+                        if (!PART) v = act_fixed<ACT>(v + bias_v[tn], a.act, a.slope);
+                        if (RES) v += rv[e][tn];
+                        if (yo[e] >= 0 && cok[tn]) dst[yo[e] + co[tn]] = v;
+                    }
+            }
+        } else {
+            // Slice partials -> LDS (the pipeline's last barrier has retired
+            // every LDS read of the stages), then each lane sums its elements
+            // (fixed column, rows tid/BN + i*256/BN) in slice order.
+            float* red = smem;  // [KG][BM][BN]
+#pragma unroll
+            for (int tm = 0; tm < TM; ++tm)
+#pragma unroll
+                for (int e = 0; e < 16; ++e)
+#pragma unroll
+                    for (int tn = 0; tn < TN; ++tn) {
+                        const int row = wave_m * WM + tm * 32 + (e >> 2) * 8 + half * 4 + (e & 3);
+                        const int col = wave_n * WN + tn * 32 + l32;
+                        red[(wg * BM + row) * BN + col] = acc[tm][tn][e];
+                    }
+            __syncthreads();
+            constexpr int E = BM * BN / 256;
+            constexpr int RSTEP = 256 / BN;
+            const int col = tid % BN;
+            const int co = n0 + col;
+            const bool cok = co < a.Cout;
+            const float bias_v = (!PART && cok) ? a.bias[co] : 0.0f;
+            float v[E];
+            int64_t yo[E], ro[E];
+#pragma unroll
+            for (int i = 0; i < E; ++i) {
+                const int row = tid / BN + i * RSTEP;
+                float sum = red[row * BN + col];
+#pragma unroll
+                for (int g = 1; g < KG; ++g) sum += red[(g * BM + row) * BN + col];
+                v[i] = sum;
+                yo[i] = s_yoff[row];
+                if (RES) ro[i] = s_roff[row];
+            }
+            float rv[E];
+            if constexpr (RES) {
+#pragma unroll
+                for (int i = 0; i < E; ++i) {
+                    const bool ok = yo[i] >= 0 && cok;
+                    const float r = a.res[ok ? ro[i] + co : 0];
+                    rv[i] = ok ? r : 0.0f;
+                }
+            }
+#pragma unroll
+            for (int i = 0; i < E; ++i) {
+                float r = v[i];
+                if (!PART) r = act_fixed<ACT>(r + bias_v, a.act, a.slope);
+                if (RES) r += rv[i];
+                if (yo[i] >= 0 && cok) dst[yo[i] + co] = r;
+            }
         }
+    };
+    using YES = std::true_type;
+    using NO = std::false_type;
+    if (a.splits > 1) {
+        epilogue(std::integral_constant<int, kActNone>{}, NO{}, YES{});
+    } else if (a.act == kActSilu) {
+        if (a.res) epilogue(std::integral_constant<int, kActSilu>{}, YES{}, NO{});
+        else epilogue(std::integral_constant<int, kActSilu>{}, NO{}, NO{});
+    } else if (a.act == kActSiluWinogradForm) {
+        if (a.res) epilogue(std::integral_constant<int, kActSiluWinogradForm>{}, YES{}, NO{});
+        else epilogue(std::integral_constant<int, kActSiluWinogradForm>{}, NO{}, NO{});
+    } else if (a.act == kActNone) {
+        if (a.res) epilogue(std::integral_constant<int, kActNone>{}, YES{}, NO{});
+        else epilogue(std::integral_constant<int, kActNone>{}, NO{}, NO{});
+    } else {
+        if (a.res) epilogue(std::integral_constant<int, kActGeneric>{}, YES{}, NO{});
+        else epilogue(std::integral_constant<int, kActGeneric>{}, NO{}, NO{});
     }
 }
 
@@ -381,7 +493,8 @@ constexpr const char* kNames[kNumConvTiles] = {"128x128", "128x64",  "64x128",  
 template <int BM, int BN, int WM, int WN, int KG, bool VEC>
 void launch_one(const ConvArgs& a, dim3 grid, hipStream_t s) {
     constexpr size_t bytes = lds_bytes<BM, BN, KG>();
-    static_assert(bytes >= sizeof(float) * KG * BM * BN, "slice reduction fits in the stage buffers");
+    static_assert(lds_stage_bytes<BM, BN, KG>() >= sizeof(float) * KG * BM * BN,
+                  "slice reduction fits in the stage buffers");
     static std::once_flag once;
     std::call_once(once, [] {
         if (bytes > 65536)

@@ -298,57 +298,69 @@ void launch_softmax(const View& out, const View& in, int axis, hipStream_t s) {
                            axis, rows);
 }
 
-// Direct convolution, one output pixel x kDirectCB output channels per lane.
-// Weights are pre-packed [ceil(Cout/CB)][Cin*KH*KW][CB] so the CB weights of
-// one (ci, kh, kw) are one contiguous, wave-uniform 64-byte read; each input
-// value loaded feeds CB FMAs.  Index math is int32 within one image.
+// Direct convolution: lane = one output pixel, CB output channels of the
+// workgroup's channel block.  Weights are pre-packed [ceil(Cout/CB)][K][CB]
+// (K = Cin*KH*KW, k = (ci, kh, kw)) so the CB weights of one k are one
+// contiguous, wave-uniform read (scalar loads); each input value loaded feeds
+// CB FMAs.  The 256 x CB result tile goes through LDS and is stored with
+// consecutive lanes on consecutive channels, so channels-last outputs are
+// written in contiguous runs.  Index math is int32 within one image.
+template <int CB>
 __global__ __launch_bounds__(256) void conv_direct_kernel(ConvDirectArgs a, int P) {
-    constexpr int CB = kDirectCB;
-    const int p = blockIdx.x * 256 + threadIdx.x;
+    __shared__ float tile[256 * (CB + 1)];
+    const int p0 = blockIdx.x * 256;
+    const int p = p0 + threadIdx.x;
     const int cob = blockIdx.y;
     const int Co = static_cast<int>(a.y.dims[1]), Ho = static_cast<int>(a.y.dims[2]), Wo = static_cast<int>(a.y.dims[3]);
     const int Ci = static_cast<int>(a.x.dims[1]), H = static_cast<int>(a.x.dims[2]), W = static_cast<int>(a.x.dims[3]);
     const int K = Ci * a.KH * a.KW;
-    const float* wb = a.wpk + static_cast<int64_t>(cob) * K * CB;
-    if (p >= P) return;
     const int HoWo = Ho * Wo;
-    const int n = p / HoWo;
-    const int rem = p - n * HoWo;
-    const int ho = rem / Wo;
-    const int wo = rem - ho * Wo;
-    const float* xb = a.x.ptr + static_cast<int64_t>(n) * a.x.str[0];
-    const int xsc = static_cast<int>(a.x.str[1]), xsh = static_cast<int>(a.x.str[2]), xsw = static_cast<int>(a.x.str[3]);
-    const int hi0 = ho * a.sh - a.ph, wi0 = wo * a.sw - a.pw;
     float acc[CB];
 #pragma unroll
     for (int j = 0; j < CB; ++j) acc[j] = 0.0f;
-    const float* wk = wb;
-    for (int c = 0; c < Ci; ++c) {
-        for (int kh = 0; kh < a.KH; ++kh) {
-            const int hi = hi0 + kh * a.dh;
-            const bool hok = static_cast<unsigned>(hi) < static_cast<unsigned>(H);
-            for (int kw = 0; kw < a.KW; ++kw, wk += CB) {
-                const int wi = wi0 + kw * a.dw;
-                const bool ok = hok && static_cast<unsigned>(wi) < static_cast<unsigned>(W);
-                const float xv = ok ? xb[c * xsc + hi * xsh + wi * xsw] : 0.0f;
+    if (p < P) {
+        const int n = p / HoWo;
+        const int rem = p - n * HoWo;
+        const int ho = rem / Wo;
+        const int wo = rem - ho * Wo;
+        const float* xb = a.x.ptr + static_cast<int64_t>(n) * a.x.str[0];
+        const int xsc = static_cast<int>(a.x.str[1]), xsh = static_cast<int>(a.x.str[2]);
+        const int xsw = static_cast<int>(a.x.str[3]);
+        const int hi0 = ho * a.sh - a.ph, wi0 = wo * a.sw - a.pw;
+        const float* wk = a.wpk + static_cast<int64_t>(cob) * K * CB;
+        for (int c = 0; c < Ci; ++c) {
+            for (int kh = 0; kh < a.KH; ++kh) {
+                const int hi = hi0 + kh * a.dh;
+                const bool hok = static_cast<unsigned>(hi) < static_cast<unsigned>(H);
+                for (int kw = 0; kw < a.KW; ++kw, wk += CB) {
+                    const int wi = wi0 + kw * a.dw;
+                    const bool ok = hok && static_cast<unsigned>(wi) < static_cast<unsigned>(W);
+                    const float xv = ok ? xb[c * xsc + hi * xsh + wi * xsw] : 0.0f;
 #pragma unroll
-                for (int j = 0; j < CB; ++j) acc[j] += xv * wk[j];
+                    for (int j = 0; j < CB; ++j) acc[j] += xv * wk[j];
+                }
             }
         }
     }
-    const int64_t yo = static_cast<int64_t>(n) * a.y.str[0] + static_cast<int64_t>(ho) * a.y.str[2] +
-                       static_cast<int64_t>(wo) * a.y.str[3];
-    const int64_t ro = a.res.ptr ? static_cast<int64_t>(n) * a.res.str[0] + static_cast<int64_t>(ho) * a.res.str[2] +
-                                       static_cast<int64_t>(wo) * a.res.str[3]
-                                 : 0;
 #pragma unroll
-    for (int j = 0; j < CB; ++j) {
+    for (int j = 0; j < CB; ++j) tile[threadIdx.x * (CB + 1) + j] = acc[j];
+    __syncthreads();
+    const int nc = min(CB, Co - cob * CB);
+    for (int idx = threadIdx.x; idx < 256 * CB; idx += 256) {
+        const int pl = idx / CB, j = idx - (idx / CB) * CB;
+        const int pp = p0 + pl;
+        if (pp >= P || j >= nc) continue;
         const int co = cob * CB + j;
-        if (co < Co) {
-            float v = apply_act(acc[j] + (a.bias ? a.bias[co] : 0.0f), a.act, a.slope);
-            if (a.res.ptr) v += a.res.ptr[ro + co * a.res.str[1]];
-            a.y.ptr[yo + co * a.y.str[1]] = v;
-        }
+        const int n = pp / HoWo;
+        const int rem = pp - n * HoWo;
+        const int ho = rem / Wo;
+        const int wo = rem - ho * Wo;
+        float v = apply_act(tile[pl * (CB + 1) + j] + (a.bias ? a.bias[co] : 0.0f), a.act, a.slope);
+        if (a.res.ptr)
+            v += a.res.ptr[static_cast<int64_t>(n) * a.res.str[0] + static_cast<int64_t>(co) * a.res.str[1] +
+                           static_cast<int64_t>(ho) * a.res.str[2] + static_cast<int64_t>(wo) * a.res.str[3]];
+        a.y.ptr[static_cast<int64_t>(n) * a.y.str[0] + static_cast<int64_t>(co) * a.y.str[1] +
+                static_cast<int64_t>(ho) * a.y.str[2] + static_cast<int64_t>(wo) * a.y.str[3]] = v;
     }
 }
 
@@ -365,12 +377,18 @@ void launch_conv_direct(const ConvDirectArgs& a, hipStream_t s) {
         for (int d = 1; d < 4; ++d) e += (v.dims[d] - 1) * std::abs(v.str[d]);
         return e;
     };
+    const int cb = direct_cb(static_cast<int>(a.y.dims[1]));
     if (P >= (int64_t{1} << 31) || extent(a.x) >= (int64_t{1} << 31) ||
-        a.x.dims[1] * a.KH * a.KW * kDirectCB >= (int64_t{1} << 31))
+        a.x.dims[1] * a.KH * a.KW * 64 >= (int64_t{1} << 31))
         throw std::runtime_error("conv_direct: shape exceeds int32 indexing");
-    const dim3 grid(static_cast<unsigned>((P + 255) / 256),
-                    static_cast<unsigned>((a.y.dims[1] + kDirectCB - 1) / kDirectCB));
-    hipLaunchKernelGGL(conv_direct_kernel, grid, dim3(256), 0, s, a, static_cast<int>(P));
+    const dim3 grid(static_cast<unsigned>((P + 255) / 256), static_cast<unsigned>((a.y.dims[1] + cb - 1) / cb));
+    const int Pi = static_cast<int>(P);
+    switch (cb) {
+        case 16: hipLaunchKernelGGL(conv_direct_kernel<16>, grid, dim3(256), 0, s, a, Pi); break;
+        case 32: hipLaunchKernelGGL(conv_direct_kernel<32>, grid, dim3(256), 0, s, a, Pi); break;
+        case 48: hipLaunchKernelGGL(conv_direct_kernel<48>, grid, dim3(256), 0, s, a, Pi); break;
+        default: hipLaunchKernelGGL(conv_direct_kernel<64>, grid, dim3(256), 0, s, a, Pi); break;
+    }
 }
 
 }  // namespace k

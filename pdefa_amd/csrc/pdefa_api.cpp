@@ -291,6 +291,18 @@ PDEFA_EXPORT EngineStatus pdefa_amd_session_step_times(EngineSession* sess, int3
     });
 }
 
+PDEFA_EXPORT EngineStatus pdefa_amd_session_step_repeat(EngineSession* sess, int32_t step, int32_t iters,
+                                                        double* out_ms) {
+    if (!sess || sess->magic != kMagicSession) return ENGINE_ERR_INVALID_HANDLE;
+    if (!out_ms) return ENGINE_ERR_NULL_PTR;
+    if (iters <= 0 || step < 0) return ENGINE_ERR_INVALID_ARG;
+    return guarded([&] {
+        clear_error();
+        *out_ms = sess->inner->repeat_step(step, iters);
+        return ENGINE_OK;
+    });
+}
+
 PDEFA_EXPORT EngineStatus pdefa_amd_session_plan(const EngineSession* sess, char* buf, size_t cap, size_t* out_len) {
     if (!sess || sess->magic != kMagicSession) return ENGINE_ERR_INVALID_HANDLE;
     return guarded([&] {

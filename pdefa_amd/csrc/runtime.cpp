@@ -89,12 +89,12 @@ std::shared_ptr<DeviceModel> upload_model(const Model& m) {
         if (p.b >= 0) std::memcpy(host.data() + p.bias_off, m.weights[p.b].data, sizeof(float) * p.cout);
         // direct-conv layout [co / CB][k][co % CB], k = (ci, kh, kw); padding stays zero
         const int K = p.cin * p.kh * p.kw;
+        const int cb = k::direct_cb(p.cout);
         const float* src = static_cast<const float*>(m.weights[p.w].data);
         float* dst = host.data() + p.dpk_off;
         for (int co = 0; co < p.cout; ++co)
             for (int kk = 0; kk < K; ++kk)
-                dst[(static_cast<size_t>(co / k::kDirectCB) * K + kk) * k::kDirectCB + co % k::kDirectCB] =
-                    src[static_cast<size_t>(co) * K + kk];
+                dst[(static_cast<size_t>(co / cb) * K + kk) * cb + co % cb] = src[static_cast<size_t>(co) * K + kk];
     }
     dm->blob_bytes = total * sizeof(float);
     PDEFA_HIP(hipMalloc(&dm->blob, dm->blob_bytes));
@@ -501,6 +501,26 @@ void Session::time_steps(std::vector<double>& ms, std::vector<std::string>& labe
         labels.push_back(prep_->launches[i].label);
     }
     for (auto& e : ev) (void)hipEventDestroy(e);
+}
+
+double Session::repeat_step(int32_t idx, int32_t iters) {
+    if (!prep_ || runs == 0) throw std::runtime_error("repeat_step needs a completed run");
+    if (idx < 0 || idx >= static_cast<int32_t>(prep_->launches.size()) || iters <= 0)
+        throw std::runtime_error("repeat_step: bad step index or count");
+    const Launch& l = prep_->launches[static_cast<size_t>(idx)];
+    launch_one(l, stream_);  // warm
+    hipEvent_t a, b;
+    PDEFA_HIP(hipEventCreate(&a));
+    PDEFA_HIP(hipEventCreate(&b));
+    PDEFA_HIP(hipEventRecord(a, stream_));
+    for (int32_t i = 0; i < iters; ++i) launch_one(l, stream_);
+    PDEFA_HIP(hipEventRecord(b, stream_));
+    PDEFA_HIP(hipEventSynchronize(b));
+    float ms = 0.0f;
+    PDEFA_HIP(hipEventElapsedTime(&ms, a, b));
+    (void)hipEventDestroy(a);
+    (void)hipEventDestroy(b);
+    return ms / iters;
 }
 
 void Session::step_stats(int32_t iters, std::vector<double>& ms, std::vector<int32_t>& kind,

@@ -69,6 +69,9 @@ class Session {
     double replay(int32_t iters);
     // Runs each step once with HIP events around it; fills per-step ms.
     void time_steps(std::vector<double>& ms, std::vector<std::string>& labels);
+    // Launches step `idx` `iters` times back to back between two HIP events
+    // on the session stream; returns the average ms per launch.
+    double repeat_step(int32_t idx, int32_t iters);
     // Average per-step device time over `iters` step-by-step replays, with the
     // step kind and its algorithmic flops (2*N*Cout*Cin*KH*KW*Ho*Wo for convs).
     void step_stats(int32_t iters, std::vector<double>& ms, std::vector<int32_t>& kind,

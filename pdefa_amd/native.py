@@ -64,6 +64,7 @@ def lib() -> C.CDLL:
             "engine_session_destroy": (None, [vp]),
             "engine_ops_matmul": (C.c_int, [vp, vp, vp]),
             "pdefa_amd_session_replay": (C.c_int, [vp, i32, C.POINTER(C.c_double)]),
+            "pdefa_amd_session_step_repeat": (C.c_int, [vp, i32, i32, C.POINTER(C.c_double)]),
             "pdefa_amd_session_plan": (C.c_int, [vp, C.c_char_p, sz, C.POINTER(sz)]),
             "pdefa_amd_session_step_times": (C.c_int, [vp, i32, C.POINTER(C.c_double), C.POINTER(i32),
                                                        C.POINTER(i64), i32, C.POINTER(i32)]),
@@ -158,6 +159,13 @@ class Engine:
               "pdefa_amd_session_step_times")
         k = min(n.value, cap)
         return (np.array(ms[:k]), np.array(kind[:k]), np.array(flops[:k], dtype=np.int64))
+
+    def step_repeat(self, step: int, iters: int) -> float:
+        """Average ms per launch of step `step` launched `iters` times back to back."""
+        ms = C.c_double()
+        check(lib().pdefa_amd_session_step_repeat(self.sess, int(step), int(iters), C.byref(ms)),
+              "pdefa_amd_session_step_repeat")
+        return ms.value
 
     def plan(self) -> str:
         buf = C.create_string_buffer(1 << 20)
