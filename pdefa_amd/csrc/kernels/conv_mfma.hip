@@ -139,6 +139,22 @@ __global__ __launch_bounds__(256) void conv_mfma_kernel(ConvArgs a) {
         s_roff[tid] = ro;
     }
 
+    // Bias of this lane's output columns, loaded now so its latency hides
+    // behind the K loop (the epilogue only reads registers).
+    const int half = lane >> 5;
+    const int l32 = lane & 31;
+    float bias_lane[KG == 1 ? TN : 1];
+    if constexpr (KG == 1) {
+#pragma unroll
+        for (int tn = 0; tn < TN; ++tn) {
+            const int co = n0 + wave_n * WN + tn * 32 + l32;
+            bias_lane[tn] = co < a.Cout ? a.bias[co] : 0.0f;
+        }
+    } else {
+        const int co = n0 + tid % BN;
+        bias_lane[0] = co < a.Cout ? a.bias[co] : 0.0f;
+    }
+
     // ---- loaders: this lane loads float4 chunk `chunk` (slice chunk / 8) of
     // rows r0 + ROW_STEP*i of the A tile and of the B tile.
     // Offsets within one image fit in int32 (checked by the launcher).
@@ -278,8 +294,6 @@ __global__ __launch_bounds__(256) void conv_mfma_kernel(ConvArgs a) {
 #pragma unroll
             for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.0f;
 
-    const int half = lane >> 5;
-    const int l32 = lane & 31;
     auto compute_step = [&](int st) {
         const float* Ab = As(st, wg);
         const float* Bb = Bs(st, wg);
@@ -358,7 +372,7 @@ __global__ __launch_bounds__(256) void conv_mfma_kernel(ConvArgs a) {
             for (int tn = 0; tn < TN; ++tn) {
                 co[tn] = n0 + wave_n * WN + tn * 32 + l32;
                 cok[tn] = co[tn] < a.Cout;
-                bias_v[tn] = (!PART && cok[tn]) ? a.bias[co[tn]] : 0.0f;
+                bias_v[tn] = PART ? 0.0f : bias_lane[tn];
             }
 #pragma unroll
             for (int tm = 0; tm < TM; ++tm) {
@@ -411,7 +425,7 @@ __global__ __launch_bounds__(256) void conv_mfma_kernel(ConvArgs a) {
             const int col = tid % BN;
             const int co = n0 + col;
             const bool cok = co < a.Cout;
-            const float bias_v = (!PART && cok) ? a.bias[co] : 0.0f;
+            const float bias_v = PART ? 0.0f : bias_lane[0];
             float v[E];
             int64_t yo[E], ro[E];
 #pragma unroll
