@@ -28,6 +28,14 @@ PDEFA_EXPORT EngineStatus pdefa_amd_session_replay(EngineSession* sess, int32_t 
 PDEFA_EXPORT EngineStatus pdefa_amd_session_step_times(EngineSession* sess, int32_t iters, double* ms, int32_t* kind,
                                                        int64_t* flops, int32_t cap, int32_t* n);
 
+/* Launches step `step` of the prepared program `iters` times back to back
+ * (after one warm-up launch) between two HIP events on the session's stream;
+ * *out_ms = average device time per launch.  Every step is idempotent (it
+ * reads its inputs and overwrites its outputs).  Requires one completed
+ * engine_session_run. */
+PDEFA_EXPORT EngineStatus pdefa_amd_session_step_repeat(EngineSession* sess, int32_t step, int32_t iters,
+                                                        double* out_ms);
+
 /* Text dump of the session's current device program (one line per kernel). */
 PDEFA_EXPORT EngineStatus pdefa_amd_session_plan(const EngineSession* sess, char* buf, size_t cap, size_t* out_len);
 

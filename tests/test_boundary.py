@@ -32,7 +32,8 @@ engine_ops_reduce_mean engine_ops_argmax engine_ops_gather engine_ops_reshape en
 engine_ops_concat engine_ops_stack engine_random_randn engine_random_rand
 """.split()
 
-EXTENSIONS = ["pdefa_amd_session_replay", "pdefa_amd_session_step_times", "pdefa_amd_session_plan",
+EXTENSIONS = ["pdefa_amd_session_replay", "pdefa_amd_session_step_times", "pdefa_amd_session_step_repeat",
+              "pdefa_amd_session_plan",
               "pdefa_amd_plan_model", "pdefa_amd_device_name"]
 
 
