@@ -18,8 +18,6 @@ namespace k {
 // 16 < Cin <= 512, and its outputs are matched only with the same function.
 __device__ __forceinline__ float silu_winograd_form(float x) {
     const float neg_x = -x;
-    if (neg_x < -88.37626f) return x;
-    if (neg_x > 88.37626f) return 0.0f;
     const float fx = neg_x * 1.44269504088896341f;
     const float n = roundf(fx);
     const float f = fx - n;
@@ -32,7 +30,10 @@ __device__ __forceinline__ float silu_winograd_form(float x) {
     p = p * f + 1.0f;
     const int32_t e = (static_cast<int32_t>(n) + 127) << 23;
     // x / d as x * (1/d) with the hardware reciprocal (1 ulp)
-    return x * __builtin_amdgcn_rcpf(1.0f + p * __int_as_float(e));
+    const float r = x * __builtin_amdgcn_rcpf(1.0f + p * __int_as_float(e));
+    // the range cut-offs are selects, not branches (the polynomial result of
+    // an out-of-range x is discarded)
+    return neg_x < -88.37626f ? x : (neg_x > 88.37626f ? 0.0f : r);
 }
 
 // SiLU for the fused conv epilogues: x * 1/(1 + 2^(-x log2 e)) with the

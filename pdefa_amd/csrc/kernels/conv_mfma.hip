@@ -542,16 +542,18 @@ int64_t packed_weight_elems(int Cout, int K) {
     return cout_pad * k_pad;
 }
 
-// Cost model in CU cycles: one workgroup's MFMA time over its K range scaled
-// by how well its tile shape keeps the matrix cores fed, plus start-up and
-// per-step costs, times the number of workgroup rounds on the 256 CUs, plus a
-// fixed per-kernel cost and, for split-K, the reduce kernel.
+// Cost model in CU cycles.  A pipeline step of a workgroup takes the longer
+// of its MFMA time (shared with the other workgroups resident on the same CU,
+// c = ceil(workgroups / 256)) and a latency floor (a step's loads, LDS round
+// trip and barrier); add workgroup start-up, a fixed per-kernel cost and, for
+// split-K, the reduce kernel and the partial traffic.  Tile efficiencies and
+// the floor are calibrated on YOLOv8 layer shapes.
 ConvLaunchShape conv_select(int64_t M, int Cout, int K, bool allow_split) {
     constexpr double kCus = 256.0;
     constexpr double kKernelCycles = 10000.0;  // launch + completion of one kernel
     constexpr double kWgCycles = 1500.0;       // workgroup start-up (first loads)
-    constexpr double kStepCycles = 150.0;      // per pipeline step (barrier, LDS latency)
-    constexpr double kEff[kNumConvTiles] = {1.0, 0.92, 0.92, 0.85, 0.8, 0.75, 0.75, 0.7};
+    constexpr double kStepFloor = 2200.0;      // latency floor of one pipeline step
+    constexpr double kEff[kNumConvTiles] = {1.0, 0.8, 0.8, 0.85, 0.8, 0.75, 0.75, 0.7};
     const int ktiles = (K + BK - 1) / BK;
     ConvLaunchShape best;
     double best_cost = 1e300;
@@ -559,15 +561,14 @@ ConvLaunchShape conv_select(int64_t M, int Cout, int K, bool allow_split) {
         const ConvTileShape& sh = kShapes[t];
         const int64_t wgs0 = ((M + sh.bm - 1) / sh.bm) * ((Cout + sh.bn - 1) / sh.bn);
         const int steps_total = (ktiles + sh.kg - 1) / sh.kg;
-        const int max_splits = allow_split ? std::min(16, std::max(1, steps_total / 4)) : 1;
+        const int max_splits = allow_split ? std::min(16, std::max(1, steps_total / 2)) : 1;
         for (int sp = 1; sp <= max_splits; ++sp) {
             const int steps = (steps_total + sp - 1) / sp;
             const int splits = (steps_total + steps - 1) / steps;
             if (splits != sp) continue;
-            const double flops_wg = 2.0 * sh.bm * sh.bn * static_cast<double>(steps) * sh.kg * BK;
-            const double wg_cycles = flops_wg / 256.0 / kEff[t] + kWgCycles + steps * kStepCycles;
-            const double rounds = std::ceil(static_cast<double>(wgs0 * splits) / kCus);
-            double cost = kKernelCycles + rounds * wg_cycles;
+            const double c = std::ceil(static_cast<double>(wgs0 * splits) / kCus);
+            const double mfma_step = 2.0 * sh.bm * sh.bn * sh.kg * BK / 256.0 / kEff[t];
+            double cost = kKernelCycles + kWgCycles + steps * std::max(c * mfma_step, kStepFloor);
             if (splits > 1) cost += kKernelCycles + static_cast<double>(splits) * M * Cout * 4.0 / 2048.0;
             if (cost < best_cost * 0.999) {
                 best_cost = cost;

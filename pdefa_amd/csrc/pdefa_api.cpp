@@ -8,6 +8,7 @@
 #include <cstring>
 #include <fstream>
 #include <memory>
+#include <sstream>
 #include <string>
 #include <vector>
 
@@ -326,8 +327,20 @@ PDEFA_EXPORT EngineStatus pdefa_amd_plan_model(const EngineModel* m, const int64
         std::vector<std::vector<int64_t>> dims(static_cast<size_t>(m->inner->num_inputs()),
                                                std::vector<int64_t>(shape, shape + ndim));
         pdefa::PlanOptions opt;
+        if (const char* r = std::getenv("PDEFA_REUSE_MEMORY")) opt.reuse_memory = r[0] != '0';
         const pdefa::Plan p = pdefa::build_plan(*m->inner, dims, opt);
-        const std::string s = pdefa::describe_plan(*m->inner, p);
+        std::string s = pdefa::describe_plan(*m->inner, p);
+        const pdefa::Schedule sc = pdefa::schedule_plan(p, 8);
+        std::ostringstream os;
+        os << "schedule streams=" << sc.n_streams << "\n";
+        for (size_t i = 0; i < sc.stream.size(); ++i) {
+            os << i << " stream=" << sc.stream[i] << " deps=";
+            for (int d : sc.deps[i]) os << d << ",";
+            os << " waits=";
+            for (int w : sc.waits[i]) os << w << ",";
+            os << "\n";
+        }
+        s += os.str();
         if (out_len) *out_len = s.size();
         if (buf && cap) {
             const size_t n = std::min(cap - 1, s.size());

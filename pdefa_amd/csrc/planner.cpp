@@ -966,6 +966,13 @@ class Planner {
 
     void allocate() {
         const int n = static_cast<int>(plan_.steps.size());
+        if (!opt_.reuse_memory) {
+            // every tensor keeps its own memory for the whole program
+            for (Buffer& b : plan_.bufs) {
+                b.first = -1;
+                b.last = n;
+            }
+        }
         for (int i = 0; i < n; ++i) {
             const Step& s = plan_.steps[i];
             touch(s.out, i);
@@ -1043,6 +1050,103 @@ std::string fmt_view(const VRef& v) {
 }
 
 }  // namespace
+
+namespace {
+
+// Arena element range [lo, hi) a view can touch (weights: none).
+std::pair<int64_t, int64_t> view_range(const Plan& p, const VRef& v) {
+    if (v.buf < 0) return {0, 0};
+    int64_t lo = p.bufs[v.buf].offset + v.off, hi = lo;
+    for (int d = 0; d < v.rank; ++d) {
+        if (v.dims[d] <= 0) return {0, 0};
+        const int64_t span = (v.dims[d] - 1) * v.str[d];
+        if (span < 0) lo += span;
+        else hi += span;
+    }
+    return {lo, hi + 1};
+}
+
+using Ranges = std::vector<std::pair<int64_t, int64_t>>;
+
+bool overlap(const Ranges& a, const Ranges& b) {
+    for (const auto& x : a)
+        for (const auto& y : b)
+            if (x.first < y.second && y.first < x.second && x.first < x.second && y.first < y.second) return true;
+    return false;
+}
+
+}  // namespace
+
+Schedule schedule_plan(const Plan& p, int max_streams) {
+    const int n = static_cast<int>(p.steps.size());
+    std::vector<Ranges> rd(n), wr(n);
+    for (int i = 0; i < n; ++i) {
+        const Step& s = p.steps[i];
+        wr[i].push_back(view_range(p, s.out));
+        rd[i].push_back(view_range(p, s.a));
+        if (s.kind == StepKind::Elt) rd[i].push_back(view_range(p, s.b));
+        if (s.has_res) rd[i].push_back(view_range(p, s.res));
+        if (s.ws_buf >= 0) {
+            const Buffer& b = p.bufs[s.ws_buf];
+            wr[i].push_back({b.offset, b.offset + b.elems});
+        }
+    }
+    Schedule sc;
+    sc.stream.assign(n, 0);
+    sc.waits.assign(n, {});
+    sc.recorded.assign(n, false);
+    sc.deps.assign(n, {});
+    const size_t words = (static_cast<size_t>(n) + 63) / 64;
+    std::vector<std::vector<uint64_t>> anc(n, std::vector<uint64_t>(words, 0));
+    auto has = [&](int j, int i) { return (anc[j][i / 64] >> (i % 64)) & 1u; };
+    std::vector<int> tail;  // last step of each stream
+    for (int j = 0; j < n; ++j) {
+        for (int i = 0; i < j; ++i)
+            if (overlap(wr[i], rd[j]) || overlap(wr[i], wr[j]) || overlap(rd[i], wr[j])) sc.deps[j].push_back(i);
+        for (int i : sc.deps[j]) {
+            anc[j][i / 64] |= uint64_t{1} << (i % 64);
+            for (size_t w = 0; w < words; ++w) anc[j][w] |= anc[i][w];
+        }
+        // direct hazards not implied by another direct hazard
+        std::vector<int> red;
+        for (int i : sc.deps[j]) {
+            bool implied = false;
+            for (int k2 : sc.deps[j])
+                if (k2 != i && has(k2, i)) {
+                    implied = true;
+                    break;
+                }
+            if (!implied) red.push_back(i);
+        }
+        // stream: continue the chain of the latest reduced dependency if it is
+        // a stream tail; else a stream whose tail is an ancestor (no false
+        // ordering); else a new stream; else the stream with the oldest tail.
+        int pick = -1;
+        for (int t = 0; t < static_cast<int>(tail.size()); ++t)
+            if (std::find(red.begin(), red.end(), tail[t]) != red.end() && (pick < 0 || tail[t] > tail[pick])) pick = t;
+        if (pick < 0)
+            for (int t = 0; t < static_cast<int>(tail.size()); ++t)
+                if (has(j, tail[t]) && (pick < 0 || tail[t] > tail[pick])) pick = t;
+        if (pick < 0 && static_cast<int>(tail.size()) < max_streams) {
+            tail.push_back(-1);
+            pick = static_cast<int>(tail.size()) - 1;
+        }
+        if (pick < 0) {
+            pick = 0;
+            for (int t = 1; t < static_cast<int>(tail.size()); ++t)
+                if (tail[t] < tail[pick]) pick = t;
+        }
+        sc.stream[j] = pick;
+        for (int i : red)
+            if (sc.stream[i] != pick) {
+                sc.waits[j].push_back(i);
+                sc.recorded[i] = true;
+            }
+        tail[pick] = j;
+    }
+    sc.n_streams = std::max<int>(1, static_cast<int>(tail.size()));
+    return sc;
+}
 
 Plan build_plan(const Model& m, const std::vector<std::vector<int64_t>>& input_dims, const PlanOptions& opt) {
     Planner p(m, input_dims, opt);

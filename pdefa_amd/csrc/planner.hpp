@@ -76,11 +76,25 @@ struct PlanOptions {
     bool split_k = true;
     int force_tile = -1;   // >= 0: use this implicit-GEMM tile for every MFMA conv (tuning, tests)
     int force_splits = 0;  // > 0 with force_tile: split-K across workgroups into this many splits
+    bool reuse_memory = true;  // share arena memory between tensors with disjoint lifetimes
     bool winograd_form_silu = true;  // match the reference's Winograd-layer SiLU
 };
 
 // Throws std::runtime_error naming the node for an unsupported op or pattern.
 Plan build_plan(const Model& m, const std::vector<std::vector<int64_t>>& input_dims, const PlanOptions& opt);
+
+// Concurrent issue of a plan: steps ordered by the arena ranges they read and
+// write (true and false data hazards); each step gets a capture stream, the
+// steps it must wait for on other streams, and whether another stream waits
+// for it.  Steps on one stream run in plan order.
+struct Schedule {
+    int n_streams = 1;
+    std::vector<int> stream;              // per step
+    std::vector<std::vector<int>> waits;  // per step: earlier steps on other streams
+    std::vector<bool> recorded;           // per step: some later step waits for it
+    std::vector<std::vector<int>> deps;   // per step: all direct hazards (before reduction)
+};
+Schedule schedule_plan(const Plan& p, int max_streams);
 
 // Human-readable dump (one line per step) for tests and debugging.
 std::string describe_plan(const Model& m, const Plan& p);

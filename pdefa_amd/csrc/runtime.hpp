@@ -105,6 +105,8 @@ class Session {
         std::vector<Launch> launches;
         hipGraph_t graph = nullptr;
         hipGraphExec_t exec = nullptr;
+        Schedule sched;                  // concurrent issue order of the captured graph
+        std::vector<hipEvent_t> events;  // per step (recorded ones only) + per extra stream join
         std::vector<float*> host_out;  // pinned
         std::vector<HostTensor> outputs;
     };
@@ -112,6 +114,7 @@ class Session {
     void prepare(const std::vector<std::vector<int64_t>>& dims);
     void release_prepared();
     void launch_all(hipStream_t s);
+    void capture_concurrent();  // records the program as a multi-stream hipGraph
     void launch_one(const Launch& l, hipStream_t s);
     void upload_inputs();
     void download_outputs();
@@ -119,6 +122,8 @@ class Session {
     Model* model_;
     std::shared_ptr<DeviceModel> dev_;
     hipStream_t stream_ = nullptr;
+    std::vector<hipStream_t> side_streams_;  // capture-only streams for concurrent branches
+    bool concurrent_ = true;
     std::vector<const HostTensor*> inputs_;
     std::unique_ptr<Prepared> prep_;
     ProfileFn prof_fn_ = nullptr;

@@ -17,7 +17,19 @@ def y8n_path(tmp_path_factory):
 def parse(text):
     head, *lines = text.strip().splitlines()
     info = dict(re.findall(r"(\w+)=(\d+)", head))
-    return {k: int(v) for k, v in info.items()}, lines
+    cut = next(i for i, l in enumerate(lines) if l.startswith("schedule"))
+    return {k: int(v) for k, v in info.items()}, lines[:cut]
+
+
+def parse_schedule(text):
+    lines = text.strip().splitlines()
+    cut = next(i for i, l in enumerate(lines) if l.startswith("schedule"))
+    out = []
+    for l in lines[cut + 1:]:
+        ints = lambda key: [int(x) for x in re.search(key + r"=([\d,]*)", l).group(1).split(",") if x]
+        out.append({"stream": int(re.search(r"stream=(\d+)", l).group(1)), "deps": ints("deps"),
+                    "waits": ints("waits")})
+    return int(re.search(r"streams=(\d+)", lines[cut]).group(1)), out
 
 
 def test_yolov8n_plan_is_zero_copy(y8n_path):
@@ -84,3 +96,32 @@ def test_run_without_gpu_reports_error(tmp_path):
     with pytest.raises(nat.NativeError, match="RUNTIME.*no HIP device"):
         eng.run(x)
     eng.close()
+
+
+@pytest.mark.parametrize("reuse", ["1", "0"])
+def test_concurrent_schedule_orders_every_hazard(y8n_path, monkeypatch, reuse):
+    """Every pair of steps that touch overlapping arena ranges (one writing) is
+    ordered by the multi-stream schedule: same stream (plan order) or a chain
+    of cross-stream waits."""
+    monkeypatch.setenv("PDEFA_REUSE_MEMORY", reuse)
+    n_streams, sched = parse_schedule(native.plan_text(y8n_path, [1, 3, 640, 640]))
+    n = len(sched)
+    succ = [[] for _ in range(n)]
+    last = {}
+    for j, st in enumerate(sched):
+        if st["stream"] in last:
+            succ[last[st["stream"]]].append(j)
+        last[st["stream"]] = j
+        for w in st["waits"]:
+            assert w < j and sched[w]["stream"] != st["stream"]
+            succ[w].append(j)
+    reach = [set() for _ in range(n)]
+    for i in reversed(range(n)):
+        for j in succ[i]:
+            reach[i].add(j)
+            reach[i] |= reach[j]
+    for j, st in enumerate(sched):
+        for i in st["deps"]:
+            assert j in reach[i], (i, j)
+    if reuse == "0":
+        assert n_streams > 1  # the detect-head branches run concurrently
