@@ -148,6 +148,32 @@ void launch_resize_nearest(const View& out, const View& in, hipStream_t s);
 // Softmax along `axis` of the logical shape.
 void launch_softmax(const View& out, const View& in, int axis, hipStream_t s);
 
+// Three chained stride-1 "same" max pools of kernel k (the SPPF block) in one
+// pass: out0 = pool_k(in), out1 = pool_k(out0) = pool_{2k-1}(in),
+// out2 = pool_k(out1) = pool_{3k-2}(in) (max composes exactly; padding never
+// wins).  Logical [N, C, H, W] views.
+void launch_maxpool_chain(const View& out0, const View& out1, const View& out2, const View& in, int k,
+                          hipStream_t s);
+
+// YOLOv8 box decode, the Detect head's DFL + dist2bbox subgraph in one pass:
+// per anchor a and side s, softmax over the R bins of x[n, :, s, a], expected
+// bin d_s = sum_b p_b * w_b (+ bias) (the 1x1 DFL conv), then with
+// (ax, ay) = anchors[n, :, a]: x1 = ax - d0, y1 = ay - d1, x2 = ax + d2,
+// y2 = ay + d3, out[n, :, a] = ((x1 + x2) / two, (y1 + y2) / two, x2 - x1,
+// y2 - y1) * strides[n, :, a] -- the same fp32 operations, in the same order,
+// as the unfused Softmax, Conv, Sub, Add, Add, Div, Sub, Concat, Mul nodes.
+struct DetectDecodeArgs {
+    View x;        // [N, R, 4, A]
+    View anchors;  // [N, 2, A] (broadcast)
+    View two;      // [N, 2, A] (broadcast)
+    View strides;  // [N, 4, A] (broadcast)
+    View out;      // [N, 4, A]
+    const float* dfl_w = nullptr;  // R floats
+    float dfl_bias = 0.0f;
+    int32_t bins = 16;
+};
+void launch_detect_decode(const DetectDecodeArgs& a, hipStream_t s);
+
 // Packs conv weights [Cout, Cin, KH, KW] (device, contiguous) into the packed
 // layout above.
 void launch_pack_conv_weights(float* dst, const float* w, int Cout, int Cin, int KH, int KW, hipStream_t s);

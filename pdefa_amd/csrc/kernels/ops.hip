@@ -298,6 +298,121 @@ void launch_softmax(const View& out, const View& in, int axis, hipStream_t s) {
                            axis, rows);
 }
 
+// SPPF: three chained k x k stride-1 same-padded max pools from one read of
+// the input window (radii r, 2r, 3r with r = k/2).  Channel fastest, so
+// channels-last views are read and written contiguously.
+template <typename I>
+__global__ __launch_bounds__(256) void maxpool_chain_kernel(IView<I> o0, IView<I> o1, IView<I> o2, IView<I> in, int r,
+                                                            I total) {
+    const I C = o0.dims[1], Ho = o0.dims[2], Wo = o0.dims[3];
+    const I H = in.dims[2], W = in.dims[3];
+    for (I i = blockIdx.x * static_cast<I>(blockDim.x) + threadIdx.x; i < total;
+         i += static_cast<I>(gridDim.x) * blockDim.x) {
+        I t = i;
+        const I c = t % C; t /= C;
+        const I w = t % Wo; t /= Wo;
+        const I h = t % Ho;
+        const I n = t / Ho;
+        const float* base = in.ptr + n * in.str[0] + c * in.str[1];
+        float m0 = -3.402823466e+38f, m1 = m0, m2 = m0;
+        for (int dy = -3 * r; dy <= 3 * r; ++dy) {
+            const I hi = h + dy;
+            if (hi < 0 || hi >= H) continue;
+            const int ay = dy < 0 ? -dy : dy;
+            for (int dx = -3 * r; dx <= 3 * r; ++dx) {
+                const I wi = w + dx;
+                if (wi < 0 || wi >= W) continue;
+                const int ax = dx < 0 ? -dx : dx;
+                const float v = base[hi * in.str[2] + wi * in.str[3]];
+                m2 = v > m2 ? v : m2;
+                if (ay <= 2 * r && ax <= 2 * r) m1 = v > m1 ? v : m1;
+                if (ay <= r && ax <= r) m0 = v > m0 ? v : m0;
+            }
+        }
+        o0.ptr[n * o0.str[0] + c * o0.str[1] + h * o0.str[2] + w * o0.str[3]] = m0;
+        o1.ptr[n * o1.str[0] + c * o1.str[1] + h * o1.str[2] + w * o1.str[3]] = m1;
+        o2.ptr[n * o2.str[0] + c * o2.str[1] + h * o2.str[2] + w * o2.str[3]] = m2;
+    }
+}
+
+void launch_maxpool_chain(const View& out0, const View& out1, const View& out2, const View& in, int k,
+                          hipStream_t s) {
+    check_view(out0, "maxpool_chain out0");
+    check_view(out1, "maxpool_chain out1");
+    check_view(out2, "maxpool_chain out2");
+    check_view(in, "maxpool_chain in");
+    if (out0.rank != 4 || out1.rank != 4 || out2.rank != 4 || in.rank != 4)
+        throw std::runtime_error("maxpool_chain: rank 4 views expected");
+    if (k < 1 || k % 2 == 0) throw std::runtime_error("maxpool_chain: odd kernel expected");
+    for (int d = 0; d < 4; ++d)
+        if (out0.dims[d] != in.dims[d] || out1.dims[d] != in.dims[d] || out2.dims[d] != in.dims[d])
+            throw std::runtime_error("maxpool_chain: same-size outputs expected");
+    const int64_t total = numel(out0);
+    if (total == 0) return;
+    if (!(fits_i32(out0) && fits_i32(out1) && fits_i32(out2) && fits_i32(in)))
+        throw std::runtime_error("maxpool_chain: views exceed int32 indexing");
+    hipLaunchKernelGGL(maxpool_chain_kernel<int32_t>, dim3(grid_for(total)), dim3(256), 0, s, iview<int32_t>(out0),
+                       iview<int32_t>(out1), iview<int32_t>(out2), iview<int32_t>(in), k / 2,
+                       static_cast<int32_t>(total));
+}
+
+// One lane per (n, anchor); see kernels.hpp for the arithmetic.  The softmax
+// matches softmax_kernel (max, exp(x - max), sum in bin order, * 1/sum) and
+// the expectation matches the direct conv's accumulation order.
+__global__ __launch_bounds__(256) void detect_decode_kernel(DetectDecodeArgs a, int32_t N, int32_t A) {
+    const int32_t i = blockIdx.x * 256 + threadIdx.x;
+    if (i >= N * A) return;
+    const int32_t n = i / A;
+    const int32_t an = i - n * A;
+    const View& x = a.x;  // offsets within int32 (checked by the launcher)
+    const int32_t xs1 = static_cast<int32_t>(x.str[1]);
+    float d[4];
+#pragma unroll
+    for (int side = 0; side < 4; ++side) {
+        const float* xs = x.ptr + static_cast<int32_t>(n * x.str[0] + side * x.str[2] + an * x.str[3]);
+        float mx = -1e30f;
+        for (int b = 0; b < a.bins; ++b) {
+            const float v = xs[b * xs1];
+            mx = v > mx ? v : mx;
+        }
+        float sum = 0.0f;
+        for (int b = 0; b < a.bins; ++b) sum += expf(xs[b * xs1] - mx);
+        const float inv = sum > 0.0f ? 1.0f / sum : 0.0f;
+        float acc = 0.0f;
+        for (int b = 0; b < a.bins; ++b) acc = fmaf(expf(xs[b * xs1] - mx) * inv, a.dfl_w[b], acc);
+        d[side] = acc + a.dfl_bias;
+    }
+    auto at = [&](const View& v, int c) {
+        return v.ptr[n * v.str[0] + c * v.str[1] + static_cast<int64_t>(an) * v.str[2]];
+    };
+    const float ax = at(a.anchors, 0), ay = at(a.anchors, 1);
+    const float x1 = ax - d[0], y1 = ay - d[1];
+    const float x2 = ax + d[2], y2 = ay + d[3];
+    const float r[4] = {(x1 + x2) / at(a.two, 0), (y1 + y2) / at(a.two, 1), x2 - x1, y2 - y1};
+#pragma unroll
+    for (int c = 0; c < 4; ++c)
+        a.out.ptr[n * a.out.str[0] + c * a.out.str[1] + static_cast<int64_t>(an) * a.out.str[2]] = r[c] * at(a.strides, c);
+}
+
+void launch_detect_decode(const DetectDecodeArgs& a, hipStream_t s) {
+    check_view(a.x, "decode x");
+    check_view(a.anchors, "decode anchors");
+    check_view(a.two, "decode divisor");
+    check_view(a.strides, "decode strides");
+    check_view(a.out, "decode out");
+    if (!a.dfl_w || a.bins < 1) throw std::runtime_error("decode: missing DFL weights");
+    if (a.x.rank != 4 || a.x.dims[1] != a.bins || a.x.dims[2] != 4) throw std::runtime_error("decode: x must be [N, R, 4, A]");
+    const int64_t N = a.x.dims[0], A = a.x.dims[3];
+    for (const View* v : {&a.anchors, &a.two, &a.strides, &a.out})
+        if (v->rank != 3 || v->dims[0] != N || v->dims[2] != A) throw std::runtime_error("decode: [N, C, A] views expected");
+    if (a.anchors.dims[1] != 2 || a.two.dims[1] != 2 || a.strides.dims[1] != 4 || a.out.dims[1] != 4)
+        throw std::runtime_error("decode: channel counts");
+    if (N * A >= (int64_t{1} << 31) || !fits_i32(a.x)) throw std::runtime_error("decode: views exceed int32 indexing");
+    if (N * A == 0) return;
+    hipLaunchKernelGGL(detect_decode_kernel, dim3(static_cast<unsigned>((N * A + 255) / 256)), dim3(256), 0, s, a,
+                       static_cast<int32_t>(N), static_cast<int32_t>(A));
+}
+
 // Direct convolution: lane = one output pixel, CB output channels of the
 // workgroup's channel block.  Weights are pre-packed [ceil(Cout/CB)][K][CB]
 // (K = Cin*KH*KW, k = (ci, kh, kw)) so the CB weights of one k are one

@@ -218,6 +218,7 @@ class Planner {
         fuse_residuals();
         assign_storage();
         emit();
+        fuse_steps();
         allocate();
         return std::move(plan_);
     }
@@ -956,6 +957,128 @@ class Planner {
         }
     }
 
+    // ---- 5b. step fusion ---------------------------------------------------
+    // Rewrites runs of emitted steps whose intermediates nothing else reads:
+    //  - SPPF: three chained stride-1 same max pools -> one pass (MaxPoolChain);
+    //  - the Detect head's DFL + dist2bbox (Softmax, 1x1 Conv to one channel,
+    //    Sub, Add, Add, Div, Sub, Mul over the anchors/strides constants) ->
+    //    one DetectDecode step, same arithmetic in the same order.
+    bool reads_buf(const Step& s, int32_t buf) const {
+        auto uses = [&](const VRef& v) { return v.buf == buf; };
+        if (uses(s.a) || (s.has_res && uses(s.res))) return true;
+        if ((s.kind == StepKind::Elt || s.kind == StepKind::DetectDecode) && (uses(s.b) || uses(s.c))) return true;
+        return false;
+    }
+    // No step outside [lo, hi] reads `buf`, and it is not a graph output.
+    bool private_buf(int32_t buf, size_t lo, size_t hi) const {
+        if (buf < 0) return false;
+        for (size_t i = 0; i < plan_.steps.size(); ++i)
+            if ((i < lo || i > hi) && reads_buf(plan_.steps[i], buf)) return false;
+        for (const VRef& o : plan_.outputs)
+            if (o.buf == buf) return false;
+        for (int32_t r : m_.graph_outputs)
+            if (vals_.count(r) && vals_.at(r).view.buf == buf) return false;
+        return true;
+    }
+    static bool is_elt(const Step& s, int op) { return s.kind == StepKind::Elt && s.elt == op; }
+    static bool is_weight_view(const VRef& v) { return v.buf == kBufWeight; }
+
+    bool match_sppf(size_t i) const {
+        const auto& st = plan_.steps;
+        if (i + 2 >= st.size()) return false;
+        const Step& p0 = st[i];
+        for (size_t j = 0; j < 3; ++j) {
+            const Step& p = st[i + j];
+            if (p.kind != StepKind::MaxPool || p.KH != p0.KH || p.KW != p0.KH || p.KH % 2 == 0 || p.sh != 1 ||
+                p.sw != 1 || p.ph != p0.KH / 2 || p.pw != p0.KH / 2)
+                return false;
+            if (p.out.rank != 4 || dims_of(p.out) != dims_of(p0.a)) return false;
+        }
+        return views_equal(st[i + 1].a, st[i].out) && views_equal(st[i + 2].a, st[i + 1].out);
+    }
+
+    bool match_decode(size_t i, Step* fused) const {
+        const auto& st = plan_.steps;
+        if (i + 7 >= st.size()) return false;
+        const Step &sm = st[i], &cv = st[i + 1], &sub = st[i + 2], &add = st[i + 3], &sum = st[i + 4],
+                   &dv = st[i + 5], &wh = st[i + 6], &mul = st[i + 7];
+        if (sm.kind != StepKind::Softmax || sm.axis != 1 || sm.a.rank != 4 || sm.a.dims[2] != 4) return false;
+        const int64_t N = sm.a.dims[0], R = sm.a.dims[1], A = sm.a.dims[3];
+        // 1x1 conv of the softmax to one channel, no activation or residual
+        if (cv.kind != StepKind::ConvDirect || !views_equal(cv.a, sm.out) || cv.KH != 1 || cv.KW != 1 || cv.sh != 1 ||
+            cv.sw != 1 || cv.ph != 0 || cv.pw != 0 || cv.act != 0 || cv.has_res || cv.out.rank != 4 ||
+            cv.out.dims[1] != 1 || cv.out.dims[2] != 4 || cv.out.dims[3] != A)
+            return false;
+        const Node& cn = m_.nodes[cv.node];
+        if (cn.inputs.size() < 2 || cn.inputs[1] > -1000) return false;
+        // distances d[side] live in cv.out; lt = sides 0..1, rb = sides 2..3
+        const VRef& D = cv.out;
+        auto side_view = [&](const VRef& v, int64_t first) {  // [N, 2, A] over sides first, first+1
+            return v.buf == D.buf && v.rank == 3 && v.dims[1] == 2 && v.dims[2] == A &&
+                   v.off == D.off + first * D.str[2] && v.str[1] == D.str[2] && v.str[2] == D.str[3];
+        };
+        auto anchors_ok = [&](const VRef& v) { return is_weight_view(v) && v.rank == 3 && v.dims[1] == 2; };
+        if (!is_elt(sub, k::kEltSub) || !anchors_ok(sub.a) || !side_view(sub.b, 0)) return false;
+        const VRef* anc_other = nullptr;
+        if (is_elt(add, k::kEltAdd) && views_equal(add.a, sub.a) && side_view(add.b, 2)) anc_other = &add.a;
+        if (is_elt(add, k::kEltAdd) && views_equal(add.b, sub.a) && side_view(add.a, 2)) anc_other = &add.b;
+        if (!anc_other) return false;
+        const bool sum_ok = is_elt(sum, k::kEltAdd) && ((views_equal(sum.a, sub.out) && views_equal(sum.b, add.out)) ||
+                                                       (views_equal(sum.a, add.out) && views_equal(sum.b, sub.out)));
+        if (!sum_ok) return false;
+        if (!is_elt(dv, k::kEltDiv) || !views_equal(dv.a, sum.out) || !is_weight_view(dv.b)) return false;
+        if (!is_elt(wh, k::kEltSub) || !views_equal(wh.a, add.out) || !views_equal(wh.b, sub.out)) return false;
+        // mul reads the [N, 4, A] concat of (cxy, wh) times the strides constant
+        if (!is_elt(mul, k::kEltMul) || !is_weight_view(mul.b) || mul.a.rank != 3 || mul.a.dims[1] != 4 ||
+            mul.a.dims[2] != A || mul.out.rank != 3)
+            return false;
+        if (!views_equal(slice_view(mul.a, 1, 0, 2), dv.out) || !views_equal(slice_view(mul.a, 1, 2, 2), wh.out))
+            return false;
+        // every intermediate is read only inside the run
+        for (int32_t b : {sm.out.buf, cv.out.buf, sub.out.buf, add.out.buf, sum.out.buf, mul.a.buf})
+            if (!private_buf(b, i, i + 7)) return false;
+        Step f;
+        f.kind = StepKind::DetectDecode;
+        f.node = sm.node;
+        f.a = sm.a;
+        f.b = sub.a;      // anchors
+        f.c = dv.b;       // divisor
+        f.res = mul.b;    // strides
+        f.has_res = false;
+        f.out = mul.out;
+        f.dfl_weight = -1000 - cn.inputs[1];
+        f.dfl_bias = (cn.inputs.size() > 2 && cn.inputs[2] <= -1000) ? -1000 - cn.inputs[2] : -1;
+        f.bins = static_cast<int32_t>(R);
+        (void)N;
+        *fused = f;
+        return true;
+    }
+
+    void fuse_steps() {
+        std::vector<Step> out;
+        auto& st = plan_.steps;
+        for (size_t i = 0; i < st.size();) {
+            if (match_sppf(i)) {  // all three outputs are still written
+                Step f = st[i];
+                f.kind = StepKind::MaxPoolChain;
+                f.b = st[i + 1].out;
+                f.c = st[i + 2].out;
+                out.push_back(f);
+                i += 3;
+                continue;
+            }
+            Step f;
+            if (match_decode(i, &f)) {
+                out.push_back(f);
+                i += 8;
+                continue;
+            }
+            out.push_back(st[i]);
+            ++i;
+        }
+        st.swap(out);
+    }
+
     // ---- 6. liveness + arena ----------------------------------------------
     void touch(const VRef& v, int step) {
         if (v.buf < 0) return;
@@ -978,6 +1101,10 @@ class Planner {
             touch(s.out, i);
             touch(s.a, i);
             if (s.kind == StepKind::Elt) touch(s.b, i);
+            if (s.kind == StepKind::MaxPoolChain) {
+                touch(s.b, i);
+                touch(s.c, i);
+            }
             if (s.has_res) touch(s.res, i);
             if (s.ws_buf >= 0) {
                 plan_.bufs[s.ws_buf].first = std::min(plan_.bufs[s.ws_buf].first, i);
@@ -1035,6 +1162,8 @@ const char* step_kind_name(StepKind k) {
         case StepKind::MaxPool: return "maxpool";
         case StepKind::Resize: return "resize";
         case StepKind::Softmax: return "softmax";
+        case StepKind::MaxPoolChain: return "maxpool_chain";
+        case StepKind::DetectDecode: return "detect_decode";
     }
     return "?";
 }
@@ -1086,6 +1215,10 @@ Schedule schedule_plan(const Plan& p, int max_streams) {
         rd[i].push_back(view_range(p, s.a));
         if (s.kind == StepKind::Elt) rd[i].push_back(view_range(p, s.b));
         if (s.has_res) rd[i].push_back(view_range(p, s.res));
+        if (s.kind == StepKind::MaxPoolChain) {
+            wr[i].push_back(view_range(p, s.b));
+            wr[i].push_back(view_range(p, s.c));
+        }
         if (s.ws_buf >= 0) {
             const Buffer& b = p.bufs[s.ws_buf];
             wr[i].push_back({b.offset, b.offset + b.elems});

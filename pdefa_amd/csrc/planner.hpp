@@ -32,12 +32,13 @@ struct VRef {
     int64_t str[k::kMaxRank] = {0, 0, 0, 0, 0, 0};
 };
 
-enum class StepKind : int32_t { ConvMfma, ConvDirect, Elt, MaxPool, Resize, Softmax };
+enum class StepKind : int32_t { ConvMfma, ConvDirect, Elt, MaxPool, Resize, Softmax, MaxPoolChain, DetectDecode };
 
 struct Step {
     StepKind kind = StepKind::Elt;
     int32_t node = -1;  // graph node the step implements (first of a fused group)
     VRef out, a, b, res;
+    VRef c;  // MaxPoolChain: third output; DetectDecode: divisor view
     bool has_res = false;
     // conv
     int32_t act = 0;
@@ -52,6 +53,10 @@ struct Step {
     float alpha = 0.0f;
     // softmax
     int32_t axis = 0;
+    // DetectDecode: the DFL conv's weight (and bias) indices, number of bins
+    int32_t dfl_weight = -1;
+    int32_t dfl_bias = -1;
+    int32_t bins = 0;
 };
 
 struct Buffer {

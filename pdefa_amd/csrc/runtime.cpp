@@ -349,6 +349,32 @@ void Session::prepare(const std::vector<std::vector<int64_t>>& dims) {
                 l.elt = s.elt;
                 l.alpha = s.alpha;
                 break;
+            case StepKind::MaxPoolChain:
+                l.out = V(s.out, "pool out0", si);
+                l.b = V(s.b, "pool out1", si);
+                l.c = V(s.c, "pool out2", si);
+                l.a = V(s.a, "pool in", si);
+                l.kh = s.KH;
+                break;
+            case StepKind::DetectDecode: {
+                k::DetectDecodeArgs& d = l.decode;
+                d.x = V(s.a, "decode x", si);
+                d.anchors = V(s.b, "decode anchors", si);
+                d.two = V(s.c, "decode divisor", si);
+                d.strides = V(s.res, "decode strides", si);
+                d.out = V(s.out, "decode out", si);
+                const HostTensor& w = model_->weights.at(static_cast<size_t>(s.dfl_weight));
+                if (w.numel() != s.bins || w.dtype != kF32) throw std::runtime_error("DFL weight shape mismatch");
+                d.dfl_w = dev_->wptr.at(static_cast<size_t>(s.dfl_weight));
+                d.dfl_bias = 0.0f;
+                if (s.dfl_bias >= 0) {
+                    const HostTensor& bt = model_->weights.at(static_cast<size_t>(s.dfl_bias));
+                    if (bt.numel() != 1 || bt.dtype != kF32) throw std::runtime_error("DFL bias shape mismatch");
+                    d.dfl_bias = static_cast<const float*>(bt.data)[0];
+                }
+                d.bins = s.bins;
+                break;
+            }
             case StepKind::MaxPool:
             case StepKind::Resize:
             case StepKind::Softmax:
@@ -395,6 +421,8 @@ void Session::launch_one(const Launch& l, hipStream_t s) {
         case StepKind::MaxPool: k::launch_maxpool(l.out, l.a, l.kh, l.kw, l.sh, l.sw, l.ph, l.pw, s); break;
         case StepKind::Resize: k::launch_resize_nearest(l.out, l.a, s); break;
         case StepKind::Softmax: k::launch_softmax(l.out, l.a, l.axis, s); break;
+        case StepKind::MaxPoolChain: k::launch_maxpool_chain(l.out, l.b, l.c, l.a, l.kh, s); break;
+        case StepKind::DetectDecode: k::launch_detect_decode(l.decode, s); break;
     }
 }
 

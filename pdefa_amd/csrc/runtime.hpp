@@ -93,7 +93,8 @@ class Session {
         int tile = 0;
         bool vec = false;
         k::ConvDirectArgs direct;
-        k::View out, a, b;
+        k::View out, a, b, c;
+        k::DetectDecodeArgs decode;
         int elt = 0;
         float alpha = 0.0f;
         int kh = 0, kw = 0, sh = 1, sw = 1, ph = 0, pw = 0, axis = 0;
