@@ -38,6 +38,7 @@
 #include <stdexcept>
 #include <string>
 #include <type_traits>
+#include <utility>
 
 namespace pdefa {
 namespace k {
@@ -64,7 +65,17 @@ constexpr size_t lds_bytes() {
 
 }  // namespace
 
-template <int BM, int BN, int WM, int WN, int KG, bool VEC>
+template <int... J, typename F>
+__device__ __forceinline__ void static_for_impl(std::integer_sequence<int, J...>, F&& f) {
+    (f(std::integral_constant<int, J>{}), ...);
+}
+// f(integral_constant<int, j>) for j = 0 .. N-1, unrolled at compile time.
+template <int N, typename F>
+__device__ __forceinline__ void static_for(F&& f) {
+    static_for_impl(std::make_integer_sequence<int, N>{}, f);
+}
+
+template <int BM, int BN, int WM, int WN, int KG, int PF, bool VEC>
 __global__ __launch_bounds__(256) void conv_mfma_kernel(ConvArgs a) {
     constexpr int WAVES_M = BM / WM;
     constexpr int WAVES_N = BN / WN;
@@ -191,7 +202,12 @@ __global__ __launch_bounds__(256) void conv_mfma_kernel(ConvArgs a) {
         kh = tap / a.KW;
         kw = tap - kh * a.KW;
     }
-    const bool cin_ge_bkt = a.Cin >= BKT;  // then a step advance wraps Cin at most once
+    // Quotients of small non-negative ints by Cin and KW as (q + 0.5) * (1/d)
+    // in fp32: the relative error stays below 2^-23 while the true quotient is
+    // at least 0.5/d from an integer for q < 2^22, so truncation is exact.
+    // Branch-free, so a pipeline iteration stays one basic block.
+    const float inv_cin = 1.0f / static_cast<float>(a.Cin);
+    const float inv_kw = 1.0f / static_cast<float>(a.KW);
 
     // B rows of this lane: packed block row of output channel n0 + r0 + ROW_STEP*i
     // (clamped to the last packed block; such columns are never stored).
@@ -204,9 +220,9 @@ __global__ __launch_bounds__(256) void conv_mfma_kernel(ConvArgs a) {
         brow[i] = a.wpk + static_cast<int64_t>(nb) * a.ktiles * (kConvBN * BK) + (co % kConvBN) * BK + cc * 4;
     }
 
-    floatx4 areg[2][A_ROWS];
-    floatx4 breg[2][B_ROWS];
-    unsigned amask[2] = {0u, 0u};
+    floatx4 areg[PF][A_ROWS];
+    floatx4 breg[PF][B_ROWS];
+    unsigned amask[PF];
 
     auto load_step = [&](int kb0, floatx4* ar, floatx4* br, unsigned& mask) {
         unsigned mk = 0;
@@ -218,31 +234,21 @@ __global__ __launch_bounds__(256) void conv_mfma_kernel(ConvArgs a) {
             for (int r = 0; r < A_ROWS; ++r) {
                 const int hi = row_hi0[r] + dy;
                 const int wi = row_wi0[r] + dx;
-                const bool ok = row_ok[r] && tap_ok && static_cast<unsigned>(hi) < static_cast<unsigned>(a.H) &&
-                                static_cast<unsigned>(wi) < static_cast<unsigned>(a.W);
+                const bool ok = row_ok[r] & tap_ok & (static_cast<unsigned>(hi) < static_cast<unsigned>(a.H)) &
+                                (static_cast<unsigned>(wi) < static_cast<unsigned>(a.W));
                 const float* p = row_base[r] + (ok ? row_off0[r] + doff : 0);
                 ar[r] = *reinterpret_cast<const floatx4*>(p);
                 mk |= static_cast<unsigned>(ok) << r;
             }
             // advance this lane's chunk to the next step's k
             ci += BKT;
-            if (cin_ge_bkt) {
-                const bool wrap = ci >= a.Cin;
-                ci = wrap ? ci - a.Cin : ci;
-                tap += wrap;
-                kw += wrap;
-                const bool row = kw == a.KW;
-                kw = row ? 0 : kw;
-                kh += row;
-            } else {
-                const int w = ci / a.Cin;
-                ci -= w * a.Cin;
-                tap += w;
-                kw += w;
-                const int rw = kw / a.KW;
-                kw -= rw * a.KW;
-                kh += rw;
-            }
+            const int w = static_cast<int>((static_cast<float>(ci) + 0.5f) * inv_cin);
+            ci -= w * a.Cin;
+            tap += w;
+            kw += w;
+            const int rw = static_cast<int>((static_cast<float>(kw) + 0.5f) * inv_kw);
+            kw -= rw * a.KW;
+            kh += rw;
         } else {
 #pragma unroll
             for (int r = 0; r < A_ROWS; ++r) {
@@ -318,38 +324,39 @@ __global__ __launch_bounds__(256) void conv_mfma_kernel(ConvArgs a) {
         }
     };
 
-    // ---- software pipeline: step t is loaded at iteration t-2, stored to LDS
-    // at iteration t-1 and multiplied at iteration t.  Iterations that load
-    // run in the (2x unrolled) main loop; the last two iterations load
-    // nothing, so no load is left in flight into the epilogue.
+    // ---- software pipeline: step t is loaded at iteration t-PF into register
+    // stage t % PF, stored to LDS stage t % 2 at iteration t-1 and multiplied
+    // at iteration t.  The main loop (unrolled to a multiple of both stage
+    // counts) runs only iterations that load; the remaining ones are unrolled
+    // after it and load only while a step is left, so no load is in flight
+    // into the epilogue.
+    constexpr int U = PF % 2 == 0 ? PF : 2 * PF;
     load_step(kb_begin, areg[0], breg[0], amask[0]);
-    if (nk > 1) load_step(kb_begin + KG, areg[1], breg[1], amask[1]);
+    static_for<PF - 1>([&](auto jc) {
+        constexpr int J = decltype(jc)::value + 1;
+        if (J < nk) load_step(kb_begin + J * KG, areg[J], breg[J], amask[J]);
+    });
     store_step(0, areg[0], breg[0], amask[0]);
     __syncthreads();
-    auto iteration = [&](int it, auto stage, auto load) {
-        constexpr int S = decltype(stage)::value;  // it % 2
-        if (decltype(load)::value) load_step(kb_begin + (it + 2) * KG, areg[S], breg[S], amask[S]);
-        compute_step(S);
-        if (it + 1 < nk) store_step(S ^ 1, areg[S ^ 1], breg[S ^ 1], amask[S ^ 1]);
+    // In the main loop both the load and the store happen unconditionally, so
+    // each iteration is one basic block and the scheduler can interleave the
+    // loads' address arithmetic and the LDS stores with the MFMA chain.
+    auto iteration = [&](int it, auto jc, bool load, bool store) {
+        constexpr int J = decltype(jc)::value;
+        constexpr int R = J % PF;  // register stage of step it
+        constexpr int L = J % 2;   // LDS stage of step it
+        if (load) load_step(kb_begin + (it + PF) * KG, areg[R], breg[R], amask[R]);
+        compute_step(L);
+        if (store) store_step(L ^ 1, areg[(R + 1) % PF], breg[(R + 1) % PF], amask[(R + 1) % PF]);
         __syncthreads();
     };
-    using S0 = std::integral_constant<int, 0>;
-    using S1 = std::integral_constant<int, 1>;
-    using LD = std::true_type;
-    using NL = std::false_type;
     int it = 0;
-    for (; it + 3 < nk; it += 2) {
-        iteration(it, S0{}, LD{});
-        iteration(it + 1, S1{}, LD{});
-    }
-    if (it + 2 < nk) iteration(it++, S0{}, LD{});
-    if ((it & 1) == 0) {
-        if (it < nk) iteration(it, S0{}, NL{});
-        if (it + 1 < nk) iteration(it + 1, S1{}, NL{});
-    } else {
-        if (it < nk) iteration(it, S1{}, NL{});
-        if (it + 1 < nk) iteration(it + 1, S0{}, NL{});
-    }
+    for (; it + U + PF <= nk; it += U)
+        static_for<U>([&](auto jc) { iteration(it + decltype(jc)::value, jc, true, true); });
+    static_for<U + PF - 1>([&](auto jc) {
+        constexpr int J = decltype(jc)::value;
+        if (it + J < nk) iteration(it + J, jc, it + J + PF < nk, it + J + 1 < nk);
+    });
 
     // ---- output.  The row table was written before the prologue barrier
     // (every split has at least one step, checked by the launcher).  A tile
@@ -504,7 +511,7 @@ constexpr ConvTileShape kShapes[kNumConvTiles] = {
 constexpr const char* kNames[kNumConvTiles] = {"128x128", "128x64",  "64x128",  "64x64",
                                                "128x32",  "64x32k2", "32x64k2", "32x32k4"};
 
-template <int BM, int BN, int WM, int WN, int KG, bool VEC>
+template <int BM, int BN, int WM, int WN, int KG, int PF, bool VEC>
 void launch_one(const ConvArgs& a, dim3 grid, hipStream_t s) {
     constexpr size_t bytes = lds_bytes<BM, BN, KG>();
     static_assert(lds_stage_bytes<BM, BN, KG>() >= sizeof(float) * KG * BM * BN,
@@ -512,18 +519,20 @@ void launch_one(const ConvArgs& a, dim3 grid, hipStream_t s) {
     static std::once_flag once;
     std::call_once(once, [] {
         if (bytes > 65536)
-            (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&conv_mfma_kernel<BM, BN, WM, WN, KG, VEC>),
+            (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&conv_mfma_kernel<BM, BN, WM, WN, KG, PF, VEC>),
                                       hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(bytes));
     });
-    hipLaunchKernelGGL((conv_mfma_kernel<BM, BN, WM, WN, KG, VEC>), grid, dim3(256), bytes, s, a);
+    hipLaunchKernelGGL((conv_mfma_kernel<BM, BN, WM, WN, KG, PF, VEC>), grid, dim3(256), bytes, s, a);
 }
+
+constexpr int kPrefetch = 2;  // register stages: loads run two steps ahead
 
 template <int BM, int BN, int WM, int WN, int KG>
 void launch_tile(const ConvArgs& a, bool vec, dim3 grid, hipStream_t s) {
     if (vec)
-        launch_one<BM, BN, WM, WN, KG, true>(a, grid, s);
+        launch_one<BM, BN, WM, WN, KG, kPrefetch, true>(a, grid, s);
     else
-        launch_one<BM, BN, WM, WN, KG, false>(a, grid, s);
+        launch_one<BM, BN, WM, WN, KG, kPrefetch, false>(a, grid, s);
 }
 
 void fail(const std::string& m) { throw std::runtime_error("conv_mfma: " + m); }
