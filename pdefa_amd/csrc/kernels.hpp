@@ -36,8 +36,8 @@ enum Act : int32_t {
     kActSiluWinogradForm = 6,
 };
 
-// Implicit-GEMM convolution tile configurations.  A workgroup is 4 waves and
-// computes a BM x BN output tile; each wave owns a WM x WN sub-tile of 32x32
+// Implicit-GEMM convolution tile configurations.  A workgroup is 4 or 8 waves
+// and computes a BM x BN output tile; each wave owns a WM x WN sub-tile of 32x32
 // MFMA blocks and one of KG interleaved K slices.  KG > 1 splits K across the
 // waves of one workgroup (partial tiles summed through LDS in slice order),
 // which multiplies the workgroup count of small layers without any
@@ -54,7 +54,14 @@ enum ConvTile : int32_t {
     kTile64x32K2 = 5,   // 2x1 waves of 32x32, K split in 2
     kTile32x64K2 = 6,   // 1x2 waves of 32x32, K split in 2
     kTile32x32K4 = 7,   // 1 wave tile of 32x32, K split in 4
-    kNumConvTiles = 8,
+    // 8-wave workgroups (512 lanes, two waves per SIMD): one wave's LDS round
+    // trip and barrier wait overlap the other's MFMAs
+    kTile128x64W8 = 8,     // 4x2 waves of 32x32
+    kTile64x64K2W8 = 9,    // 2x2 waves of 32x32, K split in 2
+    kTile128x128W8 = 10,   // 2x4 waves of 64x32
+    kTile64x128W8 = 11,    // 2x4 waves of 32x32
+    kTile32x64K4W8 = 12,   // 1x2 waves of 32x32, K split in 4
+    kNumConvTiles = 13,
 };
 ConvTileShape conv_tile_shape(int tile);
 const char* conv_tile_name(int tile);

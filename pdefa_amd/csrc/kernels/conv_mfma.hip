@@ -2,7 +2,7 @@
 //
 // GEMM view of an NHWC convolution: C[m, co] = sum_k A[m, k] * B[k, co] with
 // m = (n, ho, wo), k = (kh, kw, ci) and A gathered on the fly from the input
-// (no im2col buffer).  One workgroup = 4 waves (256 lanes) computes a BM x BN
+// (no im2col buffer).  One workgroup = 4 or 8 waves computes a BM x BN
 // output tile.  Each wave owns a WM x WN sub-tile of 32x32 MFMA blocks and one
 // of KG K slices: a pipeline step advances K by BKT = 32*KG, slice g of the
 // step (32 k wide) feeding the waves of group g.  With KG > 1 the slices'
@@ -75,16 +75,22 @@ __device__ __forceinline__ void static_for(F&& f) {
     static_for_impl(std::make_integer_sequence<int, N>{}, f);
 }
 
+template <int BM, int BN, int WM, int WN, int KG>
+constexpr int tile_threads() {
+    return 64 * (BM / WM) * (BN / WN) * KG;
+}
+
 template <int BM, int BN, int WM, int WN, int KG, int PF, bool VEC>
-__global__ __launch_bounds__(256) void conv_mfma_kernel(ConvArgs a) {
+__global__ __launch_bounds__((tile_threads<BM, BN, WM, WN, KG>())) void conv_mfma_kernel(ConvArgs a) {
     constexpr int WAVES_M = BM / WM;
     constexpr int WAVES_N = BN / WN;
-    static_assert(WAVES_M * WAVES_N * KG == 4, "4 waves per workgroup");
+    constexpr int NT = tile_threads<BM, BN, WM, WN, KG>();  // 256 or 512 lanes
+    static_assert(NT == 256 || NT == 512, "4 or 8 waves per workgroup");
     constexpr int TM = WM / 32;
     constexpr int TN = WN / 32;
     constexpr int BKT = BK * KG;            // K per pipeline step
     constexpr int CH = BKT / 4;             // float4 chunks per tile row per step
-    constexpr int ROW_STEP = 256 / CH;      // rows covered by one pass of 256 lanes
+    constexpr int ROW_STEP = NT / CH;       // rows covered by one pass of all lanes
     constexpr int A_ROWS = BM / ROW_STEP;   // A float4 loads per lane per step
     constexpr int B_ROWS = BN / ROW_STEP;   // B float4 loads per lane per step
     static_assert(WM % 32 == 0 && WN % 32 == 0 && BM % ROW_STEP == 0 && BN % ROW_STEP == 0, "tile");
@@ -427,8 +433,8 @@ __global__ __launch_bounds__(256) void conv_mfma_kernel(ConvArgs a) {
                         red[(wg * BM + row) * BN + col] = acc[tm][tn][e];
                     }
             __syncthreads();
-            constexpr int E = BM * BN / 256;
-            constexpr int RSTEP = 256 / BN;
+            constexpr int E = BM * BN / NT;
+            constexpr int RSTEP = NT / BN;
             const int col = tid % BN;
             const int co = n0 + col;
             const bool cok = co < a.Cout;
@@ -507,9 +513,12 @@ namespace {
 constexpr ConvTileShape kShapes[kNumConvTiles] = {
     {128, 128, 64, 64, 1}, {128, 64, 64, 32, 1}, {64, 128, 32, 64, 1}, {64, 64, 32, 32, 1},
     {128, 32, 32, 32, 1},  {64, 32, 32, 32, 2},  {32, 64, 32, 32, 2},  {32, 32, 32, 32, 4},
+    {128, 64, 32, 32, 1},  {64, 64, 32, 32, 2},  {128, 128, 64, 32, 1}, {64, 128, 32, 32, 1},
+    {32, 64, 32, 32, 4},
 };
-constexpr const char* kNames[kNumConvTiles] = {"128x128", "128x64",  "64x128",  "64x64",
-                                               "128x32",  "64x32k2", "32x64k2", "32x32k4"};
+constexpr const char* kNames[kNumConvTiles] = {"128x128",  "128x64",     "64x128",    "64x64",    "128x32",
+                                               "64x32k2",  "32x64k2",    "32x32k4",   "128x64w8", "64x64k2w8",
+                                               "128x128w8", "64x128w8", "32x64k4w8"};
 
 template <int BM, int BN, int WM, int WN, int KG, int PF, bool VEC>
 void launch_one(const ConvArgs& a, dim3 grid, hipStream_t s) {
@@ -522,7 +531,8 @@ void launch_one(const ConvArgs& a, dim3 grid, hipStream_t s) {
             (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&conv_mfma_kernel<BM, BN, WM, WN, KG, PF, VEC>),
                                       hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(bytes));
     });
-    hipLaunchKernelGGL((conv_mfma_kernel<BM, BN, WM, WN, KG, PF, VEC>), grid, dim3(256), bytes, s, a);
+    hipLaunchKernelGGL((conv_mfma_kernel<BM, BN, WM, WN, KG, PF, VEC>), grid,
+                       dim3(tile_threads<BM, BN, WM, WN, KG>()), bytes, s, a);
 }
 
 constexpr int kPrefetch = 2;  // register stages: loads run two steps ahead
@@ -562,7 +572,9 @@ ConvLaunchShape conv_select(int64_t M, int Cout, int K, bool allow_split) {
     constexpr double kKernelCycles = 10000.0;  // launch + completion of one kernel
     constexpr double kWgCycles = 1500.0;       // workgroup start-up (first loads)
     constexpr double kStepFloor = 2200.0;      // latency floor of one pipeline step
-    constexpr double kEff[kNumConvTiles] = {1.0, 0.8, 0.8, 0.85, 0.8, 0.75, 0.75, 0.7};
+    // 8-wave tiles stay out of the automatic choice until calibrated
+    constexpr double kEff[kNumConvTiles] = {1.0, 0.8, 0.8, 0.85, 0.8, 0.75, 0.75, 0.7,
+                                            0.01, 0.01, 0.01, 0.01, 0.01};
     const int ktiles = (K + BK - 1) / BK;
     ConvLaunchShape best;
     double best_cost = 1e300;
@@ -624,6 +636,11 @@ void launch_conv_mfma(const ConvArgs& a, int tile, bool vec, hipStream_t s) {
         case kTile64x32K2: launch_tile<64, 32, 32, 32, 2>(a, vec, grid, s); break;
         case kTile32x64K2: launch_tile<32, 64, 32, 32, 2>(a, vec, grid, s); break;
         case kTile32x32K4: launch_tile<32, 32, 32, 32, 4>(a, vec, grid, s); break;
+        case kTile128x64W8: launch_tile<128, 64, 32, 32, 1>(a, vec, grid, s); break;
+        case kTile64x64K2W8: launch_tile<64, 64, 32, 32, 2>(a, vec, grid, s); break;
+        case kTile128x128W8: launch_tile<128, 128, 64, 32, 1>(a, vec, grid, s); break;
+        case kTile64x128W8: launch_tile<64, 128, 32, 32, 1>(a, vec, grid, s); break;
+        case kTile32x64K4W8: launch_tile<32, 64, 32, 32, 4>(a, vec, grid, s); break;
     }
     if (a.splits > 1) {
         const int64_t total = M * a.Cout;

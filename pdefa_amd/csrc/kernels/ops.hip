@@ -9,6 +9,7 @@
 #include "act.hpp"
 
 #include <algorithm>
+#include <mutex>
 #include <stdexcept>
 #include <string>
 
@@ -298,40 +299,91 @@ void launch_softmax(const View& out, const View& in, int axis, hipStream_t s) {
                            axis, rows);
 }
 
-// SPPF: three chained k x k stride-1 same-padded max pools from one read of
-// the input window (radii r, 2r, 3r with r = k/2).  Channel fastest, so
-// channels-last views are read and written contiguously.
-template <typename I>
-__global__ __launch_bounds__(256) void maxpool_chain_kernel(IView<I> o0, IView<I> o1, IView<I> o2, IView<I> in, int r,
-                                                            I total) {
-    const I C = o0.dims[1], Ho = o0.dims[2], Wo = o0.dims[3];
-    const I H = in.dims[2], W = in.dims[3];
-    for (I i = blockIdx.x * static_cast<I>(blockDim.x) + threadIdx.x; i < total;
-         i += static_cast<I>(gridDim.x) * blockDim.x) {
-        I t = i;
-        const I c = t % C; t /= C;
-        const I w = t % Wo; t /= Wo;
-        const I h = t % Ho;
-        const I n = t / Ho;
-        const float* base = in.ptr + n * in.str[0] + c * in.str[1];
-        float m0 = -3.402823466e+38f, m1 = m0, m2 = m0;
-        for (int dy = -3 * r; dy <= 3 * r; ++dy) {
-            const I hi = h + dy;
-            if (hi < 0 || hi >= H) continue;
-            const int ay = dy < 0 ? -dy : dy;
-            for (int dx = -3 * r; dx <= 3 * r; ++dx) {
-                const I wi = w + dx;
-                if (wi < 0 || wi >= W) continue;
-                const int ax = dx < 0 ? -dx : dx;
-                const float v = base[hi * in.str[2] + wi * in.str[3]];
-                m2 = v > m2 ? v : m2;
-                if (ay <= 2 * r && ax <= 2 * r) m1 = v > m1 ? v : m1;
-                if (ay <= r && ax <= r) m0 = v > m0 ? v : m0;
+// SPPF: three chained k x k stride-1 same-padded max pools in one pass.  A
+// workgroup takes a T x T pixel tile of CB channels: it stages the tile plus
+// a 3r halo in LDS (outside the image: -FLT_MAX, so padding never wins), takes
+// the row maxima over radii r, 2r and 3r, then the column maxima of those:
+// the separable form of the square windows of sides 2r+1, 4r+1 and 6r+1.
+// Channel fastest, so channels-last views are read and written contiguously.
+constexpr int kPoolTile = 8;
+constexpr int kPoolCb = 16;
+constexpr int kPoolMaxR = 3;
+
+template <int r>
+__global__ __launch_bounds__(256) void maxpool_chain_kernel(IView<int32_t> o0, IView<int32_t> o1, IView<int32_t> o2,
+                                                            IView<int32_t> in, int tiles_w) {
+    constexpr int T = kPoolTile, CB = kPoolCb;
+    constexpr int R3 = 3 * r;
+    constexpr int RH = T + 2 * R3;  // staged rows and columns
+    constexpr int NL = (RH * RH * CB + 255) / 256;  // staged elements per lane
+    __shared__ float reg[RH * RH * CB];    // [RH][RH][CB]
+    __shared__ float hz[3 * RH * T * CB];  // [3][RH][T][CB]
+    const int C = o0.dims[1], H = in.dims[2], W = in.dims[3];
+    const int th = blockIdx.x / tiles_w, tw = blockIdx.x - th * tiles_w;
+    const int h0 = th * T, w0 = tw * T, c0 = blockIdx.y * CB, n = blockIdx.z;
+    const float* base = in.ptr + n * in.str[0];
+    // every lane's loads are issued before the first is waited for
+    float v[NL];
+#pragma unroll
+    for (int j = 0; j < NL; ++j) {
+        const int i = threadIdx.x + 256 * j;
+        const int c = i % CB, p = i / CB;
+        const int rx = p % RH, ry = p / RH;
+        const int h = h0 - R3 + ry, w = w0 - R3 + rx;
+        const bool ok = (i < RH * RH * CB) & (h >= 0) & (h < H) & (w >= 0) & (w < W) & (c0 + c < C);
+        const float x = base[ok ? (c0 + c) * in.str[1] + h * in.str[2] + w * in.str[3] : 0];
+        v[j] = ok ? x : -3.402823466e+38f;
+    }
+#pragma unroll
+    for (int j = 0; j < NL; ++j) {
+        const int i = threadIdx.x + 256 * j;
+        if (i < RH * RH * CB) reg[i] = v[j];
+    }
+    __syncthreads();
+    for (int i = threadIdx.x; i < RH * T * CB; i += 256) {
+        const int c = i % CB, p = i / CB;
+        const int tx = p % T, ry = p / T;
+        const float* row = reg + ry * RH * CB + c;
+        const int x = R3 + tx;
+        float m = row[x * CB];
+        float out[3];
+        int d = 1;
+#pragma unroll
+        for (int k = 0; k < 3; ++k) {
+            for (; d <= (k + 1) * r; ++d) {
+                const float a = row[(x - d) * CB], b = row[(x + d) * CB];
+                m = a > m ? a : m;
+                m = b > m ? b : m;
             }
+            out[k] = m;
         }
-        o0.ptr[n * o0.str[0] + c * o0.str[1] + h * o0.str[2] + w * o0.str[3]] = m0;
-        o1.ptr[n * o1.str[0] + c * o1.str[1] + h * o1.str[2] + w * o1.str[3]] = m1;
-        o2.ptr[n * o2.str[0] + c * o2.str[1] + h * o2.str[2] + w * o2.str[3]] = m2;
+#pragma unroll
+        for (int k = 0; k < 3; ++k) hz[((k * RH + ry) * T + tx) * CB + c] = out[k];
+    }
+    __syncthreads();
+    for (int i = threadIdx.x; i < T * T * CB; i += 256) {
+        const int c = i % CB, p = i / CB;
+        const int tx = p % T, ty = p / T;
+        const int h = h0 + ty, w = w0 + tx;
+        if (h >= H || w >= W || c0 + c >= C) continue;
+        const int y = R3 + ty;
+        float res[3];
+#pragma unroll
+        for (int k = 0; k < 3; ++k) {
+            const float* col = hz + (k * RH * T + tx) * CB + c;  // row stride T*CB
+            const int rad = (k + 1) * r;
+            float m = col[y * T * CB];
+            for (int d = 1; d <= rad; ++d) {
+                const float a = col[(y - d) * T * CB], b = col[(y + d) * T * CB];
+                m = a > m ? a : m;
+                m = b > m ? b : m;
+            }
+            res[k] = m;
+        }
+        const int cc = c0 + c;
+        o0.ptr[n * o0.str[0] + cc * o0.str[1] + h * o0.str[2] + w * o0.str[3]] = res[0];
+        o1.ptr[n * o1.str[0] + cc * o1.str[1] + h * o1.str[2] + w * o1.str[3]] = res[1];
+        o2.ptr[n * o2.str[0] + cc * o2.str[1] + h * o2.str[2] + w * o2.str[3]] = res[2];
     }
 }
 
@@ -343,22 +395,37 @@ void launch_maxpool_chain(const View& out0, const View& out1, const View& out2, 
     check_view(in, "maxpool_chain in");
     if (out0.rank != 4 || out1.rank != 4 || out2.rank != 4 || in.rank != 4)
         throw std::runtime_error("maxpool_chain: rank 4 views expected");
-    if (k < 1 || k % 2 == 0) throw std::runtime_error("maxpool_chain: odd kernel expected");
+    if (k < 1 || k % 2 == 0 || k / 2 > kPoolMaxR) throw std::runtime_error("maxpool_chain: odd kernel <= 7 expected");
     for (int d = 0; d < 4; ++d)
         if (out0.dims[d] != in.dims[d] || out1.dims[d] != in.dims[d] || out2.dims[d] != in.dims[d])
             throw std::runtime_error("maxpool_chain: same-size outputs expected");
-    const int64_t total = numel(out0);
-    if (total == 0) return;
+    if (numel(out0) == 0) return;
     if (!(fits_i32(out0) && fits_i32(out1) && fits_i32(out2) && fits_i32(in)))
         throw std::runtime_error("maxpool_chain: views exceed int32 indexing");
-    hipLaunchKernelGGL(maxpool_chain_kernel<int32_t>, dim3(grid_for(total)), dim3(256), 0, s, iview<int32_t>(out0),
-                       iview<int32_t>(out1), iview<int32_t>(out2), iview<int32_t>(in), k / 2,
-                       static_cast<int32_t>(total));
+    const int64_t N = in.dims[0], C = in.dims[1], H = in.dims[2], W = in.dims[3];
+    const int64_t tiles_h = (H + kPoolTile - 1) / kPoolTile, tiles_w = (W + kPoolTile - 1) / kPoolTile;
+    const int64_t cblocks = (C + kPoolCb - 1) / kPoolCb;
+    if (tiles_h * tiles_w > 0x7fffffff || cblocks > 65535 || N > 65535)
+        throw std::runtime_error("maxpool_chain: grid too large");
+    const dim3 grid(static_cast<unsigned>(tiles_h * tiles_w), static_cast<unsigned>(cblocks), static_cast<unsigned>(N));
+    const auto o0 = iview<int32_t>(out0), o1 = iview<int32_t>(out1), o2 = iview<int32_t>(out2);
+    const auto x = iview<int32_t>(in);
+    const int tw = static_cast<int>(tiles_w);
+    switch (k / 2) {
+        case 0: hipLaunchKernelGGL(maxpool_chain_kernel<0>, grid, dim3(256), 0, s, o0, o1, o2, x, tw); break;
+        case 1: hipLaunchKernelGGL(maxpool_chain_kernel<1>, grid, dim3(256), 0, s, o0, o1, o2, x, tw); break;
+        case 2: hipLaunchKernelGGL(maxpool_chain_kernel<2>, grid, dim3(256), 0, s, o0, o1, o2, x, tw); break;
+        default: hipLaunchKernelGGL(maxpool_chain_kernel<3>, grid, dim3(256), 0, s, o0, o1, o2, x, tw); break;
+    }
 }
 
 // One lane per (n, anchor); see kernels.hpp for the arithmetic.  The softmax
 // matches softmax_kernel (max, exp(x - max), sum in bin order, * 1/sum) and
-// the expectation matches the direct conv's accumulation order.
+// the expectation matches the direct conv's accumulation order.  R > 0: the
+// bin count is R and each side's R bins are contiguous and 16-byte aligned
+// (the Detect head's [anchor][144] rows), loaded as float4 into registers;
+// R == 0: any bin count and strides.
+template <int R>
 __global__ __launch_bounds__(256) void detect_decode_kernel(DetectDecodeArgs a, int32_t N, int32_t A) {
     const int32_t i = blockIdx.x * 256 + threadIdx.x;
     if (i >= N * A) return;
@@ -370,17 +437,43 @@ __global__ __launch_bounds__(256) void detect_decode_kernel(DetectDecodeArgs a, 
 #pragma unroll
     for (int side = 0; side < 4; ++side) {
         const float* xs = x.ptr + static_cast<int32_t>(n * x.str[0] + side * x.str[2] + an * x.str[3]);
-        float mx = -1e30f;
-        for (int b = 0; b < a.bins; ++b) {
-            const float v = xs[b * xs1];
-            mx = v > mx ? v : mx;
+        if constexpr (R > 0) {
+            float v[R];
+#pragma unroll
+            for (int q = 0; q < R / 4; ++q) {
+                const float4 t = reinterpret_cast<const float4*>(xs)[q];
+                v[4 * q] = t.x;
+                v[4 * q + 1] = t.y;
+                v[4 * q + 2] = t.z;
+                v[4 * q + 3] = t.w;
+            }
+            float mx = -1e30f;
+#pragma unroll
+            for (int b = 0; b < R; ++b) mx = v[b] > mx ? v[b] : mx;
+            float sum = 0.0f;
+#pragma unroll
+            for (int b = 0; b < R; ++b) {
+                v[b] = expf(v[b] - mx);
+                sum += v[b];
+            }
+            const float inv = sum > 0.0f ? 1.0f / sum : 0.0f;
+            float acc = 0.0f;
+#pragma unroll
+            for (int b = 0; b < R; ++b) acc = fmaf(v[b] * inv, a.dfl_w[b], acc);
+            d[side] = acc + a.dfl_bias;
+        } else {
+            float mx = -1e30f;
+            for (int b = 0; b < a.bins; ++b) {
+                const float v = xs[b * xs1];
+                mx = v > mx ? v : mx;
+            }
+            float sum = 0.0f;
+            for (int b = 0; b < a.bins; ++b) sum += expf(xs[b * xs1] - mx);
+            const float inv = sum > 0.0f ? 1.0f / sum : 0.0f;
+            float acc = 0.0f;
+            for (int b = 0; b < a.bins; ++b) acc = fmaf(expf(xs[b * xs1] - mx) * inv, a.dfl_w[b], acc);
+            d[side] = acc + a.dfl_bias;
         }
-        float sum = 0.0f;
-        for (int b = 0; b < a.bins; ++b) sum += expf(xs[b * xs1] - mx);
-        const float inv = sum > 0.0f ? 1.0f / sum : 0.0f;
-        float acc = 0.0f;
-        for (int b = 0; b < a.bins; ++b) acc = fmaf(expf(xs[b * xs1] - mx) * inv, a.dfl_w[b], acc);
-        d[side] = acc + a.dfl_bias;
     }
     auto at = [&](const View& v, int c) {
         return v.ptr[n * v.str[0] + c * v.str[1] + static_cast<int64_t>(an) * v.str[2]];
@@ -409,8 +502,13 @@ void launch_detect_decode(const DetectDecodeArgs& a, hipStream_t s) {
         throw std::runtime_error("decode: channel counts");
     if (N * A >= (int64_t{1} << 31) || !fits_i32(a.x)) throw std::runtime_error("decode: views exceed int32 indexing");
     if (N * A == 0) return;
-    hipLaunchKernelGGL(detect_decode_kernel, dim3(static_cast<unsigned>((N * A + 255) / 256)), dim3(256), 0, s, a,
-                       static_cast<int32_t>(N), static_cast<int32_t>(A));
+    const dim3 grid(static_cast<unsigned>((N * A + 255) / 256));
+    const bool vec16 = a.bins == 16 && a.x.str[1] == 1 && reinterpret_cast<uintptr_t>(a.x.ptr) % 16 == 0 &&
+                       (N == 1 || a.x.str[0] % 4 == 0) && a.x.str[2] % 4 == 0 && (A == 1 || a.x.str[3] % 4 == 0);
+    if (vec16)
+        hipLaunchKernelGGL(detect_decode_kernel<16>, grid, dim3(256), 0, s, a, static_cast<int32_t>(N), static_cast<int32_t>(A));
+    else
+        hipLaunchKernelGGL(detect_decode_kernel<0>, grid, dim3(256), 0, s, a, static_cast<int32_t>(N), static_cast<int32_t>(A));
 }
 
 // Direct convolution: lane = one output pixel, CB output channels of the
@@ -420,7 +518,7 @@ void launch_detect_decode(const DetectDecodeArgs& a, hipStream_t s) {
 // CB FMAs.  The 256 x CB result tile goes through LDS and is stored with
 // consecutive lanes on consecutive channels, so channels-last outputs are
 // written in contiguous runs.  Index math is int32 within one image.
-template <int CB>
+template <int CB, int KS>
 __global__ __launch_bounds__(256) void conv_direct_kernel(ConvDirectArgs a, int P) {
     __shared__ float tile[256 * (CB + 1)];
     const int p0 = blockIdx.x * 256;
@@ -443,6 +541,34 @@ __global__ __launch_bounds__(256) void conv_direct_kernel(ConvDirectArgs a, int 
         const int xsw = static_cast<int>(a.x.str[3]);
         const int hi0 = ho * a.sh - a.ph, wi0 = wo * a.sw - a.pw;
         const float* wk = a.wpk + static_cast<int64_t>(cob) * K * CB;
+        if constexpr (KS > 0) {
+            // KS x KS taps: tap offsets and masks once, then per input channel
+            // all KS*KS loads in flight before the FMAs
+            int off[KS * KS];
+            bool tok[KS * KS];
+#pragma unroll
+            for (int kh = 0; kh < KS; ++kh)
+#pragma unroll
+                for (int kw = 0; kw < KS; ++kw) {
+                    const int hi = hi0 + kh * a.dh, wi = wi0 + kw * a.dw;
+                    tok[kh * KS + kw] = (static_cast<unsigned>(hi) < static_cast<unsigned>(H)) &
+                                        (static_cast<unsigned>(wi) < static_cast<unsigned>(W));
+                    off[kh * KS + kw] = tok[kh * KS + kw] ? hi * xsh + wi * xsw : 0;
+                }
+            for (int c = 0; c < Ci; ++c, wk += KS * KS * CB) {
+                const float* xc = xb + c * xsc;
+                float xv[KS * KS];
+#pragma unroll
+                for (int t = 0; t < KS * KS; ++t) {
+                    const float v = xc[off[t]];
+                    xv[t] = tok[t] ? v : 0.0f;
+                }
+#pragma unroll
+                for (int t = 0; t < KS * KS; ++t)
+#pragma unroll
+                    for (int j = 0; j < CB; ++j) acc[j] += xv[t] * wk[t * CB + j];
+            }
+        } else
         for (int c = 0; c < Ci; ++c) {
             for (int kh = 0; kh < a.KH; ++kh) {
                 const int hi = hi0 + kh * a.dh;
@@ -498,11 +624,18 @@ void launch_conv_direct(const ConvDirectArgs& a, hipStream_t s) {
         throw std::runtime_error("conv_direct: shape exceeds int32 indexing");
     const dim3 grid(static_cast<unsigned>((P + 255) / 256), static_cast<unsigned>((a.y.dims[1] + cb - 1) / cb));
     const int Pi = static_cast<int>(P);
+    const bool k3 = a.KH == 3 && a.KW == 3;
     switch (cb) {
-        case 16: hipLaunchKernelGGL(conv_direct_kernel<16>, grid, dim3(256), 0, s, a, Pi); break;
-        case 32: hipLaunchKernelGGL(conv_direct_kernel<32>, grid, dim3(256), 0, s, a, Pi); break;
-        case 48: hipLaunchKernelGGL(conv_direct_kernel<48>, grid, dim3(256), 0, s, a, Pi); break;
-        default: hipLaunchKernelGGL(conv_direct_kernel<64>, grid, dim3(256), 0, s, a, Pi); break;
+        case 16:
+            if (k3) hipLaunchKernelGGL((conv_direct_kernel<16, 3>), grid, dim3(256), 0, s, a, Pi);
+            else hipLaunchKernelGGL((conv_direct_kernel<16, 0>), grid, dim3(256), 0, s, a, Pi);
+            break;
+        case 32:
+            if (k3) hipLaunchKernelGGL((conv_direct_kernel<32, 3>), grid, dim3(256), 0, s, a, Pi);
+            else hipLaunchKernelGGL((conv_direct_kernel<32, 0>), grid, dim3(256), 0, s, a, Pi);
+            break;
+        case 48: hipLaunchKernelGGL((conv_direct_kernel<48, 0>), grid, dim3(256), 0, s, a, Pi); break;
+        default: hipLaunchKernelGGL((conv_direct_kernel<64, 0>), grid, dim3(256), 0, s, a, Pi); break;
     }
 }
 

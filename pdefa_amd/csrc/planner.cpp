@@ -989,7 +989,7 @@ class Planner {
         const Step& p0 = st[i];
         for (size_t j = 0; j < 3; ++j) {
             const Step& p = st[i + j];
-            if (p.kind != StepKind::MaxPool || p.KH != p0.KH || p.KW != p0.KH || p.KH % 2 == 0 || p.sh != 1 ||
+            if (p.kind != StepKind::MaxPool || p.KH != p0.KH || p.KW != p0.KH || p.KH % 2 == 0 || p.KH > 7 || p.sh != 1 ||
                 p.sw != 1 || p.ph != p0.KH / 2 || p.pw != p0.KH / 2)
                 return false;
             if (p.out.rank != 4 || dims_of(p.out) != dims_of(p0.a)) return false;

@@ -267,6 +267,21 @@ def build_single_conv(cin: int, cout: int, k: int, stride: int, hw: int, seed: i
     return b.model([1, cin, hw, hw], [1, cout, ho, ho], [y]), x
 
 
+def build_pool_chain(n: int, c: int, h: int, w: int, k: int, seed: int = 5) -> Tuple[EngineModel, np.ndarray]:
+    """SPPF's pooling part on its own: three chained MaxPool(k, stride 1,
+    pad k//2) and the channel Concat of the input and the three results.
+    Returns the model and its seeded input x ~ N(0,1) of shape [n,c,h,w]."""
+    rng = np.random.default_rng(seed)
+    x = rng.standard_normal((n, c, h, w), dtype=np.float32)
+    b = GraphBuilder()
+    ys = [-1]
+    for i in range(3):
+        ys.append(b.node("MaxPool", f"/m/MaxPool_{i}", [ys[-1]], kernel_h=k, kernel_w=k, stride_h=1, stride_w=1,
+                         pad_h=k // 2, pad_w=k // 2))
+    cat = b.node("Concat", "/Concat", ys, axis=1)
+    return b.model([n, c, h, w], [n, 4 * c, h, w], [cat]), x
+
+
 def build_tiny(seed: int = 3) -> EngineModel:
     """A small stand-in for the reference tests' tiny.engine (a 64x64
     Conv -> AvgPool -> Linear to 4 outputs, pdefa/tests/README.md:13-39, not

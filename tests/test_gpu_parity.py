@@ -6,6 +6,7 @@ and the post-NMS detection lists are identical (same anchors, classes and
 order; coordinates and scores within the same tolerance).
 """
 import os
+import re
 
 import numpy as np
 import pytest
@@ -78,7 +79,8 @@ def test_single_conv(tmp_path, cin, cout, k, s, hw):
     assert err < 1e-4, err
 
 
-TILES = ["128x128", "128x64", "64x128", "64x64", "128x32", "64x32k2", "32x64k2", "32x32k4"]
+TILES = ["128x128", "128x64", "64x128", "64x64", "128x32", "64x32k2", "32x64k2", "32x32k4",
+         "128x64w8", "64x64k2w8", "128x128w8", "64x128w8", "32x64k4w8"]
 
 
 @pytest.mark.parametrize("tile", TILES)
@@ -101,12 +103,31 @@ def test_conv_every_tile(tmp_path, monkeypatch, tile, splits, cin, cout, k, s, h
     finally:
         eng.close()
     assert f"tile={tile}," in plan
-    kg = 4 if tile.endswith("k4") else (2 if tile.endswith("k2") else 1)
+    kslices = re.search(r"k(\d)", tile)
+    kg = int(kslices.group(1)) if kslices else 1
     steps = -(-(-(-cin * k * k // 32)) // kg)
     if splits > 1 and steps > 1:
         assert "splits=1," not in plan
     want = graph_ref.run_graph(model, [x], compat_silu=False)[0]
     assert assert_close(got, want, "conv") < 1e-4
+
+
+@pytest.mark.parametrize("n,c,h,w,k", [(2, 37, 13, 19, 5), (1, 16, 8, 8, 3), (2, 20, 23, 9, 7), (1, 128, 20, 20, 5)])
+def test_pool_chain(tmp_path, n, c, h, w, k):
+    """Three chained same-size max pools (SPPF) run as one fused step."""
+    print(f"[case] pool chain n={n} c={c} h={h} w={w} k={k}", flush=True)
+    model, x = ys.build_pool_chain(n, c, h, w, k)
+    path = str(tmp_path / "pool.engine")
+    ys.save(model, path)
+    eng = native.Engine(path)
+    try:
+        got = eng.run(x)[0]
+        plan = eng.plan()
+    finally:
+        eng.close()
+    assert " maxpool_chain " in plan
+    want = graph_ref.run_graph(model, [x])[0]
+    np.testing.assert_array_equal(got, want)
 
 
 def test_single_conv_no_act(tmp_path):
