@@ -25,6 +25,7 @@ SOURCES = [
     "model.cpp",
     "planner.cpp",
     "runtime.cpp",
+    "conv_tune.cpp",
     "engine_api.cpp",
     "host_ops.cpp",
     "pdefa_api.cpp",

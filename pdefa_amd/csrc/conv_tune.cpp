@@ -1,0 +1,160 @@
+#include "conv_tune.hpp"
+
+#include <algorithm>
+#include <array>
+#include <map>
+#include <mutex>
+#include <stdexcept>
+
+#include "runtime.hpp"
+
+namespace pdefa {
+
+namespace {
+
+constexpr size_t kMaxCandidates = 12;          // the cost model's best ones are timed
+constexpr int64_t kMaxWorkspaceBytes = 256LL << 20;  // split-K partials of one candidate
+constexpr double kKeepModelChoice = 0.97;      // another shape must beat the model's by 3%
+
+using Key = std::array<int32_t, 20>;
+
+std::mutex g_mu;
+std::map<Key, k::ConvLaunchShape> g_cache;
+
+Key make_key(const ConvQuery& q, int device) {
+    return {device, q.N,  q.H,  q.W,  q.Cin, q.Ho, q.Wo, q.Cout, q.KH, q.KW,
+            q.sh,   q.sw, q.ph, q.pw, q.dh,  q.dw, q.act, q.has_res ? 1 : 0, q.vec ? 1 : 0, 0};
+}
+
+struct DeviceBuffer {
+    float* p = nullptr;
+    explicit DeviceBuffer(int64_t elems) { PDEFA_HIP(hipMalloc(&p, static_cast<size_t>(std::max<int64_t>(elems, 1)) * 4)); }
+    ~DeviceBuffer() {
+        if (p) (void)hipFree(p);
+    }
+    DeviceBuffer(const DeviceBuffer&) = delete;
+    DeviceBuffer& operator=(const DeviceBuffer&) = delete;
+};
+
+struct Events {
+    hipEvent_t a = nullptr, b = nullptr;
+    Events() {
+        PDEFA_HIP(hipEventCreate(&a));
+        PDEFA_HIP(hipEventCreate(&b));
+    }
+    ~Events() {
+        (void)hipEventDestroy(a);
+        (void)hipEventDestroy(b);
+    }
+};
+
+// Average ms of `reps` back-to-back launches (after one untimed launch).
+double time_launch(const k::ConvArgs& a, int tile, bool vec, hipStream_t s, Events& ev, int reps) {
+    k::launch_conv_mfma(a, tile, vec, s);
+    PDEFA_HIP(hipEventRecord(ev.a, s));
+    for (int i = 0; i < reps; ++i) k::launch_conv_mfma(a, tile, vec, s);
+    PDEFA_HIP(hipEventRecord(ev.b, s));
+    PDEFA_HIP(hipEventSynchronize(ev.b));
+    float ms = 0.0f;
+    PDEFA_HIP(hipEventElapsedTime(&ms, ev.a, ev.b));
+    return static_cast<double>(ms) / reps;
+}
+
+}  // namespace
+
+k::ConvLaunchShape tune_conv(const ConvQuery& q, hipStream_t s) {
+    int device = 0;
+    PDEFA_HIP(hipGetDevice(&device));
+    const Key key = make_key(q, device);
+    std::lock_guard<std::mutex> lock(g_mu);
+    if (auto it = g_cache.find(key); it != g_cache.end()) return it->second;
+
+    const int64_t M = static_cast<int64_t>(q.N) * q.Ho * q.Wo;
+    const int K = q.KH * q.KW * q.Cin;
+    std::vector<k::ConvLaunchShape> cands = k::conv_candidates(M, q.Cout, K, true);
+    if (cands.size() > kMaxCandidates) cands.resize(kMaxCandidates);
+    const int64_t out_elems = M * q.Cout;
+    int max_splits = 1;
+    std::vector<k::ConvLaunchShape> usable;
+    for (const auto& c : cands) {
+        if (c.splits > 1 && static_cast<int64_t>(c.splits) * out_elems * 4 > kMaxWorkspaceBytes) continue;
+        usable.push_back(c);
+        max_splits = std::max(max_splits, c.splits);
+    }
+    k::ConvLaunchShape best = cands.front();
+    if (usable.size() > 1) {
+        // Scratch tensors of the layer's shape, dense channels-last; values
+        // do not affect timing (zeros).  The residual, when the layer has one,
+        // reads the output tensor itself: each element is read and then
+        // written by the same lane.
+        const int64_t x_elems = static_cast<int64_t>(q.N) * q.H * q.W * q.Cin;
+        DeviceBuffer x(x_elems), y(out_elems), w(k::packed_weight_elems(q.Cout, K)), bias(q.Cout),
+            ws(max_splits > 1 ? static_cast<int64_t>(max_splits) * out_elems : 1);
+        PDEFA_HIP(hipMemsetAsync(x.p, 0, static_cast<size_t>(x_elems) * 4, s));
+        PDEFA_HIP(hipMemsetAsync(w.p, 0, static_cast<size_t>(k::packed_weight_elems(q.Cout, K)) * 4, s));
+        PDEFA_HIP(hipMemsetAsync(bias.p, 0, static_cast<size_t>(q.Cout) * 4, s));
+        PDEFA_HIP(hipMemsetAsync(y.p, 0, static_cast<size_t>(out_elems) * 4, s));
+        k::ConvArgs a;
+        a.x = x.p;
+        a.N = q.N;
+        a.H = q.H;
+        a.W = q.W;
+        a.Cin = q.Cin;
+        a.x_sw = q.Cin;
+        a.x_sh = static_cast<int64_t>(q.W) * q.Cin;
+        a.x_sn = static_cast<int64_t>(q.H) * q.W * q.Cin;
+        a.y = y.p;
+        a.Ho = q.Ho;
+        a.Wo = q.Wo;
+        a.Cout = q.Cout;
+        a.y_sw = q.Cout;
+        a.y_sh = static_cast<int64_t>(q.Wo) * q.Cout;
+        a.y_sn = static_cast<int64_t>(q.Ho) * q.Wo * q.Cout;
+        if (q.has_res) {
+            a.res = y.p;
+            a.r_sw = a.y_sw;
+            a.r_sh = a.y_sh;
+            a.r_sn = a.y_sn;
+        }
+        a.wpk = w.p;
+        a.bias = bias.p;
+        a.KH = q.KH;
+        a.KW = q.KW;
+        a.sh = q.sh;
+        a.sw = q.sw;
+        a.ph = q.ph;
+        a.pw = q.pw;
+        a.dh = q.dh;
+        a.dw = q.dw;
+        a.K = K;
+        a.ktiles = (K + k::kConvBK - 1) / k::kConvBK;
+        a.act = q.act;
+        a.ws = ws.p;
+        Events ev;
+        // repetitions: about 100 us of timed work per candidate, at least 3
+        a.splits = usable.front().splits;
+        a.kt_per_split = usable.front().kt_per_split;
+        const double first = time_launch(a, usable.front().tile, q.vec, s, ev, 1);
+        const int reps = std::max(3, std::min(20, static_cast<int>(0.1 / std::max(first, 1e-3))));
+        double best_ms = 0.0;
+        for (size_t i = 0; i < usable.size(); ++i) {
+            a.splits = usable[i].splits;
+            a.kt_per_split = usable[i].kt_per_split;
+            const double ms = time_launch(a, usable[i].tile, q.vec, s, ev, reps);
+            if (i == 0 || ms < best_ms * kKeepModelChoice) {
+                best_ms = ms;
+                best = usable[i];
+            }
+        }
+        PDEFA_HIP(hipStreamSynchronize(s));
+    }
+    g_cache.emplace(key, best);
+    return best;
+}
+
+size_t conv_tune_cache_size() {
+    std::lock_guard<std::mutex> lock(g_mu);
+    return g_cache.size();
+}
+
+}  // namespace pdefa

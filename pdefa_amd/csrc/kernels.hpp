@@ -6,6 +6,7 @@
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
+#include <vector>
 
 namespace pdefa {
 namespace k {
@@ -105,6 +106,9 @@ struct ConvLaunchShape {
     int kt_per_split = 0;
 };
 ConvLaunchShape conv_select(int64_t M, int Cout, int K, bool allow_split);
+// Every tile with one split and with its best split count, cheapest predicted
+// first (conv_select is the first); the candidates a measured choice times.
+std::vector<ConvLaunchShape> conv_candidates(int64_t M, int Cout, int K, bool allow_split);
 
 // Host-side checks + launch.  vec selects 16-byte input loads (requires
 // Cin % 4 == 0 and 16-byte aligned pixel rows).

@@ -39,6 +39,7 @@
 #include <string>
 #include <type_traits>
 #include <utility>
+#include <vector>
 
 namespace pdefa {
 namespace k {
@@ -567,39 +568,62 @@ int64_t packed_weight_elems(int Cout, int K) {
 // trip and barrier); add workgroup start-up, a fixed per-kernel cost and, for
 // split-K, the reduce kernel and the partial traffic.  Tile efficiencies and
 // the floor are calibrated on YOLOv8 layer shapes.
-ConvLaunchShape conv_select(int64_t M, int Cout, int K, bool allow_split) {
+namespace {
+
+// Predicted cycles of one (tile, splits) launch shape.
+double conv_cost(int64_t M, int Cout, int ktiles, int t, int splits, int steps) {
     constexpr double kCus = 256.0;
     constexpr double kKernelCycles = 10000.0;  // launch + completion of one kernel
     constexpr double kWgCycles = 1500.0;       // workgroup start-up (first loads)
     constexpr double kStepFloor = 2200.0;      // latency floor of one pipeline step
-    // 8-wave tiles stay out of the automatic choice until calibrated
     constexpr double kEff[kNumConvTiles] = {1.0, 0.8, 0.8, 0.85, 0.8, 0.75, 0.75, 0.7,
-                                            0.01, 0.01, 0.01, 0.01, 0.01};
+                                            0.85, 0.85, 0.9, 0.85, 0.75};
+    // 8-wave tiles hide part of a step's latency behind the other wave of the SIMD
+    constexpr double kFloorScale[kNumConvTiles] = {1, 1, 1, 1, 1, 1, 1, 1, 0.75, 0.75, 0.75, 0.75, 0.75};
+    const ConvTileShape& sh = kShapes[t];
+    const int64_t wgs0 = ((M + sh.bm - 1) / sh.bm) * ((Cout + sh.bn - 1) / sh.bn);
+    const double c = std::ceil(static_cast<double>(wgs0 * splits) / kCus);
+    const double mfma_step = 2.0 * sh.bm * sh.bn * sh.kg * BK / 256.0 / kEff[t];
+    double cost = kKernelCycles + kWgCycles + steps * std::max(c * mfma_step, kStepFloor * kFloorScale[t]);
+    if (splits > 1) cost += kKernelCycles + static_cast<double>(splits) * M * Cout * 4.0 / 2048.0;
+    (void)ktiles;
+    return cost;
+}
+
+}  // namespace
+
+std::vector<ConvLaunchShape> conv_candidates(int64_t M, int Cout, int K, bool allow_split) {
     const int ktiles = (K + BK - 1) / BK;
-    ConvLaunchShape best;
-    double best_cost = 1e300;
+    struct Scored {
+        double cost;
+        ConvLaunchShape ls;
+    };
+    std::vector<Scored> out;
     for (int t = 0; t < kNumConvTiles; ++t) {
         const ConvTileShape& sh = kShapes[t];
-        const int64_t wgs0 = ((M + sh.bm - 1) / sh.bm) * ((Cout + sh.bn - 1) / sh.bn);
         const int steps_total = (ktiles + sh.kg - 1) / sh.kg;
         const int max_splits = allow_split ? std::min(16, std::max(1, steps_total / 2)) : 1;
+        Scored one{0.0, {}}, best{1e300, {}};
         for (int sp = 1; sp <= max_splits; ++sp) {
             const int steps = (steps_total + sp - 1) / sp;
             const int splits = (steps_total + steps - 1) / steps;
             if (splits != sp) continue;
-            const double c = std::ceil(static_cast<double>(wgs0 * splits) / kCus);
-            const double mfma_step = 2.0 * sh.bm * sh.bn * sh.kg * BK / 256.0 / kEff[t];
-            double cost = kKernelCycles + kWgCycles + steps * std::max(c * mfma_step, kStepFloor);
-            if (splits > 1) cost += kKernelCycles + static_cast<double>(splits) * M * Cout * 4.0 / 2048.0;
-            if (cost < best_cost * 0.999) {
-                best_cost = cost;
-                best.tile = t;
-                best.splits = splits;
-                best.kt_per_split = steps * sh.kg;
-            }
+            const double cost = conv_cost(M, Cout, ktiles, t, splits, steps);
+            const Scored sc{cost, {t, splits, steps * sh.kg}};
+            if (splits == 1) one = sc;
+            if (cost < best.cost * 0.999) best = sc;
         }
+        out.push_back(one);
+        if (best.ls.splits > 1) out.push_back(best);
     }
-    return best;
+    std::stable_sort(out.begin(), out.end(), [](const Scored& a, const Scored& b) { return a.cost < b.cost; });
+    std::vector<ConvLaunchShape> r;
+    for (const Scored& sc : out) r.push_back(sc.ls);
+    return r;
+}
+
+ConvLaunchShape conv_select(int64_t M, int Cout, int K, bool allow_split) {
+    return conv_candidates(M, Cout, K, allow_split).front();
 }
 
 void launch_conv_mfma(const ConvArgs& a, int tile, bool vec, hipStream_t s) {

@@ -832,7 +832,31 @@ class Planner {
             s.vec = cin % 4 == 0 && x.off % 4 == 0 && x.str[0] % 4 == 0 && x.str[2] % 4 == 0 && x.str[3] % 4 == 0;
             const int64_t M = y.dims[0] * y.dims[2] * y.dims[3];
             const int64_t K = cin * s.KH * s.KW;
-            k::ConvLaunchShape ls = k::conv_select(M, static_cast<int>(cout), static_cast<int>(K), opt_.split_k);
+            k::ConvLaunchShape ls;
+            if (opt_.tune_conv && opt_.force_tile < 0 && opt_.split_k) {
+                ConvQuery q;
+                q.N = static_cast<int32_t>(x.dims[0]);
+                q.Cin = static_cast<int32_t>(cin);
+                q.H = static_cast<int32_t>(x.dims[2]);
+                q.W = static_cast<int32_t>(x.dims[3]);
+                q.Cout = static_cast<int32_t>(cout);
+                q.Ho = static_cast<int32_t>(y.dims[2]);
+                q.Wo = static_cast<int32_t>(y.dims[3]);
+                q.KH = s.KH;
+                q.KW = s.KW;
+                q.sh = s.sh;
+                q.sw = s.sw;
+                q.ph = s.ph;
+                q.pw = s.pw;
+                q.dh = s.dh;
+                q.dw = s.dw;
+                q.act = s.act;
+                q.has_res = s.has_res;
+                q.vec = s.vec;
+                ls = opt_.tune_conv(q);
+            } else {
+                ls = k::conv_select(M, static_cast<int>(cout), static_cast<int>(K), opt_.split_k);
+            }
             if (opt_.force_tile >= 0 && opt_.force_tile < k::kNumConvTiles) {
                 const int kg = k::conv_tile_shape(opt_.force_tile).kg;
                 const int steps_total = static_cast<int>((K + k::kConvBK - 1) / k::kConvBK + kg - 1) / kg;

@@ -12,6 +12,7 @@
 
 #include <climits>
 #include <cstdint>
+#include <functional>
 #include <string>
 #include <vector>
 
@@ -77,7 +78,16 @@ struct Plan {
     int32_t n_copies = 0;                     // materialising copies the planner could not avoid
 };
 
+// Shape of one implicit-GEMM conv (channels-last input and output).
+struct ConvQuery {
+    int32_t N, H, W, Cin, Ho, Wo, Cout, KH, KW, sh, sw, ph, pw, dh, dw, act;
+    bool has_res, vec;
+};
+
 struct PlanOptions {
+    // When set, chooses the launch shape of every implicit-GEMM conv (the
+    // runtime times candidates on the device); otherwise the cost model does.
+    std::function<k::ConvLaunchShape(const ConvQuery&)> tune_conv;
     bool split_k = true;
     int force_tile = -1;   // >= 0: use this implicit-GEMM tile for every MFMA conv (tuning, tests)
     int force_splits = 0;  // > 0 with force_tile: split-K across workgroups into this many splits

@@ -1,5 +1,7 @@
 #include "runtime.hpp"
 
+#include "conv_tune.hpp"
+
 #include <algorithm>
 #include <cstdio>
 #include <cstdlib>
@@ -149,6 +151,8 @@ Session::Session(Model& m) : model_(&m) {
     if (const char* sp = std::getenv("PDEFA_CONV_SPLITS")) opts_.force_splits = std::atoi(sp);
     const char* silu = std::getenv("PDEFA_SILU");
     opts_.winograd_form_silu = !(silu && std::strcmp(silu, "exact") == 0);
+    // PDEFA_AUTOTUNE=0: conv launch shapes from the cost model alone
+    autotune_ = env_flag("PDEFA_AUTOTUNE", true);
 }
 
 Session::~Session() {
@@ -220,7 +224,9 @@ std::string step_label(const Model& m, const Step& s, int idx) {
 void Session::prepare(const std::vector<std::vector<int64_t>>& dims) {
     release_prepared();
     auto p = std::make_unique<Prepared>();
-    p->plan = build_plan(*model_, dims, opts_);
+    PlanOptions opts = opts_;
+    if (autotune_) opts.tune_conv = [this](const ConvQuery& q) { return tune_conv(q, stream_); };
+    p->plan = build_plan(*model_, dims, opts);
     const Plan& plan = p->plan;
     if (concurrent_) p->sched = schedule_plan(plan, kMaxCaptureStreams);
     PDEFA_HIP(hipMalloc(&p->arena, static_cast<size_t>(std::max<int64_t>(plan.arena_elems, 64)) * sizeof(float)));

@@ -131,6 +131,7 @@ class Session {
     void* prof_user_ = nullptr;
     bool use_graph_ = true;
     PlanOptions opts_;
+    bool autotune_ = true;  // time candidate conv launch shapes while planning
 };
 
 // C = A[M,K] @ B[K,N] on the device (the ops_matmul path); host pointers.
