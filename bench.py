@@ -2,16 +2,25 @@
 the conv roofline and the reference CPU engine timed on the host.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W]
+    python bench.py --only roofline [--calib-copy]   # the roofline layer alone (profiling runs)
+    python bench.py --ingest-pmc FETCH.csv WRITE.csv  # HBM traffic of the roofline launch -> profiles/
 
 A step is one forward of the whole YOLOv8n device program over one batch of
 synthetic letterboxed input already resident in HBM: the session's captured
 hipGraph is replayed K times after W warm-up replays, timed with HIP events
 on the session stream and with the host clock around a device synchronise on
 both sides.  Prints ONE JSON line.
+
+Roofline: the 3x3 s1 p1 64->64 conv + bias + SiLU on a 1x64x160x160 input
+(1.887 GFLOP per launch).  Its average launch duration comes from HIP events
+around back-to-back launches of that step on the session stream; `traffic`
+is read from the PMC summary that --ingest-pmc writes (FETCH_SIZE and
+WRITE_SIZE per dispatch, scaled by the same counters on a 64 MiB copy).
 """
 from __future__ import annotations
 
 import argparse
+import csv
 import json
 import os
 import statistics
@@ -36,6 +45,8 @@ CONV_ROOF = dict(cin=64, cout=64, k=3, stride=1, hw=160)
 CONV_ROOF_FLOPS = 2 * 64 * 64 * 9 * 160 * 160
 KIND_CONV_MFMA, KIND_CONV_DIRECT = 0, 1
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "conv3x3s1_64x64_160_traffic.json")
+CALIB_SHAPE = (1, 16, 1024, 1024)  # 64 MiB in, 64 MiB out: larger than all L2s together
+CALIB_BYTES = 4 * 16 * 1024 * 1024
 
 
 def log(*a):
@@ -44,15 +55,17 @@ def log(*a):
 
 def time_program(eng: native.Engine, x: np.ndarray, steps: int, warmup: int):
     """ms per forward: W warm-up replays, then K timed replays of the graph."""
-    eng.run(x)  # uploads the input, plans, captures the graph
+    t0 = time.perf_counter()
+    eng.run(x)  # uploads the input, plans (timing conv candidates), captures the graph
+    first_ms = (time.perf_counter() - t0) * 1e3
     if warmup > 0:
         eng.replay(warmup)
-    lib = native.lib()
     t0 = time.perf_counter()
     dev_ms = eng.replay(steps)
     wall_ms = (time.perf_counter() - t0) * 1e3
-    log(f"  {steps} steps: device {dev_ms:.3f} ms, host wall {wall_ms:.3f} ms")
-    return max(dev_ms, 0.0) / steps, wall_ms / steps
+    log(f"  first run (plan + tune + capture) {first_ms:.1f} ms; {steps} steps: device {dev_ms:.3f} ms, "
+        f"host wall {wall_ms:.3f} ms")
+    return max(dev_ms, 0.0) / steps, wall_ms / steps, first_ms
 
 
 def conv_stats(eng: native.Engine, iters: int):
@@ -65,28 +78,88 @@ def conv_stats(eng: native.Engine, iters: int):
                 n_steps=int(len(ms)), n_conv=int(conv.sum()))
 
 
-def roofline(tmp: str, iters: int):
-    """Average duration of the conv_mfma launch on the 3x3/s1 64->64 160x160 layer."""
+def roofline_engine(tmp: str):
     model, x = ys.build_single_conv(**CONV_ROOF, seed=7)
     path = os.path.join(tmp, "conv3x3.engine")
     ys.save(model, path)
     eng = native.Engine(path)
+    eng.run(x)
+    lines = eng.plan().splitlines()[1:]
+    idx = [i for i, l in enumerate(lines) if " conv_mfma" in l][0]
+    return eng, idx, lines[idx]
+
+
+def roofline(tmp: str, iters: int):
+    """Average duration of the conv_mfma launch on the 3x3/s1 64->64 160x160 layer."""
+    eng, idx, line = roofline_engine(tmp)
     try:
-        eng.run(x)
-        ms, kind, flops = eng.step_times(iters)
+        ms = eng.step_repeat(idx, iters)
     finally:
         eng.close()
-    i = int(np.nonzero(kind == KIND_CONV_MFMA)[0][0])
-    assert int(flops[i]) == CONV_ROOF_FLOPS
-    achieved = CONV_ROOF_FLOPS / (ms[i] * 1e-3) / 1e12
+    achieved = CONV_ROOF_FLOPS / (ms * 1e-3) / 1e12
     traffic = None
     if os.path.exists(TRAFFIC_FILE):
         with open(TRAFFIC_FILE) as f:
             traffic = json.load(f).get("hbm_bytes_per_launch")
+    shape = line.split("(")[1].split(")")[0]
     return dict(bound="mfma", achieved=round(achieved, 3), peak=MFMA_FP32_PEAK_TFLOPS, unit="TFLOP/s",
                 frac=round(achieved / MFMA_FP32_PEAK_TFLOPS, 4), traffic=traffic,
-                kernel="conv_mfma_kernel", launch_us=round(float(ms[i]) * 1e3, 2),
-                workload="conv3x3 s1 p1 64->64 1x64x160x160 +bias+SiLU")
+                kernel="conv_mfma_kernel", launch_shape=shape, launch_us=round(ms * 1e3, 2),
+                workload="conv3x3 s1 p1 64->64 1x64x160x160 +bias+SiLU, 1.887 GFLOP/launch")
+
+
+def calibration_copy(tmp: str, iters: int = 5):
+    """A plain streaming pass of known size for the PMC byte counters: ReLU of a
+    64 MiB tensor (64 MiB read, 64 MiB written per dispatch)."""
+    b = ys.GraphBuilder()
+    y = b.node("Relu", "/calib/Relu", [-1])
+    model = b.model(list(CALIB_SHAPE), list(CALIB_SHAPE), [y])
+    path = os.path.join(tmp, "calib.engine")
+    ys.save(model, path)
+    x = np.random.default_rng(0).random(CALIB_SHAPE, dtype=np.float32)
+    eng = native.Engine(path)
+    try:
+        eng.run(x)
+        ms = eng.step_repeat(0, iters)
+    finally:
+        eng.close()
+    log(f"calibration copy: {CALIB_BYTES / 2**20:.0f} MiB in + out, {ms * 1e3:.1f} us/dispatch "
+        f"({2 * CALIB_BYTES / (ms * 1e-3) / 1e9:.0f} GB/s)")
+
+
+def ingest_pmc(fetch_csv: str, write_csv: str):
+    """FETCH_SIZE / WRITE_SIZE (KiB per dispatch) of the roofline conv launches
+    and of the calibration copy -> profiles/conv3x3s1_64x64_160_traffic.json."""
+    def read(path, counter):
+        conv, calib = [], []
+        with open(path) as f:
+            for row in csv.DictReader(f):
+                if row.get("Counter_Name") != counter:
+                    continue
+                name, val = row["Kernel_Name"], float(row["Counter_Value"])
+                if "conv_mfma_kernel" in name:
+                    conv.append(val)
+                elif "eltwise_kernel" in name and int(row.get("Grid_Size", 0)) >= CALIB_BYTES // 4:
+                    calib.append(val)
+        if not conv or not calib:
+            raise SystemExit(f"{path}: no {counter} rows for the conv or the calibration copy")
+        return statistics.median(conv), statistics.median(calib), len(conv), len(calib)
+    fc, fk, nfc, nfk = read(fetch_csv, "FETCH_SIZE")
+    wc, wk, nwc, nwk = read(write_csv, "WRITE_SIZE")
+    f_scale = CALIB_BYTES / (fk * 1024.0)
+    w_scale = CALIB_BYTES / (wk * 1024.0)
+    read_b = fc * 1024.0 * f_scale
+    write_b = wc * 1024.0 * w_scale
+    algo = 4 * (64 * 160 * 160 * 2 + 64 * 64 * 9 + 64)  # input + output + weights + bias
+    out = dict(kernel="conv_mfma_kernel (3x3 s1 p1 64->64, 1x64x160x160)",
+               fetch_kib_per_dispatch=fc, write_kib_per_dispatch=wc, conv_dispatches=[nfc, nwc],
+               calib_fetch_kib=fk, calib_write_kib=wk, calib_dispatches=[nfk, nwk],
+               calib_bytes_each_way=CALIB_BYTES, fetch_scale=round(f_scale, 4), write_scale=round(w_scale, 4),
+               hbm_read_bytes_per_launch=round(read_b), hbm_write_bytes_per_launch=round(write_b),
+               hbm_bytes_per_launch=round(read_b + write_b), algorithmic_bytes_per_launch=algo)
+    with open(TRAFFIC_FILE, "w") as f:
+        json.dump(out, f, indent=1)
+    print(json.dumps(out))
 
 
 def cpu_baseline(path: str, x: np.ndarray, budget_s: float = 12.0):
@@ -120,7 +193,14 @@ def main():
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu", action="store_true", help="skip the reference CPU baseline")
+    ap.add_argument("--no-m16", action="store_true", help="skip the YOLOv8m batch-16 line")
+    ap.add_argument("--only", choices=["all", "roofline"], default="all")
+    ap.add_argument("--calib-copy", action="store_true", help="with --only roofline: also run the PMC calibration copy")
+    ap.add_argument("--ingest-pmc", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"))
     args = ap.parse_args()
+    if args.ingest_pmc:
+        ingest_pmc(*args.ingest_pmc)
+        return
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (this build has no multi-GPU path); got --gpus {args.gpus}",
               file=sys.stderr)
@@ -129,6 +209,16 @@ def main():
         return
 
     log(f"device: {native.lib().pdefa_amd_device_name().decode()}")
+    if args.only == "roofline":
+        with tempfile.TemporaryDirectory() as tmp:
+            roof = roofline(tmp, 50)
+            log(f"roofline conv3x3 [{roof['launch_shape']}]: {roof['launch_us']} us/launch, "
+                f"{roof['achieved']} TFLOP/s ({roof['frac']:.1%})")
+            if args.calib_copy:
+                calibration_copy(tmp)
+        print(json.dumps({"roofline": roof}), flush=True)
+        return
+
     with tempfile.TemporaryDirectory() as tmp:
         path = os.path.join(tmp, "yolov8n.engine")
         ys.save(ys.build_yolov8("n", seed=0), path)
@@ -138,15 +228,30 @@ def main():
             eng = native.Engine(path)
             try:
                 log(f"yolov8n b{batch}:")
-                ms, wall = time_program(eng, x, args.steps, args.warmup)
+                ms, wall, first = time_program(eng, x, args.steps, args.warmup)
                 cs = conv_stats(eng, 20)
             finally:
                 eng.close()
-            res[batch] = dict(ms=ms, wall=wall, ips=batch * 1000.0 / ms, **cs)
+            res[batch] = dict(ms=ms, wall=wall, first=first, ips=batch * 1000.0 / ms, **cs)
             log(f"  {res[batch]['ips']:.1f} images/s, {ms:.4f} ms/step; convs {cs['conv_ms']:.4f} ms "
                 f"({cs['conv_tflops']:.2f} TFLOP/s over {cs['n_conv']} convs, {cs['n_steps']} steps)")
+        m16 = None
+        if not args.no_m16:
+            mpath = os.path.join(tmp, "yolov8m.engine")
+            ys.save(ys.build_yolov8("m", seed=1), mpath)
+            x, _ = ys.yolo_inputs(16)
+            eng = native.Engine(mpath)
+            try:
+                log("yolov8m b16:")
+                ms, wall, first = time_program(eng, x, max(5, args.steps // 10), max(1, args.warmup // 10))
+            finally:
+                eng.close()
+            m16 = dict(value=round(16000.0 / ms, 2), unit="images/s", ms_per_step=round(ms, 4),
+                       first_run_ms=round(first, 1))
+            log(f"  {m16['value']} images/s")
         roof = roofline(tmp, 50)
-        log(f"roofline conv3x3: {roof['launch_us']} us/launch, {roof['achieved']} TFLOP/s ({roof['frac']:.1%})")
+        log(f"roofline conv3x3 [{roof['launch_shape']}]: {roof['launch_us']} us/launch, "
+            f"{roof['achieved']} TFLOP/s ({roof['frac']:.1%})")
         cpu = None
         if not args.no_cpu:
             x1, _ = ys.yolo_inputs(1)
@@ -173,7 +278,9 @@ def main():
                    "input": "1x3x640x640 fp32", "output": "1x84x8400"},
         "b8": {"value": round(b8["ips"], 2), "unit": "images/s", "ms_per_step": round(b8["ms"], 5),
                "conv_tflops": round(b8["conv_tflops"], 3)},
+        "yolov8m_b16": m16,
         "conv_tflops_b1": round(b1["conv_tflops"], 3),
+        "first_run_ms": {"b1": round(b1["first"], 1), "b8": round(b8["first"], 1)},
         "roofline": roof,
         "cpu_baseline": cpu,
     }
