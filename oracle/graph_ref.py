@@ -261,10 +261,16 @@ def _silu_consumer(model, conv):
     return mul.outputs[0]
 
 
-def run_graph(model: EngineModel, inputs, dtype=np.float64, compat_silu=True):
+def run_graph(model: EngineModel, inputs, dtype=np.float64, compat_silu=True, flip=None, flip_tol=1e-5):
     """Evaluates the graph on `inputs` (list of NCHW arrays); returns outputs
     as float32 arrays in graph_outputs order.  compat_silu=False evaluates the
-    true SiLU everywhere."""
+    true SiLU everywhere.
+
+    flip: optional predicate on a conv node's name.  On the compat-SiLU layers
+    it accepts, every element whose pre-activation lies within flip_tol
+    (relative, see silu_winograd_compat_branches) of one of the form's jumps
+    takes the other side of the jump: the output an fp32 computation gets when
+    its rounding lands there on the other side."""
     inter = {}
     skip = set()
 
@@ -295,7 +301,13 @@ def run_graph(model: EngineModel, inputs, dtype=np.float64, compat_silu=True):
             if silu is not None:
                 if compat_silu and winograd_path(x.shape[1], w.shape[2], w.shape[3],
                                                  stride, dil, 1):
-                    y = silu_winograd_compat(y.astype(np.float32)).astype(dtype)
+                    y32 = y.astype(np.float32)
+                    straight = silu_winograd_compat(y32)
+                    if flip is not None and flip(node.name):
+                        y_lo, y_hi, unstable = silu_winograd_compat_branches(y32, tol=flip_tol)
+                        other = np.where(straight == y_lo, y_hi, y_lo)
+                        straight = np.where(unstable, other, straight)
+                    y = straight.astype(dtype)
                 else:
                     y = y / (1.0 + np.exp(-y))
                 inter[node.outputs[0]] = y

@@ -21,6 +21,7 @@ ARCH = os.environ.get("PDEFA_OFFLOAD_ARCH", "gfx950")
 
 SOURCES = [
     "kernels/conv_mfma.hip",
+    "kernels/conv_wino.hip",
     "kernels/ops.hip",
     "model.cpp",
     "planner.cpp",

@@ -23,7 +23,7 @@ std::map<Key, k::ConvLaunchShape> g_cache;
 
 Key make_key(const ConvQuery& q, int device) {
     return {device, q.N,  q.H,  q.W,  q.Cin, q.Ho, q.Wo, q.Cout, q.KH, q.KW,
-            q.sh,   q.sw, q.ph, q.pw, q.dh,  q.dw, q.act, q.has_res ? 1 : 0, q.vec ? 1 : 0, 0};
+            q.sh,   q.sw, q.ph, q.pw, q.dh,  q.dw, q.act, q.has_res ? 1 : 0, q.vec ? 1 : 0, q.wino ? 1 : 0};
 }
 
 struct DeviceBuffer {
@@ -48,11 +48,18 @@ struct Events {
     }
 };
 
+void launch(const k::ConvArgs& a, int tile, bool vec, hipStream_t s) {
+    if (k::is_wino_tile(tile))
+        k::launch_conv_wino(a, tile == k::kTileWino64 ? 64 : 32, s);
+    else
+        k::launch_conv_mfma(a, tile, vec, s);
+}
+
 // Average ms of `reps` back-to-back launches (after one untimed launch).
 double time_launch(const k::ConvArgs& a, int tile, bool vec, hipStream_t s, Events& ev, int reps) {
-    k::launch_conv_mfma(a, tile, vec, s);
+    launch(a, tile, vec, s);
     PDEFA_HIP(hipEventRecord(ev.a, s));
-    for (int i = 0; i < reps; ++i) k::launch_conv_mfma(a, tile, vec, s);
+    for (int i = 0; i < reps; ++i) launch(a, tile, vec, s);
     PDEFA_HIP(hipEventRecord(ev.b, s));
     PDEFA_HIP(hipEventSynchronize(ev.b));
     float ms = 0.0f;
@@ -71,8 +78,11 @@ k::ConvLaunchShape tune_conv(const ConvQuery& q, hipStream_t s) {
 
     const int64_t M = static_cast<int64_t>(q.N) * q.Ho * q.Wo;
     const int K = q.KH * q.KW * q.Cin;
-    std::vector<k::ConvLaunchShape> cands = k::conv_candidates(M, q.Cout, K, true);
-    if (cands.size() > kMaxCandidates) cands.resize(kMaxCandidates);
+    std::vector<k::ConvLaunchShape> all = k::conv_candidates(M, q.Cout, K, true, q.wino, q.Cin);
+    // the cost model's best implicit-GEMM shapes, plus every Winograd shape
+    std::vector<k::ConvLaunchShape> cands;
+    for (const auto& c : all)
+        if (k::is_wino_tile(c.tile) || cands.size() < kMaxCandidates) cands.push_back(c);
     const int64_t out_elems = M * q.Cout;
     int max_splits = 1;
     std::vector<k::ConvLaunchShape> usable;
@@ -88,10 +98,12 @@ k::ConvLaunchShape tune_conv(const ConvQuery& q, hipStream_t s) {
         // reads the output tensor itself: each element is read and then
         // written by the same lane.
         const int64_t x_elems = static_cast<int64_t>(q.N) * q.H * q.W * q.Cin;
-        DeviceBuffer x(x_elems), y(out_elems), w(k::packed_weight_elems(q.Cout, K)), bias(q.Cout),
+        const int64_t w_elems = std::max(k::packed_weight_elems(q.Cout, K),
+                                         q.wino ? k::wino_packed_elems(q.Cout, q.Cin) : int64_t{0});
+        DeviceBuffer x(x_elems), y(out_elems), w(w_elems), bias(q.Cout),
             ws(max_splits > 1 ? static_cast<int64_t>(max_splits) * out_elems : 1);
         PDEFA_HIP(hipMemsetAsync(x.p, 0, static_cast<size_t>(x_elems) * 4, s));
-        PDEFA_HIP(hipMemsetAsync(w.p, 0, static_cast<size_t>(k::packed_weight_elems(q.Cout, K)) * 4, s));
+        PDEFA_HIP(hipMemsetAsync(w.p, 0, static_cast<size_t>(w_elems) * 4, s));
         PDEFA_HIP(hipMemsetAsync(bias.p, 0, static_cast<size_t>(q.Cout) * 4, s));
         PDEFA_HIP(hipMemsetAsync(y.p, 0, static_cast<size_t>(out_elems) * 4, s));
         k::ConvArgs a;

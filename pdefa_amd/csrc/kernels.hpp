@@ -62,8 +62,13 @@ enum ConvTile : int32_t {
     kTile128x128W8 = 10,   // 2x4 waves of 64x32
     kTile64x128W8 = 11,    // 2x4 waves of 32x32
     kTile32x64K4W8 = 12,   // 1x2 waves of 32x32, K split in 4
-    kNumConvTiles = 13,
+    kNumConvTiles = 13,    // implicit-GEMM tiles
+    // Winograd F(2x2,3x3) kernel (3x3 stride-1 convs), 32 tiles x BN channels
+    kTileWino64 = 13,
+    kTileWino32 = 14,
+    kNumConvShapes = 15,
 };
+inline bool is_wino_tile(int tile) { return tile == kTileWino64 || tile == kTileWino32; }
 ConvTileShape conv_tile_shape(int tile);
 const char* conv_tile_name(int tile);
 
@@ -105,14 +110,27 @@ struct ConvLaunchShape {
     int splits = 1;
     int kt_per_split = 0;
 };
-ConvLaunchShape conv_select(int64_t M, int Cout, int K, bool allow_split);
-// Every tile with one split and with its best split count, cheapest predicted
-// first (conv_select is the first); the candidates a measured choice times.
-std::vector<ConvLaunchShape> conv_candidates(int64_t M, int Cout, int K, bool allow_split);
+ConvLaunchShape conv_select(int64_t M, int Cout, int K, bool allow_split, bool wino_ok = false, int Cin = 0);
+// Every tile with one split and with its best split count (and, with
+// wino_ok, the Winograd kernel for a 3x3 stride-1 layer of Cin channels),
+// cheapest predicted first (conv_select is the first); the candidates a
+// measured choice times.
+std::vector<ConvLaunchShape> conv_candidates(int64_t M, int Cout, int K, bool allow_split, bool wino_ok = false,
+                                             int Cin = 0);
 
 // Host-side checks + launch.  vec selects 16-byte input loads (requires
 // Cin % 4 == 0 and 16-byte aligned pixel rows).
 void launch_conv_mfma(const ConvArgs& a, int tile, bool vec, hipStream_t s);
+
+// Winograd F(2x2,3x3) on MFMA for 3x3 / stride 1 / dilation 1 convs with
+// Cin % 4 == 0 and Cin >= 8 (any padding).  a.wpk holds the transformed
+// weights U = G g G^T as [16][ceil(Cin/8)*2][ceil(Cout/64)*64][4]
+// (launch_pack_wino_weights from the OIHW weights); splits must be 1.
+// bn = 32 or 64 output channels per workgroup.
+bool wino_eligible(int KH, int KW, int sh, int sw, int dh, int dw, int Cin);
+int64_t wino_packed_elems(int Cout, int Cin);
+void launch_conv_wino(const ConvArgs& a, int bn, hipStream_t s);
+void launch_pack_wino_weights(float* dst, const float* w_oihw, int Cout, int Cin, hipStream_t s);
 
 // Direct convolution over arbitrary strided NCHW-logical views (any layout),
 // for layers the implicit GEMM does not take: tiny Cin (the 3-channel stem,

@@ -554,7 +554,11 @@ ConvTileShape conv_tile_shape(int tile) {
     if (tile < 0 || tile >= kNumConvTiles) return {0, 0, 0, 0, 0};
     return kShapes[tile];
 }
-const char* conv_tile_name(int tile) { return tile >= 0 && tile < kNumConvTiles ? kNames[tile] : "?"; }
+const char* conv_tile_name(int tile) {
+    if (tile == kTileWino64) return "wino64";
+    if (tile == kTileWino32) return "wino32";
+    return tile >= 0 && tile < kNumConvTiles ? kNames[tile] : "?";
+}
 
 int64_t packed_weight_elems(int Cout, int K) {
     const int64_t cout_pad = (Cout + kConvBN - 1) / kConvBN * kConvBN;
@@ -592,7 +596,7 @@ double conv_cost(int64_t M, int Cout, int ktiles, int t, int splits, int steps) 
 
 }  // namespace
 
-std::vector<ConvLaunchShape> conv_candidates(int64_t M, int Cout, int K, bool allow_split) {
+std::vector<ConvLaunchShape> conv_candidates(int64_t M, int Cout, int K, bool allow_split, bool wino_ok, int Cin) {
     const int ktiles = (K + BK - 1) / BK;
     struct Scored {
         double cost;
@@ -616,14 +620,27 @@ std::vector<ConvLaunchShape> conv_candidates(int64_t M, int Cout, int K, bool al
         out.push_back(one);
         if (best.ls.splits > 1) out.push_back(best);
     }
+    if (wino_ok) {
+        // 32 output 2x2 tiles x BN channels per workgroup, 8 input channels per
+        // step, 16*BN/32 MFMAs of 64 cycles per wave and step, no barrier in the loop
+        const int64_t tiles = (M + 3) / 4;  // about M/4 2x2 tiles
+        const int steps = (Cin + 7) / 8;
+        for (int bn : {64, 32}) {
+            const int64_t wgs = (tiles + 31) / 32 * ((Cout + bn - 1) / bn);
+            const double c = std::ceil(static_cast<double>(wgs) / 256.0);
+            const double step = std::max(c * 16.0 * (bn / 32) * 64.0 / 0.8, 1400.0);
+            const double cost = 10000.0 + 3000.0 + steps * step;
+            out.push_back({cost, {bn == 64 ? kTileWino64 : kTileWino32, 1, ktiles}});
+        }
+    }
     std::stable_sort(out.begin(), out.end(), [](const Scored& a, const Scored& b) { return a.cost < b.cost; });
     std::vector<ConvLaunchShape> r;
     for (const Scored& sc : out) r.push_back(sc.ls);
     return r;
 }
 
-ConvLaunchShape conv_select(int64_t M, int Cout, int K, bool allow_split) {
-    return conv_candidates(M, Cout, K, allow_split).front();
+ConvLaunchShape conv_select(int64_t M, int Cout, int K, bool allow_split, bool wino_ok, int Cin) {
+    return conv_candidates(M, Cout, K, allow_split, wino_ok, Cin).front();
 }
 
 void launch_conv_mfma(const ConvArgs& a, int tile, bool vec, hipStream_t s) {

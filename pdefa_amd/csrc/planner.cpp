@@ -832,6 +832,9 @@ class Planner {
             s.vec = cin % 4 == 0 && x.off % 4 == 0 && x.str[0] % 4 == 0 && x.str[2] % 4 == 0 && x.str[3] % 4 == 0;
             const int64_t M = y.dims[0] * y.dims[2] * y.dims[3];
             const int64_t K = cin * s.KH * s.KW;
+            // The Winograd kernel needs the transformed weights packed at model
+            // load for exactly these layers, and 16-byte aligned input pixels.
+            const bool wino = s.vec && k::wino_eligible(s.KH, s.KW, s.sh, s.sw, s.dh, s.dw, static_cast<int>(cin));
             k::ConvLaunchShape ls;
             if (opt_.tune_conv && opt_.force_tile < 0 && opt_.split_k) {
                 ConvQuery q;
@@ -853,11 +856,15 @@ class Planner {
                 q.act = s.act;
                 q.has_res = s.has_res;
                 q.vec = s.vec;
+                q.wino = wino;
                 ls = opt_.tune_conv(q);
             } else {
-                ls = k::conv_select(M, static_cast<int>(cout), static_cast<int>(K), opt_.split_k);
+                ls = k::conv_select(M, static_cast<int>(cout), static_cast<int>(K), opt_.split_k, wino,
+                                    static_cast<int>(cin));
             }
-            if (opt_.force_tile >= 0 && opt_.force_tile < k::kNumConvTiles) {
+            if (k::is_wino_tile(opt_.force_tile)) {
+                if (wino) ls = {opt_.force_tile, 1, static_cast<int>((K + k::kConvBK - 1) / k::kConvBK)};
+            } else if (opt_.force_tile >= 0 && opt_.force_tile < k::kNumConvTiles) {
                 const int kg = k::conv_tile_shape(opt_.force_tile).kg;
                 const int steps_total = static_cast<int>((K + k::kConvBK - 1) / k::kConvBK + kg - 1) / kg;
                 const int want = std::max(1, std::min(opt_.force_splits, steps_total));

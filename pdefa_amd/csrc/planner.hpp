@@ -82,6 +82,7 @@ struct Plan {
 struct ConvQuery {
     int32_t N, H, W, Cin, Ho, Wo, Cout, KH, KW, sh, sw, ph, pw, dh, dw, act;
     bool has_res, vec;
+    bool wino;  // the Winograd kernel applies (3x3, stride 1, dilation 1, Cin % 4 == 0)
 };
 
 struct PlanOptions {

@@ -56,8 +56,9 @@ std::shared_ptr<DeviceModel> upload_model(const Model& m) {
         total += align_up(static_cast<size_t>(std::max<int64_t>(1, m.weights[i].numel())));
     }
     struct PackPlan {
-        size_t node, wpk_off, bias_off, dpk_off;
+        size_t node, wpk_off, bias_off, dpk_off, wino_off;
         int cout, cin, kh, kw, w, b;
+        bool wino;
     };
     std::vector<PackPlan> pp;
     for (size_t i = 0; i < m.nodes.size(); ++i) {
@@ -81,6 +82,13 @@ std::shared_ptr<DeviceModel> upload_model(const Model& m) {
         total += align_up(static_cast<size_t>(p.cout));
         p.dpk_off = total;
         total += align_up(static_cast<size_t>(k::direct_packed_elems(p.cout, p.kh * p.kw * p.cin)));
+        const OpParams& op = n.params;
+        p.wino = k::wino_eligible(p.kh, p.kw, static_cast<int>(op.stride_h), static_cast<int>(op.stride_w),
+                                  static_cast<int>(op.dil_h), static_cast<int>(op.dil_w), p.cin);
+        if (p.wino) {
+            p.wino_off = total;
+            total += align_up(static_cast<size_t>(k::wino_packed_elems(p.cout, p.cin)));
+        }
         pp.push_back(p);
     }
     total = std::max<size_t>(total, kAlignFloats);
@@ -115,6 +123,11 @@ std::shared_ptr<DeviceModel> upload_model(const Model& m) {
             pk.dpk = dm->blob + p.dpk_off;
             k::launch_pack_conv_weights(pk.wpk, dm->wptr[p.w], p.cout, p.cin, p.kh, p.kw, s);
             PDEFA_HIP(hipGetLastError());
+            if (p.wino) {
+                pk.wino = dm->blob + p.wino_off;
+                k::launch_pack_wino_weights(pk.wino, dm->wptr[p.w], p.cout, p.cin, s);
+                PDEFA_HIP(hipGetLastError());
+            }
         }
         PDEFA_HIP(hipStreamSynchronize(s));
     } catch (...) {
@@ -144,7 +157,7 @@ Session::Session(Model& m) : model_(&m) {
     opts_.reuse_memory = !concurrent_;
     opts_.split_k = env_flag("PDEFA_SPLITK", true);
     if (const char* t = std::getenv("PDEFA_CONV_TILE")) {
-        for (int i = 0; i < k::kNumConvTiles; ++i)
+        for (int i = 0; i < k::kNumConvShapes; ++i)
             if (std::strcmp(t, k::conv_tile_name(i)) == 0) opts_.force_tile = i;
         if (opts_.force_tile < 0) throw std::runtime_error(std::string("PDEFA_CONV_TILE: unknown tile ") + t);
     }
@@ -293,7 +306,12 @@ void Session::prepare(const std::vector<std::vector<int64_t>>& dims) {
                 }
                 const HostTensor& wt = model_->weights.at(-1000 - n.inputs[1]);
                 if (wt.dims[0] != c.Cout || wt.dims[1] != c.Cin) throw std::runtime_error("conv weight shape mismatch");
-                c.wpk = pk.wpk;
+                if (k::is_wino_tile(s.tile)) {
+                    if (!pk.wino) throw std::runtime_error("Winograd weights were not packed: " + n.name);
+                    c.wpk = pk.wino;
+                } else {
+                    c.wpk = pk.wpk;
+                }
                 c.bias = pk.bias;
                 c.KH = s.KH;
                 c.KW = s.KW;
@@ -421,7 +439,12 @@ void Session::prepare(const std::vector<std::vector<int64_t>>& dims) {
 
 void Session::launch_one(const Launch& l, hipStream_t s) {
     switch (l.kind) {
-        case StepKind::ConvMfma: k::launch_conv_mfma(l.conv, l.tile, l.vec, s); break;
+        case StepKind::ConvMfma:
+            if (k::is_wino_tile(l.tile))
+                k::launch_conv_wino(l.conv, l.tile == k::kTileWino64 ? 64 : 32, s);
+            else
+                k::launch_conv_mfma(l.conv, l.tile, l.vec, s);
+            break;
         case StepKind::ConvDirect: k::launch_conv_direct(l.direct, s); break;
         case StepKind::Elt: k::launch_eltwise(l.elt, l.out, l.a, l.b, l.alpha, s); break;
         case StepKind::MaxPool: k::launch_maxpool(l.out, l.a, l.kh, l.kw, l.sh, l.sw, l.ph, l.pw, s); break;

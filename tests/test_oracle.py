@@ -267,3 +267,22 @@ def test_compiled_reference_matmul():
     a = rng.standard_normal((70, 130), dtype=np.float32)
     b = rng.standard_normal((130, 45), dtype=np.float32)
     np.testing.assert_allclose(ref_lib.matmul(a, b), a.astype(np.float64) @ b, atol=1e-4, rtol=1e-4)
+
+
+def test_flip_takes_the_other_side_of_each_jump():
+    """run_graph(flip=...) puts every compat-SiLU element within flip_tol of a
+    jump on the other branch; with a tolerance covering every input all of a
+    Winograd-path layer's elements switch branch."""
+    model, x = ys.build_single_conv(32, 8, 3, 1, 6, seed=2)
+    pre_model, _ = ys.build_single_conv(32, 8, 3, 1, 6, seed=2, silu=False)
+    pre = graph_ref.run_graph(pre_model, [x])[0]
+    straight = graph_ref.silu_winograd_compat(pre)
+    lo, hi, unstable = graph_ref.silu_winograd_compat_branches(pre, tol=0.6)
+    assert unstable.all()
+    want = np.where(straight == lo, hi, lo)
+    got = graph_ref.run_graph(model, [x], flip=lambda name: True, flip_tol=0.6)[0]
+    np.testing.assert_array_equal(got, want)
+    # each branch is the form with n one apart: they differ, by ~2% of |x| at the jump
+    assert not np.array_equal(lo, hi)
+    # no flip predicate: the straight compat form
+    np.testing.assert_array_equal(graph_ref.run_graph(model, [x])[0], straight)
