@@ -515,12 +515,17 @@ void launch_detect_decode(const DetectDecodeArgs& a, hipStream_t s) {
 // workgroup's channel block.  Weights are pre-packed [ceil(Cout/CB)][K][CB]
 // (K = Cin*KH*KW, k = (ci, kh, kw)) so the CB weights of one k are one
 // contiguous, wave-uniform read (scalar loads); each input value loaded feeds
-// CB FMAs.  The 256 x CB result tile goes through LDS and is stored with
-// consecutive lanes on consecutive channels, so channels-last outputs are
-// written in contiguous runs.  Index math is int32 within one image.
-template <int CB, int KS>
+// CB FMAs.  Index math is int32 within one image.
+//
+// KS = 3: 3x3 taps, the nine loads of each input channel in flight before its
+// FMAs.  CL: the output block is channels-last and whole
+// (and so is the residual), so each lane applies bias + activation (ACT, or
+// the runtime code for kActGeneric) in registers and stores its pixel's CB
+// channels as float4 runs; otherwise the 256 x CB result tile goes through
+// LDS and is stored with consecutive lanes on consecutive channels.
+template <int CB, int KS, bool CL, int ACT>
 __global__ __launch_bounds__(256) void conv_direct_kernel(ConvDirectArgs a, int P) {
-    __shared__ float tile[256 * (CB + 1)];
+    __shared__ float tile[CL ? 1 : 256 * (CB + 1)];
     const int p0 = blockIdx.x * 256;
     const int p = p0 + threadIdx.x;
     const int cob = blockIdx.y;
@@ -531,19 +536,18 @@ __global__ __launch_bounds__(256) void conv_direct_kernel(ConvDirectArgs a, int 
     float acc[CB];
 #pragma unroll
     for (int j = 0; j < CB; ++j) acc[j] = 0.0f;
-    if (p < P) {
-        const int n = p / HoWo;
-        const int rem = p - n * HoWo;
-        const int ho = rem / Wo;
-        const int wo = rem - ho * Wo;
+    const int pc = p < P ? p : P - 1;  // lanes past the end compute a valid pixel, store nothing
+    const int n = pc / HoWo;
+    const int rem = pc - n * HoWo;
+    const int ho = rem / Wo;
+    const int wo = rem - ho * Wo;
+    {
         const float* xb = a.x.ptr + static_cast<int64_t>(n) * a.x.str[0];
         const int xsc = static_cast<int>(a.x.str[1]), xsh = static_cast<int>(a.x.str[2]);
         const int xsw = static_cast<int>(a.x.str[3]);
         const int hi0 = ho * a.sh - a.ph, wi0 = wo * a.sw - a.pw;
         const float* wk = a.wpk + static_cast<int64_t>(cob) * K * CB;
         if constexpr (KS > 0) {
-            // KS x KS taps: tap offsets and masks once, then per input channel
-            // all KS*KS loads in flight before the FMAs
             int off[KS * KS];
             bool tok[KS * KS];
 #pragma unroll
@@ -568,42 +572,91 @@ __global__ __launch_bounds__(256) void conv_direct_kernel(ConvDirectArgs a, int 
 #pragma unroll
                     for (int j = 0; j < CB; ++j) acc[j] += xv[t] * wk[t * CB + j];
             }
-        } else
-        for (int c = 0; c < Ci; ++c) {
-            for (int kh = 0; kh < a.KH; ++kh) {
-                const int hi = hi0 + kh * a.dh;
-                const bool hok = static_cast<unsigned>(hi) < static_cast<unsigned>(H);
-                for (int kw = 0; kw < a.KW; ++kw, wk += CB) {
-                    const int wi = wi0 + kw * a.dw;
-                    const bool ok = hok && static_cast<unsigned>(wi) < static_cast<unsigned>(W);
-                    const float xv = ok ? xb[c * xsc + hi * xsh + wi * xsw] : 0.0f;
+        } else {
+            for (int c = 0; c < Ci; ++c) {
+                for (int kh = 0; kh < a.KH; ++kh) {
+                    const int hi = hi0 + kh * a.dh;
+                    const bool hok = static_cast<unsigned>(hi) < static_cast<unsigned>(H);
+                    for (int kw = 0; kw < a.KW; ++kw, wk += CB) {
+                        const int wi = wi0 + kw * a.dw;
+                        const bool ok = hok && static_cast<unsigned>(wi) < static_cast<unsigned>(W);
+                        const float xv = ok ? xb[c * xsc + hi * xsh + wi * xsw] : 0.0f;
 #pragma unroll
-                    for (int j = 0; j < CB; ++j) acc[j] += xv * wk[j];
+                        for (int j = 0; j < CB; ++j) acc[j] += xv * wk[j];
+                    }
                 }
             }
         }
     }
+    if constexpr (CL) {
+        if (p >= P) return;
+        const int c0 = cob * CB;
+        float* yp = a.y.ptr + static_cast<int64_t>(n) * a.y.str[0] + static_cast<int64_t>(ho) * a.y.str[2] +
+                    static_cast<int64_t>(wo) * a.y.str[3] + c0;
+        const float* rp = a.res.ptr ? a.res.ptr + static_cast<int64_t>(n) * a.res.str[0] +
+                                          static_cast<int64_t>(ho) * a.res.str[2] +
+                                          static_cast<int64_t>(wo) * a.res.str[3] + c0
+                                    : nullptr;
 #pragma unroll
-    for (int j = 0; j < CB; ++j) tile[threadIdx.x * (CB + 1) + j] = acc[j];
-    __syncthreads();
-    const int nc = min(CB, Co - cob * CB);
-    for (int idx = threadIdx.x; idx < 256 * CB; idx += 256) {
-        const int pl = idx / CB, j = idx - (idx / CB) * CB;
-        const int pp = p0 + pl;
-        if (pp >= P || j >= nc) continue;
-        const int co = cob * CB + j;
-        const int n = pp / HoWo;
-        const int rem = pp - n * HoWo;
-        const int ho = rem / Wo;
-        const int wo = rem - ho * Wo;
-        float v = apply_act(tile[pl * (CB + 1) + j] + (a.bias ? a.bias[co] : 0.0f), a.act, a.slope);
-        if (a.res.ptr)
-            v += a.res.ptr[static_cast<int64_t>(n) * a.res.str[0] + static_cast<int64_t>(co) * a.res.str[1] +
-                           static_cast<int64_t>(ho) * a.res.str[2] + static_cast<int64_t>(wo) * a.res.str[3]];
-        a.y.ptr[static_cast<int64_t>(n) * a.y.str[0] + static_cast<int64_t>(co) * a.y.str[1] +
-                static_cast<int64_t>(ho) * a.y.str[2] + static_cast<int64_t>(wo) * a.y.str[3]] = v;
+        for (int q = 0; q < CB / 4; ++q) {
+            float4 v;
+            float* vv = reinterpret_cast<float*>(&v);
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+                vv[e] = act_fixed<ACT>(acc[4 * q + e] + (a.bias ? a.bias[c0 + 4 * q + e] : 0.0f), a.act, a.slope);
+            if (rp) {
+                const float4 r = reinterpret_cast<const float4*>(rp)[q];
+                v.x += r.x;
+                v.y += r.y;
+                v.z += r.z;
+                v.w += r.w;
+            }
+            reinterpret_cast<float4*>(yp)[q] = v;
+        }
+        return;
+    } else {
+#pragma unroll
+        for (int j = 0; j < CB; ++j) tile[threadIdx.x * (CB + 1) + j] = acc[j];
+        __syncthreads();
+        const int nc = min(CB, Co - cob * CB);
+        for (int idx = threadIdx.x; idx < 256 * CB; idx += 256) {
+            const int pl = idx / CB, j = idx - (idx / CB) * CB;
+            const int pp = p0 + pl;
+            if (pp >= P || j >= nc) continue;
+            const int co = cob * CB + j;
+            const int nn = pp / HoWo;
+            const int rr = pp - nn * HoWo;
+            const int oh = rr / Wo;
+            const int ow = rr - oh * Wo;
+            float v = apply_act(tile[pl * (CB + 1) + j] + (a.bias ? a.bias[co] : 0.0f), a.act, a.slope);
+            if (a.res.ptr)
+                v += a.res.ptr[static_cast<int64_t>(nn) * a.res.str[0] + static_cast<int64_t>(co) * a.res.str[1] +
+                               static_cast<int64_t>(oh) * a.res.str[2] + static_cast<int64_t>(ow) * a.res.str[3]];
+            a.y.ptr[static_cast<int64_t>(nn) * a.y.str[0] + static_cast<int64_t>(co) * a.y.str[1] +
+                    static_cast<int64_t>(oh) * a.y.str[2] + static_cast<int64_t>(ow) * a.y.str[3]] = v;
+        }
     }
 }
+
+namespace {
+
+template <int CB, int KS, bool CL>
+void launch_direct_act(const ConvDirectArgs& a, dim3 grid, int P, hipStream_t s) {
+    if (CL && a.act == kActSilu)
+        hipLaunchKernelGGL((conv_direct_kernel<CB, KS, CL, kActSilu>), grid, dim3(256), 0, s, a, P);
+    else
+        hipLaunchKernelGGL((conv_direct_kernel<CB, KS, CL, kActGeneric>), grid, dim3(256), 0, s, a, P);
+}
+
+template <int CB>
+void launch_direct_cb(const ConvDirectArgs& a, dim3 grid, int P, bool k3, bool cl, hipStream_t s) {
+    if (k3 && cl) launch_direct_act<CB, 3, true>(a, grid, P, s);
+    else if (k3) launch_direct_act<CB, 3, false>(a, grid, P, s);
+    else if (cl) launch_direct_act<CB, 0, true>(a, grid, P, s);
+    else launch_direct_act<CB, 0, false>(a, grid, P, s);
+}
+
+}  // namespace
 
 void launch_conv_direct(const ConvDirectArgs& a, hipStream_t s) {
     check_view(a.x, "conv_direct x");
@@ -625,17 +678,17 @@ void launch_conv_direct(const ConvDirectArgs& a, hipStream_t s) {
     const dim3 grid(static_cast<unsigned>((P + 255) / 256), static_cast<unsigned>((a.y.dims[1] + cb - 1) / cb));
     const int Pi = static_cast<int>(P);
     const bool k3 = a.KH == 3 && a.KW == 3;
+    // channels-last output (and residual) with whole 16-byte aligned channel blocks
+    auto cl_view = [&](const View& v) {
+        return v.str[1] == 1 && v.str[0] % 4 == 0 && v.str[2] % 4 == 0 && v.str[3] % 4 == 0 &&
+               reinterpret_cast<uintptr_t>(v.ptr) % 16 == 0;
+    };
+    const bool cl = a.y.dims[1] % cb == 0 && cl_view(a.y) && (!a.res.ptr || cl_view(a.res));
     switch (cb) {
-        case 16:
-            if (k3) hipLaunchKernelGGL((conv_direct_kernel<16, 3>), grid, dim3(256), 0, s, a, Pi);
-            else hipLaunchKernelGGL((conv_direct_kernel<16, 0>), grid, dim3(256), 0, s, a, Pi);
-            break;
-        case 32:
-            if (k3) hipLaunchKernelGGL((conv_direct_kernel<32, 3>), grid, dim3(256), 0, s, a, Pi);
-            else hipLaunchKernelGGL((conv_direct_kernel<32, 0>), grid, dim3(256), 0, s, a, Pi);
-            break;
-        case 48: hipLaunchKernelGGL((conv_direct_kernel<48, 0>), grid, dim3(256), 0, s, a, Pi); break;
-        default: hipLaunchKernelGGL((conv_direct_kernel<64, 0>), grid, dim3(256), 0, s, a, Pi); break;
+        case 16: launch_direct_cb<16>(a, grid, Pi, k3, cl, s); break;
+        case 32: launch_direct_cb<32>(a, grid, Pi, k3, cl, s); break;
+        case 48: launch_direct_cb<48>(a, grid, Pi, k3, cl, s); break;
+        default: launch_direct_cb<64>(a, grid, Pi, k3, cl, s); break;
     }
 }
 
