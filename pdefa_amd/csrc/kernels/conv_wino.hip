@@ -46,6 +46,8 @@ namespace {
 constexpr int kWT = 32;  // tiles per workgroup (GEMM rows)
 constexpr int kCK = 8;   // input channels per K step (4 per lane half)
 constexpr int kXcds = 8;
+constexpr int kMaxCin = 4096;
+constexpr int kXchRow = kWT + 4;  // exchange rows: 32 tiles + 4 floats of padding
 
 int wino_cin_pad(int Cin) { return (Cin + kCK - 1) / kCK * kCK; }
 int wino_cout_pad(int Cout) { return (Cout + 63) / 64 * 64; }
@@ -54,8 +56,13 @@ void fail(const std::string& m) { throw std::runtime_error("conv_wino: " + m); }
 
 }  // namespace
 
+// Patch positions outside the image read this instead of the input (their
+// lanes then need no per-element mask): zeros, one channel run of any Cin.
+__device__ __attribute__((aligned(16))) float g_wino_zero[kMaxCin];
+
 bool wino_eligible(int KH, int KW, int sh, int sw, int dh, int dw, int Cin) {
-    return KH == 3 && KW == 3 && sh == 1 && sw == 1 && dh == 1 && dw == 1 && Cin % 4 == 0 && Cin >= 8;
+    return KH == 3 && KW == 3 && sh == 1 && sw == 1 && dh == 1 && dw == 1 && Cin % 4 == 0 && Cin >= 8 &&
+           Cin <= kMaxCin;
 }
 
 int64_t wino_packed_elems(int Cout, int Cin) {
@@ -104,7 +111,7 @@ __global__ void pack_wino_weights_kernel(float* dst, const float* w, int Cout, i
 template <int BN, int ACT, bool RES>
 __global__ __launch_bounds__(256) void conv_wino_kernel(ConvArgs a, int tiles_h, int tiles_w) {
     constexpr int CB = BN / 32;  // 32-wide channel blocks per wave
-    __shared__ float xch[4 * 2 * kWT * BN];  // [row i][column c][tile][channel]
+    __shared__ __attribute__((aligned(16))) float xch[4 * 2 * BN * kXchRow];  // [row i][column c][channel][tile]
     // per tile of the workgroup: output / residual offset of its (0, 0) pixel
     // and which of its four pixels exist (bit 0: the tile, 1: column 1, 2: row 1)
     __shared__ int64_t s_yoff[kWT], s_roff[kWT];
@@ -168,17 +175,17 @@ __global__ __launch_bounds__(256) void conv_wino_kernel(ConvArgs a, int tiles_h,
     const int rb = wi_row == 0 ? 2 : (wi_row == 2 ? 1 : (wi_row == 1 ? 2 : 3));
     const float sg = wi_row == 1 ? 1.0f : -1.0f;
     const float* xb = a.x + static_cast<int64_t>(n) * a.x_sn;  // offsets within one image fit int32
-    int off[2][4];
-    bool okp[2][4];
+    // channel-0 address of each patch position, the zero run outside the image
+    const float* pp[2][4];
 #pragma unroll
     for (int r = 0; r < 2; ++r) {
         const int hi = 2 * th - a.ph + (r == 0 ? ra : rb);
 #pragma unroll
         for (int b = 0; b < 4; ++b) {
             const int wi = 2 * tw - a.pw + b;
-            okp[r][b] = t_ok & (static_cast<unsigned>(hi) < static_cast<unsigned>(a.H)) &
-                        (static_cast<unsigned>(wi) < static_cast<unsigned>(a.W));
-            off[r][b] = okp[r][b] ? hi * static_cast<int>(a.x_sh) + wi * static_cast<int>(a.x_sw) : 0;
+            const bool ok = t_ok & (static_cast<unsigned>(hi) < static_cast<unsigned>(a.H)) &
+                            (static_cast<unsigned>(wi) < static_cast<unsigned>(a.W));
+            pp[r][b] = ok ? xb + (hi * static_cast<int>(a.x_sh) + wi * static_cast<int>(a.x_sw)) : g_wino_zero;
         }
     }
     // U float4 of (position (i, j), channel group, this lane's output channel of block cb)
@@ -186,14 +193,14 @@ __global__ __launch_bounds__(256) void conv_wino_kernel(ConvArgs a, int tiles_h,
 
     floatx4 dreg[2][2][4];
     floatx4 ureg[2][4][CB];
+    // Channels past Cin (the last step's upper half when Cin % 8 == 4) read the
+    // last 4 channels again; their U rows are zero, so they add nothing.
     auto load = [&](int s, floatx4 (&d)[2][4], floatx4 (&u)[4][CB]) {
-        const int c = s * kCK + half * 4;
-        const bool c_ok = c < a.Cin;
+        const int c = min(s * kCK + half * 4, a.Cin - 4);
 #pragma unroll
         for (int r = 0; r < 2; ++r)
 #pragma unroll
-            for (int b = 0; b < 4; ++b)
-                d[r][b] = *reinterpret_cast<const floatx4*>(xb + (c_ok ? off[r][b] + c : 0));
+            for (int b = 0; b < 4; ++b) d[r][b] = *reinterpret_cast<const floatx4*>(pp[r][b] + c);
         const int cg = s * (kCK / 4) + half;
 #pragma unroll
         for (int j = 0; j < 4; ++j)
@@ -213,15 +220,10 @@ __global__ __launch_bounds__(256) void conv_wino_kernel(ConvArgs a, int tiles_h,
     // V = (B^T d B) row i for the 4 channels of this lane half (zero outside
     // the image and past Cin), then the step's MFMAs
     auto compute = [&](int s, const floatx4 (&d)[2][4], const floatx4 (&u)[4][CB]) {
-        const bool c_ok = s * kCK + half * 4 < a.Cin;
-        const floatx4 zero = {0.0f, 0.0f, 0.0f, 0.0f};
+        (void)s;
         floatx4 sv[4];
 #pragma unroll
-        for (int b = 0; b < 4; ++b) {
-            const floatx4 da = (okp[0][b] & c_ok) ? d[0][b] : zero;
-            const floatx4 db = (okp[1][b] & c_ok) ? d[1][b] : zero;
-            sv[b] = da + sg * db;
-        }
+        for (int b = 0; b < 4; ++b) sv[b] = d[0][b] + sg * d[1][b];
         floatx4 v[4];
         v[0] = sv[0] - sv[2];
         v[1] = sv[1] + sv[2];
@@ -263,46 +265,61 @@ __global__ __launch_bounds__(256) void conv_wino_kernel(ConvArgs a, int tiles_h,
         compute(s, dreg[0], ureg[0]);
     }
 
-    // column transform in registers: P[i][0] = M0 + M1 + M2, P[i][1] = M1 - M2 - M3
-    // (32x32 block register e of lane l: tile row 8*(e/4) + 4*(l/32) + e%4, column l%32)
+    // column transform in registers: P[i][0] = M0 + M1 + M2, P[i][1] = M1 - M2 - M3.
+    // 32x32 block register e of lane l holds tile row 8*(e/4) + 4*(l/32) + e%4,
+    // column l%32: registers 4q..4q+3 are four consecutive tiles, stored as one
+    // 16-byte run of the [channel][tile] exchange (rows padded to 36 floats).
 #pragma unroll
     for (int cb = 0; cb < CB; ++cb)
 #pragma unroll
-        for (int e = 0; e < 16; ++e) {
-            const int trow = 8 * (e >> 2) + 4 * half + (e & 3);
+        for (int qd = 0; qd < 4; ++qd) {
             const int col = cb * 32 + l32;
-            const float m0 = acc[0][cb][e], m1 = acc[1][cb][e], m2 = acc[2][cb][e], m3 = acc[3][cb][e];
-            xch[((wi_row * 2 + 0) * kWT + trow) * BN + col] = m0 + m1 + m2;
-            xch[((wi_row * 2 + 1) * kWT + trow) * BN + col] = m1 - m2 - m3;
+            const int trow = 8 * qd + 4 * half;
+            floatx4 p0, p1;
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                const int e = 4 * qd + k;
+                const float m0 = acc[0][cb][e], m1 = acc[1][cb][e], m2 = acc[2][cb][e], m3 = acc[3][cb][e];
+                p0[k] = m0 + m1 + m2;
+                p1[k] = m1 - m2 - m3;
+            }
+            *reinterpret_cast<floatx4*>(&xch[((wi_row * 2 + 0) * BN + col) * kXchRow + trow]) = p0;
+            *reinterpret_cast<floatx4*>(&xch[((wi_row * 2 + 1) * BN + col) * kXchRow + trow]) = p1;
         }
     __syncthreads();
 
-    // row transform, bias, activation, residual: lane = (tile row, channel),
-    // channel fastest; every LDS read, then every residual load, then every
-    // store of the lane in flight together (straight-line, predicated)
+    // row transform, bias, activation, residual: lane = (channel, blocks of 4
+    // tile rows), channel fastest; every LDS read, then every residual load,
+    // then every store of the lane in flight together (straight-line, predicated)
     constexpr int RPT = kWT * BN / 256;  // tile rows per lane
-    constexpr int RSTEP = 256 / BN;
+    constexpr int NB = RPT / 4;          // blocks of 4 tile rows per lane
+    constexpr int GSTEP = 256 / BN;      // lanes per channel
     const int co = n0 + e_col;
     const bool co_ok = co < a.Cout;
     float yv[RPT][4];
     int64_t yo[RPT], ro[RPT];
     int vm[RPT];
 #pragma unroll
-    for (int k = 0; k < RPT; ++k) {
-        const int trow = tid / BN + k * RSTEP;
-        float p[4][2];
+    for (int bk = 0; bk < NB; ++bk) {
+        const int trow0 = 4 * (tid / BN + bk * GSTEP);
+        floatx4 p[4][2];
 #pragma unroll
         for (int i = 0; i < 4; ++i)
 #pragma unroll
-            for (int c = 0; c < 2; ++c) p[i][c] = xch[((i * 2 + c) * kWT + trow) * BN + e_col];
+            for (int c = 0; c < 2; ++c)
+                p[i][c] = *reinterpret_cast<const floatx4*>(&xch[((i * 2 + c) * BN + e_col) * kXchRow + trow0]);
 #pragma unroll
-        for (int c = 0; c < 2; ++c) {
-            yv[k][c] = p[0][c] + p[1][c] + p[2][c];      // output row 0, column c
-            yv[k][2 + c] = p[1][c] - p[2][c] - p[3][c];  // output row 1, column c
+        for (int k = 0; k < 4; ++k) {
+            const int rk = bk * 4 + k;
+#pragma unroll
+            for (int c = 0; c < 2; ++c) {
+                yv[rk][c] = p[0][c][k] + p[1][c][k] + p[2][c][k];      // output row 0, column c
+                yv[rk][2 + c] = p[1][c][k] - p[2][c][k] - p[3][c][k];  // output row 1, column c
+            }
+            yo[rk] = s_yoff[trow0 + k];
+            ro[rk] = s_roff[trow0 + k];
+            vm[rk] = co_ok ? s_vm[trow0 + k] : 0;
         }
-        yo[k] = s_yoff[trow];
-        ro[k] = s_roff[trow];
-        vm[k] = co_ok ? s_vm[trow] : 0;
     }
     // pixel q = (r, c) = (q / 2, q % 2) exists when bit 0, and bit 1 for c = 1, bit 2 for r = 1
     auto pix_ok = [](int m, int q) { return (m & 1) && (!(q & 1) || (m & 2)) && (!(q & 2) || (m & 4)); };
