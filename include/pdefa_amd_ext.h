@@ -1,6 +1,7 @@
 /* pdefa_amd_ext.h — entry points of libpdefa_native.so with no counterpart in
- * the reference.  They serve benchmarking and testing of the device program;
- * the drop-in ABI (engine_c_api.h, pdefa_c_api.h) does not depend on them.
+ * the reference.  They serve benchmarking and testing of the device program,
+ * and the on-device letterbox input; the drop-in ABI (engine_c_api.h,
+ * pdefa_c_api.h) does not depend on them.
  */
 #ifndef PDEFA_AMD_EXT_H
 #define PDEFA_AMD_EXT_H
@@ -9,6 +10,7 @@
 #include <stdint.h>
 
 #include "engine_c_api.h"
+#include "pdefa_c_api.h"
 
 #ifdef __cplusplus
 extern "C" {
@@ -35,6 +37,29 @@ PDEFA_EXPORT EngineStatus pdefa_amd_session_step_times(EngineSession* sess, int3
  * engine_session_run. */
 PDEFA_EXPORT EngineStatus pdefa_amd_session_step_repeat(EngineSession* sess, int32_t step, int32_t iters,
                                                         double* out_ms);
+
+/* On-device letterbox input (no counterpart in the reference, whose
+ * pdefa_preprocess_letterbox, imageloader/src/preprocess.cpp:15-144, runs on
+ * the host): input `input_index` of the session becomes the letterbox of the
+ * `count` images (batch = count, planar F32 [count, 3, target_h, target_w],
+ * with cfg's target size, scale and pad value), computed on the GPU at the
+ * next engine_session_run from the images' 8-bit pixels, which are copied
+ * into pinned memory by this call (the images may be freed afterwards).
+ * metas_out (count entries, may be NULL) receives each image's
+ * PdefaPreprocessMeta, as pdefa_preprocess_letterbox would.  The values
+ * equal pdefa_preprocess_letterbox's bit for bit.  engine_session_set_input
+ * on the same index replaces it. */
+PDEFA_EXPORT EngineStatus pdefa_amd_session_set_images(EngineSession* sess, int32_t input_index, int32_t count,
+                                                       const PdefaImage* const* images,
+                                                       const PdefaPreprocessConfig* cfg,
+                                                       PdefaPreprocessMeta* metas_out);
+
+/* A PdefaImage holding a copy of `width` x `height` interleaved 8-bit pixels
+ * with `channels` = 1, 3 or 4 (no counterpart in the reference, which builds
+ * images only by decoding files, pdefa_c_api.cpp:28-82); free it with
+ * pdefa_image_free.  NULL on invalid arguments (pdefa_last_error says why). */
+PDEFA_EXPORT PdefaImage* pdefa_amd_image_from_pixels(const uint8_t* pixels, int32_t width, int32_t height,
+                                                     int32_t channels);
 
 /* Text dump of the session's current device program (one line per kernel). */
 PDEFA_EXPORT EngineStatus pdefa_amd_session_plan(const EngineSession* sess, char* buf, size_t cap, size_t* out_len);

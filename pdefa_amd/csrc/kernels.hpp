@@ -150,6 +150,18 @@ struct ConvDirectArgs {
 };
 void launch_conv_direct(const ConvDirectArgs& a, hipStream_t s);
 
+// Letterbox of one interleaved 8-bit image (ch = 1, 3 or 4) into the planar
+// fp32 tensor dst[3][th][tw]: the scaled window (sw x sh at px, py) is
+// bilinear-sampled with inv = 1/ratio, the rest is `pad`.
+struct LetterboxArgs {
+    const uint8_t* src = nullptr;
+    int32_t w = 0, h = 0, ch = 0;
+    float* dst = nullptr;
+    int32_t tw = 0, th = 0, sw = 0, sh = 0, px = 0, py = 0;
+    float inv = 1.0f, scale = 1.0f, pad = 0.0f;
+};
+void launch_letterbox(const LetterboxArgs& a, hipStream_t s);
+
 // Elementwise over out's logical shape; a/b are broadcast views of the same rank.
 enum EltOp : int32_t {
     kEltCopy = 0,

@@ -511,6 +511,62 @@ void launch_detect_decode(const DetectDecodeArgs& a, hipStream_t s) {
         hipLaunchKernelGGL(detect_decode_kernel<0>, grid, dim3(256), 0, s, a, static_cast<int32_t>(N), static_cast<int32_t>(A));
 }
 
+// Letterbox of one interleaved 8-bit image into a planar fp32 [3, th, tw]
+// tensor (imageloader/src/preprocess.cpp:15-144): lane = one output pixel,
+// three channels.  Pixels outside the scaled window take the pad value as
+// is; inside, source x = dx * (1/ratio) truncated, x0 clamped to w-2, and
+// (p00*w0 + p10*w1)*wy0 + (p01*w0 + p11*w1)*wy1 with the scale folded into
+// the row weights, every product and sum rounded separately (contraction
+// into fused multiply-adds is off here: it would also take fx = sx - x0
+// from the unrounded product), as the host path computes it.
+__global__ __launch_bounds__(256) void letterbox_kernel(LetterboxArgs a) {
+#pragma clang fp contract(off)
+    const int idx = blockIdx.x * 256 + threadIdx.x;
+    if (idx >= a.tw * a.th) return;
+    const int oy = idx / a.tw, ox = idx - oy * a.tw;
+    const int dx = ox - a.px, dy = oy - a.py;
+    const size_t plane = static_cast<size_t>(a.tw) * a.th;
+    float v[3] = {a.pad, a.pad, a.pad};
+    if (dx >= 0 && dx < a.sw && dy >= 0 && dy < a.sh) {
+        const float sx = static_cast<float>(dx) * a.inv;
+        int x0 = static_cast<int>(sx);
+        if (x0 > a.w - 2 && a.w > 1) x0 = a.w - 2;
+        const int x1 = x0 + 1 < a.w ? x0 + 1 : x0;
+        const float fx = sx - static_cast<float>(x0);
+        const float sy = static_cast<float>(dy) * a.inv;
+        int y0 = static_cast<int>(sy);
+        if (y0 > a.h - 2 && a.h > 1) y0 = a.h - 2;
+        const int y1 = y0 + 1 < a.h ? y0 + 1 : y0;
+        const float fy = sy - static_cast<float>(y0);
+        const float wy0 = (1.0f - fy) * a.scale, wy1 = fy * a.scale;
+        const float w0 = 1.0f - fx, w1 = fx;
+        const uint8_t* r0 = a.src + static_cast<size_t>(y0) * a.w * a.ch;
+        const uint8_t* r1 = a.src + static_cast<size_t>(y1) * a.w * a.ch;
+#pragma unroll
+        for (int c = 0; c < 3; ++c) {
+            const int sc = a.ch == 1 ? 0 : c;
+            const float p00 = r0[x0 * a.ch + sc], p10 = r0[x1 * a.ch + sc];
+            const float p01 = r1[x0 * a.ch + sc], p11 = r1[x1 * a.ch + sc];
+            const float top = p00 * w0 + p10 * w1;
+            const float bot = p01 * w0 + p11 * w1;
+            v[c] = top * wy0 + bot * wy1;
+        }
+    }
+#pragma unroll
+    for (int c = 0; c < 3; ++c) a.dst[c * plane + idx] = v[c];
+}
+
+void launch_letterbox(const LetterboxArgs& a, hipStream_t s) {
+    if (!a.src || !a.dst) throw std::runtime_error("letterbox: null pointer");
+    if (a.w <= 0 || a.h <= 0 || (a.ch != 1 && a.ch != 3 && a.ch != 4)) throw std::runtime_error("letterbox: image");
+    if (a.tw <= 0 || a.th <= 0 || static_cast<int64_t>(a.tw) * a.th >= (int64_t{1} << 31))
+        throw std::runtime_error("letterbox: target size");
+    if (a.sw < 1 || a.sh < 1 || a.px < 0 || a.py < 0 || a.px + a.sw > a.tw || a.py + a.sh > a.th)
+        throw std::runtime_error("letterbox: geometry");
+    const int64_t total = static_cast<int64_t>(a.tw) * a.th;
+    hipLaunchKernelGGL(letterbox_kernel, dim3(static_cast<unsigned>((total + 255) / 256)), dim3(256), 0, s, a);
+}
+
 // Direct convolution: lane = one output pixel, CB output channels of the
 // workgroup's channel block.  Weights are pre-packed [ceil(Cout/CB)][K][CB]
 // (K = Cin*KH*KW, k = (ci, kh, kw)) so the CB weights of one k are one

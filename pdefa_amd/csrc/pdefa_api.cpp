@@ -12,6 +12,7 @@
 #include <string>
 #include <vector>
 
+#include "letterbox.hpp"
 #include "../../include/pdefa_amd_ext.h"
 #include "../../include/pdefa_c_api.h"
 #include "api_internal.hpp"
@@ -85,10 +86,9 @@ std::unique_ptr<PdefaImage> load_pnm(const std::string& path, std::string* why) 
 // with the scale folded into the row weights; pad value written raw; NCHW.
 void letterbox(const PdefaImage& img, int tw, int th, float scale, float pad, float* out, PdefaPreprocessMeta* m) {
     const int sw_src = img.width, sh_src = img.height, ch = img.channels;
-    const float ratio = std::min(static_cast<float>(tw) / sw_src, static_cast<float>(th) / sh_src);
-    const int sw = std::clamp(static_cast<int>(std::round(sw_src * ratio)), 1, tw);
-    const int sh = std::clamp(static_cast<int>(std::round(sh_src * ratio)), 1, th);
-    const int px = (tw - sw) / 2, py = (th - sh) / 2;
+    const pdefa::LetterboxGeometry g = pdefa::letterbox_geometry(sw_src, sh_src, tw, th);
+    const float ratio = g.ratio;
+    const int sw = g.scaled_w, sh = g.scaled_h, px = g.pad_x, py = g.pad_y;
     const size_t plane = static_cast<size_t>(tw) * th;
     std::fill(out, out + 3 * plane, pad);
     const float inv = 1.0f / ratio;
@@ -300,6 +300,68 @@ PDEFA_EXPORT EngineStatus pdefa_amd_session_step_repeat(EngineSession* sess, int
     return guarded([&] {
         clear_error();
         *out_ms = sess->inner->repeat_step(step, iters);
+        return ENGINE_OK;
+    });
+}
+
+PDEFA_EXPORT PdefaImage* pdefa_amd_image_from_pixels(const uint8_t* pixels, int32_t width, int32_t height,
+                                                     int32_t channels) {
+    clear_error();
+    if (!pixels || width <= 0 || height <= 0 || (channels != 1 && channels != 3 && channels != 4)) {
+        set_error("image_from_pixels: null pixels, empty size or unsupported channel count");
+        return nullptr;
+    }
+    try {
+        auto img = std::make_unique<PdefaImage>();
+        img->width = width;
+        img->height = height;
+        img->channels = channels;
+        img->pixels.assign(pixels, pixels + static_cast<size_t>(width) * height * channels);
+        return img.release();
+    } catch (const std::exception& e) {
+        set_error(e.what());
+        return nullptr;
+    }
+}
+
+PDEFA_EXPORT EngineStatus pdefa_amd_session_set_images(EngineSession* sess, int32_t input_index, int32_t count,
+                                                       const PdefaImage* const* images,
+                                                       const PdefaPreprocessConfig* cfg,
+                                                       PdefaPreprocessMeta* metas_out) {
+    if (!sess || sess->magic != kMagicSession) return ENGINE_ERR_INVALID_HANDLE;
+    if (!images || !cfg) return ENGINE_ERR_NULL_PTR;
+    if (count <= 0 || cfg->target_w <= 0 || cfg->target_h <= 0) return ENGINE_ERR_INVALID_ARG;
+    return guarded([&] {
+        clear_error();
+        std::vector<pdefa::ImageRef> refs;
+        for (int32_t i = 0; i < count; ++i) {
+            const PdefaImage* im = images[i];
+            if (!im) {
+                set_error("image is NULL");
+                return ENGINE_ERR_NULL_PTR;
+            }
+            if (im->pixels.empty() || im->width <= 0 || im->height <= 0 ||
+                (im->channels != 1 && im->channels != 3 && im->channels != 4)) {
+                set_error("image is empty or has an unsupported channel count");
+                return ENGINE_ERR_INVALID_ARG;
+            }
+            refs.push_back({im->pixels.data(), im->width, im->height, im->channels});
+        }
+        const std::vector<pdefa::LetterboxGeometry> geo =
+            sess->inner->set_images(input_index, refs, cfg->target_w, cfg->target_h, cfg->scale, cfg->pad_value);
+        if (metas_out)
+            for (int32_t i = 0; i < count; ++i) {
+                PdefaPreprocessMeta& m = metas_out[i];
+                m.target_w = cfg->target_w;
+                m.target_h = cfg->target_h;
+                m.orig_w = refs[i].width;
+                m.orig_h = refs[i].height;
+                m.pad_x = geo[i].pad_x;
+                m.pad_y = geo[i].pad_y;
+                m.scaled_w = geo[i].scaled_w;
+                m.scaled_h = geo[i].scaled_h;
+                m.ratio = geo[i].ratio;
+            }
         return ENGINE_OK;
     });
 }

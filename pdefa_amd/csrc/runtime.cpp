@@ -175,11 +175,61 @@ Session::~Session() {
     }
     for (hipStream_t s : side_streams_) (void)hipStreamDestroy(s);
     if (stream_) (void)hipStreamDestroy(stream_);
+    if (dev_px_) (void)hipFree(dev_px_);
+    if (host_px_) (void)hipHostFree(host_px_);
 }
 
 void Session::set_input(int32_t idx, const HostTensor* t) {
     if (idx < 0 || idx >= static_cast<int32_t>(inputs_.size())) return;  // ignored, as the reference does
     inputs_[idx] = t;
+    if (idx < static_cast<int32_t>(staged_.size())) staged_[idx].images.clear();
+}
+
+std::vector<LetterboxGeometry> Session::set_images(int32_t idx, const std::vector<ImageRef>& images, int32_t tw,
+                                                   int32_t th, float scale, float pad) {
+    if (idx < 0 || idx >= static_cast<int32_t>(inputs_.size())) throw std::runtime_error("input index out of range");
+    if (images.empty()) throw std::runtime_error("set_images: no images");
+    if (tw <= 0 || th <= 0) throw std::runtime_error("set_images: target size must be positive");
+    if (!device_available()) throw std::runtime_error("no HIP device available for the session");
+    size_t total = 0;
+    for (const ImageRef& im : images) {
+        if (!im.pixels || im.width <= 0 || im.height <= 0 || (im.channels != 1 && im.channels != 3 && im.channels != 4))
+            throw std::runtime_error("set_images: empty image or unsupported channel count");
+        total += static_cast<size_t>(im.width) * im.height * im.channels;
+        total = (total + 255) / 256 * 256;
+    }
+    // the previous run's upload has finished reading the pinned staging
+    if (stream_) PDEFA_HIP(hipStreamSynchronize(stream_));
+    if (total > host_px_cap_) {
+        if (host_px_) (void)hipHostFree(host_px_);
+        host_px_ = nullptr;
+        host_px_cap_ = 0;
+        PDEFA_HIP(hipHostMalloc(reinterpret_cast<void**>(&host_px_), total, hipHostMallocDefault));
+        host_px_cap_ = total;
+    }
+    if (staged_.size() < inputs_.size()) staged_.resize(inputs_.size());
+    StagedInput& st = staged_[idx];
+    st.images.clear();
+    st.tw = tw;
+    st.th = th;
+    st.scale = scale;
+    st.pad = pad;
+    std::vector<LetterboxGeometry> geo;
+    size_t off = 0;
+    for (const ImageRef& im : images) {
+        const size_t n = static_cast<size_t>(im.width) * im.height * im.channels;
+        std::memcpy(host_px_ + off, im.pixels, n);
+        StagedImage si;
+        si.offset = off;
+        si.img = im;
+        si.img.pixels = nullptr;
+        si.g = letterbox_geometry(im.width, im.height, tw, th);
+        st.images.push_back(si);
+        geo.push_back(si.g);
+        off = (off + n + 255) / 256 * 256;
+    }
+    inputs_[idx] = nullptr;
+    return geo;
 }
 
 const HostTensor* Session::output(int32_t idx) const {
@@ -497,8 +547,44 @@ void Session::launch_all(hipStream_t s) {
 void Session::upload_inputs() {
     const Plan& plan = prep_->plan;
     for (size_t i = 0; i < inputs_.size(); ++i) {
-        const HostTensor* t = inputs_[i];
         float* dst = prep_->arena + plan.bufs.at(plan.input_bufs[i]).offset;
+        if (i < staged_.size() && !staged_[i].images.empty()) {
+            const StagedInput& st = staged_[i];
+            const StagedImage& last = st.images.back();
+            const size_t bytes = last.offset + static_cast<size_t>(last.img.width) * last.img.height * last.img.channels;
+            if (bytes > dev_px_cap_) {
+                PDEFA_HIP(hipStreamSynchronize(stream_));
+                if (dev_px_) (void)hipFree(dev_px_);
+                dev_px_ = nullptr;
+                dev_px_cap_ = 0;
+                PDEFA_HIP(hipMalloc(reinterpret_cast<void**>(&dev_px_), bytes));
+                dev_px_cap_ = bytes;
+            }
+            PDEFA_HIP(hipMemcpyAsync(dev_px_, host_px_, bytes, hipMemcpyHostToDevice, stream_));
+            const size_t plane = static_cast<size_t>(st.tw) * st.th;
+            for (size_t b = 0; b < st.images.size(); ++b) {
+                const StagedImage& si = st.images[b];
+                k::LetterboxArgs la;
+                la.src = dev_px_ + si.offset;
+                la.w = si.img.width;
+                la.h = si.img.height;
+                la.ch = si.img.channels;
+                la.dst = dst + b * 3 * plane;
+                la.tw = st.tw;
+                la.th = st.th;
+                la.sw = si.g.scaled_w;
+                la.sh = si.g.scaled_h;
+                la.px = si.g.pad_x;
+                la.py = si.g.pad_y;
+                la.inv = 1.0f / si.g.ratio;
+                la.scale = st.scale;
+                la.pad = st.pad;
+                k::launch_letterbox(la, stream_);
+            }
+            PDEFA_HIP(hipGetLastError());
+            continue;
+        }
+        const HostTensor* t = inputs_[i];
         PDEFA_HIP(hipMemcpyAsync(dst, t->data, t->nbytes, hipMemcpyHostToDevice, stream_));
     }
 }
@@ -516,6 +602,11 @@ void Session::run() {
     if (!device_available()) throw std::runtime_error("no HIP device available for the session");
     std::vector<std::vector<int64_t>> dims;
     for (size_t i = 0; i < inputs_.size(); ++i) {
+        if (i < staged_.size() && !staged_[i].images.empty()) {
+            const StagedInput& st = staged_[i];
+            dims.push_back({static_cast<int64_t>(st.images.size()), 3, st.th, st.tw});
+            continue;
+        }
         const HostTensor* t = inputs_[i];
         if (!t) throw std::runtime_error("input " + std::to_string(i) + " is not set");
         if (t->dtype != kF32) throw std::runtime_error("input " + std::to_string(i) + " must be F32");

@@ -15,6 +15,7 @@
 
 #include "host_tensor.hpp"
 #include "kernels.hpp"
+#include "letterbox.hpp"
 #include "model.hpp"
 #include "planner.hpp"
 
@@ -62,6 +63,14 @@ class Session {
     int32_t num_inputs() const { return model_->num_inputs(); }
     int32_t num_outputs() const { return model_->num_outputs(); }
     void set_input(int32_t idx, const HostTensor* t);
+    // Input `idx` becomes the letterbox of `images` (batch = images.size(),
+    // planar fp32 [n, 3, th, tw]) computed on the device at the next run: the
+    // 8-bit pixels are copied now into pinned staging memory (the caller may
+    // release them), uploaded and letterboxed on the session stream before
+    // the program.  Returns each image's geometry.  set_input(idx, ...)
+    // replaces it.
+    std::vector<LetterboxGeometry> set_images(int32_t idx, const std::vector<ImageRef>& images, int32_t tw,
+                                              int32_t th, float scale, float pad);
     void run();  // throws
     const HostTensor* output(int32_t idx) const;
 
@@ -120,6 +129,24 @@ class Session {
     void launch_one(const Launch& l, hipStream_t s);
     void upload_inputs();
     void download_outputs();
+
+    // Device letterbox input (set_images): pinned copy of the pixels, the
+    // device buffer they are uploaded to, and per image its geometry.
+    struct StagedImage {
+        size_t offset = 0;
+        ImageRef img;  // pixels unused (they live in host_px_ at offset)
+        LetterboxGeometry g;
+    };
+    struct StagedInput {
+        std::vector<StagedImage> images;
+        int32_t tw = 0, th = 0;
+        float scale = 1.0f, pad = 0.0f;
+    };
+    std::vector<StagedInput> staged_;  // per input; empty images = host tensor input
+    uint8_t* host_px_ = nullptr;       // pinned
+    size_t host_px_cap_ = 0;
+    uint8_t* dev_px_ = nullptr;
+    size_t dev_px_cap_ = 0;
 
     Model* model_;
     std::shared_ptr<DeviceModel> dev_;

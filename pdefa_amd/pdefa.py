@@ -123,6 +123,9 @@ def _lib() -> C.CDLL:
         "pdefa_load_image_as_tensor": (st, [C.c_char_p, i32, i32, pvp]),
         "pdefa_map_box_to_original": (st, [C.POINTER(f32), C.POINTER(_PreMeta), C.POINTER(f32)]),
         "pdefa_map_point_to_original": (st, [C.POINTER(f32), C.POINTER(f32), C.POINTER(_PreMeta)]),
+        # extensions (include/pdefa_amd_ext.h)
+        "pdefa_amd_image_from_pixels": (vp, [C.POINTER(C.c_uint8), i32, i32, i32]),
+        "pdefa_amd_session_set_images": (st, [vp, i32, i32, pvp, C.POINTER(_PreConfig), C.POINTER(_PreMeta)]),
     }
     for name in ("add", "sub", "mul", "div"):
         sig[f"engine_ops_{name}"] = (st, [vp, vp, pvp])
@@ -538,6 +541,23 @@ class Image:
         except Exception:
             pass
 
+    @classmethod
+    def from_array(cls, arr) -> "Image":
+        """An image holding a copy of an HxW or HxWxC (C = 1, 3, 4) uint8 array
+        (extension: the reference builds images only from files)."""
+        import numpy as np
+        a = np.ascontiguousarray(arr, dtype=np.uint8)
+        if a.ndim == 2:
+            a = a[:, :, None]
+        if a.ndim != 3 or a.shape[2] not in (1, 3, 4) or a.shape[0] == 0 or a.shape[1] == 0:
+            raise PdefaError(f"from_array: expected HxW or HxWxC (C = 1, 3, 4) uint8, got shape {a.shape}")
+        h = _lib().pdefa_amd_image_from_pixels(a.ctypes.data_as(C.POINTER(C.c_uint8)), a.shape[1], a.shape[0],
+                                               a.shape[2])
+        if not h:
+            raw = _lib().pdefa_last_error()
+            raise PdefaError(f"from_array: {raw.decode('utf-8', 'replace') if raw else 'unknown'}")
+        return cls(h)
+
     @property
     def width(self) -> int:
         return int(_lib().pdefa_image_width(self._handle))
@@ -718,6 +738,24 @@ class Session:
     def set_input(self, index: int, tensor: Tensor) -> None:
         _check(_lib().engine_session_set_input(self._handle, int(index), tensor.raw), "session_set_input")
         self._input_refs[index] = tensor
+
+    def set_images(self, index: int, images, target_w: int = 640, target_h: int = 640, scale: float = 1.0 / 255.0,
+                   pad_value: float = 0.0) -> List[PreprocessMeta]:
+        """Input `index` becomes the letterbox of `images` (a batch), computed
+        on the GPU at the next run from their 8-bit pixels; same values as
+        preprocess_letterbox on each image.  Returns the per-image metas
+        (extension, include/pdefa_amd_ext.h)."""
+        imgs = [im if isinstance(im, Image) else Image.from_array(im) for im in images]
+        if not imgs:
+            raise PdefaError("set_images: no images")
+        arr = (C.c_void_p * len(imgs))(*[im._handle.value for im in imgs])
+        cfg = _PreConfig(target_w, target_h, scale, pad_value)
+        metas = (_PreMeta * len(imgs))()
+        _check(_lib().pdefa_amd_session_set_images(self._handle, int(index), len(imgs),
+                                                   C.cast(arr, C.POINTER(C.c_void_p)), C.byref(cfg), metas),
+               "session_set_images")
+        self._input_refs.pop(index, None)
+        return [PreprocessMeta.from_c(m) for m in metas]
 
     def run(self) -> None:
         _check(_lib().engine_session_run(self._handle), "session_run")

@@ -334,3 +334,93 @@ def test_batch_inference(tmp_path):
         s.set_input(0, t)
         s.run()
         assert np.allclose(out.to_numpy(), s.output(0).to_numpy(), atol=1e-4, rtol=1e-4)
+
+
+# ---------------------------------------------------------------- on-device letterbox (extension)
+
+def _synthetic_images():
+    rng = np.random.default_rng(21)
+    return [rng.integers(0, 256, (720, 1280, 3), dtype=np.uint8),
+            rng.integers(0, 256, (768, 1024, 3), dtype=np.uint8),
+            rng.integers(0, 256, (800, 800), dtype=np.uint8),         # gray
+            rng.integers(0, 256, (517, 333, 4), dtype=np.uint8),      # RGBA
+            rng.integers(0, 256, (1, 1, 3), dtype=np.uint8),          # 1x1
+            rng.integers(0, 256, (3, 2, 3), dtype=np.uint8)]
+
+
+def test_image_from_array_roundtrip():
+    a = np.arange(2 * 3 * 4, dtype=np.uint8).reshape(2, 3, 4)
+    im = pdefa.Image.from_array(a)
+    assert (im.width, im.height, im.channels) == (3, 2, 4)
+    assert im.tobytes() == a.tobytes()
+    g = pdefa.Image.from_array(np.full((5, 7), 9, np.uint8))
+    assert (g.width, g.height, g.channels) == (7, 5, 1)
+    with pytest.raises(pdefa.PdefaError):
+        pdefa.Image.from_array(np.zeros((4, 4, 2), np.uint8))
+    with pytest.raises(pdefa.PdefaError):
+        pdefa.Image.from_array(np.zeros((0, 4, 3), np.uint8))
+
+
+def test_from_array_letterbox_matches_numpy_restatement():
+    """Host letterbox of an in-memory image = the numpy restatement (which
+    follows imageloader/src/preprocess.cpp:15-144) within 1 ulp-scale."""
+    img = _synthetic_images()[0]
+    t, meta = pdefa.preprocess_letterbox(pdefa.Image.from_array(img), 640, 640, 1 / 255, 114 / 255)
+    want, wmeta = ys.letterbox(img, 640, 640, 1 / 255, 114 / 255)
+    assert (meta.pad_x, meta.pad_y, meta.scaled_w, meta.scaled_h) == (wmeta["pad_x"], wmeta["pad_y"],
+                                                                       wmeta["scaled_w"], wmeta["scaled_h"])
+    np.testing.assert_allclose(t.to_numpy(), want, atol=1e-6, rtol=0)
+
+
+def _identity_engine(tmp_path):
+    """Input -> Mul by 1 -> output: the letterboxed tensor itself, exactly (the
+    letterbox extrapolates past the last source pixel when it upscales, so
+    values can be negative)."""
+    b = ys.GraphBuilder()
+    one = b.const("/id/one", np.ones(1, np.float32))
+    y = b.node("Mul", "/id/Mul", [-1, one])
+    path = str(tmp_path / "identity.engine")
+    ys.save(b.model([1, 3, 640, 640], [1, 3, 640, 640], [y]), path)
+    return path
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("tw,th", [(640, 640), (320, 256)])
+def test_device_letterbox_bit_exact(tmp_path, tw, th):
+    """set_images (letterbox on the GPU from 8-bit pixels) equals the host
+    pdefa_preprocess_letterbox bit for bit, metas included, over RGB, gray,
+    RGBA, 1x1 and 3x2 images in one batch."""
+    ctx = pdefa.Context()
+    model = pdefa.Model(ctx, _identity_engine(tmp_path))
+    imgs = [pdefa.Image.from_array(a) for a in _synthetic_images()]
+    host = [pdefa.preprocess_letterbox(im, tw, th, 1 / 255, 114 / 255) for im in imgs]
+    s = pdefa.Session(ctx, model)
+    metas = s.set_images(0, imgs, tw, th, 1 / 255, 114 / 255)
+    s.run()
+    got = s.output(0).to_numpy()
+    assert got.shape == (len(imgs), 3, th, tw)
+    for i, (t, m) in enumerate(host):
+        assert metas[i] == m
+        np.testing.assert_array_equal(got[i:i + 1], t.to_numpy())
+    # set_input replaces the device letterbox input
+    s.set_input(0, host[0][0])
+    s.run()
+    np.testing.assert_array_equal(s.output(0).to_numpy(), host[0][0].to_numpy())
+
+
+@pytest.mark.gpu
+def test_batch_inference_device_preprocess(tmp_path):
+    """BatchInference with the letterbox on the GPU gives the host path's
+    outputs and metas exactly."""
+    path = str(tmp_path / "y.engine")
+    ys.save(ys.build_yolov8("n", seed=0, imgsz=160), path)
+    paths = [write_ppm(tmp_path / f"im{i}.ppm", 60 + 10 * i, 50, (30 * i, 100, 200 - 20 * i)) for i in range(3)]
+    ctx = pdefa.Context()
+    model = pdefa.Model(ctx, path)
+    with pdefa.BatchInference(ctx, model, batch_size=2, num_threads=2) as batch:
+        host = batch.run(paths, 160, 160)
+    with pdefa.BatchInference(ctx, model, batch_size=2, num_threads=2, device_preprocess=True) as batch:
+        dev = batch.run(paths, 160, 160)
+    for (a, ma), (b, mb) in zip(host, dev):
+        assert ma == mb
+        np.testing.assert_array_equal(a.to_numpy(), b.to_numpy())
