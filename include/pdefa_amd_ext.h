@@ -61,6 +61,31 @@ PDEFA_EXPORT EngineStatus pdefa_amd_session_set_images(EngineSession* sess, int3
 PDEFA_EXPORT PdefaImage* pdefa_amd_image_from_pixels(const uint8_t* pixels, int32_t width, int32_t height,
                                                      int32_t channels);
 
+/* One detection of pdefa_amd_session_decode: the box in original-image
+ * pixels (letterbox-mapped when a meta is given), score and class as the
+ * reference's decode_yolo returns them (its Python floats are doubles), and
+ * the head anchor the detection came from. */
+typedef struct {
+    double x1, y1, x2, y2, conf;
+    int32_t cls;
+    int32_t anchor;
+} PdefaAmdDetection;
+
+/* YOLO decode + per-class greedy NMS of output `output_index` of the last
+ * engine_session_run, on the GPU (no counterpart in the reference, whose
+ * decode_yolo runs in Python, pdefa/python/src/pdefa/_bindings.py:1095-1212,
+ * with the same results: same detections, order and double values).  The
+ * output must be a [N, 4 + classes, A] head resident from that run.  metas:
+ * NULL (boxes stay in input pixels) or one PdefaPreprocessMeta per image
+ * (n_metas == N).  dets receives N * max_det entries (image i's first
+ * counts[i] entries at dets + i * max_det, best first); counts receives N.
+ * At most 16384 anchors per image may pass conf_thres (ENGINE_ERR_RUNTIME
+ * otherwise). */
+PDEFA_EXPORT EngineStatus pdefa_amd_session_decode(EngineSession* sess, int32_t output_index,
+                                                   const PdefaPreprocessMeta* metas, int32_t n_metas,
+                                                   double conf_thres, double iou_thres, int32_t max_det,
+                                                   PdefaAmdDetection* dets, int32_t* counts);
+
 /* Text dump of the session's current device program (one line per kernel). */
 PDEFA_EXPORT EngineStatus pdefa_amd_session_plan(const EngineSession* sess, char* buf, size_t cap, size_t* out_len);
 

@@ -23,6 +23,7 @@ SOURCES = [
     "kernels/conv_mfma.hip",
     "kernels/conv_wino.hip",
     "kernels/ops.hip",
+    "kernels/yolo_decode.hip",
     "model.cpp",
     "planner.cpp",
     "runtime.cpp",

@@ -162,6 +162,33 @@ struct LetterboxArgs {
 };
 void launch_letterbox(const LetterboxArgs& a, hipStream_t s);
 
+// YOLO head decode + per-class greedy NMS (the reference's decode_yolo in
+// float64), per image of a [N, 4 + classes, A] head; see yolo_decode.hip.
+struct YoloDetection {
+    double x1, y1, x2, y2, conf;
+    int32_t cls, anchor;
+};
+constexpr int kYoloMaxCandidates = 16384;  // anchors passing conf_thres per image
+struct YoloDecodeArgs {
+    const float* out = nullptr;  // head element (n, c, a) at out[n*sn + c*sc + a*sa]
+    int64_t sn = 0, sc = 0, sa = 0;
+    int32_t N = 0, C = 0, A = 0;
+    double conf = 0.25, iou = 0.45;
+    int32_t max_det = 300;
+    int32_t max_cand = 0, max_cand_pow2 = 0;  // candidate capacity (<= A) and its power-of-two ceiling
+    const double* meta = nullptr;  // per image: ratio, pad_x, pad_y, orig_w, orig_h; nullptr = no mapping
+    // workspace, per image: boxes [A][4], class [A], keys [A], run info [A]; counts [N]
+    double* boxes = nullptr;
+    int32_t* cls = nullptr;
+    unsigned long long* keys = nullptr;
+    int32_t* seg = nullptr;
+    int32_t* counts = nullptr;
+    // results: dets [N][max_det], ndet [N] (-1: more than max_cand candidates)
+    YoloDetection* dets = nullptr;
+    int32_t* ndet = nullptr;
+};
+void launch_yolo_decode(const YoloDecodeArgs& a, hipStream_t s);
+
 // Elementwise over out's logical shape; a/b are broadcast views of the same rank.
 enum EltOp : int32_t {
     kEltCopy = 0,

@@ -366,6 +366,40 @@ PDEFA_EXPORT EngineStatus pdefa_amd_session_set_images(EngineSession* sess, int3
     });
 }
 
+PDEFA_EXPORT EngineStatus pdefa_amd_session_decode(EngineSession* sess, int32_t output_index,
+                                                   const PdefaPreprocessMeta* metas, int32_t n_metas,
+                                                   double conf_thres, double iou_thres, int32_t max_det,
+                                                   PdefaAmdDetection* dets, int32_t* counts) {
+    if (!sess || sess->magic != kMagicSession) return ENGINE_ERR_INVALID_HANDLE;
+    if (!counts || (max_det > 0 && !dets)) return ENGINE_ERR_NULL_PTR;
+    if (max_det < 0 || n_metas < 0 || (n_metas > 0 && !metas)) return ENGINE_ERR_INVALID_ARG;
+    return guarded([&] {
+        clear_error();
+        std::vector<double> m;
+        for (int32_t i = 0; i < n_metas; ++i)
+            m.insert(m.end(), {static_cast<double>(metas[i].ratio), static_cast<double>(metas[i].pad_x),
+                               static_cast<double>(metas[i].pad_y), static_cast<double>(metas[i].orig_w),
+                               static_cast<double>(metas[i].orig_h)});
+        const auto res = sess->inner->decode(output_index, m, conf_thres, iou_thres, max_det);
+        static_assert(sizeof(PdefaAmdDetection) == sizeof(pdefa::k::YoloDetection), "detection layout");
+        for (size_t i = 0; i < res.size(); ++i) {
+            counts[i] = static_cast<int32_t>(res[i].size());
+            for (size_t j = 0; j < res[i].size(); ++j) {
+                const pdefa::k::YoloDetection& d = res[i][j];
+                PdefaAmdDetection& o = dets[i * static_cast<size_t>(max_det) + j];
+                o.x1 = d.x1;
+                o.y1 = d.y1;
+                o.x2 = d.x2;
+                o.y2 = d.y2;
+                o.conf = d.conf;
+                o.cls = d.cls;
+                o.anchor = d.anchor;
+            }
+        }
+        return ENGINE_OK;
+    });
+}
+
 PDEFA_EXPORT EngineStatus pdefa_amd_session_plan(const EngineSession* sess, char* buf, size_t cap, size_t* out_len) {
     if (!sess || sess->magic != kMagicSession) return ENGINE_ERR_INVALID_HANDLE;
     return guarded([&] {

@@ -177,6 +177,104 @@ Session::~Session() {
     if (stream_) (void)hipStreamDestroy(stream_);
     if (dev_px_) (void)hipFree(dev_px_);
     if (host_px_) (void)hipHostFree(host_px_);
+    if (dec_ws_) (void)hipFree(dec_ws_);
+    if (dec_host_) (void)hipHostFree(dec_host_);
+}
+
+std::vector<std::vector<k::YoloDetection>> Session::decode(int32_t idx, const std::vector<double>& metas, double conf,
+                                                           double iou, int32_t max_det) {
+    if (!prep_ || runs == 0) throw std::runtime_error("decode needs a completed run");
+    const Plan& plan = prep_->plan;
+    if (idx < 0 || idx >= static_cast<int32_t>(plan.outputs.size())) throw std::runtime_error("output index out of range");
+    const VRef& o = plan.outputs[idx];
+    const auto& od = plan.output_dims[idx];
+    std::vector<int64_t> dims(od.begin(), od.end());
+    while (dims.size() > 3 && dims.front() == 1) dims.erase(dims.begin());
+    if (o.rank != static_cast<int32_t>(od.size()) || dims.size() != 3)
+        throw std::runtime_error("decode: output must be [N, 4 + classes, A]");
+    if (max_det < 0) throw std::runtime_error("decode: max_det must be >= 0");
+    const int32_t N = static_cast<int32_t>(dims[0]), C = static_cast<int32_t>(dims[1]), A = static_cast<int32_t>(dims[2]);
+    if (!metas.empty() && metas.size() != static_cast<size_t>(5) * N)
+        throw std::runtime_error("decode: one letterbox meta per image expected");
+    const int r = o.rank;
+    k::YoloDecodeArgs a;
+    a.out = prep_->arena + plan.bufs.at(o.buf).offset + o.off;
+    a.sn = o.str[r - 3];
+    a.sc = o.str[r - 2];
+    a.sa = o.str[r - 1];
+    a.N = N;
+    a.C = C;
+    a.A = A;
+    a.conf = conf;
+    a.iou = iou;
+    a.max_det = max_det;
+    a.max_cand = std::min(A, k::kYoloMaxCandidates);
+    a.max_cand_pow2 = 1;
+    while (a.max_cand_pow2 < a.max_cand) a.max_cand_pow2 <<= 1;
+    // workspace: boxes, keys (8-byte), class, run info, counts, ndet, metas, detections
+    auto up8 = [](size_t b) { return (b + 255) / 256 * 256; };
+    const size_t na = static_cast<size_t>(N) * A;
+    const size_t b_boxes = up8(na * 4 * sizeof(double)), b_keys = up8(na * 8), b_cls = up8(na * 4), b_seg = up8(na * 4);
+    const size_t b_cnt = up8(static_cast<size_t>(N) * 4), b_ndet = up8(static_cast<size_t>(N) * 4);
+    const size_t b_meta = up8(static_cast<size_t>(N) * 5 * sizeof(double));
+    const size_t b_dets = up8(static_cast<size_t>(N) * std::max(max_det, 1) * sizeof(k::YoloDetection));
+    const size_t need = b_boxes + b_keys + b_cls + b_seg + b_cnt + b_ndet + b_meta + b_dets;
+    PDEFA_HIP(hipStreamSynchronize(stream_));
+    if (need > dec_ws_bytes_) {
+        if (dec_ws_) (void)hipFree(dec_ws_);
+        dec_ws_ = nullptr;
+        dec_ws_bytes_ = 0;
+        PDEFA_HIP(hipMalloc(&dec_ws_, need));
+        dec_ws_bytes_ = need;
+    }
+    const size_t host_need = b_ndet + b_dets + b_meta;
+    if (host_need > dec_host_bytes_) {
+        if (dec_host_) (void)hipHostFree(dec_host_);
+        dec_host_ = nullptr;
+        dec_host_bytes_ = 0;
+        PDEFA_HIP(hipHostMalloc(&dec_host_, host_need, hipHostMallocDefault));
+        dec_host_bytes_ = host_need;
+    }
+    char* w = static_cast<char*>(dec_ws_);
+    a.boxes = reinterpret_cast<double*>(w);
+    w += b_boxes;
+    a.keys = reinterpret_cast<unsigned long long*>(w);
+    w += b_keys;
+    a.cls = reinterpret_cast<int32_t*>(w);
+    w += b_cls;
+    a.seg = reinterpret_cast<int32_t*>(w);
+    w += b_seg;
+    a.counts = reinterpret_cast<int32_t*>(w);
+    w += b_cnt;
+    a.ndet = reinterpret_cast<int32_t*>(w);
+    w += b_ndet;
+    double* dmeta = reinterpret_cast<double*>(w);
+    w += b_meta;
+    a.dets = reinterpret_cast<k::YoloDetection*>(w);
+    char* h = static_cast<char*>(dec_host_);
+    int32_t* h_ndet = reinterpret_cast<int32_t*>(h);
+    k::YoloDetection* h_dets = reinterpret_cast<k::YoloDetection*>(h + b_ndet);
+    double* h_meta = reinterpret_cast<double*>(h + b_ndet + b_dets);
+    if (!metas.empty()) {
+        std::memcpy(h_meta, metas.data(), metas.size() * sizeof(double));
+        PDEFA_HIP(hipMemcpyAsync(dmeta, h_meta, metas.size() * sizeof(double), hipMemcpyHostToDevice, stream_));
+        a.meta = dmeta;
+    }
+    k::launch_yolo_decode(a, stream_);
+    PDEFA_HIP(hipGetLastError());
+    PDEFA_HIP(hipMemcpyAsync(h_ndet, a.ndet, static_cast<size_t>(N) * 4, hipMemcpyDeviceToHost, stream_));
+    if (max_det > 0)
+        PDEFA_HIP(hipMemcpyAsync(h_dets, a.dets, static_cast<size_t>(N) * max_det * sizeof(k::YoloDetection),
+                                 hipMemcpyDeviceToHost, stream_));
+    PDEFA_HIP(hipStreamSynchronize(stream_));
+    std::vector<std::vector<k::YoloDetection>> out(N);
+    for (int32_t i = 0; i < N; ++i) {
+        if (h_ndet[i] < 0)
+            throw std::runtime_error("decode: more than " + std::to_string(a.max_cand) +
+                                     " anchors pass conf_thres in one image");
+        out[i].assign(h_dets + static_cast<size_t>(i) * max_det, h_dets + static_cast<size_t>(i) * max_det + h_ndet[i]);
+    }
+    return out;
 }
 
 void Session::set_input(int32_t idx, const HostTensor* t) {

@@ -73,6 +73,12 @@ class Session {
                                               int32_t th, float scale, float pad);
     void run();  // throws
     const HostTensor* output(int32_t idx) const;
+    // YOLO decode + per-class NMS of output `idx` (a [N, 4 + classes, A] head
+    // resident from the last run) on the device; metas: 5 doubles per image
+    // (ratio, pad_x, pad_y, orig_w, orig_h) or empty for no letterbox
+    // mapping.  Returns each image's detections in the reference's order.
+    std::vector<std::vector<k::YoloDetection>> decode(int32_t idx, const std::vector<double>& metas, double conf,
+                                                      double iou, int32_t max_det);
 
     // Re-runs the prepared program `iters` times on the input already in HBM
     // (no host copies); returns the elapsed device time in ms (HIP events).
@@ -143,6 +149,11 @@ class Session {
         float scale = 1.0f, pad = 0.0f;
     };
     std::vector<StagedInput> staged_;  // per input; empty images = host tensor input
+    // decode workspace (device, grow-only) and its pinned result staging
+    void* dec_ws_ = nullptr;
+    size_t dec_ws_bytes_ = 0;
+    void* dec_host_ = nullptr;
+    size_t dec_host_bytes_ = 0;
     uint8_t* host_px_ = nullptr;       // pinned
     size_t host_px_cap_ = 0;
     uint8_t* dev_px_ = nullptr;

@@ -126,6 +126,8 @@ def _lib() -> C.CDLL:
         # extensions (include/pdefa_amd_ext.h)
         "pdefa_amd_image_from_pixels": (vp, [C.POINTER(C.c_uint8), i32, i32, i32]),
         "pdefa_amd_session_set_images": (st, [vp, i32, i32, pvp, C.POINTER(_PreConfig), C.POINTER(_PreMeta)]),
+        "pdefa_amd_session_decode": (st, [vp, i32, C.POINTER(_PreMeta), i32, C.c_double, C.c_double, i32,
+                                          C.POINTER(_Detection), C.POINTER(i32)]),
     }
     for name in ("add", "sub", "mul", "div"):
         sig[f"engine_ops_{name}"] = (st, [vp, vp, pvp])
@@ -136,6 +138,12 @@ def _lib() -> C.CDLL:
         fn.restype, fn.argtypes = res, args
     _lib_cache = L
     return L
+
+
+class _Detection(C.Structure):
+    # PdefaAmdDetection (include/pdefa_amd_ext.h)
+    _fields_ = [("x1", C.c_double), ("y1", C.c_double), ("x2", C.c_double), ("y2", C.c_double),
+                ("conf", C.c_double), ("cls", C.c_int32), ("anchor", C.c_int32)]
 
 
 class PdefaError(RuntimeError):
@@ -775,10 +783,42 @@ class Session:
         _check(_lib().engine_session_debug_intermediate(self._handle, int(idx), C.byref(h)), "debug_intermediate")
         return Tensor(h, owns=False)
 
+    def decode(self, metas=None, conf_thres: float = 0.25, iou_thres: float = 0.45, max_det: int = 300,
+               output_index: int = 0, with_anchor: bool = False) -> List[List[dict]]:
+        """decode_yolo of every image of output `output_index` (the [N, 4 +
+        classes, A] head of the last run), computed on the GPU: the same
+        detections, order and values as decode_yolo on each image.  metas:
+        None or one PreprocessMeta per image (extension, include/pdefa_amd_ext.h)."""
+        n_img = int(self.output(output_index).shape[0])
+        if metas is not None and len(metas) != n_img:
+            raise PdefaError(f"decode: {len(metas)} metas for {n_img} images")
+        cm = (_PreMeta * n_img)(*[m.to_c() for m in metas]) if metas is not None else None
+        dets = (_Detection * max(1, n_img * max_det))()
+        counts = (C.c_int32 * n_img)()
+        _check(_lib().pdefa_amd_session_decode(self._handle, int(output_index), cm, n_img if cm is not None else 0,
+                                               float(conf_thres), float(iou_thres), int(max_det), dets, counts),
+               "session_decode")
+        out = []
+        for i in range(n_img):
+            rows = []
+            for j in range(counts[i]):
+                d = dets[i * max_det + j]
+                r = {"x1": d.x1, "y1": d.y1, "x2": d.x2, "y2": d.y2, "conf": d.conf, "cls": int(d.cls)}
+                if with_anchor:
+                    r["anchor"] = int(d.anchor)
+                rows.append(r)
+            out.append(rows)
+        return out
+
     def run_and_decode(self, meta: Optional[PreprocessMeta] = None, conf_thres: float = 0.25,
                        iou_thres: float = 0.45) -> List[dict]:
+        """run() then decode_yolo of image 0 of output 0; the decode runs on the
+        GPU (Session.decode) with decode_yolo's results."""
         self.run()
-        return decode_yolo(self.output(0), meta, conf_thres, iou_thres)
+        res = self.decode([meta] if meta is not None else None, conf_thres, iou_thres)
+        if len(res) != 1:
+            raise PdefaError(f"decode_yolo: unexpected output shape {tuple(self.output(0).shape)}")
+        return res[0]
 
 
 # ---------------------------------------------------------------- decode

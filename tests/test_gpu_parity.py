@@ -408,3 +408,86 @@ def test_yolov8m_b16_vs_reference_golden(tmp_path):
     for i in (2, 9, 15):
         single = run_engine(path, x[i:i + 1])[0]
         assert_close_anchors(out[i:i + 1], single, f"yolov8m b16 image {i} vs b1")
+
+
+# ---- YOLO decode + NMS on the device (extension) against the oracle's restatement
+
+def _head_engine(tmp_path, c, a):
+    """Input [N, c, a] -> Mul by 1 -> output: a session whose output is any head."""
+    b = ys.GraphBuilder()
+    one = b.const("/id/one", np.ones(1, np.float32))
+    y = b.node("Mul", "/id/Mul", [-1, one])
+    path = str(tmp_path / "head.engine")
+    ys.save(b.model([1, c, a], [1, c, a], [y]), path)
+    return path
+
+
+def _np_tensor(a):
+    import ctypes
+    from pdefa_amd import pdefa
+    a = np.ascontiguousarray(a, np.float32)
+    t = pdefa.tensor_empty(list(a.shape))
+    pdefa._check(pdefa._lib().engine_tensor_copy_from(t.raw, ctypes.c_void_p(a.ctypes.data), a.nbytes), "copy")
+    return t
+
+
+def _device_decode(path, heads, metas=None, **kw):
+    from pdefa_amd import pdefa
+    ctx = pdefa.Context()
+    model = pdefa.Model(ctx, path)
+    s = pdefa.Session(ctx, model)
+    s.set_input(0, _np_tensor(heads))
+    s.run()
+    return s.decode(metas, with_anchor=True, **kw)
+
+
+def _tricky_heads(n, nc, a, seed):
+    """Heads with score ties inside and across classes, many candidates of one
+    class, duplicate and nested boxes, values on coarse grids so that equal
+    scores and IoUs at the threshold occur."""
+    rng = np.random.default_rng(seed)
+    h = np.zeros((n, 4 + nc, a), np.float32)
+    h[:, 0] = rng.integers(0, 64, (n, a)) * 4.0
+    h[:, 1] = rng.integers(0, 64, (n, a)) * 4.0
+    h[:, 2] = rng.integers(1, 16, (n, a)) * 8.0
+    h[:, 3] = rng.integers(1, 16, (n, a)) * 8.0
+    h[:, 4:] = rng.integers(0, 17, (n, nc, a)) / 16.0
+    h[:, 4 + min(3, nc - 1), : a // 3] = 0.9375  # one crowded class
+    h[:, :4, 10:20] = h[:, :4, 0:1]  # duplicate boxes
+    return h
+
+
+@pytest.mark.parametrize("n,nc,a,conf,iou,max_det", [(1, 80, 8400, 0.25, 0.45, 300), (3, 5, 1000, 0.5, 0.5, 300),
+                                                    (2, 7, 777, 0.0625, 0.3, 50), (1, 3, 300, 2.0, 0.45, 300),
+                                                    (2, 4, 2000, 0.001, 0.65, 1000)])
+def test_device_decode_matches_reference_restatement(tmp_path, n, nc, a, conf, iou, max_det):
+    print(f"[case] device decode n={n} nc={nc} a={a} conf={conf}", flush=True)
+    heads = _tricky_heads(n, nc, a, seed=a + n)
+    path = _head_engine(tmp_path, 4 + nc, a)
+    got = _device_decode(path, heads, conf_thres=conf, iou_thres=iou, max_det=max_det)
+    assert len(got) == n
+    for i in range(n):
+        want = decode_ref.decode(heads[i].tolist(), None, conf, iou, max_det)
+        assert got[i] == want, (i, len(got[i]), len(want))
+
+
+def test_device_decode_yolov8n_with_metas(yolov8n):
+    """Batch of 3 letterboxed images: device decode = decode_yolo = the
+    oracle's restatement, with the letterbox mapping."""
+    from pdefa_amd import pdefa
+    print("[case] yolov8n b3 device decode", flush=True)
+    model, path = yolov8n
+    x, metas = ys.yolo_inputs(3)
+    ctx = pdefa.Context()
+    m = pdefa.Model(ctx, path)
+    s = pdefa.Session(ctx, m)
+    s.set_input(0, _np_tensor(x))
+    s.run()
+    pm = [pdefa.PreprocessMeta(**md) for md in metas]
+    got = s.decode(pm, with_anchor=True)
+    out = s.output(0).to_numpy()
+    for i in range(3):
+        want = decode_ref.decode(out[i].tolist(), metas[i])
+        assert got[i] == want
+        assert [{k: v for k, v in d.items() if k != "anchor"} for d in got[i]] == decode_yolo(out[i:i + 1], metas[i])
+    assert sum(len(g) for g in got) > 0
