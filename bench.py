@@ -174,6 +174,52 @@ def ingest_pmc(fetch_csv: str, write_csv: str):
     print(json.dumps(out))
 
 
+def pipeline(path: str, batch: int = 8, iters: int = 20):
+    """8-bit images in host memory -> post-NMS detections in host memory, per
+    batch of YOLOv8n: letterbox (on the GPU from the pixels), the program and
+    decode + NMS (on the GPU), against the same session fed by the host
+    letterbox with decode_yolo on the host."""
+    from pdefa_amd import pdefa
+
+    raws = [ys.synth_image(i, *ys.ASPECT_SIZES[i % len(ys.ASPECT_SIZES)]) for i in range(batch)]
+    imgs = [pdefa.Image.from_array(a) for a in raws]
+    ctx = pdefa.Context()
+    model = pdefa.Model(ctx, path)
+    s = pdefa.Session(ctx, model)
+    args = (640, 640, 1.0 / 255.0, 114.0 / 255.0)
+
+    def device_pass():
+        metas = s.set_images(0, imgs, *args)
+        s.run()
+        return s.decode(metas)
+
+    def host_pass():
+        pre = [pdefa.preprocess_letterbox(im, *args) for im in imgs]
+        s.set_input(0, pdefa.ops_concat([t for t, _ in pre], axis=0))
+        s.run()
+        out = s.output(0).to_numpy()
+        return [pdefa.decode_yolo(out[i:i + 1], pre[i][1]) for i in range(batch)]
+
+    dev, host = device_pass(), host_pass()
+    same = all([{k: v for k, v in d.items()} for d in a] == b for a, b in zip(dev, host))
+    t0 = time.perf_counter()
+    for _ in range(iters):
+        device_pass()
+    dev_ms = (time.perf_counter() - t0) * 1e3 / iters
+    h_iters = max(1, iters // 4)
+    t0 = time.perf_counter()
+    for _ in range(h_iters):
+        host_pass()
+    host_ms = (time.perf_counter() - t0) * 1e3 / h_iters
+    n_det = sum(len(d) for d in dev)
+    return dict(workload=f"YOLOv8n b{batch}: {batch} synthetic 8-bit images (1280x720, 1024x768, 800x800) in host "
+                         f"memory -> post-NMS detections ({n_det} boxes) in host memory",
+                value=round(batch * 1000.0 / dev_ms, 2), unit="images/s", ms_per_batch=round(dev_ms, 3),
+                host_pre_post=dict(value=round(batch * 1000.0 / host_ms, 2), ms_per_batch=round(host_ms, 3),
+                                   note="host letterbox (C++), H2D of the float tensor, host decode_yolo"),
+                same_detections=bool(same))
+
+
 def cpu_baseline(path: str, x: np.ndarray, budget_s: float = 12.0):
     """The reference CPU engine (oracle/_ref, built from the reference sources)
     on the same YOLOv8n b1 workload: median Session::run over a bounded sample."""
@@ -264,6 +310,10 @@ def main():
         roof = roofline(tmp, 50)
         log(f"roofline conv3x3 [{roof['launch_shape']}]: {roof['launch_us']} us/launch, "
             f"{roof['achieved']} TFLOP/s ({roof['frac']:.1%})")
+        pipe = pipeline(path)
+        log(f"pipeline b8 (pixels -> detections): {pipe['value']} images/s with letterbox + decode on the GPU, "
+            f"{pipe['host_pre_post']['value']} images/s with them on the host; same detections: "
+            f"{pipe['same_detections']}")
         cpu = None
         if not args.no_cpu:
             x1, _ = ys.yolo_inputs(1)
@@ -293,6 +343,7 @@ def main():
         "yolov8m_b16": m16,
         "conv_tflops_b1": round(b1["conv_tflops"], 3),
         "first_run_ms": {"b1": round(b1["first"], 1), "b8": round(b8["first"], 1)},
+        "pipeline_b8": pipe,
         "roofline": roof,
         "cpu_baseline": cpu,
     }
