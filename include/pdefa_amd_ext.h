@@ -22,17 +22,20 @@ extern "C" {
  * stream.  Requires one completed engine_session_run. */
 PDEFA_EXPORT EngineStatus pdefa_amd_session_replay(EngineSession* sess, int32_t iters, double* out_ms);
 
-/* Average device time of each step of the prepared program over `iters`
- * step-by-step replays (HIP events between launches on the session stream).
- * Per step: ms[i], kind[i] (0 conv_mfma, 1 conv_direct, 2 eltwise,
- * 3 maxpool, 4 resize, 5 softmax) and flops[i] (2*N*Cout*Cin*KH*KW*Ho*Wo for
- * convs, else 0).  *n = number of steps; at most `cap` entries are written. */
+/* Average device time of each launch of the prepared program over `iters`
+ * launch-by-launch replays (HIP events between launches on the session
+ * stream).  A launch is one step of the plan, or several convs issued as one
+ * grouped launch.  Per launch: ms[i], kind[i] (0 conv_mfma, 1 conv_direct,
+ * 2 eltwise, 3 maxpool, 4 resize, 5 softmax, 6 maxpool chain, 7 detect decode)
+ * and flops[i] (sum of 2*N*Cout*Cin*KH*KW*Ho*Wo over its convs, else 0).
+ * *n = number of launches; at most `cap` entries are written. */
 PDEFA_EXPORT EngineStatus pdefa_amd_session_step_times(EngineSession* sess, int32_t iters, double* ms, int32_t* kind,
                                                        int64_t* flops, int32_t cap, int32_t* n);
 
-/* Launches step `step` of the prepared program `iters` times back to back
- * (after one warm-up launch) between two HIP events on the session's stream;
- * *out_ms = average device time per launch.  Every step is idempotent (it
+/* Issues launch `step` of the prepared program (numbered as in
+ * pdefa_amd_session_step_times) `iters` times back to back (after one warm-up
+ * launch) between two HIP events on the session's stream; *out_ms = average
+ * device time per launch.  Every launch is idempotent (it
  * reads its inputs and overwrites its outputs).  Requires one completed
  * engine_session_run. */
 PDEFA_EXPORT EngineStatus pdefa_amd_session_step_repeat(EngineSession* sess, int32_t step, int32_t iters,
@@ -90,7 +93,10 @@ PDEFA_EXPORT EngineStatus pdefa_amd_session_decode(EngineSession* sess, int32_t 
 PDEFA_EXPORT EngineStatus pdefa_amd_session_plan(const EngineSession* sess, char* buf, size_t cap, size_t* out_len);
 
 /* Plans `m` for inputs of the given shape without touching a GPU and returns
- * the program text (planner tests on hosts without a device). */
+ * the program text (planner tests on hosts without a device).  With
+ * PDEFA_PLAN_GROUP_ALL=1 in the environment, launch shapes come from the cost
+ * model and every conv group the grouping pass offers is taken (a test of the
+ * reordering that grouped launches imply). */
 PDEFA_EXPORT EngineStatus pdefa_amd_plan_model(const EngineModel* m, const int64_t* shape, int32_t ndim, char* buf,
                                                size_t cap, size_t* out_len);
 

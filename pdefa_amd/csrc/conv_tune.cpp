@@ -3,6 +3,7 @@
 #include <algorithm>
 #include <array>
 #include <map>
+#include <memory>
 #include <mutex>
 #include <stdexcept>
 
@@ -18,8 +19,11 @@ constexpr double kKeepModelChoice = 0.97;      // another shape must beat the mo
 
 using Key = std::array<int32_t, 20>;
 
+using GroupKey = std::vector<int32_t>;
+
 std::mutex g_mu;
 std::map<Key, k::ConvLaunchShape> g_cache;
+std::map<GroupKey, ConvGroupTiming> g_group_cache;
 
 Key make_key(const ConvQuery& q, int device) {
     return {device, q.N,  q.H,  q.W,  q.Cin, q.Ho, q.Wo, q.Cout, q.KH, q.KW,
@@ -55,58 +59,29 @@ void launch(const k::ConvArgs& a, int tile, bool vec, hipStream_t s) {
         k::launch_conv_mfma(a, tile, vec, s);
 }
 
-// Average ms of `reps` back-to-back launches (after one untimed launch).
-double time_launch(const k::ConvArgs& a, int tile, bool vec, hipStream_t s, Events& ev, int reps) {
-    launch(a, tile, vec, s);
-    PDEFA_HIP(hipEventRecord(ev.a, s));
-    for (int i = 0; i < reps; ++i) launch(a, tile, vec, s);
-    PDEFA_HIP(hipEventRecord(ev.b, s));
-    PDEFA_HIP(hipEventSynchronize(ev.b));
-    float ms = 0.0f;
-    PDEFA_HIP(hipEventElapsedTime(&ms, ev.a, ev.b));
-    return static_cast<double>(ms) / reps;
-}
-
-}  // namespace
-
-k::ConvLaunchShape tune_conv(const ConvQuery& q, hipStream_t s) {
-    int device = 0;
-    PDEFA_HIP(hipGetDevice(&device));
-    const Key key = make_key(q, device);
-    std::lock_guard<std::mutex> lock(g_mu);
-    if (auto it = g_cache.find(key); it != g_cache.end()) return it->second;
-
-    const int64_t M = static_cast<int64_t>(q.N) * q.Ho * q.Wo;
-    const int K = q.KH * q.KW * q.Cin;
-    std::vector<k::ConvLaunchShape> all = k::conv_candidates(M, q.Cout, K, true, q.wino, q.Cin);
-    // the cost model's best implicit-GEMM shapes, plus every Winograd shape
-    std::vector<k::ConvLaunchShape> cands;
-    for (const auto& c : all)
-        if (k::is_wino_tile(c.tile) || cands.size() < kMaxCandidates) cands.push_back(c);
-    const int64_t out_elems = M * q.Cout;
-    int max_splits = 1;
-    std::vector<k::ConvLaunchShape> usable;
-    for (const auto& c : cands) {
-        if (c.splits > 1 && static_cast<int64_t>(c.splits) * out_elems * 4 > kMaxWorkspaceBytes) continue;
-        usable.push_back(c);
-        max_splits = std::max(max_splits, c.splits);
-    }
-    k::ConvLaunchShape best = cands.front();
-    if (usable.size() > 1) {
-        // Scratch tensors of the layer's shape, dense channels-last; values
-        // do not affect timing (zeros).  The residual, when the layer has one,
-        // reads the output tensor itself: each element is read and then
-        // written by the same lane.
-        const int64_t x_elems = static_cast<int64_t>(q.N) * q.H * q.W * q.Cin;
-        const int64_t w_elems = std::max(k::packed_weight_elems(q.Cout, K),
-                                         q.wino ? k::wino_packed_elems(q.Cout, q.Cin) : int64_t{0});
-        DeviceBuffer x(x_elems), y(out_elems), w(w_elems), bias(q.Cout),
-            ws(max_splits > 1 ? static_cast<int64_t>(max_splits) * out_elems : 1);
+// Dense channels-last scratch tensors of one layer's shape; values do not
+// affect timing (zeros).  The residual, when the layer has one, reads the
+// output tensor itself: each element is read and then written by the same
+// lane.
+struct LayerScratch {
+    int64_t x_elems, out_elems, w_elems;
+    DeviceBuffer x, y, w, bias, ws;
+    k::ConvArgs a;
+    LayerScratch(const ConvQuery& q, int max_splits, hipStream_t s)
+        : x_elems(static_cast<int64_t>(q.N) * q.H * q.W * q.Cin),
+          out_elems(static_cast<int64_t>(q.N) * q.Ho * q.Wo * q.Cout),
+          w_elems(std::max(k::packed_weight_elems(q.Cout, q.KH * q.KW * q.Cin),
+                           q.wino ? k::wino_packed_elems(q.Cout, q.Cin) : int64_t{0})),
+          x(x_elems),
+          y(out_elems),
+          w(w_elems),
+          bias(q.Cout),
+          ws(max_splits > 1 ? static_cast<int64_t>(max_splits) * out_elems : 1) {
         PDEFA_HIP(hipMemsetAsync(x.p, 0, static_cast<size_t>(x_elems) * 4, s));
         PDEFA_HIP(hipMemsetAsync(w.p, 0, static_cast<size_t>(w_elems) * 4, s));
         PDEFA_HIP(hipMemsetAsync(bias.p, 0, static_cast<size_t>(q.Cout) * 4, s));
         PDEFA_HIP(hipMemsetAsync(y.p, 0, static_cast<size_t>(out_elems) * 4, s));
-        k::ConvArgs a;
+        const int K = q.KH * q.KW * q.Cin;
         a.x = x.p;
         a.N = q.N;
         a.H = q.H;
@@ -142,17 +117,64 @@ k::ConvLaunchShape tune_conv(const ConvQuery& q, hipStream_t s) {
         a.ktiles = (K + k::kConvBK - 1) / k::kConvBK;
         a.act = q.act;
         a.ws = ws.p;
+    }
+    void shape(const k::ConvLaunchShape& ls) {
+        a.splits = ls.splits;
+        a.kt_per_split = ls.kt_per_split;
+    }
+};
+
+// Average ms per repetition of `body` (after one untimed call).
+template <typename F>
+double time_reps(F&& body, hipStream_t s, Events& ev, int reps) {
+    body();
+    PDEFA_HIP(hipEventRecord(ev.a, s));
+    for (int i = 0; i < reps; ++i) body();
+    PDEFA_HIP(hipEventRecord(ev.b, s));
+    PDEFA_HIP(hipEventSynchronize(ev.b));
+    float ms = 0.0f;
+    PDEFA_HIP(hipEventElapsedTime(&ms, ev.a, ev.b));
+    return static_cast<double>(ms) / reps;
+}
+
+// Repetitions for about 100 us of timed work, at least 3.
+int reps_for(double first_ms) { return std::max(3, std::min(20, static_cast<int>(0.1 / std::max(first_ms, 1e-3)))); }
+
+}  // namespace
+
+k::ConvLaunchShape tune_conv(const ConvQuery& q, hipStream_t s) {
+    int device = 0;
+    PDEFA_HIP(hipGetDevice(&device));
+    const Key key = make_key(q, device);
+    std::lock_guard<std::mutex> lock(g_mu);
+    if (auto it = g_cache.find(key); it != g_cache.end()) return it->second;
+
+    const int64_t M = static_cast<int64_t>(q.N) * q.Ho * q.Wo;
+    const int K = q.KH * q.KW * q.Cin;
+    std::vector<k::ConvLaunchShape> all = k::conv_candidates(M, q.Cout, K, true, q.wino, q.Cin);
+    // the cost model's best implicit-GEMM shapes, plus every Winograd shape
+    std::vector<k::ConvLaunchShape> cands;
+    for (const auto& c : all)
+        if (k::is_wino_tile(c.tile) || cands.size() < kMaxCandidates) cands.push_back(c);
+    const int64_t out_elems = M * q.Cout;
+    int max_splits = 1;
+    std::vector<k::ConvLaunchShape> usable;
+    for (const auto& c : cands) {
+        if (c.splits > 1 && static_cast<int64_t>(c.splits) * out_elems * 4 > kMaxWorkspaceBytes) continue;
+        usable.push_back(c);
+        max_splits = std::max(max_splits, c.splits);
+    }
+    k::ConvLaunchShape best = cands.front();
+    if (usable.size() > 1) {
+        LayerScratch L(q, max_splits, s);
         Events ev;
-        // repetitions: about 100 us of timed work per candidate, at least 3
-        a.splits = usable.front().splits;
-        a.kt_per_split = usable.front().kt_per_split;
-        const double first = time_launch(a, usable.front().tile, q.vec, s, ev, 1);
-        const int reps = std::max(3, std::min(20, static_cast<int>(0.1 / std::max(first, 1e-3))));
+        L.shape(usable.front());
+        const double first = time_reps([&] { launch(L.a, usable.front().tile, q.vec, s); }, s, ev, 1);
+        const int reps = reps_for(first);
         double best_ms = 0.0;
         for (size_t i = 0; i < usable.size(); ++i) {
-            a.splits = usable[i].splits;
-            a.kt_per_split = usable[i].kt_per_split;
-            const double ms = time_launch(a, usable[i].tile, q.vec, s, ev, reps);
+            L.shape(usable[i]);
+            const double ms = time_reps([&] { launch(L.a, usable[i].tile, q.vec, s); }, s, ev, reps);
             if (i == 0 || ms < best_ms * kKeepModelChoice) {
                 best_ms = ms;
                 best = usable[i];
@@ -162,6 +184,56 @@ k::ConvLaunchShape tune_conv(const ConvQuery& q, hipStream_t s) {
     }
     g_cache.emplace(key, best);
     return best;
+}
+
+ConvGroupTiming tune_conv_group(const std::vector<ConvQuery>& qs, const std::vector<k::ConvLaunchShape>& solo,
+                                hipStream_t s) {
+    if (qs.size() != solo.size() || qs.size() < 2 || qs.size() > static_cast<size_t>(k::kMaxConvGroup))
+        throw std::runtime_error("tune_conv_group: bad group");
+    int device = 0;
+    PDEFA_HIP(hipGetDevice(&device));
+    GroupKey key;
+    for (size_t i = 0; i < qs.size(); ++i) {
+        const Key k1 = make_key(qs[i], device);
+        key.insert(key.end(), k1.begin(), k1.end());
+        key.push_back(solo[i].tile);
+        key.push_back(solo[i].splits);
+        key.push_back(solo[i].kt_per_split);
+    }
+    std::lock_guard<std::mutex> lock(g_mu);
+    if (auto it = g_group_cache.find(key); it != g_group_cache.end()) return it->second;
+
+    std::vector<std::unique_ptr<LayerScratch>> L;
+    for (size_t i = 0; i < qs.size(); ++i) {
+        if (!qs[i].vec) throw std::runtime_error("tune_conv_group: grouped layers need vector loads");
+        L.push_back(std::make_unique<LayerScratch>(qs[i], solo[i].splits, s));
+        L.back()->shape(solo[i]);
+    }
+    Events ev;
+    auto separate = [&] {
+        for (size_t i = 0; i < qs.size(); ++i) launch(L[i]->a, solo[i].tile, qs[i].vec, s);
+    };
+    ConvGroupTiming r;
+    const int reps = reps_for(time_reps(separate, s, ev, 1));
+    r.separate_ms = time_reps(separate, s, ev, reps);
+    std::vector<k::ConvArgs> probs(qs.size());
+    for (int t = 0; t < k::kNumConvTiles; ++t) {
+        const int kg = k::conv_tile_shape(t).kg;
+        for (size_t i = 0; i < qs.size(); ++i) {
+            probs[i] = L[i]->a;
+            probs[i].splits = 1;
+            probs[i].kt_per_split = (probs[i].ktiles + kg - 1) / kg * kg;
+        }
+        const double ms = time_reps(
+            [&] { k::launch_conv_mfma_group(probs.data(), static_cast<int>(probs.size()), t, s); }, s, ev, reps);
+        if (r.tile < 0 || ms < r.group_ms) {
+            r.tile = t;
+            r.group_ms = ms;
+        }
+    }
+    PDEFA_HIP(hipStreamSynchronize(s));
+    g_group_cache.emplace(std::move(key), r);
+    return r;
 }
 
 size_t conv_tune_cache_size() {

@@ -6,6 +6,8 @@
 
 #include <hip/hip_runtime.h>
 
+#include <vector>
+
 #include "kernels.hpp"
 #include "planner.hpp"
 
@@ -13,6 +15,12 @@ namespace pdefa {
 
 // Called while planning, outside any stream capture; synchronises `s`.
 k::ConvLaunchShape tune_conv(const ConvQuery& q, hipStream_t s);
+
+// Times independent layers run one after another, each with its own launch
+// shape `solo`, against one grouped launch for every implicit-GEMM tile
+// (kept per process like tune_conv's choices).
+ConvGroupTiming tune_conv_group(const std::vector<ConvQuery>& qs, const std::vector<k::ConvLaunchShape>& solo,
+                                hipStream_t s);
 
 // Number of shapes chosen by measurement so far (tests and diagnostics).
 size_t conv_tune_cache_size();

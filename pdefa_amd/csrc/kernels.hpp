@@ -122,6 +122,18 @@ std::vector<ConvLaunchShape> conv_candidates(int64_t M, int Cout, int K, bool al
 // Cin % 4 == 0 and 16-byte aligned pixel rows).
 void launch_conv_mfma(const ConvArgs& a, int tile, bool vec, hipStream_t s);
 
+// Independent convolutions (no split-K, vector loads) issued as one launch of
+// one tile shape: workgroups of every problem run side by side, so several
+// small layers fill the chip together instead of one after another.
+constexpr int kMaxConvGroup = 8;
+struct ConvGroupArgs {
+    int32_t count = 0;
+    int32_t tile_begin[kMaxConvGroup + 1] = {};  // prefix sums of the problems' tile counts
+    int32_t m_tiles[kMaxConvGroup] = {};         // m blocks of each problem
+    ConvArgs p[kMaxConvGroup];
+};
+void launch_conv_mfma_group(const ConvArgs* probs, int count, int tile, hipStream_t s);
+
 // Winograd F(2x2,3x3) on MFMA for 3x3 / stride 1 / dilation 1 convs with
 // Cin % 4 == 0 and Cin >= 8 (any padding).  a.wpk holds the transformed
 // weights U = G g G^T as [16][ceil(Cin/8)*2][ceil(Cout/64)*64][4]

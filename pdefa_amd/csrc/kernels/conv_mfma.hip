@@ -81,8 +81,16 @@ constexpr int tile_threads() {
     return 64 * (BM / WM) * (BN / WN) * KG;
 }
 
+// XCD-aware tile order: dispatch slot `lin` (of `total`) runs on XCD lin % 8;
+// give each XCD a contiguous range of tile indices.
+__device__ __forceinline__ int xcd_tile(int lin, int total) {
+    const int q = total / kXcds, rmd = total % kXcds, xcd = lin % kXcds;
+    return xcd * q + min(xcd, rmd) + lin / kXcds;
+}
+
+// One BM x BN output tile (m block bx, n block by) of K split bz of problem a.
 template <int BM, int BN, int WM, int WN, int KG, int PF, bool VEC>
-__global__ __launch_bounds__((tile_threads<BM, BN, WM, WN, KG>())) void conv_mfma_kernel(ConvArgs a) {
+__device__ __forceinline__ void conv_tile(const ConvArgs& a, const int bx, const int by, const int bz) {
     constexpr int WAVES_M = BM / WM;
     constexpr int WAVES_N = BN / WN;
     constexpr int NT = tile_threads<BM, BN, WM, WN, KG>();  // 256 or 512 lanes
@@ -110,18 +118,6 @@ __global__ __launch_bounds__((tile_threads<BM, BN, WM, WN, KG>())) void conv_mfm
     const int wave_n = (wave / KG) / WAVES_M;
     const int HoWo = a.Ho * a.Wo;
     const int M = a.N * HoWo;
-
-    // XCD-aware tile order: dispatch slot `lin` runs on XCD lin % 8; give each
-    // XCD a contiguous range of (m-tile fastest) tile indices.
-    const int gx = gridDim.x, gxy = gridDim.x * gridDim.y;
-    const int total = gxy * gridDim.z;
-    const int lin = blockIdx.x + gx * blockIdx.y + gxy * blockIdx.z;
-    const int q = total / kXcds, rmd = total % kXcds, xcd = lin % kXcds;
-    const int tile_id = xcd * q + min(xcd, rmd) + lin / kXcds;
-    const int bz = tile_id / gxy;
-    const int bxy = tile_id - bz * gxy;
-    const int by = bxy / gx;
-    const int bx = bxy - by * gx;
 
     const int m0 = bx * BM;
     const int n0 = by * BN;
@@ -489,6 +485,32 @@ __global__ __launch_bounds__((tile_threads<BM, BN, WM, WN, KG>())) void conv_mfm
     }
 }
 
+// One problem; grid (m tiles, n tiles, K splits), tiles in XCD order with the
+// m tile fastest (neighbouring output rows share input rows, all tiles of one
+// n block share weights).
+template <int BM, int BN, int WM, int WN, int KG, int PF, bool VEC>
+__global__ __launch_bounds__((tile_threads<BM, BN, WM, WN, KG>())) void conv_mfma_kernel(ConvArgs a) {
+    const int gx = gridDim.x, gxy = gridDim.x * gridDim.y;
+    const int tile_id = xcd_tile(blockIdx.x + gx * blockIdx.y + gxy * blockIdx.z, gxy * gridDim.z);
+    const int bz = tile_id / gxy;
+    const int bxy = tile_id - bz * gxy;
+    const int by = bxy / gx;
+    conv_tile<BM, BN, WM, WN, KG, PF, VEC>(a, bxy - by * gx, by, bz);
+}
+
+// Several independent problems in one launch (no split-K): a 1-D grid over
+// the concatenated tile lists, problem p owning tiles
+// [tile_begin[p], tile_begin[p + 1]) with its m tile fastest.
+template <int BM, int BN, int WM, int WN, int KG, int PF, bool VEC>
+__global__ __launch_bounds__((tile_threads<BM, BN, WM, WN, KG>())) void conv_mfma_group_kernel(ConvGroupArgs g) {
+    const int tile_id = xcd_tile(blockIdx.x, gridDim.x);
+    int p = 0;
+    while (p + 1 < g.count && tile_id >= g.tile_begin[p + 1]) ++p;
+    const int local = tile_id - g.tile_begin[p];
+    const int by = local / g.m_tiles[p];
+    conv_tile<BM, BN, WM, WN, KG, PF, VEC>(g.p[p], local - by * g.m_tiles[p], by, 0);
+}
+
 // Sums split-K partials in split order, then bias + activation + residual.
 __global__ __launch_bounds__(256) void conv_splitk_reduce(ConvArgs a) {
     const int HoWo = a.Ho * a.Wo;
@@ -534,6 +556,21 @@ void launch_one(const ConvArgs& a, dim3 grid, hipStream_t s) {
     });
     hipLaunchKernelGGL((conv_mfma_kernel<BM, BN, WM, WN, KG, PF, VEC>), grid,
                        dim3(tile_threads<BM, BN, WM, WN, KG>()), bytes, s, a);
+}
+
+template <int BM, int BN, int WM, int WN, int KG, int PF>
+void launch_group(const ConvGroupArgs& g, hipStream_t s) {
+    constexpr size_t bytes = lds_bytes<BM, BN, KG>();
+    static std::once_flag once;
+    std::call_once(once, [] {
+        if (bytes > 65536)
+            (void)hipFuncSetAttribute(
+                reinterpret_cast<const void*>(&conv_mfma_group_kernel<BM, BN, WM, WN, KG, PF, true>),
+                hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(bytes));
+    });
+    hipLaunchKernelGGL((conv_mfma_group_kernel<BM, BN, WM, WN, KG, PF, true>),
+                       dim3(static_cast<unsigned>(g.tile_begin[g.count])), dim3(tile_threads<BM, BN, WM, WN, KG>()),
+                       bytes, s, g);
 }
 
 constexpr int kPrefetch = 2;  // register stages: loads run two steps ahead
@@ -643,9 +680,9 @@ ConvLaunchShape conv_select(int64_t M, int Cout, int K, bool allow_split, bool w
     return conv_candidates(M, Cout, K, allow_split, wino_ok, Cin).front();
 }
 
-void launch_conv_mfma(const ConvArgs& a, int tile, bool vec, hipStream_t s) {
-    const ConvTileShape sh = conv_tile_shape(tile);
-    if (sh.bm == 0) fail("unknown tile");
+namespace {
+
+void check_conv(const ConvArgs& a, const ConvTileShape& sh, bool vec) {
     if (!a.x || !a.y || !a.wpk || !a.bias) fail("null pointer");
     if (a.N <= 0 || a.H <= 0 || a.W <= 0 || a.Cin <= 0 || a.Ho <= 0 || a.Wo <= 0 || a.Cout <= 0) fail("empty shape");
     if (a.K != a.KH * a.KW * a.Cin) fail("K mismatch");
@@ -665,6 +702,15 @@ void launch_conv_mfma(const ConvArgs& a, int tile, bool vec, hipStream_t s) {
         if ((reinterpret_cast<uintptr_t>(a.x) & 15) || (a.x_sn & 3) || (a.x_sh & 3) || (a.x_sw & 3))
             fail("vector loads need 16-byte aligned rows");
     }
+}
+
+}  // namespace
+
+void launch_conv_mfma(const ConvArgs& a, int tile, bool vec, hipStream_t s) {
+    const ConvTileShape sh = conv_tile_shape(tile);
+    if (sh.bm == 0) fail("unknown tile");
+    check_conv(a, sh, vec);
+    const int64_t M = static_cast<int64_t>(a.N) * a.Ho * a.Wo;
     const int64_t gx = (M + sh.bm - 1) / sh.bm, gy = (a.Cout + sh.bn - 1) / sh.bn;
     if (gx * gy * a.splits >= (int64_t{1} << 31) || gy > 65535 || a.splits > 65535) fail("grid too large");
     const dim3 grid(static_cast<unsigned>(gx), static_cast<unsigned>(gy), static_cast<unsigned>(a.splits));
@@ -687,6 +733,43 @@ void launch_conv_mfma(const ConvArgs& a, int tile, bool vec, hipStream_t s) {
         const int64_t total = M * a.Cout;
         const unsigned blocks = static_cast<unsigned>(std::min<int64_t>((total + 255) / 256, 65535));
         hipLaunchKernelGGL(conv_splitk_reduce, dim3(blocks), dim3(256), 0, s, a);
+    }
+}
+
+void launch_conv_mfma_group(const ConvArgs* probs, int count, int tile, hipStream_t s) {
+    const ConvTileShape sh = conv_tile_shape(tile);
+    if (sh.bm == 0) fail("unknown tile");
+    if (count < 1 || count > kMaxConvGroup) fail("group size out of range");
+    ConvGroupArgs g;
+    g.count = count;
+    int64_t total = 0;
+    for (int i = 0; i < count; ++i) {
+        const ConvArgs& a = probs[i];
+        check_conv(a, sh, true);
+        if (a.splits != 1) fail("grouped problems take no split-K");
+        const int64_t M = static_cast<int64_t>(a.N) * a.Ho * a.Wo;
+        const int64_t gx = (M + sh.bm - 1) / sh.bm, gy = (a.Cout + sh.bn - 1) / sh.bn;
+        g.tile_begin[i] = static_cast<int32_t>(total);
+        g.m_tiles[i] = static_cast<int32_t>(gx);
+        g.p[i] = a;
+        total += gx * gy;
+        if (total >= (int64_t{1} << 31)) fail("grid too large");
+    }
+    g.tile_begin[count] = static_cast<int32_t>(total);
+    switch (tile) {
+        case kTile128x128: launch_group<128, 128, 64, 64, 1, kPrefetch>(g, s); break;
+        case kTile128x64: launch_group<128, 64, 64, 32, 1, kPrefetch>(g, s); break;
+        case kTile64x128: launch_group<64, 128, 32, 64, 1, kPrefetch>(g, s); break;
+        case kTile64x64: launch_group<64, 64, 32, 32, 1, kPrefetch>(g, s); break;
+        case kTile128x32: launch_group<128, 32, 32, 32, 1, kPrefetch>(g, s); break;
+        case kTile64x32K2: launch_group<64, 32, 32, 32, 2, kPrefetch>(g, s); break;
+        case kTile32x64K2: launch_group<32, 64, 32, 32, 2, kPrefetch>(g, s); break;
+        case kTile32x32K4: launch_group<32, 32, 32, 32, 4, kPrefetch>(g, s); break;
+        case kTile128x64W8: launch_group<128, 64, 32, 32, 1, kPrefetch>(g, s); break;
+        case kTile64x64K2W8: launch_group<64, 64, 32, 32, 2, kPrefetch>(g, s); break;
+        case kTile128x128W8: launch_group<128, 128, 64, 32, 1, kPrefetch>(g, s); break;
+        case kTile64x128W8: launch_group<64, 128, 32, 32, 1, kPrefetch>(g, s); break;
+        case kTile32x64K4W8: launch_group<32, 64, 32, 32, 4, kPrefetch>(g, s); break;
     }
 }
 

@@ -424,6 +424,22 @@ PDEFA_EXPORT EngineStatus pdefa_amd_plan_model(const EngineModel* m, const int64
                                                std::vector<int64_t>(shape, shape + ndim));
         pdefa::PlanOptions opt;
         if (const char* r = std::getenv("PDEFA_REUSE_MEMORY")) opt.reuse_memory = r[0] != '0';
+        if (const char* g = std::getenv("PDEFA_PLAN_GROUP_ALL"); g && g[0] == '1') {
+            // Host-only stand-ins for the device measurements: launch shapes
+            // from the cost model, and every group the grouping pass offers
+            // is taken (tests of the reordering it implies).
+            opt.tune_conv = [](const pdefa::ConvQuery& q) {
+                const int64_t M = static_cast<int64_t>(q.N) * q.Ho * q.Wo;
+                return pdefa::k::conv_select(M, q.Cout, q.KH * q.KW * q.Cin, true, q.wino, q.Cin);
+            };
+            opt.tune_group = [](const std::vector<pdefa::ConvQuery>& qs, const std::vector<pdefa::k::ConvLaunchShape>&) {
+                pdefa::ConvGroupTiming t;
+                t.tile = pdefa::k::kTile32x32K4;
+                t.separate_ms = static_cast<double>(qs.size());
+                t.group_ms = 1.0;
+                return t;
+            };
+        }
         const pdefa::Plan p = pdefa::build_plan(*m->inner, dims, opt);
         std::string s = pdefa::describe_plan(*m->inner, p);
         const pdefa::Schedule sc = pdefa::schedule_plan(p, 8);

@@ -14,6 +14,9 @@ namespace {
 
 using Dims = std::vector<int64_t>;
 
+// A grouped launch must beat the separate launches it replaces by 3%.
+constexpr double kGroupGain = 0.97;
+
 [[noreturn]] void fail(const Model& m, int node, const std::string& msg) {
     std::string where = node >= 0 && node < static_cast<int>(m.nodes.size())
                             ? " (node " + std::to_string(node) + " '" + m.nodes[node].name + "' " +
@@ -205,6 +208,82 @@ struct Val {
     VRef nhwc_view;
 };
 
+// Launch-shape query of an implicit-GEMM conv step.
+ConvQuery conv_query(const Step& s) {
+    ConvQuery q;
+    q.N = static_cast<int32_t>(s.a.dims[0]);
+    q.Cin = static_cast<int32_t>(s.a.dims[1]);
+    q.H = static_cast<int32_t>(s.a.dims[2]);
+    q.W = static_cast<int32_t>(s.a.dims[3]);
+    q.Cout = static_cast<int32_t>(s.out.dims[1]);
+    q.Ho = static_cast<int32_t>(s.out.dims[2]);
+    q.Wo = static_cast<int32_t>(s.out.dims[3]);
+    q.KH = s.KH;
+    q.KW = s.KW;
+    q.sh = s.sh;
+    q.sw = s.sw;
+    q.ph = s.ph;
+    q.pw = s.pw;
+    q.dh = s.dh;
+    q.dw = s.dw;
+    q.act = s.act;
+    q.has_res = s.has_res;
+    q.vec = s.vec;
+    q.wino = s.vec && k::wino_eligible(s.KH, s.KW, s.sh, s.sw, s.dh, s.dw, q.Cin);
+    return q;
+}
+
+// The views a step reads and writes (model weights included; they are never
+// written).  A split-K workspace counts as a write of its whole buffer.
+void step_views(const Step& s, std::vector<VRef>& rd, std::vector<VRef>& wr) {
+    rd.clear();
+    wr.clear();
+    wr.push_back(s.out);
+    rd.push_back(s.a);
+    if (s.has_res) rd.push_back(s.res);
+    switch (s.kind) {
+        case StepKind::Elt: rd.push_back(s.b); break;
+        case StepKind::MaxPoolChain:
+            wr.push_back(s.b);
+            wr.push_back(s.c);
+            break;
+        case StepKind::DetectDecode:
+            rd.push_back(s.b);
+            rd.push_back(s.c);
+            rd.push_back(s.res);
+            break;
+        default: break;
+    }
+}
+
+// Whether two views of planned buffers may share an element.  Distinct
+// buffers never do before memory is assigned; two views of one buffer are
+// disjoint when they are slices of one parent along one axis with disjoint
+// index ranges there (the producers of one concat buffer).
+bool views_may_overlap(const VRef& a, const VRef& b) {
+    if (a.buf < 0 || b.buf < 0 || a.buf != b.buf) return false;
+    if (a.rank != b.rank) return true;
+    for (int d = 0; d < a.rank; ++d)
+        if (a.str[d] != b.str[d]) return true;
+    const int64_t diff = b.off - a.off;
+    for (int d = 0; d < a.rank; ++d) {
+        if (a.str[d] <= 0 || diff % a.str[d] != 0) continue;
+        bool same_other = true;
+        int64_t row = INT64_MAX;  // smallest stride of the other (non-trivial) axes
+        for (int e = 0; e < a.rank; ++e) {
+            if (e == d) continue;
+            if (a.dims[e] != b.dims[e]) same_other = false;
+            if (a.dims[e] > 1) row = std::min(row, a.str[e]);
+        }
+        if (!same_other) continue;
+        const int64_t kk = diff / a.str[d];
+        const bool disjoint = kk >= a.dims[d] || kk + b.dims[d] <= 0;
+        const int64_t span = std::max(a.dims[d], kk + b.dims[d]) - std::min<int64_t>(0, kk);
+        if (disjoint && (row == INT64_MAX || span * a.str[d] <= row)) return false;
+    }
+    return true;
+}
+
 class Planner {
    public:
     Planner(const Model& m, const std::vector<Dims>& in_dims, const PlanOptions& opt)
@@ -219,6 +298,7 @@ class Planner {
         assign_storage();
         emit();
         fuse_steps();
+        group_convs();
         allocate();
         return std::move(plan_);
     }
@@ -837,27 +917,7 @@ class Planner {
             const bool wino = s.vec && k::wino_eligible(s.KH, s.KW, s.sh, s.sw, s.dh, s.dw, static_cast<int>(cin));
             k::ConvLaunchShape ls;
             if (opt_.tune_conv && opt_.force_tile < 0 && opt_.split_k) {
-                ConvQuery q;
-                q.N = static_cast<int32_t>(x.dims[0]);
-                q.Cin = static_cast<int32_t>(cin);
-                q.H = static_cast<int32_t>(x.dims[2]);
-                q.W = static_cast<int32_t>(x.dims[3]);
-                q.Cout = static_cast<int32_t>(cout);
-                q.Ho = static_cast<int32_t>(y.dims[2]);
-                q.Wo = static_cast<int32_t>(y.dims[3]);
-                q.KH = s.KH;
-                q.KW = s.KW;
-                q.sh = s.sh;
-                q.sw = s.sw;
-                q.ph = s.ph;
-                q.pw = s.pw;
-                q.dh = s.dh;
-                q.dw = s.dw;
-                q.act = s.act;
-                q.has_res = s.has_res;
-                q.vec = s.vec;
-                q.wino = wino;
-                ls = opt_.tune_conv(q);
+                ls = opt_.tune_conv(conv_query(s));
             } else {
                 ls = k::conv_select(M, static_cast<int>(cout), static_cast<int>(K), opt_.split_k, wino,
                                     static_cast<int>(cin));
@@ -1111,6 +1171,101 @@ class Planner {
     }
 
     // ---- 6. liveness + arena ----------------------------------------------
+    bool groupable(const Step& s) const { return s.kind == StepKind::ConvMfma && s.vec; }
+
+    // Reorders the program by list scheduling (the earliest ready step first)
+    // and, where independent implicit-GEMM convs are ready together, asks the
+    // measurement whether one grouped launch beats their own launches; a
+    // group grows one ready conv at a time while each addition pays.
+    void group_convs() {
+        if (!opt_.tune_group || !opt_.tune_conv || opt_.force_tile >= 0 || !opt_.split_k) return;
+        std::vector<Step>& st = plan_.steps;
+        const int n = static_cast<int>(st.size());
+        std::vector<std::vector<VRef>> rd(n), wr(n);
+        for (int i = 0; i < n; ++i) step_views(st[i], rd[i], wr[i]);
+        for (int i = 0; i < n; ++i)
+            if (st[i].ws_buf >= 0) {
+                VRef w;
+                w.buf = st[i].ws_buf;
+                w.rank = 1;
+                w.dims[0] = plan_.bufs[st[i].ws_buf].elems;
+                w.str[0] = 1;
+                wr[i].push_back(w);
+            }
+        auto hit = [](const std::vector<VRef>& x, const std::vector<VRef>& y) {
+            for (const VRef& u : x)
+                for (const VRef& v : y)
+                    if (views_may_overlap(u, v)) return true;
+            return false;
+        };
+        std::vector<std::vector<int>> deps(n);
+        for (int j = 0; j < n; ++j)
+            for (int i = 0; i < j; ++i)
+                if (hit(wr[i], rd[j]) || hit(wr[i], wr[j]) || hit(rd[i], wr[j])) deps[j].push_back(i);
+
+        std::vector<char> done(n, 0);
+        std::vector<Step> out;
+        int32_t next_group = 0;
+        while (static_cast<int>(out.size()) < n) {
+            std::vector<int> ready;
+            for (int j = 0; j < n; ++j) {
+                if (done[j]) continue;
+                bool ok = true;
+                for (int i : deps[j])
+                    if (!done[i]) {
+                        ok = false;
+                        break;
+                    }
+                if (ok) ready.push_back(j);
+            }
+            std::vector<int> S = {ready.front()};
+            int tile = -1;
+            if (groupable(st[S[0]])) {
+                double cur_ms = 0.0, sep_ms = 0.0;
+                for (size_t r = 1; r < ready.size() && S.size() < static_cast<size_t>(k::kMaxConvGroup); ++r) {
+                    const int c = ready[r];
+                    if (!groupable(st[c])) continue;
+                    std::vector<int> T = S;
+                    T.push_back(c);
+                    std::vector<ConvQuery> qs;
+                    std::vector<k::ConvLaunchShape> solo;
+                    for (int t : T) {
+                        qs.push_back(conv_query(st[t]));
+                        solo.push_back({st[t].tile, st[t].splits, st[t].kt_per_split});
+                    }
+                    const ConvGroupTiming g = opt_.tune_group(qs, solo);
+                    if (g.tile < 0) continue;
+                    // S alone costs cur_ms (grouped) or sep_ms (one conv); c alone
+                    // costs what the separate launches of T add to those of S
+                    const double base = (S.size() == 1 ? g.separate_ms : cur_ms + (g.separate_ms - sep_ms));
+                    if (g.group_ms < kGroupGain * base) {
+                        S = T;
+                        tile = g.tile;
+                        cur_ms = g.group_ms;
+                        sep_ms = g.separate_ms;
+                    }
+                }
+            }
+            std::sort(S.begin(), S.end());
+            for (int j : S) {
+                Step s = st[j];
+                if (S.size() > 1) {
+                    const int kg = k::conv_tile_shape(tile).kg;
+                    const int ktiles = static_cast<int>((s.a.dims[1] * s.KH * s.KW + k::kConvBK - 1) / k::kConvBK);
+                    s.group = next_group;
+                    s.tile = tile;
+                    s.splits = 1;
+                    s.kt_per_split = (ktiles + kg - 1) / kg * kg;
+                    s.ws_buf = -1;
+                }
+                out.push_back(s);
+                done[j] = 1;
+            }
+            if (S.size() > 1) ++next_group;
+        }
+        st = std::move(out);
+    }
+
     void touch(const VRef& v, int step) {
         if (v.buf < 0) return;
         Buffer& b = plan_.bufs[v.buf];
@@ -1127,19 +1282,32 @@ class Planner {
                 b.last = n;
             }
         }
+        // The steps of one grouped launch run at the same time: each of them
+        // uses its buffers over the whole span of the group.
+        std::vector<int> lo(n), hi(n);
+        for (int i = 0; i < n; ++i) {
+            const int32_t g = plan_.steps[i].group;
+            lo[i] = (g >= 0 && i > 0 && plan_.steps[i - 1].group == g) ? lo[i - 1] : i;
+        }
+        for (int i = n - 1; i >= 0; --i) {
+            const int32_t g = plan_.steps[i].group;
+            hi[i] = (g >= 0 && i + 1 < n && plan_.steps[i + 1].group == g) ? hi[i + 1] : i;
+        }
         for (int i = 0; i < n; ++i) {
             const Step& s = plan_.steps[i];
-            touch(s.out, i);
-            touch(s.a, i);
-            if (s.kind == StepKind::Elt) touch(s.b, i);
-            if (s.kind == StepKind::MaxPoolChain) {
-                touch(s.b, i);
-                touch(s.c, i);
-            }
-            if (s.has_res) touch(s.res, i);
-            if (s.ws_buf >= 0) {
-                plan_.bufs[s.ws_buf].first = std::min(plan_.bufs[s.ws_buf].first, i);
-                plan_.bufs[s.ws_buf].last = std::max(plan_.bufs[s.ws_buf].last, i);
+            for (int t : {lo[i], hi[i]}) {
+                touch(s.out, t);
+                touch(s.a, t);
+                if (s.kind == StepKind::Elt) touch(s.b, t);
+                if (s.kind == StepKind::MaxPoolChain) {
+                    touch(s.b, t);
+                    touch(s.c, t);
+                }
+                if (s.has_res) touch(s.res, t);
+                if (s.ws_buf >= 0) {
+                    plan_.bufs[s.ws_buf].first = std::min(plan_.bufs[s.ws_buf].first, t);
+                    plan_.bufs[s.ws_buf].last = std::max(plan_.bufs[s.ws_buf].last, t);
+                }
             }
         }
         for (int b : plan_.input_bufs) {
@@ -1326,7 +1494,9 @@ std::string describe_plan(const Model& m, const Plan& p) {
         os << i << " " << step_kind_name(s.kind);
         if (s.kind == StepKind::Elt) os << "(" << s.elt << ")";
         if (s.kind == StepKind::ConvMfma)
-            os << "(tile=" << k::conv_tile_name(s.tile) << ",vec=" << s.vec << ",splits=" << s.splits << ",act=" << s.act << ")";
+            os << "(tile=" << k::conv_tile_name(s.tile) << ",vec=" << s.vec << ",splits=" << s.splits << ",act=" << s.act
+               << ")";
+        if (s.group >= 0) os << " group=" << s.group;
         if (s.kind == StepKind::ConvDirect) os << "(act=" << s.act << ")";
         os << " node=" << s.node;
         if (s.node >= 0) os << " '" << m.nodes[s.node].name << "'";
@@ -1335,6 +1505,9 @@ std::string describe_plan(const Model& m, const Plan& p) {
         if (s.has_res) os << " res=" << fmt_view(s.res);
         os << "\n";
     }
+    os << "arena";  // element offset of every buffer
+    for (size_t b = 0; b < p.bufs.size(); ++b) os << " b" << b << "@" << p.bufs[b].offset;
+    os << "\n";
     return os.str();
 }
 

@@ -49,6 +49,9 @@ struct Step {
     bool vec = false;
     int32_t splits = 1, kt_per_split = 0;
     int32_t ws_buf = -1;
+    // >= 0: consecutive ConvMfma steps with the same id run as one grouped
+    // launch of their common tile (k::launch_conv_mfma_group)
+    int32_t group = -1;
     // eltwise
     int32_t elt = 0;
     float alpha = 0.0f;
@@ -85,10 +88,22 @@ struct ConvQuery {
     bool wino;  // the Winograd kernel applies (3x3, stride 1, dilation 1, Cin % 4 == 0)
 };
 
+// Measured comparison of independent convs launched one by one (each with
+// its own launch shape) against one grouped launch of the fastest tile.
+struct ConvGroupTiming {
+    int tile = -1;             // fastest implicit-GEMM tile for the grouped launch
+    double group_ms = 0.0;     // its time
+    double separate_ms = 0.0;  // the layers launched one by one
+};
+
 struct PlanOptions {
     // When set, chooses the launch shape of every implicit-GEMM conv (the
     // runtime times candidates on the device); otherwise the cost model does.
     std::function<k::ConvLaunchShape(const ConvQuery&)> tune_conv;
+    // When set (with tune_conv), independent convs that are ready at the same
+    // point of the program are reordered next to each other and issued as one
+    // grouped launch wherever the measurement says that is faster.
+    std::function<ConvGroupTiming(const std::vector<ConvQuery>&, const std::vector<k::ConvLaunchShape>&)> tune_group;
     bool split_k = true;
     int force_tile = -1;   // >= 0: use this implicit-GEMM tile for every MFMA conv (tuning, tests)
     int force_splits = 0;  // > 0 with force_tile: split-K across workgroups into this many splits

@@ -166,6 +166,15 @@ Session::Session(Model& m) : model_(&m) {
     opts_.winograd_form_silu = !(silu && std::strcmp(silu, "exact") == 0);
     // PDEFA_AUTOTUNE=0: conv launch shapes from the cost model alone
     autotune_ = env_flag("PDEFA_AUTOTUNE", true);
+    // PDEFA_GROUP=0: every conv keeps its own launch (no grouped launches)
+    group_convs_ = env_flag("PDEFA_GROUP", true);
+    // PDEFA_GROUP_TILE=<tile>: take every group the planner offers, with this
+    // implicit-GEMM tile (tests of the grouped kernel)
+    if (const char* t = std::getenv("PDEFA_GROUP_TILE")) {
+        for (int i = 0; i < k::kNumConvTiles; ++i)
+            if (std::strcmp(t, k::conv_tile_name(i)) == 0) group_tile_ = i;
+        if (group_tile_ < 0) throw std::runtime_error(std::string("PDEFA_GROUP_TILE: unknown tile ") + t);
+    }
 }
 
 Session::~Session() {
@@ -386,7 +395,24 @@ void Session::prepare(const std::vector<std::vector<int64_t>>& dims) {
     release_prepared();
     auto p = std::make_unique<Prepared>();
     PlanOptions opts = opts_;
-    if (autotune_) opts.tune_conv = [this](const ConvQuery& q) { return tune_conv(q, stream_); };
+    if (autotune_) {
+        opts.tune_conv = [this](const ConvQuery& q) { return tune_conv(q, stream_); };
+        // grouped launches change the program order; the concurrent capture
+        // keeps one launch per step
+        if (group_convs_ && !concurrent_)
+            opts.tune_group = [this](const std::vector<ConvQuery>& qs, const std::vector<k::ConvLaunchShape>& solo) {
+                return tune_conv_group(qs, solo, stream_);
+            };
+        if (group_convs_ && !concurrent_ && group_tile_ >= 0)
+            opts.tune_group = [t = group_tile_](const std::vector<ConvQuery>& qs,
+                                                const std::vector<k::ConvLaunchShape>&) {
+                ConvGroupTiming g;  // every offered group, with this tile
+                g.tile = t;
+                g.group_ms = 1.0;
+                g.separate_ms = static_cast<double>(qs.size());
+                return g;
+            };
+    }
     p->plan = build_plan(*model_, dims, opts);
     const Plan& plan = p->plan;
     if (concurrent_) p->sched = schedule_plan(plan, kMaxCaptureStreams);
@@ -561,6 +587,16 @@ void Session::prepare(const std::vector<std::vector<int64_t>>& dims) {
                 l.axis = s.axis;
                 break;
         }
+        // a member of a grouped launch joins the launch of the previous step
+        if (s.group >= 0 && i > 0 && plan.steps[i - 1].group == s.group) {
+            Launch& g = prep_->launches.back();
+            if (g.group.empty()) g.group.push_back(g.conv);
+            g.group.push_back(l.conv);
+            g.label += " + " + l.label;
+            if (g.group.size() > static_cast<size_t>(k::kMaxConvGroup) || !l.vec || l.tile != g.tile)
+                throw std::runtime_error("bad conv group at step " + std::to_string(i));
+            continue;
+        }
         prep_->launches.push_back(std::move(l));
     }
     for (int32_t b : plan.input_bufs)
@@ -588,7 +624,9 @@ void Session::prepare(const std::vector<std::vector<int64_t>>& dims) {
 void Session::launch_one(const Launch& l, hipStream_t s) {
     switch (l.kind) {
         case StepKind::ConvMfma:
-            if (k::is_wino_tile(l.tile))
+            if (!l.group.empty())
+                k::launch_conv_mfma_group(l.group.data(), static_cast<int>(l.group.size()), l.tile, s);
+            else if (k::is_wino_tile(l.tile))
                 k::launch_conv_wino(l.conv, l.tile == k::kTileWino64 ? 64 : 32, s);
             else
                 k::launch_conv_mfma(l.conv, l.tile, l.vec, s);
@@ -835,8 +873,11 @@ void Session::step_stats(int32_t iters, std::vector<double>& ms, std::vector<int
         const Launch& l = prep_->launches[i];
         kind[i] = static_cast<int32_t>(l.kind);
         if (l.kind == StepKind::ConvMfma) {
-            const k::ConvArgs& c = l.conv;
-            flops[i] = 2LL * c.N * c.Cout * c.Cin * c.KH * c.KW * static_cast<int64_t>(c.Ho) * c.Wo;
+            auto conv_flops = [](const k::ConvArgs& c) {
+                return 2LL * c.N * c.Cout * c.Cin * c.KH * c.KW * static_cast<int64_t>(c.Ho) * c.Wo;
+            };
+            if (l.group.empty()) flops[i] = conv_flops(l.conv);
+            for (const k::ConvArgs& c : l.group) flops[i] += conv_flops(c);
         } else if (l.kind == StepKind::ConvDirect) {
             const k::ConvDirectArgs& d = l.direct;
             flops[i] = 2LL * d.y.dims[0] * d.y.dims[1] * d.x.dims[1] * d.KH * d.KW * d.y.dims[2] * d.y.dims[3];

@@ -83,13 +83,16 @@ class Session {
     // Re-runs the prepared program `iters` times on the input already in HBM
     // (no host copies); returns the elapsed device time in ms (HIP events).
     double replay(int32_t iters);
-    // Runs each step once with HIP events around it; fills per-step ms.
+    // Launches are the plan's steps, except that a grouped launch issues
+    // several conv steps at once.
+    // Runs each launch once with HIP events around it; fills per-launch ms.
     void time_steps(std::vector<double>& ms, std::vector<std::string>& labels);
-    // Launches step `idx` `iters` times back to back between two HIP events
+    // Issues launch `idx` `iters` times back to back between two HIP events
     // on the session stream; returns the average ms per launch.
     double repeat_step(int32_t idx, int32_t iters);
-    // Average per-step device time over `iters` step-by-step replays, with the
-    // step kind and its algorithmic flops (2*N*Cout*Cin*KH*KW*Ho*Wo for convs).
+    // Average per-launch device time over `iters` launch-by-launch replays,
+    // with the kind and the algorithmic flops (2*N*Cout*Cin*KH*KW*Ho*Wo summed
+    // over the launch's convs).
     void step_stats(int32_t iters, std::vector<double>& ms, std::vector<int32_t>& kind,
                     std::vector<int64_t>& flops);
 
@@ -106,6 +109,7 @@ class Session {
     struct Launch {
         StepKind kind;
         k::ConvArgs conv;
+        std::vector<k::ConvArgs> group;  // grouped launch: every member (conv is the first)
         int tile = 0;
         bool vec = false;
         k::ConvDirectArgs direct;
@@ -171,6 +175,8 @@ class Session {
     bool use_graph_ = true;
     PlanOptions opts_;
     bool autotune_ = true;  // time candidate conv launch shapes while planning
+    bool group_convs_ = true;  // grouped launches of independent convs (measured)
+    int group_tile_ = -1;      // >= 0: every offered group is taken with this tile
 };
 
 // C = A[M,K] @ B[K,N] on the device (the ops_matmul path); host pointers.

@@ -280,10 +280,12 @@ def test_yolov8n_b8_batch_matches_b1(yolov8n):
 
 def test_concurrent_capture_matches_serial(yolov8n, monkeypatch):
     """Parallel graph branches (PDEFA_CONCURRENT=1, one buffer per tensor) give
-    the same bits as the serial capture: same kernels, same launch shapes."""
+    the same bits as the serial capture without grouped launches (which the
+    concurrent capture does not use): same kernels, same launch shapes."""
     print("[case] yolov8n b2 concurrent capture", flush=True)
     model, path = yolov8n
     x, _ = ys.yolo_inputs(2)
+    monkeypatch.setenv("PDEFA_GROUP", "0")
     serial = run_engine(path, x)[0]
     monkeypatch.setenv("PDEFA_CONCURRENT", "1")
     eng = native.Engine(path)
@@ -294,6 +296,49 @@ def test_concurrent_capture_matches_serial(yolov8n, monkeypatch):
         eng.close()
     assert np.array_equal(par, serial)
     assert np.array_equal(again, serial)
+
+
+@pytest.mark.parametrize("tile", ["32x32k4", "64x64", "32x64k2", "128x64w8", "32x64k4w8"])
+def test_grouped_launches(yolov8n, monkeypatch, tile):
+    """Every conv group the planner offers taken with one tile: independent
+    convs of different shapes, activations and output slices (the Detect
+    head's with the neck's) share one launch.  Same detections as the
+    oracle network, and within tolerance of separate launches."""
+    print(f"[case] yolov8n b1 grouped launches tile={tile}", flush=True)
+    model, path = yolov8n
+    x, _ = ys.yolo_inputs(1)
+    monkeypatch.setenv("PDEFA_GROUP_TILE", tile)
+    eng = native.Engine(path)
+    try:
+        got = eng.run(x)[0]
+        again = eng.run(x)[0]
+        plan = eng.plan()
+    finally:
+        eng.close()
+    groups = set(re.findall(r" group=(\d+)", plan))
+    assert len(groups) >= 6
+    assert all(f"tile={tile}," in l for l in plan.splitlines() if " group=" in l)
+    assert np.array_equal(got, again)
+    monkeypatch.delenv("PDEFA_GROUP_TILE")
+    monkeypatch.setenv("PDEFA_GROUP", "0")
+    solo = run_engine(path, x)[0]
+    assert_close_anchors(got, solo, "grouped vs separate launches")
+    assert_network_close(got, model, x, f"grouped ({tile}) vs oracle")
+
+
+def test_measured_grouping_at_batch1(yolov8n):
+    """With measured choices (the default), batch 1 takes grouped launches."""
+    print("[case] yolov8n b1 measured grouping", flush=True)
+    model, path = yolov8n
+    x, _ = ys.yolo_inputs(1)
+    eng = native.Engine(path)
+    try:
+        got = eng.run(x)[0]
+        plan = eng.plan()
+    finally:
+        eng.close()
+    assert re.search(r" group=\d+", plan)
+    assert_network_close(got, model, x, "b1 (measured grouping) vs oracle")
 
 
 def test_autotune_off_within_tolerance(yolov8n, monkeypatch):

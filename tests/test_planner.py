@@ -2,6 +2,7 @@
 import ctypes as C
 import re
 
+import numpy as np
 import pytest
 
 from pdefa_amd import native, yolo_synth as ys
@@ -17,8 +18,14 @@ def y8n_path(tmp_path_factory):
 def parse(text):
     head, *lines = text.strip().splitlines()
     info = dict(re.findall(r"(\w+)=(\d+)", head))
-    cut = next(i for i, l in enumerate(lines) if l.startswith("schedule"))
+    cut = next(i for i, l in enumerate(lines) if l.startswith("arena"))
     return {k: int(v) for k, v in info.items()}, lines[:cut]
+
+
+def arena_offsets(text):
+    """{buffer id: element offset in the arena}."""
+    line = next(l for l in text.splitlines() if l.startswith("arena"))
+    return {int(b): int(o) for b, o in re.findall(r" b(\d+)@(\d+)", line)}
 
 
 def parse_schedule(text):
@@ -131,3 +138,85 @@ def test_concurrent_schedule_orders_every_hazard(y8n_path, monkeypatch, reuse):
             assert j in reach[i], (i, j)
     if reuse == "0":
         assert n_streams > 1  # the detect-head branches run concurrently
+
+
+VIEW = re.compile(r" (out|a|b|res)=b(\d+)\+(\d+)\[([\d,]+)\]s\[([\d,]+)\]")
+
+
+def view_elems(off, dims, strides):
+    """Exact element offsets a strided view touches (with repeats)."""
+    idx = np.zeros((), dtype=np.int64) + off
+    for d, s in zip(dims, strides):
+        idx = idx[..., None] + np.arange(d, dtype=np.int64) * s
+    return idx.ravel()
+
+
+def step_access(line):
+    """[(buf, role, element offsets)] of one plan line."""
+    return [(int(buf), role, view_elems(int(off), [int(x) for x in dims.split(",")],
+                                        [int(x) for x in strides.split(",")]))
+            for role, buf, off, dims, strides in VIEW.findall(line)]
+
+
+def touched(lines):
+    """Per step {buf: (read mask, written mask)} over each buffer's extent."""
+    acc = [step_access(l) for l in lines]
+    size = {}
+    for a in acc:
+        for buf, _, e in a:
+            size[buf] = max(size.get(buf, 0), int(e.max()) + 1)
+    out = []
+    for a in acc:
+        d = {}
+        for buf, role, e in a:
+            r, w = d.setdefault(buf, (np.zeros(size[buf], bool), np.zeros(size[buf], bool)))
+            (w if role == "out" else r)[e] = True
+        out.append(d)
+    return out
+
+
+@pytest.mark.parametrize("shape", [[1, 3, 640, 640], [4, 3, 640, 640]])
+def test_grouped_plan_keeps_every_hazard_in_order(y8n_path, monkeypatch, shape):
+    """Grouped launches reorder the program (list scheduling).  With every
+    offered group taken (host stand-in for the device measurement), each
+    pair of steps that touch a common element of one buffer, one of them
+    writing it, runs in its original order; group members are consecutive,
+    share one tile and take no split-K."""
+    base = parse(native.plan_text(y8n_path, shape))[1]
+    monkeypatch.setenv("PDEFA_PLAN_GROUP_ALL", "1")
+    text = native.plan_text(y8n_path, shape)
+    grouped = parse(text)[1]
+    node = lambda l: int(re.search(r" node=(\d+)", l).group(1))
+    assert sorted(map(node, grouped)) == sorted(map(node, base))
+    pos = {node(l): i for i, l in enumerate(grouped)}
+    acc = touched(base)
+    hazards = 0
+    for j in range(len(base)):
+        for i in range(j):
+            for buf, (ri, wi) in acc[i].items():
+                if buf not in acc[j]:
+                    continue
+                rj, wj = acc[j][buf]
+                if (wi & rj).any() or (wi & wj).any() or (ri & wj).any():
+                    hazards += 1
+                    assert pos[node(base[i])] < pos[node(base[j])], (base[i][:60], base[j][:60])
+    assert hazards > 60
+    groups = {}
+    for i, l in enumerate(grouped):
+        m = re.search(r" group=(\d+)", l)
+        if m:
+            groups.setdefault(int(m.group(1)), []).append(i)
+    assert len(groups) >= 6  # the Detect head's convs ride along the neck
+    arena = arena_offsets(text)
+    for members in groups.values():
+        assert members == list(range(members[0], members[0] + len(members))) and 2 <= len(members) <= 8
+        tiles = {re.search(r"tile=([^,]+),", grouped[i]).group(1) for i in members}
+        assert len(tiles) == 1 and all("splits=1," in grouped[i] and "vec=1" in grouped[i] for i in members)
+        # members run at the same time: none writes arena memory another
+        # member reads or writes (buffers that share memory must not meet)
+        acc = {i: [(role, e + arena[buf]) for buf, role, e in step_access(grouped[i])] for i in members}
+        for i in members:
+            wi = np.concatenate([e for role, e in acc[i] if role == "out"])
+            for j in members:
+                if j != i:
+                    assert not np.intersect1d(wi, np.concatenate([e for _, e in acc[j]])).size, (i, j)
