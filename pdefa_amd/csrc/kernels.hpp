@@ -251,6 +251,11 @@ struct DetectDecodeArgs {
     const float* dfl_w = nullptr;  // R floats
     float dfl_bias = 0.0f;
     int32_t bins = 16;
+    // optional (cls.ptr != nullptr): cls_out = sigmoid(cls), both [N, C, A];
+    // one pass over the head rows when each anchor's row holds its 4*16 box
+    // bins followed by its C class scores
+    View cls;
+    View cls_out;
 };
 void launch_detect_decode(const DetectDecodeArgs& a, hipStream_t s);
 

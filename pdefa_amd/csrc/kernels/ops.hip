@@ -69,6 +69,9 @@ bool fits_i32(const View& v) {
     return ext < (int64_t{1} << 31) && n < (int64_t{1} << 31);
 }
 
+// Logistic sigmoid, as the Sigmoid operator evaluates it.
+__device__ __forceinline__ float sigmoid_elt(float x) { return 1.0f / (1.0f + expf(-x)); }
+
 template <typename I>
 __global__ __launch_bounds__(256) void eltwise_kernel(int op, IView<I> out, IView<I> a, IView<I> b, float alpha,
                                                       I total) {
@@ -90,7 +93,7 @@ __global__ __launch_bounds__(256) void eltwise_kernel(int op, IView<I> out, IVie
             case kEltSub: r = x - b.ptr[bo]; break;
             case kEltMul: r = x * b.ptr[bo]; break;
             case kEltDiv: r = x / b.ptr[bo]; break;
-            case kEltSigmoid: r = 1.0f / (1.0f + expf(-x)); break;
+            case kEltSigmoid: r = sigmoid_elt(x); break;
             case kEltRelu: r = x > 0.0f ? x : 0.0f; break;
             case kEltTanh: r = tanhf(x); break;
             case kEltLeaky: r = x > 0.0f ? x : x * alpha; break;
@@ -419,9 +422,42 @@ void launch_maxpool_chain(const View& out0, const View& out1, const View& out2, 
     }
 }
 
-// One lane per (n, anchor); see kernels.hpp for the arithmetic.  The softmax
-// matches softmax_kernel (max, exp(x - max), sum in bin order, * 1/sum) and
-// the expectation matches the direct conv's accumulation order.  R > 0: the
+// DFL expectation of one side: softmax over the R bins (max, exp(x - max),
+// sum in bin order, * 1/sum, as softmax_kernel) and the weighted sum in bin
+// order (the direct conv's accumulation order) plus the bias.
+template <int R>
+__device__ __forceinline__ float dfl_side(float (&v)[R], const float* w, float bias) {
+    float mx = -1e30f;
+#pragma unroll
+    for (int b = 0; b < R; ++b) mx = v[b] > mx ? v[b] : mx;
+    float sum = 0.0f;
+#pragma unroll
+    for (int b = 0; b < R; ++b) {
+        v[b] = expf(v[b] - mx);
+        sum += v[b];
+    }
+    const float inv = sum > 0.0f ? 1.0f / sum : 0.0f;
+    float acc = 0.0f;
+#pragma unroll
+    for (int b = 0; b < R; ++b) acc = fmaf(v[b] * inv, w[b], acc);
+    return acc + bias;
+}
+
+// dist2bbox of one anchor from its four side distances d, then * stride.
+__device__ __forceinline__ void decode_box(const DetectDecodeArgs& a, int32_t n, int32_t an, const float (&d)[4]) {
+    auto at = [&](const View& v, int c) {
+        return v.ptr[n * v.str[0] + c * v.str[1] + static_cast<int64_t>(an) * v.str[2]];
+    };
+    const float ax = at(a.anchors, 0), ay = at(a.anchors, 1);
+    const float x1 = ax - d[0], y1 = ay - d[1];
+    const float x2 = ax + d[2], y2 = ay + d[3];
+    const float r[4] = {(x1 + x2) / at(a.two, 0), (y1 + y2) / at(a.two, 1), x2 - x1, y2 - y1};
+#pragma unroll
+    for (int c = 0; c < 4; ++c)
+        a.out.ptr[n * a.out.str[0] + c * a.out.str[1] + static_cast<int64_t>(an) * a.out.str[2]] = r[c] * at(a.strides, c);
+}
+
+// One lane per (n, anchor); see kernels.hpp for the arithmetic.  R > 0: the
 // bin count is R and each side's R bins are contiguous and 16-byte aligned
 // (the Detect head's [anchor][144] rows), loaded as float4 into registers;
 // R == 0: any bin count and strides.
@@ -447,20 +483,7 @@ __global__ __launch_bounds__(256) void detect_decode_kernel(DetectDecodeArgs a, 
                 v[4 * q + 2] = t.z;
                 v[4 * q + 3] = t.w;
             }
-            float mx = -1e30f;
-#pragma unroll
-            for (int b = 0; b < R; ++b) mx = v[b] > mx ? v[b] : mx;
-            float sum = 0.0f;
-#pragma unroll
-            for (int b = 0; b < R; ++b) {
-                v[b] = expf(v[b] - mx);
-                sum += v[b];
-            }
-            const float inv = sum > 0.0f ? 1.0f / sum : 0.0f;
-            float acc = 0.0f;
-#pragma unroll
-            for (int b = 0; b < R; ++b) acc = fmaf(v[b] * inv, a.dfl_w[b], acc);
-            d[side] = acc + a.dfl_bias;
+            d[side] = dfl_side<R>(v, a.dfl_w, a.dfl_bias);
         } else {
             float mx = -1e30f;
             for (int b = 0; b < a.bins; ++b) {
@@ -475,16 +498,63 @@ __global__ __launch_bounds__(256) void detect_decode_kernel(DetectDecodeArgs a, 
             d[side] = acc + a.dfl_bias;
         }
     }
-    auto at = [&](const View& v, int c) {
-        return v.ptr[n * v.str[0] + c * v.str[1] + static_cast<int64_t>(an) * v.str[2]];
-    };
-    const float ax = at(a.anchors, 0), ay = at(a.anchors, 1);
-    const float x1 = ax - d[0], y1 = ay - d[1];
-    const float x2 = ax + d[2], y2 = ay + d[3];
-    const float r[4] = {(x1 + x2) / at(a.two, 0), (y1 + y2) / at(a.two, 1), x2 - x1, y2 - y1};
+    decode_box(a, n, an, d);
+}
+
+// The whole head output of kHeadAnchors consecutive anchors of one image per
+// workgroup, when each anchor's row holds its 4*R box bins followed by its C
+// class scores (row stride S floats, the Detect head's [anchor][144] concat):
+// the rows are read once, coalesced, into LDS (row pitch S + 1 floats, so the
+// per-anchor reads below hit distinct banks); lane (side, anchor) takes one
+// side's DFL expectation, 64 lanes decode the boxes, and the class sigmoids
+// are written class-major with consecutive lanes on consecutive anchors.
+constexpr int kHeadAnchors = 64;
+template <int R>
+__global__ __launch_bounds__(256) void detect_head_kernel(DetectDecodeArgs a, int32_t A, int32_t C, int32_t S) {
+    extern __shared__ __attribute__((aligned(16))) float rows[];
+    __shared__ float dist[4][kHeadAnchors];
+    const int tid = threadIdx.x;
+    const int32_t tiles = (A + kHeadAnchors - 1) / kHeadAnchors;
+    const int32_t n = blockIdx.x / tiles;
+    const int32_t a0 = (blockIdx.x - n * tiles) * kHeadAnchors;
+    const int cnt = min(kHeadAnchors, A - a0);
+    const int P = S + 1;
+    const float4* src = reinterpret_cast<const float4*>(a.x.ptr + n * a.x.str[0] + static_cast<int64_t>(a0) * S);
+    const int q4 = cnt * S / 4;
+    for (int q = tid; q < q4; q += 256) {
+        const float4 v = src[q];
+        const int e = 4 * q;
+        const int r = e / S;
+        float* dst = rows + r * P + (e - r * S);
+        dst[0] = v.x;
+        dst[1] = v.y;
+        dst[2] = v.z;
+        dst[3] = v.w;
+    }
+    __syncthreads();
+    {
+        const int an = tid % kHeadAnchors, side = tid / kHeadAnchors;
+        float d = 0.0f;
+        if (an < cnt) {
+            float v[R];
+            const float* b = rows + an * P + side * R;
 #pragma unroll
-    for (int c = 0; c < 4; ++c)
-        a.out.ptr[n * a.out.str[0] + c * a.out.str[1] + static_cast<int64_t>(an) * a.out.str[2]] = r[c] * at(a.strides, c);
+            for (int i = 0; i < R; ++i) v[i] = b[i];
+            d = dfl_side<R>(v, a.dfl_w, a.dfl_bias);
+        }
+        dist[side][an] = d;
+    }
+    __syncthreads();
+    if (tid < cnt) {
+        const float d[4] = {dist[0][tid], dist[1][tid], dist[2][tid], dist[3][tid]};
+        decode_box(a, n, a0 + tid, d);
+    }
+    const View& o = a.cls_out;
+    float* ob = o.ptr + n * o.str[0] + static_cast<int64_t>(a0) * o.str[2];
+    for (int q = tid; q < C * kHeadAnchors; q += 256) {
+        const int c = q / kHeadAnchors, an = q - c * kHeadAnchors;
+        if (an < cnt) ob[c * o.str[1] + an * o.str[2]] = sigmoid_elt(rows[an * P + 4 * R + c]);
+    }
 }
 
 void launch_detect_decode(const DetectDecodeArgs& a, hipStream_t s) {
@@ -501,7 +571,29 @@ void launch_detect_decode(const DetectDecodeArgs& a, hipStream_t s) {
     if (a.anchors.dims[1] != 2 || a.two.dims[1] != 2 || a.strides.dims[1] != 4 || a.out.dims[1] != 4)
         throw std::runtime_error("decode: channel counts");
     if (N * A >= (int64_t{1} << 31) || !fits_i32(a.x)) throw std::runtime_error("decode: views exceed int32 indexing");
+    int64_t C = 0;
+    if (a.cls.ptr) {
+        check_view(a.cls, "decode class scores");
+        check_view(a.cls_out, "decode class out");
+        if (a.cls.rank != 3 || a.cls_out.rank != 3 || a.cls.dims[0] != N || a.cls.dims[2] != A ||
+            a.cls_out.dims[0] != N || a.cls_out.dims[2] != A || a.cls_out.dims[1] != a.cls.dims[1])
+            throw std::runtime_error("decode: class views must be [N, C, A]");
+        C = a.cls.dims[1];
+    }
     if (N * A == 0) return;
+    // the fused path: rows of [4*16 box bins | C class scores], stride S
+    const int64_t S = a.x.str[3];
+    const bool head = C > 0 && a.bins == 16 && a.x.str[1] == 1 && a.x.str[2] == 16 && S % 4 == 0 && S >= 64 + C &&
+                      S + 1 <= 255 && a.cls.ptr == a.x.ptr + 64 && a.cls.str[1] == 1 && a.cls.str[2] == S &&
+                      (N == 1 || (a.cls.str[0] == a.x.str[0] && a.x.str[0] % 4 == 0)) &&
+                      reinterpret_cast<uintptr_t>(a.x.ptr) % 16 == 0;
+    if (head) {
+        const int64_t tiles = (A + kHeadAnchors - 1) / kHeadAnchors;
+        const size_t lds = sizeof(float) * kHeadAnchors * static_cast<size_t>(S + 1);
+        hipLaunchKernelGGL(detect_head_kernel<16>, dim3(static_cast<unsigned>(N * tiles)), dim3(256), lds, s, a,
+                           static_cast<int32_t>(A), static_cast<int32_t>(C), static_cast<int32_t>(S));
+        return;
+    }
     const dim3 grid(static_cast<unsigned>((N * A + 255) / 256));
     const bool vec16 = a.bins == 16 && a.x.str[1] == 1 && reinterpret_cast<uintptr_t>(a.x.ptr) % 16 == 0 &&
                        (N == 1 || a.x.str[0] % 4 == 0) && a.x.str[2] % 4 == 0 && (A == 1 || a.x.str[3] % 4 == 0);
@@ -509,6 +601,7 @@ void launch_detect_decode(const DetectDecodeArgs& a, hipStream_t s) {
         hipLaunchKernelGGL(detect_decode_kernel<16>, grid, dim3(256), 0, s, a, static_cast<int32_t>(N), static_cast<int32_t>(A));
     else
         hipLaunchKernelGGL(detect_decode_kernel<0>, grid, dim3(256), 0, s, a, static_cast<int32_t>(N), static_cast<int32_t>(A));
+    if (C > 0) launch_eltwise(kEltSigmoid, a.cls_out, a.cls, a.cls, 0.0f, s);
 }
 
 // Letterbox of one interleaved 8-bit image into a planar fp32 [3, th, tw]

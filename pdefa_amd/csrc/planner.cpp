@@ -251,6 +251,10 @@ void step_views(const Step& s, std::vector<VRef>& rd, std::vector<VRef>& wr) {
             rd.push_back(s.b);
             rd.push_back(s.c);
             rd.push_back(s.res);
+            if (s.cls_in.buf != -1) {
+                rd.push_back(s.cls_in);
+                wr.push_back(s.cls_out);
+            }
             break;
         default: break;
     }
@@ -1058,6 +1062,7 @@ class Planner {
         auto uses = [&](const VRef& v) { return v.buf == buf; };
         if (uses(s.a) || (s.has_res && uses(s.res))) return true;
         if ((s.kind == StepKind::Elt || s.kind == StepKind::DetectDecode) && (uses(s.b) || uses(s.c))) return true;
+        if (s.kind == StepKind::DetectDecode && s.cls_in.buf != -1 && uses(s.cls_in)) return true;
         return false;
     }
     // No step outside [lo, hi] reads `buf`, and it is not a graph output.
@@ -1160,8 +1165,18 @@ class Planner {
             }
             Step f;
             if (match_decode(i, &f)) {
-                out.push_back(f);
                 i += 8;
+                // the class-score sigmoid right after it (Detect's
+                // cat(dbox, cls.sigmoid())) joins the same pass
+                if (i < st.size() && is_elt(st[i], k::kEltSigmoid) && st[i].a.rank == 3 && st[i].out.rank == 3 &&
+                    st[i].a.dims[0] == f.out.dims[0] && st[i].a.dims[2] == f.out.dims[2] &&
+                    st[i].out.dims[0] == f.out.dims[0] && st[i].out.dims[1] == st[i].a.dims[1] &&
+                    st[i].out.dims[2] == f.out.dims[2]) {
+                    f.cls_in = st[i].a;
+                    f.cls_out = st[i].out;
+                    ++i;
+                }
+                out.push_back(f);
                 continue;
             }
             out.push_back(st[i]);
@@ -1304,6 +1319,10 @@ class Planner {
                     touch(s.c, t);
                 }
                 if (s.has_res) touch(s.res, t);
+                if (s.kind == StepKind::DetectDecode && s.cls_in.buf != -1) {
+                    touch(s.cls_in, t);
+                    touch(s.cls_out, t);
+                }
                 if (s.ws_buf >= 0) {
                     plan_.bufs[s.ws_buf].first = std::min(plan_.bufs[s.ws_buf].first, t);
                     plan_.bufs[s.ws_buf].last = std::max(plan_.bufs[s.ws_buf].last, t);
@@ -1418,6 +1437,10 @@ Schedule schedule_plan(const Plan& p, int max_streams) {
             wr[i].push_back(view_range(p, s.b));
             wr[i].push_back(view_range(p, s.c));
         }
+        if (s.kind == StepKind::DetectDecode && s.cls_in.buf != -1) {
+            rd[i].push_back(view_range(p, s.cls_in));
+            wr[i].push_back(view_range(p, s.cls_out));
+        }
         if (s.ws_buf >= 0) {
             const Buffer& b = p.bufs[s.ws_buf];
             wr[i].push_back({b.offset, b.offset + b.elems});
@@ -1503,6 +1526,8 @@ std::string describe_plan(const Model& m, const Plan& p) {
         os << " out=" << fmt_view(s.out) << " a=" << fmt_view(s.a);
         if (s.kind == StepKind::Elt && s.elt >= k::kEltAdd && s.elt <= k::kEltDiv) os << " b=" << fmt_view(s.b);
         if (s.has_res) os << " res=" << fmt_view(s.res);
+        if (s.kind == StepKind::DetectDecode && s.cls_in.buf != -1)
+            os << " cls=" << fmt_view(s.cls_in) << " clsout=" << fmt_view(s.cls_out);
         os << "\n";
     }
     os << "arena";  // element offset of every buffer

@@ -57,10 +57,13 @@ struct Step {
     float alpha = 0.0f;
     // softmax
     int32_t axis = 0;
-    // DetectDecode: the DFL conv's weight (and bias) indices, number of bins
+    // DetectDecode: the DFL conv's weight (and bias) indices, number of bins,
+    // and optionally (cls_in.buf != -1) the class scores whose sigmoid it
+    // also writes to cls_out
     int32_t dfl_weight = -1;
     int32_t dfl_bias = -1;
     int32_t bins = 0;
+    VRef cls_in, cls_out;
 };
 
 struct Buffer {

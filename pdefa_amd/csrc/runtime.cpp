@@ -571,6 +571,10 @@ void Session::prepare(const std::vector<std::vector<int64_t>>& dims) {
                     d.dfl_bias = static_cast<const float*>(bt.data)[0];
                 }
                 d.bins = s.bins;
+                if (s.cls_in.buf != -1) {
+                    d.cls = V(s.cls_in, "decode class scores", si);
+                    d.cls_out = V(s.cls_out, "decode class out", si);
+                }
                 break;
             }
             case StepKind::MaxPool:

@@ -278,6 +278,23 @@ def test_yolov8n_b8_batch_matches_b1(yolov8n):
     assert_network_close(got[7:8], model, x[7:8], "b8 image 7 vs oracle")
 
 
+@pytest.mark.parametrize("nc", [20, 3])
+def test_head_class_counts(tmp_path, nc):
+    """Detect heads of other class counts at 320x320: with nc = 20 each
+    anchor's row [64 box bins | 20 scores] takes the one-pass head kernel
+    (decode + class sigmoid), with nc = 3 (rows of 67 floats, not whole
+    16-byte chunks) the decode kernel plus a separate sigmoid; both match
+    the oracle network."""
+    print(f"[case] yolov8n 320x320 nc={nc}", flush=True)
+    model = ys.build_yolov8("n", seed=3, nc=nc, imgsz=320)
+    path = str(tmp_path / f"y8n_nc{nc}.engine")
+    ys.save(model, path)
+    x = np.random.default_rng(nc).random((1, 3, 320, 320), dtype=np.float32)
+    got = run_engine(path, x)[0]
+    assert got.shape == (1, 4 + nc, 2100)
+    assert_network_close(got, model, x, f"nc={nc} vs oracle")
+
+
 def test_concurrent_capture_matches_serial(yolov8n, monkeypatch):
     """Parallel graph branches (PDEFA_CONCURRENT=1, one buffer per tensor) give
     the same bits as the serial capture without grouped launches (which the

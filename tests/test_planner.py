@@ -50,19 +50,21 @@ def test_yolov8n_plan_is_zero_copy(y8n_path):
     direct = [l for l in convs if " conv_direct" in l]
     assert len(direct) == 1 and "/model.0/conv/Conv" in direct[0]
     assert not any("copy" in l for l in lines)
-    # SiLU + Sigmoid/Mul fused: no standalone sigmoid except the class head
-    assert sum("eltwise(5)" in l for l in lines) == 1
+    # SiLU + Sigmoid/Mul fused into conv epilogues, the class-head sigmoid
+    # into the decode step: no standalone sigmoid
+    assert sum("eltwise(5)" in l for l in lines) == 0
     # residual adds of the 6 backbone bottlenecks live in conv epilogues
     assert sum(" res=" in l for l in lines) == 6
     # SPPF's three chained max-pools run as one step
     pools = [l for l in lines if " maxpool" in l]
     assert len(pools) == 1 and " maxpool_chain " in pools[0]
-    # DFL softmax + 1x1 conv + dist2bbox + stride scale run as one step, so
-    # the box head leaves no standalone softmax or eltwise add/sub/div/mul
+    # DFL softmax + 1x1 conv + dist2bbox + stride scale + the class sigmoid
+    # run as one step: no standalone softmax or eltwise step is left
     dec = [l for l in lines if " detect_decode " in l]
     assert len(dec) == 1 and "/model.22/dfl/Softmax" in dec[0]
+    assert " cls=b" in dec[0] and " clsout=b0+33600[1,80,8400]" in dec[0]
     assert not any(" softmax" in l for l in lines)
-    assert sum("eltwise(" in l for l in lines) == 1  # the class-head sigmoid
+    assert not any("eltwise(" in l for l in lines)
     # Winograd-form SiLU exactly on 3x3/s1 layers with 16 < Cin <= 512
     for l in convs:
         if "act=6" in l:
@@ -72,7 +74,8 @@ def test_yolov8n_plan_is_zero_copy(y8n_path):
 def test_yolov8n_plan_batch8(y8n_path):
     info, lines = parse(native.plan_text(y8n_path, [8, 3, 640, 640]))
     assert info["copies"] == 0
-    assert lines[-1].split(" out=")[1].startswith("b0+33600[8,80,8400]")
+    assert lines[-1].split(" out=")[1].startswith("b0+0[8,4,8400]")
+    assert lines[-1].split(" clsout=")[1].startswith("b0+33600[8,80,8400]")
 
 
 def test_single_conv_plan(tmp_path):
@@ -140,7 +143,8 @@ def test_concurrent_schedule_orders_every_hazard(y8n_path, monkeypatch, reuse):
         assert n_streams > 1  # the detect-head branches run concurrently
 
 
-VIEW = re.compile(r" (out|a|b|res)=b(\d+)\+(\d+)\[([\d,]+)\]s\[([\d,]+)\]")
+VIEW = re.compile(r" (out|a|b|res|cls|clsout)=b(\d+)\+(\d+)\[([\d,]+)\]s\[([\d,]+)\]")
+WRITES = ("out", "clsout")
 
 
 def view_elems(off, dims, strides):
@@ -170,7 +174,7 @@ def touched(lines):
         d = {}
         for buf, role, e in a:
             r, w = d.setdefault(buf, (np.zeros(size[buf], bool), np.zeros(size[buf], bool)))
-            (w if role == "out" else r)[e] = True
+            (w if role in WRITES else r)[e] = True
         out.append(d)
     return out
 
@@ -216,7 +220,7 @@ def test_grouped_plan_keeps_every_hazard_in_order(y8n_path, monkeypatch, shape):
         # member reads or writes (buffers that share memory must not meet)
         acc = {i: [(role, e + arena[buf]) for buf, role, e in step_access(grouped[i])] for i in members}
         for i in members:
-            wi = np.concatenate([e for role, e in acc[i] if role == "out"])
+            wi = np.concatenate([e for role, e in acc[i] if role in WRITES])
             for j in members:
                 if j != i:
                     assert not np.intersect1d(wi, np.concatenate([e for _, e in acc[j]])).size, (i, j)
