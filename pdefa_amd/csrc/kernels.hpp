@@ -102,6 +102,11 @@ struct ConvArgs {
     float* ws = nullptr;
     int32_t splits = 1;
     int32_t kt_per_split = 0;  // multiple of the tile's KG
+    // optional nearest 2x upsample of the result, written alongside y:
+    // up[n, 2ho + i, 2wo + j, co] = y[n, ho, wo, co] for i, j in {0, 1}
+    // (channels-last, n/h/w strides), e.g. straight into a concat buffer
+    float* up = nullptr;
+    int64_t u_sn = 0, u_sh = 0, u_sw = 0;
 };
 
 // Tile and split-K choice for an implicit GEMM of this shape on the 256 CUs.

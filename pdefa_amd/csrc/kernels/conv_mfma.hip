@@ -54,14 +54,15 @@ constexpr int LDS_STRIDE = BK + 4;  // floats; 16-byte aligned rows, conflict-fr
 constexpr int kXcds = 8;
 
 // Stage buffers (two stages of KG A and B slices), then the per-row output
-// offset table of the epilogue (two int64 per tile row).
+// offset table of the epilogue (three int64 per tile row: output, residual,
+// upsampled output).
 template <int BM, int BN, int KG>
 constexpr size_t lds_stage_bytes() {
     return sizeof(float) * 2 * KG * (BM + BN) * LDS_STRIDE;
 }
 template <int BM, int BN, int KG>
 constexpr size_t lds_bytes() {
-    return lds_stage_bytes<BM, BN, KG>() + 2 * sizeof(int64_t) * BM;
+    return lds_stage_bytes<BM, BN, KG>() + 3 * sizeof(int64_t) * BM;
 }
 
 }  // namespace
@@ -89,7 +90,9 @@ __device__ __forceinline__ int xcd_tile(int lin, int total) {
 }
 
 // One BM x BN output tile (m block bx, n block by) of K split bz of problem a.
-template <int BM, int BN, int WM, int WN, int KG, int PF, bool VEC>
+// UPK: the build for problems with an upsampled copy (a.up), kept apart so
+// that its larger epilogue does not raise every other build's register count.
+template <int BM, int BN, int WM, int WN, int KG, int PF, bool VEC, bool UPK>
 __device__ __forceinline__ void conv_tile(const ConvArgs& a, const int bx, const int by, const int bz) {
     constexpr int WAVES_M = BM / WM;
     constexpr int WAVES_N = BN / WN;
@@ -131,9 +134,10 @@ __device__ __forceinline__ void conv_tile(const ConvArgs& a, const int bx, const
     // Built once here, read after the pipeline's barriers.
     int64_t* s_yoff = reinterpret_cast<int64_t*>(reinterpret_cast<char*>(smem) + lds_stage_bytes<BM, BN, KG>());
     int64_t* s_roff = s_yoff + BM;
+    int64_t* s_uoff = s_roff + BM;
     if (tid < BM) {
         const int m = m0 + tid;
-        int64_t yo = -1, ro = 0;
+        int64_t yo = -1, ro = 0, uo = 0;
         if (m < M) {
             if (a.splits > 1) {
                 yo = (static_cast<int64_t>(bz) * M + m) * a.Cout;
@@ -147,10 +151,14 @@ __device__ __forceinline__ void conv_tile(const ConvArgs& a, const int bx, const
                 if (a.res)
                     ro = static_cast<int64_t>(n) * a.r_sn + static_cast<int64_t>(ho) * a.r_sh +
                          static_cast<int64_t>(wo) * a.r_sw;
+                if (a.up)
+                    uo = static_cast<int64_t>(n) * a.u_sn + static_cast<int64_t>(2 * ho) * a.u_sh +
+                         static_cast<int64_t>(2 * wo) * a.u_sw;
             }
         }
         s_yoff[tid] = yo;
         s_roff[tid] = ro;
+        s_uoff[tid] = uo;
     }
 
     // Bias of this lane's output columns, loaded now so its latency hides
@@ -368,11 +376,20 @@ __device__ __forceinline__ void conv_tile(const ConvArgs& a, const int bx, const
     // hoisted into template arguments so each lane's elements are straight-line
     // code: all row offsets (LDS) first, then all residual loads, then all
     // stores, every load or store of the tile in flight together.
-    auto epilogue = [&](auto act_c, auto res_c, auto part_c) {
+    auto epilogue = [&](auto act_c, auto res_c, auto part_c, auto up_c) {
         constexpr int ACT = decltype(act_c)::value;
         constexpr bool RES = decltype(res_c)::value;
         constexpr bool PART = decltype(part_c)::value;
+        constexpr bool UP = decltype(up_c)::value;
         float* dst = PART ? a.ws : a.y;
+        // the four upsampled copies of an element at row offset uo, column co
+        auto store_up = [&](int64_t uo, int co, float v) {
+            float* u = a.up + uo + co;
+            u[0] = v;
+            u[a.u_sw] = v;
+            u[a.u_sh] = v;
+            u[a.u_sh + a.u_sw] = v;
+        };
         if constexpr (KG == 1) {
             // 32x32 block register e of lane l holds row 8*(e/4) + 4*(l/32) + e%4, column l%32.
             int co[TN];
@@ -386,12 +403,13 @@ __device__ __forceinline__ void conv_tile(const ConvArgs& a, const int bx, const
             }
 #pragma unroll
             for (int tm = 0; tm < TM; ++tm) {
-                int64_t yo[16], ro[16];
+                int64_t yo[16], ro[16], uo[16];
 #pragma unroll
                 for (int e = 0; e < 16; ++e) {
                     const int row = wave_m * WM + tm * 32 + (e >> 2) * 8 + half * 4 + (e & 3);
                     yo[e] = s_yoff[row];
                     if (RES) ro[e] = s_roff[row];
+                    if (UP) uo[e] = s_uoff[row];
                 }
                 float rv[16][TN];
                 if constexpr (RES) {
@@ -411,7 +429,10 @@ __device__ __forceinline__ void conv_tile(const ConvArgs& a, const int bx, const
                         float v = acc[tm][tn][e];
                         if (!PART) v = act_fixed<ACT>(v + bias_v[tn], a.act, a.slope);
                         if (RES) v += rv[e][tn];
-                        if (yo[e] >= 0 && cok[tn]) dst[yo[e] + co[tn]] = v;
+                        if (yo[e] >= 0 && cok[tn]) {
+                            dst[yo[e] + co[tn]] = v;
+                            if (UP) store_up(uo[e], co[tn], v);
+                        }
                     }
             }
         } else {
@@ -437,7 +458,7 @@ __device__ __forceinline__ void conv_tile(const ConvArgs& a, const int bx, const
             const bool cok = co < a.Cout;
             const float bias_v = PART ? 0.0f : bias_lane[0];
             float v[E];
-            int64_t yo[E], ro[E];
+            int64_t yo[E], ro[E], uo[E];
 #pragma unroll
             for (int i = 0; i < E; ++i) {
                 const int row = tid / BN + i * RSTEP;
@@ -447,6 +468,7 @@ __device__ __forceinline__ void conv_tile(const ConvArgs& a, const int bx, const
                 v[i] = sum;
                 yo[i] = s_yoff[row];
                 if (RES) ro[i] = s_roff[row];
+                if (UP) uo[i] = s_uoff[row];
             }
             float rv[E];
             if constexpr (RES) {
@@ -462,53 +484,62 @@ __device__ __forceinline__ void conv_tile(const ConvArgs& a, const int bx, const
                 float r = v[i];
                 if (!PART) r = act_fixed<ACT>(r + bias_v, a.act, a.slope);
                 if (RES) r += rv[i];
-                if (yo[i] >= 0 && cok) dst[yo[i] + co] = r;
+                if (yo[i] >= 0 && cok) {
+                    dst[yo[i] + co] = r;
+                    if (UP) store_up(uo[i], co, r);
+                }
             }
         }
     };
     using YES = std::true_type;
     using NO = std::false_type;
+    using SILU = std::integral_constant<int, kActSilu>;
+    using GENERIC = std::integral_constant<int, kActGeneric>;
     if (a.splits > 1) {
-        epilogue(std::integral_constant<int, kActNone>{}, NO{}, YES{});
+        epilogue(std::integral_constant<int, kActNone>{}, NO{}, YES{}, NO{});
+    } else if constexpr (UPK) {  // upsampled copy (the FPN's Resize inputs: SiLU, no residual)
+        if (a.act == kActSilu && !a.res) epilogue(SILU{}, NO{}, NO{}, YES{});
+        else if (a.res) epilogue(GENERIC{}, YES{}, NO{}, YES{});
+        else epilogue(GENERIC{}, NO{}, NO{}, YES{});
     } else if (a.act == kActSilu) {
-        if (a.res) epilogue(std::integral_constant<int, kActSilu>{}, YES{}, NO{});
-        else epilogue(std::integral_constant<int, kActSilu>{}, NO{}, NO{});
+        if (a.res) epilogue(SILU{}, YES{}, NO{}, NO{});
+        else epilogue(SILU{}, NO{}, NO{}, NO{});
     } else if (a.act == kActSiluWinogradForm) {
-        if (a.res) epilogue(std::integral_constant<int, kActSiluWinogradForm>{}, YES{}, NO{});
-        else epilogue(std::integral_constant<int, kActSiluWinogradForm>{}, NO{}, NO{});
+        if (a.res) epilogue(std::integral_constant<int, kActSiluWinogradForm>{}, YES{}, NO{}, NO{});
+        else epilogue(std::integral_constant<int, kActSiluWinogradForm>{}, NO{}, NO{}, NO{});
     } else if (a.act == kActNone) {
-        if (a.res) epilogue(std::integral_constant<int, kActNone>{}, YES{}, NO{});
-        else epilogue(std::integral_constant<int, kActNone>{}, NO{}, NO{});
+        if (a.res) epilogue(std::integral_constant<int, kActNone>{}, YES{}, NO{}, NO{});
+        else epilogue(std::integral_constant<int, kActNone>{}, NO{}, NO{}, NO{});
     } else {
-        if (a.res) epilogue(std::integral_constant<int, kActGeneric>{}, YES{}, NO{});
-        else epilogue(std::integral_constant<int, kActGeneric>{}, NO{}, NO{});
+        if (a.res) epilogue(GENERIC{}, YES{}, NO{}, NO{});
+        else epilogue(GENERIC{}, NO{}, NO{}, NO{});
     }
 }
 
 // One problem; grid (m tiles, n tiles, K splits), tiles in XCD order with the
 // m tile fastest (neighbouring output rows share input rows, all tiles of one
 // n block share weights).
-template <int BM, int BN, int WM, int WN, int KG, int PF, bool VEC>
+template <int BM, int BN, int WM, int WN, int KG, int PF, bool VEC, bool UPK>
 __global__ __launch_bounds__((tile_threads<BM, BN, WM, WN, KG>())) void conv_mfma_kernel(ConvArgs a) {
     const int gx = gridDim.x, gxy = gridDim.x * gridDim.y;
     const int tile_id = xcd_tile(blockIdx.x + gx * blockIdx.y + gxy * blockIdx.z, gxy * gridDim.z);
     const int bz = tile_id / gxy;
     const int bxy = tile_id - bz * gxy;
     const int by = bxy / gx;
-    conv_tile<BM, BN, WM, WN, KG, PF, VEC>(a, bxy - by * gx, by, bz);
+    conv_tile<BM, BN, WM, WN, KG, PF, VEC, UPK>(a, bxy - by * gx, by, bz);
 }
 
 // Several independent problems in one launch (no split-K): a 1-D grid over
 // the concatenated tile lists, problem p owning tiles
 // [tile_begin[p], tile_begin[p + 1]) with its m tile fastest.
-template <int BM, int BN, int WM, int WN, int KG, int PF, bool VEC>
+template <int BM, int BN, int WM, int WN, int KG, int PF, bool VEC, bool UPK>
 __global__ __launch_bounds__((tile_threads<BM, BN, WM, WN, KG>())) void conv_mfma_group_kernel(ConvGroupArgs g) {
     const int tile_id = xcd_tile(blockIdx.x, gridDim.x);
     int p = 0;
     while (p + 1 < g.count && tile_id >= g.tile_begin[p + 1]) ++p;
     const int local = tile_id - g.tile_begin[p];
     const int by = local / g.m_tiles[p];
-    conv_tile<BM, BN, WM, WN, KG, PF, VEC>(g.p[p], local - by * g.m_tiles[p], by, 0);
+    conv_tile<BM, BN, WM, WN, KG, PF, VEC, UPK>(g.p[p], local - by * g.m_tiles[p], by, 0);
 }
 
 // Sums split-K partials in split order, then bias + activation + residual.
@@ -528,6 +559,13 @@ __global__ __launch_bounds__(256) void conv_splitk_reduce(ConvArgs a) {
         float v = apply_act(s + a.bias[col], a.act, a.slope);
         if (a.res) v += a.res[n * a.r_sn + ho * a.r_sh + wo * a.r_sw + col];
         a.y[n * a.y_sn + ho * a.y_sh + wo * a.y_sw + col] = v;
+        if (a.up) {
+            float* u = a.up + n * a.u_sn + 2 * ho * a.u_sh + 2 * wo * a.u_sw + col;
+            u[0] = v;
+            u[a.u_sw] = v;
+            u[a.u_sh] = v;
+            u[a.u_sh + a.u_sw] = v;
+        }
     }
 }
 
@@ -543,7 +581,7 @@ constexpr const char* kNames[kNumConvTiles] = {"128x128",  "128x64",     "64x128
                                                "64x32k2",  "32x64k2",    "32x32k4",   "128x64w8", "64x64k2w8",
                                                "128x128w8", "64x128w8", "32x64k4w8"};
 
-template <int BM, int BN, int WM, int WN, int KG, int PF, bool VEC>
+template <int BM, int BN, int WM, int WN, int KG, int PF, bool VEC, bool UPK>
 void launch_one(const ConvArgs& a, dim3 grid, hipStream_t s) {
     constexpr size_t bytes = lds_bytes<BM, BN, KG>();
     static_assert(lds_stage_bytes<BM, BN, KG>() >= sizeof(float) * KG * BM * BN,
@@ -551,39 +589,54 @@ void launch_one(const ConvArgs& a, dim3 grid, hipStream_t s) {
     static std::once_flag once;
     std::call_once(once, [] {
         if (bytes > 65536)
-            (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&conv_mfma_kernel<BM, BN, WM, WN, KG, PF, VEC>),
-                                      hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(bytes));
+            (void)hipFuncSetAttribute(
+                reinterpret_cast<const void*>(&conv_mfma_kernel<BM, BN, WM, WN, KG, PF, VEC, UPK>),
+                hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(bytes));
     });
-    hipLaunchKernelGGL((conv_mfma_kernel<BM, BN, WM, WN, KG, PF, VEC>), grid,
+    hipLaunchKernelGGL((conv_mfma_kernel<BM, BN, WM, WN, KG, PF, VEC, UPK>), grid,
                        dim3(tile_threads<BM, BN, WM, WN, KG>()), bytes, s, a);
 }
 
-template <int BM, int BN, int WM, int WN, int KG, int PF>
-void launch_group(const ConvGroupArgs& g, hipStream_t s) {
+template <int BM, int BN, int WM, int WN, int KG, int PF, bool UPK>
+void launch_group_up(const ConvGroupArgs& g, hipStream_t s) {
     constexpr size_t bytes = lds_bytes<BM, BN, KG>();
     static std::once_flag once;
     std::call_once(once, [] {
         if (bytes > 65536)
             (void)hipFuncSetAttribute(
-                reinterpret_cast<const void*>(&conv_mfma_group_kernel<BM, BN, WM, WN, KG, PF, true>),
+                reinterpret_cast<const void*>(&conv_mfma_group_kernel<BM, BN, WM, WN, KG, PF, true, UPK>),
                 hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(bytes));
     });
-    hipLaunchKernelGGL((conv_mfma_group_kernel<BM, BN, WM, WN, KG, PF, true>),
+    hipLaunchKernelGGL((conv_mfma_group_kernel<BM, BN, WM, WN, KG, PF, true, UPK>),
                        dim3(static_cast<unsigned>(g.tile_begin[g.count])), dim3(tile_threads<BM, BN, WM, WN, KG>()),
                        bytes, s, g);
 }
 
+template <int BM, int BN, int WM, int WN, int KG, int PF>
+void launch_group(const ConvGroupArgs& g, hipStream_t s) {
+    bool up = false;
+    for (int i = 0; i < g.count; ++i) up = up || g.p[i].up != nullptr;
+    if (up)
+        launch_group_up<BM, BN, WM, WN, KG, PF, true>(g, s);
+    else
+        launch_group_up<BM, BN, WM, WN, KG, PF, false>(g, s);
+}
+
 constexpr int kPrefetch = 2;  // register stages: loads run two steps ahead
+
+void fail(const std::string& m) { throw std::runtime_error("conv_mfma: " + m); }
 
 template <int BM, int BN, int WM, int WN, int KG>
 void launch_tile(const ConvArgs& a, bool vec, dim3 grid, hipStream_t s) {
-    if (vec)
-        launch_one<BM, BN, WM, WN, KG, kPrefetch, true>(a, grid, s);
-    else
-        launch_one<BM, BN, WM, WN, KG, kPrefetch, false>(a, grid, s);
+    if (a.up) {
+        if (!vec) fail("an upsampled output needs vector loads");
+        launch_one<BM, BN, WM, WN, KG, kPrefetch, true, true>(a, grid, s);
+    } else if (vec) {
+        launch_one<BM, BN, WM, WN, KG, kPrefetch, true, false>(a, grid, s);
+    } else {
+        launch_one<BM, BN, WM, WN, KG, kPrefetch, false, false>(a, grid, s);
+    }
 }
-
-void fail(const std::string& m) { throw std::runtime_error("conv_mfma: " + m); }
 
 }  // namespace
 
@@ -694,6 +747,7 @@ void check_conv(const ConvArgs& a, const ConvTileShape& sh, bool vec) {
         static_cast<int64_t>(a.splits - 1) * a.kt_per_split >= a.ktiles)
         fail("bad split");
     if (a.splits > 1 && !a.ws) fail("split-K without workspace");
+    if (a.up && (a.u_sn < 0 || a.u_sh < 0 || a.u_sw < 0)) fail("negative upsample strides");
     if (a.x_sh < 0 || a.x_sw < 0 ||
         static_cast<int64_t>(a.H - 1) * a.x_sh + static_cast<int64_t>(a.W - 1) * a.x_sw + a.Cin >= (int64_t{1} << 31))
         fail("input image extent exceeds int32 offsets");

@@ -241,6 +241,7 @@ void step_views(const Step& s, std::vector<VRef>& rd, std::vector<VRef>& wr) {
     wr.push_back(s.out);
     rd.push_back(s.a);
     if (s.has_res) rd.push_back(s.res);
+    if (s.kind == StepKind::ConvMfma && s.up.buf != -1) wr.push_back(s.up);
     switch (s.kind) {
         case StepKind::Elt: rd.push_back(s.b); break;
         case StepKind::MaxPoolChain:
@@ -1163,6 +1164,21 @@ class Planner {
                 i += 3;
                 continue;
             }
+            // a conv whose output feeds a nearest 2x Resize right after it also
+            // writes the upsampled copy (the FPN's upsample into its concat)
+            if (st[i].kind == StepKind::ConvMfma && st[i].vec && !k::is_wino_tile(st[i].tile) && i + 1 < st.size() &&
+                st[i + 1].kind == StepKind::Resize && views_equal(st[i + 1].a, st[i].out)) {
+                const VRef& y = st[i].out;
+                const VRef& u = st[i + 1].out;
+                if (u.rank == 4 && y.rank == 4 && u.dims[0] == y.dims[0] && u.dims[1] == y.dims[1] &&
+                    u.dims[2] == 2 * y.dims[2] && u.dims[3] == 2 * y.dims[3] && u.str[1] == 1 && u.buf >= 0) {
+                    Step f = st[i];
+                    f.up = u;
+                    out.push_back(f);
+                    i += 2;
+                    continue;
+                }
+            }
             Step f;
             if (match_decode(i, &f)) {
                 i += 8;
@@ -1323,6 +1339,7 @@ class Planner {
                     touch(s.cls_in, t);
                     touch(s.cls_out, t);
                 }
+                if (s.kind == StepKind::ConvMfma && s.up.buf != -1) touch(s.up, t);
                 if (s.ws_buf >= 0) {
                     plan_.bufs[s.ws_buf].first = std::min(plan_.bufs[s.ws_buf].first, t);
                     plan_.bufs[s.ws_buf].last = std::max(plan_.bufs[s.ws_buf].last, t);
@@ -1441,6 +1458,7 @@ Schedule schedule_plan(const Plan& p, int max_streams) {
             rd[i].push_back(view_range(p, s.cls_in));
             wr[i].push_back(view_range(p, s.cls_out));
         }
+        if (s.kind == StepKind::ConvMfma && s.up.buf != -1) wr[i].push_back(view_range(p, s.up));
         if (s.ws_buf >= 0) {
             const Buffer& b = p.bufs[s.ws_buf];
             wr[i].push_back({b.offset, b.offset + b.elems});
@@ -1526,6 +1544,7 @@ std::string describe_plan(const Model& m, const Plan& p) {
         os << " out=" << fmt_view(s.out) << " a=" << fmt_view(s.a);
         if (s.kind == StepKind::Elt && s.elt >= k::kEltAdd && s.elt <= k::kEltDiv) os << " b=" << fmt_view(s.b);
         if (s.has_res) os << " res=" << fmt_view(s.res);
+        if (s.kind == StepKind::ConvMfma && s.up.buf != -1) os << " up=" << fmt_view(s.up);
         if (s.kind == StepKind::DetectDecode && s.cls_in.buf != -1)
             os << " cls=" << fmt_view(s.cls_in) << " clsout=" << fmt_view(s.cls_out);
         os << "\n";

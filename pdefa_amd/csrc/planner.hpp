@@ -49,6 +49,9 @@ struct Step {
     bool vec = false;
     int32_t splits = 1, kt_per_split = 0;
     int32_t ws_buf = -1;
+    // ConvMfma: nearest 2x upsample of out, written by the same epilogue
+    // (up.buf == -1: none); it replaces the Resize step that read out
+    VRef up;
     // >= 0: consecutive ConvMfma steps with the same id run as one grouped
     // launch of their common tile (k::launch_conv_mfma_group)
     int32_t group = -1;

@@ -501,6 +501,16 @@ void Session::prepare(const std::vector<std::vector<int64_t>>& dims) {
                 c.slope = s.slope;
                 c.splits = s.splits;
                 c.kt_per_split = s.kt_per_split;
+                if (s.up.buf != -1) {
+                    const k::View u = V(s.up, "conv upsampled out", si);
+                    if (u.str[1] != 1 || u.dims[0] != c.N || u.dims[1] != c.Cout || u.dims[2] != 2 * c.Ho ||
+                        u.dims[3] != 2 * c.Wo)
+                        throw std::runtime_error("conv upsampled output must be channels-last [N, Cout, 2Ho, 2Wo]");
+                    c.up = u.ptr;
+                    c.u_sn = u.str[0];
+                    c.u_sh = u.str[2];
+                    c.u_sw = u.str[3];
+                }
                 if (s.splits > 1) {
                     const Buffer& wb = plan.bufs.at(s.ws_buf);
                     const int64_t need = static_cast<int64_t>(s.splits) * c.N * c.Ho * c.Wo * c.Cout;

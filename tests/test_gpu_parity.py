@@ -278,6 +278,27 @@ def test_yolov8n_b8_batch_matches_b1(yolov8n):
     assert_network_close(got[7:8], model, x[7:8], "b8 image 7 vs oracle")
 
 
+def test_yolov8n_forced_split_k(yolov8n, monkeypatch):
+    """Every implicit-GEMM conv on one tile with K split across workgroups:
+    the reduce kernel's epilogue (activation, residual add, the FPN's
+    upsampled copy) against the oracle network."""
+    print("[case] yolov8n b1 forced split-K 32x32k4 x3", flush=True)
+    model, path = yolov8n
+    x, _ = ys.yolo_inputs(1)
+    monkeypatch.setenv("PDEFA_CONV_TILE", "32x32k4")
+    monkeypatch.setenv("PDEFA_CONV_SPLITS", "3")
+    eng = native.Engine(path)
+    try:
+        got = eng.run(x)[0]
+        plan = eng.plan()
+    finally:
+        eng.close()
+    lines = plan.splitlines()
+    assert any(" up=b" in l and "splits=1," not in l for l in lines)
+    assert any(" res=b" in l and "splits=1," not in l for l in lines)
+    assert_network_close(got, model, x, "forced split-K vs oracle")
+
+
 @pytest.mark.parametrize("nc", [20, 3])
 def test_head_class_counts(tmp_path, nc):
     """Detect heads of other class counts at 320x320: with nc = 20 each

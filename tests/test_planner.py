@@ -55,6 +55,11 @@ def test_yolov8n_plan_is_zero_copy(y8n_path):
     assert sum("eltwise(5)" in l for l in lines) == 0
     # residual adds of the 6 backbone bottlenecks live in conv epilogues
     assert sum(" res=" in l for l in lines) == 6
+    # the FPN's two nearest 2x upsamples are written by the convs that
+    # produce their inputs, straight into the concat buffers
+    assert not any(" resize " in l for l in lines)
+    ups = [l for l in lines if " up=b" in l]
+    assert len(ups) == 2 and all("/cv2/conv/Conv" in l for l in ups)
     # SPPF's three chained max-pools run as one step
     pools = [l for l in lines if " maxpool" in l]
     assert len(pools) == 1 and " maxpool_chain " in pools[0]
@@ -143,8 +148,8 @@ def test_concurrent_schedule_orders_every_hazard(y8n_path, monkeypatch, reuse):
         assert n_streams > 1  # the detect-head branches run concurrently
 
 
-VIEW = re.compile(r" (out|a|b|res|cls|clsout)=b(\d+)\+(\d+)\[([\d,]+)\]s\[([\d,]+)\]")
-WRITES = ("out", "clsout")
+VIEW = re.compile(r" (out|a|b|res|cls|clsout|up)=b(\d+)\+(\d+)\[([\d,]+)\]s\[([\d,]+)\]")
+WRITES = ("out", "clsout", "up")
 
 
 def view_elems(off, dims, strides):
