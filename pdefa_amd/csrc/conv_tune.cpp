@@ -17,7 +17,7 @@ constexpr size_t kMaxCandidates = 12;          // the cost model's best ones are
 constexpr int64_t kMaxWorkspaceBytes = 256LL << 20;  // split-K partials of one candidate
 constexpr double kKeepModelChoice = 0.97;      // another shape must beat the model's by 3%
 
-using Key = std::array<int32_t, 20>;
+using Key = std::array<int32_t, 21>;
 
 using GroupKey = std::vector<int32_t>;
 
@@ -26,8 +26,8 @@ std::map<Key, k::ConvLaunchShape> g_cache;
 std::map<GroupKey, ConvGroupTiming> g_group_cache;
 
 Key make_key(const ConvQuery& q, int device) {
-    return {device, q.N,  q.H,  q.W,  q.Cin, q.Ho, q.Wo, q.Cout, q.KH, q.KW,
-            q.sh,   q.sw, q.ph, q.pw, q.dh,  q.dw, q.act, q.has_res ? 1 : 0, q.vec ? 1 : 0, q.wino ? 1 : 0};
+    return {device, q.N,  q.H,  q.W,  q.Cin, q.Ho, q.Wo, q.Cout, q.KH, q.KW, q.sh,
+            q.sw,   q.ph, q.pw, q.dh, q.dw,  q.act, q.has_res ? 1 : 0, q.vec ? 1 : 0, q.wino ? 1 : 0, q.groups};
 }
 
 struct DeviceBuffer {
@@ -64,14 +64,14 @@ void launch(const k::ConvArgs& a, int tile, bool vec, hipStream_t s) {
 // output tensor itself: each element is read and then written by the same
 // lane.
 struct LayerScratch {
-    int64_t x_elems, out_elems, w_elems;
+    int64_t x_elems, out_elems, w_group, w_elems;
     DeviceBuffer x, y, w, bias, ws;
     k::ConvArgs a;
     LayerScratch(const ConvQuery& q, int max_splits, hipStream_t s)
         : x_elems(static_cast<int64_t>(q.N) * q.H * q.W * q.Cin),
           out_elems(static_cast<int64_t>(q.N) * q.Ho * q.Wo * q.Cout),
-          w_elems(std::max(k::packed_weight_elems(q.Cout, q.KH * q.KW * q.Cin),
-                           q.wino ? k::wino_packed_elems(q.Cout, q.Cin) : int64_t{0})),
+          w_group(k::packed_weight_elems(q.Cout / q.groups, q.KH * q.KW * (q.Cin / q.groups))),
+          w_elems(std::max(w_group * q.groups, q.wino ? k::wino_packed_elems(q.Cout, q.Cin) : int64_t{0})),
           x(x_elems),
           y(out_elems),
           w(w_elems),
@@ -81,19 +81,21 @@ struct LayerScratch {
         PDEFA_HIP(hipMemsetAsync(w.p, 0, static_cast<size_t>(w_elems) * 4, s));
         PDEFA_HIP(hipMemsetAsync(bias.p, 0, static_cast<size_t>(q.Cout) * 4, s));
         PDEFA_HIP(hipMemsetAsync(y.p, 0, static_cast<size_t>(out_elems) * 4, s));
-        const int K = q.KH * q.KW * q.Cin;
+        const int K = q.KH * q.KW * (q.Cin / q.groups);
         a.x = x.p;
         a.N = q.N;
         a.H = q.H;
         a.W = q.W;
-        a.Cin = q.Cin;
+        a.Cin = q.Cin / q.groups;
+        a.groups = q.groups;
+        a.w_group = w_group;
         a.x_sw = q.Cin;
         a.x_sh = static_cast<int64_t>(q.W) * q.Cin;
         a.x_sn = static_cast<int64_t>(q.H) * q.W * q.Cin;
         a.y = y.p;
         a.Ho = q.Ho;
         a.Wo = q.Wo;
-        a.Cout = q.Cout;
+        a.Cout = q.Cout / q.groups;
         a.y_sw = q.Cout;
         a.y_sh = static_cast<int64_t>(q.Wo) * q.Cout;
         a.y_sn = static_cast<int64_t>(q.Ho) * q.Wo * q.Cout;
@@ -150,8 +152,9 @@ k::ConvLaunchShape tune_conv(const ConvQuery& q, hipStream_t s) {
     if (auto it = g_cache.find(key); it != g_cache.end()) return it->second;
 
     const int64_t M = static_cast<int64_t>(q.N) * q.Ho * q.Wo;
-    const int K = q.KH * q.KW * q.Cin;
-    std::vector<k::ConvLaunchShape> all = k::conv_candidates(M, q.Cout, K, true, q.wino, q.Cin);
+    const int K = q.KH * q.KW * (q.Cin / q.groups);  // per group
+    std::vector<k::ConvLaunchShape> all =
+        k::conv_candidates(M * q.groups, q.Cout / q.groups, K, true, q.wino, q.Cin);
     // the cost model's best implicit-GEMM shapes, plus every Winograd shape
     std::vector<k::ConvLaunchShape> cands;
     for (const auto& c : all)

@@ -102,6 +102,14 @@ struct ConvArgs {
     float* ws = nullptr;
     int32_t splits = 1;
     int32_t kt_per_split = 0;  // multiple of the tile's KG
+    // groups > 1: a grouped convolution.  Cin, Cout, K and ktiles are then per
+    // group: group g reads input channels [g*Cin, (g+1)*Cin), writes output
+    // channels [g*Cout, (g+1)*Cout) (and the same channels of res and up),
+    // takes packed weights wpk + g*w_group and biases bias + g*Cout; the grid
+    // runs splits*groups in z and a split-K workspace holds
+    // [groups][splits][M][Cout].
+    int32_t groups = 1;
+    int64_t w_group = 0;
     // optional nearest 2x upsample of the result, written alongside y:
     // up[n, 2ho + i, 2wo + j, co] = y[n, ho, wo, co] for i, j in {0, 1}
     // (channels-last, n/h/w strides), e.g. straight into a concat buffer
@@ -164,8 +172,15 @@ struct ConvDirectArgs {
     int32_t KH = 1, KW = 1, sh = 1, sw = 1, ph = 0, pw = 0, dh = 1, dw = 1;
     int32_t act = 0;
     float slope = 0.01f;
+    // groups > 1: grouped convolution with Cin/groups input channels per
+    // group (depthwise when that is 1); wpk is then [KH*KW][Cin/groups][Cout]
+    // (output channel fastest, k::grouped_direct_packed_elems)
+    int32_t groups = 1;
 };
 void launch_conv_direct(const ConvDirectArgs& a, hipStream_t s);
+inline int64_t grouped_direct_packed_elems(int Cout, int Cin_g, int KH, int KW) {
+    return static_cast<int64_t>(KH) * KW * Cin_g * Cout;
+}
 
 // Letterbox of one interleaved 8-bit image (ch = 1, 3 or 4) into the planar
 // fp32 tensor dst[3][th][tw]: the scaled window (sw x sh at px, py) is

@@ -93,7 +93,8 @@ __device__ __forceinline__ int xcd_tile(int lin, int total) {
 // UPK: the build for problems with an upsampled copy (a.up), kept apart so
 // that its larger epilogue does not raise every other build's register count.
 template <int BM, int BN, int WM, int WN, int KG, int PF, bool VEC, bool UPK>
-__device__ __forceinline__ void conv_tile(const ConvArgs& a, const int bx, const int by, const int bz) {
+__device__ __forceinline__ void conv_tile(const ConvArgs& a, const int bx, const int by, const int bz,
+                                          const int grp) {
     constexpr int WAVES_M = BM / WM;
     constexpr int WAVES_N = BN / WN;
     constexpr int NT = tile_threads<BM, BN, WM, WN, KG>();  // 256 or 512 lanes
@@ -121,6 +122,9 @@ __device__ __forceinline__ void conv_tile(const ConvArgs& a, const int bx, const
     const int wave_n = (wave / KG) / WAVES_M;
     const int HoWo = a.Ho * a.Wo;
     const int M = a.N * HoWo;
+    // group grp of a grouped conv: its channel offsets (0 when groups == 1)
+    const int64_t g_in = static_cast<int64_t>(grp) * a.Cin;
+    const int64_t g_out = static_cast<int64_t>(grp) * a.Cout;
 
     const int m0 = bx * BM;
     const int n0 = by * BN;
@@ -140,20 +144,20 @@ __device__ __forceinline__ void conv_tile(const ConvArgs& a, const int bx, const
         int64_t yo = -1, ro = 0, uo = 0;
         if (m < M) {
             if (a.splits > 1) {
-                yo = (static_cast<int64_t>(bz) * M + m) * a.Cout;
+                yo = ((static_cast<int64_t>(grp) * a.splits + bz) * M + m) * a.Cout;
             } else {
                 const int n = m / HoWo;
                 const int rem = m - n * HoWo;
                 const int ho = rem / a.Wo;
                 const int wo = rem - ho * a.Wo;
                 yo = static_cast<int64_t>(n) * a.y_sn + static_cast<int64_t>(ho) * a.y_sh +
-                     static_cast<int64_t>(wo) * a.y_sw;
+                     static_cast<int64_t>(wo) * a.y_sw + g_out;
                 if (a.res)
                     ro = static_cast<int64_t>(n) * a.r_sn + static_cast<int64_t>(ho) * a.r_sh +
-                         static_cast<int64_t>(wo) * a.r_sw;
+                         static_cast<int64_t>(wo) * a.r_sw + g_out;
                 if (a.up)
                     uo = static_cast<int64_t>(n) * a.u_sn + static_cast<int64_t>(2 * ho) * a.u_sh +
-                         static_cast<int64_t>(2 * wo) * a.u_sw;
+                         static_cast<int64_t>(2 * wo) * a.u_sw + g_out;
             }
         }
         s_yoff[tid] = yo;
@@ -170,11 +174,11 @@ __device__ __forceinline__ void conv_tile(const ConvArgs& a, const int bx, const
 #pragma unroll
         for (int tn = 0; tn < TN; ++tn) {
             const int co = n0 + wave_n * WN + tn * 32 + l32;
-            bias_lane[tn] = co < a.Cout ? a.bias[co] : 0.0f;
+            bias_lane[tn] = co < a.Cout ? a.bias[g_out + co] : 0.0f;
         }
     } else {
         const int co = n0 + tid % BN;
-        bias_lane[0] = co < a.Cout ? a.bias[co] : 0.0f;
+        bias_lane[0] = co < a.Cout ? a.bias[g_out + co] : 0.0f;
     }
 
     // ---- loaders: this lane loads float4 chunk `chunk` (slice chunk / 8) of
@@ -202,7 +206,7 @@ __device__ __forceinline__ void conv_tile(const ConvArgs& a, const int bx, const
         row_hi0[r] = ho * a.sh - a.ph;
         row_wi0[r] = wo * a.sw - a.pw;
         row_off0[r] = row_hi0[r] * xsh + row_wi0[r] * xsw;
-        row_base[r] = a.x + static_cast<int64_t>(n) * a.x_sn;
+        row_base[r] = a.x + static_cast<int64_t>(n) * a.x_sn + g_in;
     }
     // (tap, ci, kh, kw) of this lane's chunk in the next step to load
     int tap = 0, ci = 0, kh = 0, kw = 0;
@@ -228,7 +232,8 @@ __device__ __forceinline__ void conv_tile(const ConvArgs& a, const int bx, const
     for (int i = 0; i < B_ROWS; ++i) {
         const int co = n0 + r0 + ROW_STEP * i;
         const int nb = min(co / kConvBN, nblocks - 1);
-        brow[i] = a.wpk + static_cast<int64_t>(nb) * a.ktiles * (kConvBN * BK) + (co % kConvBN) * BK + cc * 4;
+        brow[i] = a.wpk + grp * a.w_group + static_cast<int64_t>(nb) * a.ktiles * (kConvBN * BK) +
+                  (co % kConvBN) * BK + cc * 4;
     }
 
     floatx4 areg[PF][A_ROWS];
@@ -523,10 +528,11 @@ template <int BM, int BN, int WM, int WN, int KG, int PF, bool VEC, bool UPK>
 __global__ __launch_bounds__((tile_threads<BM, BN, WM, WN, KG>())) void conv_mfma_kernel(ConvArgs a) {
     const int gx = gridDim.x, gxy = gridDim.x * gridDim.y;
     const int tile_id = xcd_tile(blockIdx.x + gx * blockIdx.y + gxy * blockIdx.z, gxy * gridDim.z);
-    const int bz = tile_id / gxy;
+    const int bz = tile_id / gxy;  // group * splits + split
     const int bxy = tile_id - bz * gxy;
     const int by = bxy / gx;
-    conv_tile<BM, BN, WM, WN, KG, PF, VEC, UPK>(a, bxy - by * gx, by, bz);
+    const int grp = bz / a.splits;
+    conv_tile<BM, BN, WM, WN, KG, PF, VEC, UPK>(a, bxy - by * gx, by, bz - grp * a.splits, grp);
 }
 
 // Several independent problems in one launch (no split-K): a 1-D grid over
@@ -539,28 +545,33 @@ __global__ __launch_bounds__((tile_threads<BM, BN, WM, WN, KG>())) void conv_mfm
     while (p + 1 < g.count && tile_id >= g.tile_begin[p + 1]) ++p;
     const int local = tile_id - g.tile_begin[p];
     const int by = local / g.m_tiles[p];
-    conv_tile<BM, BN, WM, WN, KG, PF, VEC, UPK>(g.p[p], local - by * g.m_tiles[p], by, 0);
+    conv_tile<BM, BN, WM, WN, KG, PF, VEC, UPK>(g.p[p], local - by * g.m_tiles[p], by, 0, 0);
 }
 
 // Sums split-K partials in split order, then bias + activation + residual.
 __global__ __launch_bounds__(256) void conv_splitk_reduce(ConvArgs a) {
     const int HoWo = a.Ho * a.Wo;
     const int M = a.N * HoWo;
-    const int total = M * a.Cout;
+    const int per_group = M * a.Cout;
+    const int total = per_group * a.groups;
     for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < total; i += gridDim.x * blockDim.x) {
-        const int m = i / a.Cout;
-        const int col = i - m * a.Cout;
+        const int grp = i / per_group;
+        const int ig = i - grp * per_group;
+        const int m = ig / a.Cout;
+        const int col = ig - m * a.Cout;
+        const int64_t slab = static_cast<int64_t>(grp) * a.splits;
         float s = 0.0f;
-        for (int z = 0; z < a.splits; ++z) s += a.ws[(static_cast<int64_t>(z) * M + m) * a.Cout + col];
+        for (int z = 0; z < a.splits; ++z) s += a.ws[((slab + z) * M + m) * a.Cout + col];
         const int n = m / HoWo;
         const int rem = m - n * HoWo;
         const int ho = rem / a.Wo;
         const int wo = rem - ho * a.Wo;
-        float v = apply_act(s + a.bias[col], a.act, a.slope);
-        if (a.res) v += a.res[n * a.r_sn + ho * a.r_sh + wo * a.r_sw + col];
-        a.y[n * a.y_sn + ho * a.y_sh + wo * a.y_sw + col] = v;
+        const int64_t c = static_cast<int64_t>(grp) * a.Cout + col;  // channel of the whole conv
+        float v = apply_act(s + a.bias[c], a.act, a.slope);
+        if (a.res) v += a.res[n * a.r_sn + ho * a.r_sh + wo * a.r_sw + c];
+        a.y[n * a.y_sn + ho * a.y_sh + wo * a.y_sw + c] = v;
         if (a.up) {
-            float* u = a.up + n * a.u_sn + 2 * ho * a.u_sh + 2 * wo * a.u_sw + col;
+            float* u = a.up + n * a.u_sn + 2 * ho * a.u_sh + 2 * wo * a.u_sw + c;
             u[0] = v;
             u[a.u_sw] = v;
             u[a.u_sh] = v;
@@ -741,7 +752,9 @@ void check_conv(const ConvArgs& a, const ConvTileShape& sh, bool vec) {
     if (a.K != a.KH * a.KW * a.Cin) fail("K mismatch");
     if (a.ktiles != (a.K + BK - 1) / BK) fail("ktiles mismatch");
     const int64_t M = static_cast<int64_t>(a.N) * a.Ho * a.Wo;
-    if (M * std::max(a.Cout, 1) >= (int64_t{1} << 31)) fail("M * Cout too large");
+    if (a.groups < 1) fail("groups < 1");
+    if (M * std::max(a.Cout, 1) * a.groups >= (int64_t{1} << 31)) fail("M * Cout too large");
+    if (a.groups > 1 && a.w_group < packed_weight_elems(a.Cout, a.K)) fail("packed weights per group too small");
     if (a.splits < 1 || a.kt_per_split < 1 || a.kt_per_split % sh.kg != 0 ||
         static_cast<int64_t>(a.splits) * a.kt_per_split < a.ktiles ||
         static_cast<int64_t>(a.splits - 1) * a.kt_per_split >= a.ktiles)
@@ -766,8 +779,9 @@ void launch_conv_mfma(const ConvArgs& a, int tile, bool vec, hipStream_t s) {
     check_conv(a, sh, vec);
     const int64_t M = static_cast<int64_t>(a.N) * a.Ho * a.Wo;
     const int64_t gx = (M + sh.bm - 1) / sh.bm, gy = (a.Cout + sh.bn - 1) / sh.bn;
-    if (gx * gy * a.splits >= (int64_t{1} << 31) || gy > 65535 || a.splits > 65535) fail("grid too large");
-    const dim3 grid(static_cast<unsigned>(gx), static_cast<unsigned>(gy), static_cast<unsigned>(a.splits));
+    const int64_t gz = static_cast<int64_t>(a.splits) * a.groups;
+    if (gx * gy * gz >= (int64_t{1} << 31) || gy > 65535 || gz > 65535) fail("grid too large");
+    const dim3 grid(static_cast<unsigned>(gx), static_cast<unsigned>(gy), static_cast<unsigned>(gz));
     switch (tile) {
         case kTile128x128: launch_tile<128, 128, 64, 64, 1>(a, vec, grid, s); break;
         case kTile128x64: launch_tile<128, 64, 64, 32, 1>(a, vec, grid, s); break;
@@ -784,7 +798,7 @@ void launch_conv_mfma(const ConvArgs& a, int tile, bool vec, hipStream_t s) {
         case kTile32x64K4W8: launch_tile<32, 64, 32, 32, 4>(a, vec, grid, s); break;
     }
     if (a.splits > 1) {
-        const int64_t total = M * a.Cout;
+        const int64_t total = M * a.Cout * a.groups;
         const unsigned blocks = static_cast<unsigned>(std::min<int64_t>((total + 255) / 256, 65535));
         hipLaunchKernelGGL(conv_splitk_reduce, dim3(blocks), dim3(256), 0, s, a);
     }
@@ -801,6 +815,7 @@ void launch_conv_mfma_group(const ConvArgs* probs, int count, int tile, hipStrea
         const ConvArgs& a = probs[i];
         check_conv(a, sh, true);
         if (a.splits != 1) fail("grouped problems take no split-K");
+        if (a.groups != 1) fail("grouped launches take no grouped convs");
         const int64_t M = static_cast<int64_t>(a.N) * a.Ho * a.Wo;
         const int64_t gx = (M + sh.bm - 1) / sh.bm, gy = (a.Cout + sh.bn - 1) / sh.bn;
         g.tile_begin[i] = static_cast<int32_t>(total);

@@ -371,6 +371,7 @@ void launch_conv_wino(const ConvArgs& a, int bn, hipStream_t s) {
     if (bn != 32 && bn != 64) fail("bn must be 32 or 64");
     if (!a.x || !a.y || !a.wpk || !a.bias) fail("null pointer");
     if (a.up) fail("no upsampled output on the Winograd path");
+    if (a.groups != 1) fail("grouped convs take the implicit GEMM");
     if (!wino_eligible(a.KH, a.KW, a.sh, a.sw, a.dh, a.dw, a.Cin)) fail("not a 3x3 stride-1 conv with Cin % 4 == 0");
     if (a.N <= 0 || a.H <= 0 || a.W <= 0 || a.Cout <= 0) fail("empty shape");
     if (a.Ho != a.H + 2 * a.ph - 2 || a.Wo != a.W + 2 * a.pw - 2 || a.Ho <= 0 || a.Wo <= 0) fail("output size");

@@ -807,6 +807,46 @@ void launch_direct_cb(const ConvDirectArgs& a, dim3 grid, int P, bool k3, bool c
 
 }  // namespace
 
+// Grouped convolution (groups > 1, few channels per group: depthwise and
+// the like): lane = (output pixel, output channel), channel fastest, so that
+// channels-last inputs, the [tap][ci][Cout] weights and channels-last outputs
+// are read and written at consecutive addresses across a wave.  The sum
+// starts from the bias and runs over the taps (kh, kw) in order, then the
+// group's input channels.  Input offsets within one image fit int32
+// (checked by the launcher).
+__global__ __launch_bounds__(256) void conv_grouped_kernel(ConvDirectArgs a, int32_t total) {
+    const int32_t idx = blockIdx.x * 256 + threadIdx.x;
+    if (idx >= total) return;
+    const int32_t C = static_cast<int32_t>(a.y.dims[1]), Ho = static_cast<int32_t>(a.y.dims[2]),
+                  Wo = static_cast<int32_t>(a.y.dims[3]);
+    const int32_t co = idx % C;
+    int32_t t = idx / C;
+    const int32_t wo = t % Wo;
+    t /= Wo;
+    const int32_t ho = t % Ho;
+    const int32_t n = t / Ho;
+    const int32_t cout_g = C / a.groups, cin_g = static_cast<int32_t>(a.x.dims[1]) / a.groups;
+    const int32_t H = static_cast<int32_t>(a.x.dims[2]), W = static_cast<int32_t>(a.x.dims[3]);
+    const int32_t xs1 = static_cast<int32_t>(a.x.str[1]), xs2 = static_cast<int32_t>(a.x.str[2]),
+                  xs3 = static_cast<int32_t>(a.x.str[3]);
+    const float* xb = a.x.ptr + n * a.x.str[0] + static_cast<int64_t>(co / cout_g) * cin_g * a.x.str[1];
+    float acc = a.bias ? a.bias[co] : 0.0f;
+    for (int kh = 0; kh < a.KH; ++kh) {
+        const int32_t ih = ho * a.sh - a.ph + kh * a.dh;
+        if (static_cast<uint32_t>(ih) >= static_cast<uint32_t>(H)) continue;
+        for (int kw = 0; kw < a.KW; ++kw) {
+            const int32_t iw = wo * a.sw - a.pw + kw * a.dw;
+            if (static_cast<uint32_t>(iw) >= static_cast<uint32_t>(W)) continue;
+            const float* xp = xb + ih * xs2 + iw * xs3;
+            const float* wp = a.wpk + static_cast<int64_t>((kh * a.KW + kw) * cin_g) * C + co;
+            for (int ci = 0; ci < cin_g; ++ci) acc = fmaf(xp[ci * xs1], wp[static_cast<int64_t>(ci) * C], acc);
+        }
+    }
+    float v = apply_act(acc, a.act, a.slope);
+    if (a.res.ptr) v += a.res.ptr[n * a.res.str[0] + co * a.res.str[1] + ho * a.res.str[2] + wo * a.res.str[3]];
+    a.y.ptr[n * a.y.str[0] + co * a.y.str[1] + ho * a.y.str[2] + wo * a.y.str[3]] = v;
+}
+
 void launch_conv_direct(const ConvDirectArgs& a, hipStream_t s) {
     check_view(a.x, "conv_direct x");
     check_view(a.y, "conv_direct y");
@@ -820,6 +860,18 @@ void launch_conv_direct(const ConvDirectArgs& a, hipStream_t s) {
         for (int d = 1; d < 4; ++d) e += (v.dims[d] - 1) * std::abs(v.str[d]);
         return e;
     };
+    if (a.groups > 1) {
+        if (a.x.dims[1] % a.groups != 0 || a.y.dims[1] % a.groups != 0)
+            throw std::runtime_error("conv_direct: channels not divisible by groups");
+        if (a.res.ptr && (a.res.dims[1] != a.y.dims[1] || a.res.dims[2] != a.y.dims[2]))
+            throw std::runtime_error("conv_direct: residual shape");
+        const int64_t total = P * a.y.dims[1];
+        if (total >= (int64_t{1} << 31) || extent(a.x) >= (int64_t{1} << 31))
+            throw std::runtime_error("conv_direct: shape exceeds int32 indexing");
+        hipLaunchKernelGGL(conv_grouped_kernel, dim3(static_cast<unsigned>((total + 255) / 256)), dim3(256), 0, s, a,
+                           static_cast<int32_t>(total));
+        return;
+    }
     const int cb = direct_cb(static_cast<int>(a.y.dims[1]));
     if (P >= (int64_t{1} << 31) || extent(a.x) >= (int64_t{1} << 31) ||
         a.x.dims[1] * a.KH * a.KW * 64 >= (int64_t{1} << 31))

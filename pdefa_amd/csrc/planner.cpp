@@ -212,7 +212,7 @@ struct Val {
 ConvQuery conv_query(const Step& s) {
     ConvQuery q;
     q.N = static_cast<int32_t>(s.a.dims[0]);
-    q.Cin = static_cast<int32_t>(s.a.dims[1]);
+    q.Cin = static_cast<int32_t>(s.a.dims[1]);  // all channels (groups of Cin / groups)
     q.H = static_cast<int32_t>(s.a.dims[2]);
     q.W = static_cast<int32_t>(s.a.dims[3]);
     q.Cout = static_cast<int32_t>(s.out.dims[1]);
@@ -229,7 +229,8 @@ ConvQuery conv_query(const Step& s) {
     q.act = s.act;
     q.has_res = s.has_res;
     q.vec = s.vec;
-    q.wino = s.vec && k::wino_eligible(s.KH, s.KW, s.sh, s.sw, s.dh, s.dw, q.Cin);
+    q.groups = s.groups;
+    q.wino = s.vec && s.groups == 1 && k::wino_eligible(s.KH, s.KW, s.sh, s.sw, s.dh, s.dw, q.Cin);
     return q;
 }
 
@@ -508,8 +509,8 @@ class Planner {
                     const Dims x = dims(e.in[0], e.node);
                     const Dims w = dims(e.in[1], e.node);
                     if (x.size() != 4 || w.size() != 4) fail(m_, e.node, "conv expects rank-4 input and weight");
-                    if (p.groups > 1) fail(m_, e.node, "grouped conv unsupported");
-                    if (x[1] != w[1]) fail(m_, e.node, "conv channel mismatch");
+                    const int64_t G = std::max<int64_t>(1, p.groups);
+                    if (x[1] != w[1] * G || w[0] % G != 0) fail(m_, e.node, "conv channel mismatch");
                     if (!val(e.in[1]).is_weight) fail(m_, e.node, "conv weight must be a constant");
                     if (e.in.size() > 2 && !val(e.in[2]).is_weight) fail(m_, e.node, "conv bias must be a constant");
                     const int64_t ho = (x[2] + 2 * p.pad_h - ((w[2] - 1) * p.dil_h + 1)) / p.stride_h + 1;
@@ -882,9 +883,13 @@ class Planner {
         const Node& n = m_.nodes[e.node];
         const OpParams& p = n.params;
         const Dims& wd = val(e.in[1]).dims;
+        const int64_t G = std::max<int64_t>(1, p.groups);
         // Tiny-Cin layers (the 3-channel stem) and tiny-Cout layers go to the
-        // direct kernel, which reads any layout (no channels-last input copy).
-        const bool small = wd[0] < 8 || (wd[1] % 4 != 0 && wd[1] * wd[2] * wd[3] <= 64);
+        // direct kernel, which reads any layout (no channels-last input copy);
+        // so do grouped convs with few channels per group (depthwise), while
+        // the others run their groups through the implicit GEMM.
+        const bool small = G > 1 ? (wd[1] < 8 || wd[1] % 4 != 0 || wd[0] / G < 8)
+                                 : (wd[0] < 8 || (wd[1] % 4 != 0 && wd[1] * wd[2] * wd[3] <= 64));
         const VRef x = small ? input_view(e.in[0]) : conv_input_view(e.in[0], e.node);
         const VRef y = val(e.out).view;
         Step s;
@@ -899,13 +904,14 @@ class Planner {
         s.pw = static_cast<int32_t>(p.pad_w);
         s.dh = static_cast<int32_t>(p.dil_h);
         s.dw = static_cast<int32_t>(p.dil_w);
-        const int64_t cin = wd[1], cout = wd[0];
+        s.groups = static_cast<int32_t>(G);
+        const int64_t cin = wd[1], cout = wd[0];  // input channels per group, all output channels
         s.act = e.act;
         s.slope = e.slope;
         // The reference routes 3x3/s1/d1 convs with 16 < Cin <= 512 to its Winograd
         // kernel (conv2d.cpp:602-631), whose fused SiLU is the polynomial form.
         const bool winograd = s.KH == 3 && s.KW == 3 && s.sh == 1 && s.sw == 1 && s.dh == 1 && s.dw == 1 && cin > 16 &&
-                              cin <= 512;
+                              cin <= 512 && G == 1;
         if (s.act == k::kActSilu && winograd && opt_.winograd_form_silu) s.act = k::kActSiluWinogradForm;
         if (e.res != INT32_MIN) {
             s.has_res = true;
@@ -919,12 +925,12 @@ class Planner {
             const int64_t K = cin * s.KH * s.KW;
             // The Winograd kernel needs the transformed weights packed at model
             // load for exactly these layers, and 16-byte aligned input pixels.
-            const bool wino = s.vec && k::wino_eligible(s.KH, s.KW, s.sh, s.sw, s.dh, s.dw, static_cast<int>(cin));
+            const bool wino = s.vec && G == 1 && k::wino_eligible(s.KH, s.KW, s.sh, s.sw, s.dh, s.dw, static_cast<int>(cin));
             k::ConvLaunchShape ls;
             if (opt_.tune_conv && opt_.force_tile < 0 && opt_.split_k) {
                 ls = opt_.tune_conv(conv_query(s));
             } else {
-                ls = k::conv_select(M, static_cast<int>(cout), static_cast<int>(K), opt_.split_k, wino,
+                ls = k::conv_select(M * G, static_cast<int>(cout / G), static_cast<int>(K), opt_.split_k, wino,
                                     static_cast<int>(cin));
             }
             if (k::is_wino_tile(opt_.force_tile)) {
@@ -1202,7 +1208,7 @@ class Planner {
     }
 
     // ---- 6. liveness + arena ----------------------------------------------
-    bool groupable(const Step& s) const { return s.kind == StepKind::ConvMfma && s.vec; }
+    bool groupable(const Step& s) const { return s.kind == StepKind::ConvMfma && s.vec && s.groups == 1; }
 
     // Reorders the program by list scheduling (the earliest ready step first)
     // and, where independent implicit-GEMM convs are ready together, asks the
@@ -1282,7 +1288,8 @@ class Planner {
                 Step s = st[j];
                 if (S.size() > 1) {
                     const int kg = k::conv_tile_shape(tile).kg;
-                    const int ktiles = static_cast<int>((s.a.dims[1] * s.KH * s.KW + k::kConvBK - 1) / k::kConvBK);
+                    const int ktiles =
+                        static_cast<int>((s.a.dims[1] / s.groups * s.KH * s.KW + k::kConvBK - 1) / k::kConvBK);
                     s.group = next_group;
                     s.tile = tile;
                     s.splits = 1;
@@ -1539,6 +1546,7 @@ std::string describe_plan(const Model& m, const Plan& p) {
                << ")";
         if (s.group >= 0) os << " group=" << s.group;
         if (s.kind == StepKind::ConvDirect) os << "(act=" << s.act << ")";
+        if ((s.kind == StepKind::ConvMfma || s.kind == StepKind::ConvDirect) && s.groups > 1) os << " groups=" << s.groups;
         os << " node=" << s.node;
         if (s.node >= 0) os << " '" << m.nodes[s.node].name << "'";
         os << " out=" << fmt_view(s.out) << " a=" << fmt_view(s.a);

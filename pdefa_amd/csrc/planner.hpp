@@ -49,6 +49,7 @@ struct Step {
     bool vec = false;
     int32_t splits = 1, kt_per_split = 0;
     int32_t ws_buf = -1;
+    int32_t groups = 1;  // conv groups (the weight holds Cin / groups input channels)
     // ConvMfma: nearest 2x upsample of out, written by the same epilogue
     // (up.buf == -1: none); it replaces the Resize step that read out
     VRef up;
@@ -92,6 +93,7 @@ struct ConvQuery {
     int32_t N, H, W, Cin, Ho, Wo, Cout, KH, KW, sh, sw, ph, pw, dh, dw, act;
     bool has_res, vec;
     bool wino;  // the Winograd kernel applies (3x3, stride 1, dilation 1, Cin % 4 == 0)
+    int32_t groups = 1;  // Cin and Cout count all channels
 };
 
 // Measured comparison of independent convs launched one by one (each with

@@ -57,7 +57,7 @@ std::shared_ptr<DeviceModel> upload_model(const Model& m) {
     }
     struct PackPlan {
         size_t node, wpk_off, bias_off, dpk_off, wino_off;
-        int cout, cin, kh, kw, w, b;
+        int cout, cin, kh, kw, w, b, groups;  // cin: per group
         bool wino;
     };
     std::vector<PackPlan> pp;
@@ -76,15 +76,20 @@ std::shared_ptr<DeviceModel> upload_model(const Model& m) {
         p.w = w;
         p.b = (n.inputs.size() > 2 && n.inputs[2] <= -1000) ? -1000 - n.inputs[2] : -1;
         if (p.b >= 0 && m.weights[p.b].numel() < p.cout) p.b = -1;
+        const OpParams& op = n.params;
+        p.groups = static_cast<int>(std::max<int64_t>(1, op.groups));
+        if (p.cout % p.groups != 0) continue;  // the planner reports the mismatch
+        const int64_t w_group = k::packed_weight_elems(p.cout / p.groups, p.kh * p.kw * p.cin);
         p.wpk_off = total;
-        total += align_up(static_cast<size_t>(k::packed_weight_elems(p.cout, p.kh * p.kw * p.cin)));
+        total += align_up(static_cast<size_t>(w_group * p.groups));
         p.bias_off = total;
         total += align_up(static_cast<size_t>(p.cout));
         p.dpk_off = total;
-        total += align_up(static_cast<size_t>(k::direct_packed_elems(p.cout, p.kh * p.kw * p.cin)));
-        const OpParams& op = n.params;
-        p.wino = k::wino_eligible(p.kh, p.kw, static_cast<int>(op.stride_h), static_cast<int>(op.stride_w),
-                                  static_cast<int>(op.dil_h), static_cast<int>(op.dil_w), p.cin);
+        total += align_up(static_cast<size_t>(p.groups > 1 ? k::grouped_direct_packed_elems(p.cout, p.cin, p.kh, p.kw)
+                                                           : k::direct_packed_elems(p.cout, p.kh * p.kw * p.cin)));
+        p.wino = p.groups == 1 && k::wino_eligible(p.kh, p.kw, static_cast<int>(op.stride_h),
+                                                   static_cast<int>(op.stride_w), static_cast<int>(op.dil_h),
+                                                   static_cast<int>(op.dil_w), p.cin);
         if (p.wino) {
             p.wino_off = total;
             total += align_up(static_cast<size_t>(k::wino_packed_elems(p.cout, p.cin)));
@@ -98,11 +103,20 @@ std::shared_ptr<DeviceModel> upload_model(const Model& m) {
         if (m.weights[i].nbytes) std::memcpy(host.data() + woff[i], m.weights[i].data, m.weights[i].nbytes);
     for (const auto& p : pp) {
         if (p.b >= 0) std::memcpy(host.data() + p.bias_off, m.weights[p.b].data, sizeof(float) * p.cout);
-        // direct-conv layout [co / CB][k][co % CB], k = (ci, kh, kw); padding stays zero
         const int K = p.cin * p.kh * p.kw;
-        const int cb = k::direct_cb(p.cout);
         const float* src = static_cast<const float*>(m.weights[p.w].data);
         float* dst = host.data() + p.dpk_off;
+        if (p.groups > 1) {
+            // grouped direct layout [kh*KW + kw][ci][co], output channel fastest
+            for (int co = 0; co < p.cout; ++co)
+                for (int ci = 0; ci < p.cin; ++ci)
+                    for (int t = 0; t < p.kh * p.kw; ++t)
+                        dst[(static_cast<size_t>(t) * p.cin + ci) * p.cout + co] =
+                            src[(static_cast<size_t>(co) * p.cin + ci) * p.kh * p.kw + t];
+            continue;
+        }
+        // direct-conv layout [co / CB][k][co % CB], k = (ci, kh, kw); padding stays zero
+        const int cb = k::direct_cb(p.cout);
         for (int co = 0; co < p.cout; ++co)
             for (int kk = 0; kk < K; ++kk)
                 dst[(static_cast<size_t>(co / cb) * K + kk) * cb + co % cb] = src[static_cast<size_t>(co) * K + kk];
@@ -121,8 +135,16 @@ std::shared_ptr<DeviceModel> upload_model(const Model& m) {
             pk.wpk = dm->blob + p.wpk_off;
             pk.bias = dm->blob + p.bias_off;
             pk.dpk = dm->blob + p.dpk_off;
-            k::launch_pack_conv_weights(pk.wpk, dm->wptr[p.w], p.cout, p.cin, p.kh, p.kw, s);
-            PDEFA_HIP(hipGetLastError());
+            pk.groups = p.groups;
+            // group g: weight rows [g*Cout/G, (g+1)*Cout/G) packed at g * w_group
+            const int cout_g = p.cout / p.groups;
+            const int64_t w_group = k::packed_weight_elems(cout_g, p.kh * p.kw * p.cin);
+            for (int g = 0; g < p.groups; ++g) {
+                k::launch_pack_conv_weights(pk.wpk + g * w_group,
+                                            dm->wptr[p.w] + static_cast<int64_t>(g) * cout_g * p.cin * p.kh * p.kw,
+                                            cout_g, p.cin, p.kh, p.kw, s);
+                PDEFA_HIP(hipGetLastError());
+            }
             if (p.wino) {
                 pk.wino = dm->blob + p.wino_off;
                 k::launch_pack_wino_weights(pk.wino, dm->wptr[p.w], p.cout, p.cin, s);
@@ -457,14 +479,15 @@ void Session::prepare(const std::vector<std::vector<int64_t>>& dims) {
                 k::ConvArgs& c = l.conv;
                 c.x = x.ptr;
                 c.N = static_cast<int32_t>(x.dims[0]);
-                c.Cin = static_cast<int32_t>(x.dims[1]);
+                c.groups = s.groups;
+                c.Cin = static_cast<int32_t>(x.dims[1] / s.groups);  // per group
                 c.H = static_cast<int32_t>(x.dims[2]);
                 c.W = static_cast<int32_t>(x.dims[3]);
                 c.x_sn = x.str[0];
                 c.x_sh = x.str[2];
                 c.x_sw = x.str[3];
                 c.y = y.ptr;
-                c.Cout = static_cast<int32_t>(y.dims[1]);
+                c.Cout = static_cast<int32_t>(y.dims[1] / s.groups);
                 c.Ho = static_cast<int32_t>(y.dims[2]);
                 c.Wo = static_cast<int32_t>(y.dims[3]);
                 c.y_sn = y.str[0];
@@ -479,7 +502,9 @@ void Session::prepare(const std::vector<std::vector<int64_t>>& dims) {
                     c.r_sw = r.str[3];
                 }
                 const HostTensor& wt = model_->weights.at(-1000 - n.inputs[1]);
-                if (wt.dims[0] != c.Cout || wt.dims[1] != c.Cin) throw std::runtime_error("conv weight shape mismatch");
+                if (wt.dims[0] != static_cast<int64_t>(c.Cout) * s.groups || wt.dims[1] != c.Cin ||
+                    x.dims[1] != static_cast<int64_t>(c.Cin) * s.groups || pk.groups != s.groups)
+                    throw std::runtime_error("conv weight shape mismatch");
                 if (k::is_wino_tile(s.tile)) {
                     if (!pk.wino) throw std::runtime_error("Winograd weights were not packed: " + n.name);
                     c.wpk = pk.wino;
@@ -497,6 +522,7 @@ void Session::prepare(const std::vector<std::vector<int64_t>>& dims) {
                 c.dw = s.dw;
                 c.K = c.KH * c.KW * c.Cin;
                 c.ktiles = (c.K + k::kConvBK - 1) / k::kConvBK;
+                c.w_group = k::packed_weight_elems(c.Cout, c.K);
                 c.act = s.act;
                 c.slope = s.slope;
                 c.splits = s.splits;
@@ -533,8 +559,11 @@ void Session::prepare(const std::vector<std::vector<int64_t>>& dims) {
                 if (s.has_res) d.res = V(s.res, "conv res", si);
                 const int w = -1000 - n.inputs[1];
                 const HostTensor& wt = model_->weights.at(w);
-                if (wt.dims[0] != d.y.dims[1] || wt.dims[1] != d.x.dims[1]) throw std::runtime_error("conv weight shape mismatch");
+                if (wt.dims[0] != d.y.dims[1] || wt.dims[1] * s.groups != d.x.dims[1])
+                    throw std::runtime_error("conv weight shape mismatch");
                 const DeviceModel::Pack& pk = dev_->packs.at(s.node);
+                if (pk.groups != s.groups) throw std::runtime_error("conv weights packed for other groups");
+                d.groups = s.groups;
                 if (!pk.dpk || !pk.bias) throw std::runtime_error("conv weights not packed");
                 d.wpk = pk.dpk;
                 d.bias = pk.bias;
@@ -888,13 +917,14 @@ void Session::step_stats(int32_t iters, std::vector<double>& ms, std::vector<int
         kind[i] = static_cast<int32_t>(l.kind);
         if (l.kind == StepKind::ConvMfma) {
             auto conv_flops = [](const k::ConvArgs& c) {
-                return 2LL * c.N * c.Cout * c.Cin * c.KH * c.KW * static_cast<int64_t>(c.Ho) * c.Wo;
+                return 2LL * c.N * c.Cout * c.groups * c.Cin * c.KH * c.KW * static_cast<int64_t>(c.Ho) * c.Wo;
             };
             if (l.group.empty()) flops[i] = conv_flops(l.conv);
             for (const k::ConvArgs& c : l.group) flops[i] += conv_flops(c);
         } else if (l.kind == StepKind::ConvDirect) {
             const k::ConvDirectArgs& d = l.direct;
-            flops[i] = 2LL * d.y.dims[0] * d.y.dims[1] * d.x.dims[1] * d.KH * d.KW * d.y.dims[2] * d.y.dims[3];
+            flops[i] = 2LL * d.y.dims[0] * d.y.dims[1] * (d.x.dims[1] / d.groups) * d.KH * d.KW * d.y.dims[2] *
+                       d.y.dims[3];
         }
     }
 }

@@ -42,6 +42,7 @@ struct DeviceModel {
         float* bias = nullptr;  // Cout floats, zeros when the conv has no bias
         float* dpk = nullptr;   // direct-conv layout (k::direct_packed_elems)
         float* wino = nullptr;  // Winograd-transformed weights (3x3 stride-1 convs only)
+        int groups = 1;         // wpk holds one packed block per group; dpk the grouped layout
     };
     std::vector<Pack> packs;  // by node index (empty for non-conv nodes)
     ~DeviceModel();

@@ -245,26 +245,53 @@ def build_yolov8(scale: str = "n", seed: int = 0, nc: int = 80, imgsz: int = 640
 
 
 def build_single_conv(cin: int, cout: int, k: int, stride: int, hw: int, seed: int = 7,
-                      silu: bool = True) -> Tuple[EngineModel, np.ndarray]:
-    """One Conv2d(k, stride, pad k//2) + bias (+ SiLU as Sigmoid*Mul) graph.
+                      silu: bool = True, groups: int = 1) -> Tuple[EngineModel, np.ndarray]:
+    """One Conv2d(k, stride, pad k//2, groups) + bias (+ SiLU as Sigmoid*Mul)
+    graph.
 
     Returns the model and its seeded input x ~ U[0,1) of shape [1,cin,hw,hw].
-    Seed stream: x, then W (Kaiming-uniform, bound sqrt(6/fan_in)), then
-    b ~ U[-0.1, 0.1]."""
+    Seed stream: x, then W [cout, cin/groups, k, k] (Kaiming-uniform, bound
+    sqrt(6/fan_in)), then b ~ U[-0.1, 0.1]."""
     rng = np.random.default_rng(seed)
     x = rng.random((1, cin, hw, hw), dtype=np.float32)
-    w = kaiming_uniform(rng, (cout, cin, k, k))
+    w = kaiming_uniform(rng, (cout, cin // groups, k, k))
     bias = rng.uniform(-0.1, 0.1, size=cout).astype(np.float32)
     b = GraphBuilder()
     wi, bi = b.const("conv.weight", w), b.const("conv.bias", bias)
     p = k // 2
     y = b.node("Conv", "/conv/Conv", [-1, wi, bi], stride_h=stride, stride_w=stride,
-               pad_h=p, pad_w=p, dil_h=1, dil_w=1, groups=1)
+               pad_h=p, pad_w=p, dil_h=1, dil_w=1, groups=groups)
     if silu:
         sg = b.node("Sigmoid", "/act/Sigmoid", [y])
         y = b.node("Mul", "/act/Mul", [y, sg])
     ho = (hw + 2 * p - k) // stride + 1
     return b.model([1, cin, hw, hw], [1, cout, ho, ho], [y]), x
+
+
+def build_scdown(cin: int, cout: int, hw: int, n: int = 1, seed: int = 11) -> Tuple[EngineModel, np.ndarray]:
+    """YOLOv10's SCDown block: a 1x1 Conv-SiLU to cout channels, then a 3x3
+    stride-2 depthwise Conv (groups = cout, no activation), and a grouped 3x3
+    Conv-SiLU (groups = cout / 8) whose output is added to the depthwise one.
+    Returns the model and its seeded input x ~ U[0,1) of shape [n,cin,hw,hw]."""
+    rng = np.random.default_rng(seed)
+    x = rng.random((n, cin, hw, hw), dtype=np.float32)
+    b = GraphBuilder()
+
+    def conv(name, src, ci, co, k, stride, groups, silu):
+        w = b.const(name + ".weight", kaiming_uniform(rng, (co, ci // groups, k, k)))
+        bias = b.const(name + ".bias", rng.uniform(-0.1, 0.1, size=co).astype(np.float32))
+        y = b.node("Conv", f"/{name}/conv/Conv", [src, w, bias], stride_h=stride, stride_w=stride, pad_h=k // 2,
+                   pad_w=k // 2, dil_h=1, dil_w=1, groups=groups)
+        if silu:
+            y = b.node("Mul", f"/{name}/act/Mul", [y, b.node("Sigmoid", f"/{name}/act/Sigmoid", [y])])
+        return y
+
+    y1 = conv("cv1", -1, cin, cout, 1, 1, 1, True)
+    y2 = conv("cv2", y1, cout, cout, 3, 2, cout, False)
+    y3 = conv("cv3", y2, cout, cout, 3, 1, cout // 8, True)
+    out = b.node("Add", "/add/Add", [y2, y3])
+    ho = (hw - 1) // 2 + 1
+    return b.model([n, cin, hw, hw], [n, cout, ho, ho], [out]), x
 
 
 def build_pool_chain(n: int, c: int, h: int, w: int, k: int, seed: int = 5) -> Tuple[EngineModel, np.ndarray]:

@@ -278,6 +278,62 @@ def test_yolov8n_b8_batch_matches_b1(yolov8n):
     assert_network_close(got[7:8], model, x[7:8], "b8 image 7 vs oracle")
 
 
+GROUPED_CASES = [
+    # cin, cout, k, stride, hw, groups, forced launch shape
+    (64, 64, 3, 1, 80, 64, None),      # depthwise
+    (96, 96, 3, 2, 41, 96, None),      # depthwise, stride 2, odd size
+    (32, 64, 3, 1, 24, 32, None),      # depthwise with 2 outputs per channel
+    (48, 96, 5, 2, 17, 8, None),       # 6 in / 12 out per group, 5x5
+    (64, 64, 3, 1, 40, 4, None),       # 16 channels per group: implicit GEMM
+    (128, 256, 1, 1, 20, 8, None),     # pointwise, 16 -> 32 per group
+    (256, 256, 3, 2, 20, 2, None),     # two groups of 128
+    (256, 256, 3, 2, 20, 2, ("64x64", "3")),   # the same with K split across workgroups
+    (64, 128, 3, 1, 30, 4, ("32x32k4", "2")),
+]
+
+
+@pytest.mark.parametrize("cin,cout,k,s,hw,groups,forced", GROUPED_CASES)
+def test_grouped_conv(tmp_path, monkeypatch, cin, cout, k, s, hw, groups, forced):
+    """Grouped and depthwise convs (the reference's depthwise kernel and
+    grouped GEMM, conv2d.cpp:576-597) against the oracle."""
+    print(f"[case] grouped conv cin={cin} cout={cout} k={k} s={s} hw={hw} groups={groups} forced={forced}",
+          flush=True)
+    if forced:
+        monkeypatch.setenv("PDEFA_CONV_TILE", forced[0])
+        monkeypatch.setenv("PDEFA_CONV_SPLITS", forced[1])
+    model, x = ys.build_single_conv(cin, cout, k, s, hw, seed=cin + hw, groups=groups)
+    path = str(tmp_path / "g.engine")
+    ys.save(model, path)
+    eng = native.Engine(path)
+    try:
+        got = eng.run(x)[0]
+        plan = eng.plan()
+    finally:
+        eng.close()
+    assert f" groups={groups} " in plan
+    if forced:
+        assert f"tile={forced[0]}," in plan and "splits=1," not in plan
+    want = graph_ref.run_graph(model, [x])[0]
+    assert_close(got, want, f"grouped conv g={groups}")
+
+
+def test_scdown_block(tmp_path):
+    """YOLOv10's SCDown (1x1 Conv-SiLU, 3x3 s2 depthwise, grouped 3x3 whose
+    residual add lands in its epilogue) at batch 2 against the oracle."""
+    print("[case] scdown 64->128 40x40 n=2", flush=True)
+    model, x = ys.build_scdown(64, 128, 40, n=2)
+    path = str(tmp_path / "s.engine")
+    ys.save(model, path)
+    eng = native.Engine(path)
+    try:
+        got = eng.run(x)[0]
+        plan = eng.plan()
+    finally:
+        eng.close()
+    assert " res=b" in plan
+    assert_close(got, graph_ref.run_graph(model, [x])[0], "scdown")
+
+
 def test_yolov8n_forced_split_k(yolov8n, monkeypatch):
     """Every implicit-GEMM conv on one tile with K split across workgroups:
     the reduce kernel's epilogue (activation, residual add, the FPN's

@@ -140,6 +140,55 @@ def test_oracle_single_conv_vs_golden(name, args):
     check_samples(out, g, atol=2e-5, rtol=2e-5)
 
 
+@pytest.mark.parametrize("name,args,groups", [("dwconv3x3_s1_64_80", (64, 64, 3, 1, 80), 64),
+                                              ("dwconv3x3_s2_96_41", (96, 96, 3, 2, 41), 96),
+                                              ("gconv3x3_g4_64_40", (64, 64, 3, 1, 40), 4),
+                                              ("gconv3x3_g16_32_40", (32, 32, 3, 1, 40), 16)])
+def test_oracle_grouped_conv_vs_golden(name, args, groups):
+    """Depthwise and grouped convs against the reference's own results
+    (its depthwise kernel and grouped GEMM, conv2d.cpp:576-597)."""
+    g = golden(name)
+    assert g["groups"] == groups
+    model, x = ys.build_single_conv(*args, seed=7, groups=groups)
+    import hashlib
+    assert hashlib.sha256(x.tobytes()).hexdigest() == g["input_sha256"]
+    out = graph_ref.run_graph(model, [x])[0]
+    assert list(out.shape) == g["shape"]
+    check_samples(out, g, atol=2e-5, rtol=2e-5)
+
+
+def test_grouped_conv_matches_brute_force():
+    """Grouped conv against a seven-loop sum whose input channel is picked
+    per output channel: output channel o sums input channels
+    (o // (Cout/G)) * Cin/G + j (a wrong group mapping fails here)."""
+    rng = np.random.default_rng(5)
+    n, c, h, w_, co, g, k, s, p = 2, 6, 7, 6, 9, 3, 3, 2, 1
+    x = rng.standard_normal((n, c, h, w_))
+    wt = rng.standard_normal((co, c // g, k, k))
+    b = rng.standard_normal(co)
+    ho, wo = (h + 2 * p - k) // s + 1, (w_ + 2 * p - k) // s + 1
+    want = np.zeros((n, co, ho, wo))
+    xp = np.pad(x, ((0, 0), (0, 0), (p, p), (p, p)))
+    for i in range(n):
+        for o in range(co):
+            for y in range(ho):
+                for xx in range(wo):
+                    acc = b[o]
+                    for j in range(c // g):
+                        ci = (o // (co // g)) * (c // g) + j
+                        for a in range(k):
+                            for bb in range(k):
+                                acc += xp[i, ci, y * s + a, xx * s + bb] * wt[o, j, a, bb]
+                    want[i, o, y, xx] = acc
+    np.testing.assert_allclose(graph_ref.conv2d(x, wt, b, (s, s), (p, p), groups=g), want, rtol=1e-12, atol=1e-12)
+    # depthwise: every channel on its own
+    wd = rng.standard_normal((c, 1, k, k))
+    got = graph_ref.conv2d(x, wd, None, (1, 1), (1, 1), groups=c)
+    for ci in range(c):
+        np.testing.assert_allclose(got[:, ci:ci + 1], graph_ref.conv2d_direct(x[:, ci:ci + 1], wd[ci:ci + 1],
+                                                                              None, (1, 1), (1, 1)), atol=1e-12)
+
+
 @pytest.fixture(scope="module")
 def yolov8n_model():
     return ys.build_yolov8("n", seed=0)
@@ -233,6 +282,29 @@ needs_ref = pytest.mark.skipif(not ref_lib.available(), reason="oracle/_ref not 
 def test_oracle_vs_compiled_reference_conv(tmp_path, cin, cout, k, s, hw):
     model, x = ys.build_single_conv(cin, cout, k, s, hw, seed=cin + hw)
     path = str(tmp_path / "c.engine")
+    ys.save(model, path)
+    r = ref_lib.RefSession(path).run(x)[0]
+    o = graph_ref.run_graph(model, [x])[0]
+    np.testing.assert_allclose(o, r, atol=2e-5, rtol=2e-5)
+
+
+@needs_ref
+@pytest.mark.parametrize("cin,cout,k,s,hw,groups", [(64, 64, 3, 1, 20, 64), (96, 96, 3, 2, 21, 96),
+                                                    (64, 64, 3, 1, 20, 4), (32, 32, 3, 1, 20, 16),
+                                                    (32, 64, 3, 1, 12, 32), (48, 96, 5, 2, 17, 8)])
+def test_oracle_vs_compiled_reference_grouped_conv(tmp_path, cin, cout, k, s, hw, groups):
+    model, x = ys.build_single_conv(cin, cout, k, s, hw, seed=cin + hw, groups=groups)
+    path = str(tmp_path / "g.engine")
+    ys.save(model, path)
+    r = ref_lib.RefSession(path).run(x)[0]
+    o = graph_ref.run_graph(model, [x])[0]
+    np.testing.assert_allclose(o, r, atol=2e-5, rtol=2e-5)
+
+
+@needs_ref
+def test_oracle_vs_compiled_reference_scdown(tmp_path):
+    model, x = ys.build_scdown(64, 128, 40, n=2)
+    path = str(tmp_path / "s.engine")
     ys.save(model, path)
     r = ref_lib.RefSession(path).run(x)[0]
     o = graph_ref.run_graph(model, [x])[0]

@@ -229,3 +229,28 @@ def test_grouped_plan_keeps_every_hazard_in_order(y8n_path, monkeypatch, shape):
             for j in members:
                 if j != i:
                     assert not np.intersect1d(wi, np.concatenate([e for _, e in acc[j]])).size, (i, j)
+
+
+@pytest.mark.parametrize("cin,cout,groups,kind", [(64, 64, 64, "conv_direct"), (32, 64, 32, "conv_direct"),
+                                                  (32, 32, 16, "conv_direct"), (64, 64, 4, "conv_mfma"),
+                                                  (128, 256, 8, "conv_mfma")])
+def test_grouped_conv_plan(tmp_path, cin, cout, groups, kind):
+    """Depthwise and few-channel groups take the grouped direct kernel; groups
+    of 8 or more channels (a multiple of 4) the implicit GEMM, one grid
+    slice per group; the Winograd-form SiLU never applies to grouped convs."""
+    model, x = ys.build_single_conv(cin, cout, 3, 1, 20, groups=groups)
+    path = str(tmp_path / "g.engine")
+    ys.save(model, path)
+    _, lines = parse(native.plan_text(path, list(x.shape)))
+    conv = [l for l in lines if " conv_" in l]
+    assert len(conv) == 1 and f" {kind}(" in conv[0] and f" groups={groups} " in conv[0]
+    assert "act=5" in conv[0]
+
+
+def test_grouped_channel_mismatch_is_reported(tmp_path):
+    model, x = ys.build_single_conv(64, 64, 3, 1, 20, groups=4)
+    model.nodes[0].params["groups"] = 8  # weight holds 16 input channels per group
+    path = str(tmp_path / "bad.engine")
+    ys.save(model, path)
+    with pytest.raises(native.NativeError, match="channel mismatch"):
+        native.plan_text(path, list(x.shape))
