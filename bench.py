@@ -68,6 +68,20 @@ def time_program(eng: native.Engine, x: np.ndarray, steps: int, warmup: int):
     return max(dev_ms, 0.0) / steps, wall_ms / steps, first_ms
 
 
+def launch_count(plan: str) -> int:
+    """Launches of a prepared program: one per plan step, except that
+    consecutive steps of one conv group share a grouped launch."""
+    n, prev = 0, None
+    for line in plan.splitlines()[1:]:
+        if line.startswith("arena"):
+            break
+        g = line.split(" group=")[1].split()[0] if " group=" in line else None
+        if g is None or g != prev:
+            n += 1
+        prev = g
+    return n
+
+
 def conv_stats(eng: native.Engine, iters: int):
     ms, kind, flops = eng.step_times(iters)
     conv = (kind == KIND_CONV_MFMA) | (kind == KIND_CONV_DIRECT)
@@ -252,7 +266,11 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu", action="store_true", help="skip the reference CPU baseline")
     ap.add_argument("--no-m16", action="store_true", help="skip the YOLOv8m batch-16 line")
-    ap.add_argument("--only", choices=["all", "roofline"], default="all")
+    ap.add_argument("--no-pipeline", action="store_true", help="skip the pixels-to-detections pipeline line")
+    ap.add_argument("--only", choices=["all", "roofline", "program"], default="all",
+                    help="program: plan YOLOv8n at --batch, then only warm-up and timed graph replays "
+                         "(a kernel trace's last steps x launches dispatches are the timed forwards)")
+    ap.add_argument("--batch", type=int, default=1, help="with --only program: the batch size")
     ap.add_argument("--calib-copy", action="store_true", help="with --only roofline: also run the PMC calibration copy")
     ap.add_argument("--ingest-pmc", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"))
     args = ap.parse_args()
@@ -267,6 +285,23 @@ def main():
         return
 
     log(f"device: {native.lib().pdefa_amd_device_name().decode()}")
+    if args.only == "program":
+        with tempfile.TemporaryDirectory() as tmp:
+            path = os.path.join(tmp, "yolov8n.engine")
+            ys.save(ys.build_yolov8("n", seed=0), path)
+            x, _ = ys.yolo_inputs(args.batch)
+            eng = native.Engine(path)
+            try:
+                log(f"yolov8n b{args.batch}:")
+                ms, wall, first = time_program(eng, x, args.steps, args.warmup)
+                launches = launch_count(eng.plan())
+            finally:
+                eng.close()
+        print(json.dumps({"program": {"workload": f"yolov8n_640_b{args.batch}", "batch": args.batch,
+                                      "launches": launches, "steps": args.steps, "warmup": args.warmup,
+                                      "ms_per_step": round(ms, 5),
+                                      "images_per_s": round(args.batch * 1000.0 / ms, 2)}}), flush=True)
+        return
     if args.only == "roofline":
         with tempfile.TemporaryDirectory() as tmp:
             roof = roofline(tmp, 50)
@@ -310,10 +345,12 @@ def main():
         roof = roofline(tmp, 50)
         log(f"roofline conv3x3 [{roof['launch_shape']}]: {roof['launch_us']} us/launch, "
             f"{roof['achieved']} TFLOP/s ({roof['frac']:.1%})")
-        pipe = pipeline(path)
-        log(f"pipeline b8 (pixels -> detections): {pipe['value']} images/s with letterbox + decode on the GPU, "
-            f"{pipe['host_pre_post']['value']} images/s with them on the host; same detections: "
-            f"{pipe['same_detections']}")
+        pipe = None
+        if not args.no_pipeline:
+            pipe = pipeline(path)
+            log(f"pipeline b8 (pixels -> detections): {pipe['value']} images/s with letterbox + decode on the GPU, "
+                f"{pipe['host_pre_post']['value']} images/s with them on the host; same detections: "
+                f"{pipe['same_detections']}")
         cpu = None
         if not args.no_cpu:
             x1, _ = ys.yolo_inputs(1)
