@@ -181,6 +181,10 @@ void launch_conv_direct(const ConvDirectArgs& a, hipStream_t s);
 inline int64_t grouped_direct_packed_elems(int Cout, int Cin_g, int KH, int KW) {
     return static_cast<int64_t>(KH) * KW * Cin_g * Cout;
 }
+// Packs OIHW weights [Cout][Cin_g][KH][KW] (device, contiguous) into the
+// direct-kernel layout of ConvDirectArgs::wpk (grouped when groups > 1).
+void launch_pack_direct_weights(float* dst, const float* w, int Cout, int Cin_g, int KH, int KW, int groups,
+                                hipStream_t s);
 
 // Letterbox of one interleaved 8-bit image (ch = 1, 3 or 4) into the planar
 // fp32 tensor dst[3][th][tw]: the scaled window (sw x sh at px, py) is

@@ -847,6 +847,46 @@ __global__ __launch_bounds__(256) void conv_grouped_kernel(ConvDirectArgs a, int
     a.y.ptr[n * a.y.str[0] + co * a.y.str[1] + ho * a.y.str[2] + wo * a.y.str[3]] = v;
 }
 
+// Direct-kernel weight layouts from the OIHW weights [Cout][Cin/G][KH][KW]:
+// groups == 1: [ceil(Cout/CB)][Cin*KH*KW][CB] (CB = direct_cb(Cout), zero
+// padded past Cout); groups > 1: [KH*KW][Cin/G][Cout].  One lane per
+// destination element.
+__global__ void pack_direct_weights_kernel(float* dst, const float* w, int Cout, int Cin_g, int KH, int KW, int groups,
+                                           int cb, int64_t total) {
+    const int K = Cin_g * KH * KW;
+    const int taps = KH * KW;
+    for (int64_t i = blockIdx.x * static_cast<int64_t>(blockDim.x) + threadIdx.x; i < total;
+         i += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+        float v = 0.0f;
+        if (groups > 1) {
+            const int co = static_cast<int>(i % Cout);
+            const int64_t t = i / Cout;
+            const int ci = static_cast<int>(t % Cin_g);
+            const int tap = static_cast<int>(t / Cin_g);
+            v = w[(static_cast<int64_t>(co) * Cin_g + ci) * taps + tap];
+        } else {
+            const int c = static_cast<int>(i % cb);
+            const int64_t t = i / cb;
+            const int kk = static_cast<int>(t % K);
+            const int co = static_cast<int>(t / K) * cb + c;
+            if (co < Cout) v = w[static_cast<int64_t>(co) * K + kk];
+        }
+        dst[i] = v;
+    }
+}
+
+void launch_pack_direct_weights(float* dst, const float* w, int Cout, int Cin_g, int KH, int KW, int groups,
+                                hipStream_t s) {
+    if (!dst || !w || Cout <= 0 || Cin_g <= 0 || KH <= 0 || KW <= 0 || groups <= 0)
+        throw std::runtime_error("pack_direct_weights: bad arguments");
+    const int K = Cin_g * KH * KW;
+    const int64_t total =
+        groups > 1 ? grouped_direct_packed_elems(Cout, Cin_g, KH, KW) : direct_packed_elems(Cout, K);
+    const unsigned blocks = static_cast<unsigned>(std::min<int64_t>((total + 255) / 256, 65535));
+    hipLaunchKernelGGL(pack_direct_weights_kernel, dim3(blocks), dim3(256), 0, s, dst, w, Cout, Cin_g, KH, KW, groups,
+                       direct_cb(Cout), total);
+}
+
 void launch_conv_direct(const ConvDirectArgs& a, hipStream_t s) {
     check_view(a.x, "conv_direct x");
     check_view(a.y, "conv_direct y");

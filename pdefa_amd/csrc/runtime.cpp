@@ -49,6 +49,9 @@ DeviceModel::~DeviceModel() {
 std::shared_ptr<DeviceModel> upload_model(const Model& m) {
     auto dm = std::make_shared<DeviceModel>();
     PDEFA_HIP(hipGetDevice(&dm->device));
+    // Blob layout: [raw weights | conv biases], copied from the host, then
+    // every packed conv weight layout, written on the device from the raw
+    // weights (the host never touches those regions).
     std::vector<size_t> woff(m.weights.size());
     size_t total = 0;
     for (size_t i = 0; i < m.weights.size(); ++i) {
@@ -79,51 +82,36 @@ std::shared_ptr<DeviceModel> upload_model(const Model& m) {
         const OpParams& op = n.params;
         p.groups = static_cast<int>(std::max<int64_t>(1, op.groups));
         if (p.cout % p.groups != 0) continue;  // the planner reports the mismatch
-        const int64_t w_group = k::packed_weight_elems(p.cout / p.groups, p.kh * p.kw * p.cin);
-        p.wpk_off = total;
-        total += align_up(static_cast<size_t>(w_group * p.groups));
-        p.bias_off = total;
-        total += align_up(static_cast<size_t>(p.cout));
-        p.dpk_off = total;
-        total += align_up(static_cast<size_t>(p.groups > 1 ? k::grouped_direct_packed_elems(p.cout, p.cin, p.kh, p.kw)
-                                                           : k::direct_packed_elems(p.cout, p.kh * p.kw * p.cin)));
         p.wino = p.groups == 1 && k::wino_eligible(p.kh, p.kw, static_cast<int>(op.stride_h),
                                                    static_cast<int>(op.stride_w), static_cast<int>(op.dil_h),
                                                    static_cast<int>(op.dil_w), p.cin);
+        p.bias_off = total;
+        total += align_up(static_cast<size_t>(p.cout));
+        pp.push_back(p);
+    }
+    const size_t host_floats = std::max<size_t>(total, kAlignFloats);
+    total = host_floats;
+    for (auto& p : pp) {
+        const int64_t w_group = k::packed_weight_elems(p.cout / p.groups, p.kh * p.kw * p.cin);
+        p.wpk_off = total;
+        total += align_up(static_cast<size_t>(w_group * p.groups));
+        p.dpk_off = total;
+        total += align_up(static_cast<size_t>(p.groups > 1 ? k::grouped_direct_packed_elems(p.cout, p.cin, p.kh, p.kw)
+                                                           : k::direct_packed_elems(p.cout, p.kh * p.kw * p.cin)));
         if (p.wino) {
             p.wino_off = total;
             total += align_up(static_cast<size_t>(k::wino_packed_elems(p.cout, p.cin)));
         }
-        pp.push_back(p);
     }
-    total = std::max<size_t>(total, kAlignFloats);
-    // Host image of the blob: raw weights + zeroed pack/bias regions (biases filled in).
-    std::vector<float> host(total, 0.0f);
+    // host image of the uploaded part (alignment gaps and absent biases zero)
+    std::vector<float> host(host_floats, 0.0f);
     for (size_t i = 0; i < m.weights.size(); ++i)
         if (m.weights[i].nbytes) std::memcpy(host.data() + woff[i], m.weights[i].data, m.weights[i].nbytes);
-    for (const auto& p : pp) {
+    for (const auto& p : pp)
         if (p.b >= 0) std::memcpy(host.data() + p.bias_off, m.weights[p.b].data, sizeof(float) * p.cout);
-        const int K = p.cin * p.kh * p.kw;
-        const float* src = static_cast<const float*>(m.weights[p.w].data);
-        float* dst = host.data() + p.dpk_off;
-        if (p.groups > 1) {
-            // grouped direct layout [kh*KW + kw][ci][co], output channel fastest
-            for (int co = 0; co < p.cout; ++co)
-                for (int ci = 0; ci < p.cin; ++ci)
-                    for (int t = 0; t < p.kh * p.kw; ++t)
-                        dst[(static_cast<size_t>(t) * p.cin + ci) * p.cout + co] =
-                            src[(static_cast<size_t>(co) * p.cin + ci) * p.kh * p.kw + t];
-            continue;
-        }
-        // direct-conv layout [co / CB][k][co % CB], k = (ci, kh, kw); padding stays zero
-        const int cb = k::direct_cb(p.cout);
-        for (int co = 0; co < p.cout; ++co)
-            for (int kk = 0; kk < K; ++kk)
-                dst[(static_cast<size_t>(co / cb) * K + kk) * cb + co % cb] = src[static_cast<size_t>(co) * K + kk];
-    }
     dm->blob_bytes = total * sizeof(float);
     PDEFA_HIP(hipMalloc(&dm->blob, dm->blob_bytes));
-    PDEFA_HIP(hipMemcpy(dm->blob, host.data(), dm->blob_bytes, hipMemcpyHostToDevice));
+    PDEFA_HIP(hipMemcpy(dm->blob, host.data(), host_floats * sizeof(float), hipMemcpyHostToDevice));
     dm->wptr.resize(m.weights.size());
     for (size_t i = 0; i < m.weights.size(); ++i) dm->wptr[i] = dm->blob + woff[i];
     dm->packs.resize(m.nodes.size());
@@ -145,6 +133,8 @@ std::shared_ptr<DeviceModel> upload_model(const Model& m) {
                                             cout_g, p.cin, p.kh, p.kw, s);
                 PDEFA_HIP(hipGetLastError());
             }
+            k::launch_pack_direct_weights(pk.dpk, dm->wptr[p.w], p.cout, p.cin, p.kh, p.kw, p.groups, s);
+            PDEFA_HIP(hipGetLastError());
             if (p.wino) {
                 pk.wino = dm->blob + p.wino_off;
                 k::launch_pack_wino_weights(pk.wino, dm->wptr[p.w], p.cout, p.cin, s);
