@@ -62,11 +62,12 @@ enum ConvTile : int32_t {
     kTile128x128W8 = 10,   // 2x4 waves of 64x32
     kTile64x128W8 = 11,    // 2x4 waves of 32x32
     kTile32x64K4W8 = 12,   // 1x2 waves of 32x32, K split in 4
-    kNumConvTiles = 13,    // implicit-GEMM tiles
+    kTile32x32K8W8 = 13,   // 1 wave tile of 32x32, K split in 8 (small-M, long-K layers)
+    kNumConvTiles = 14,    // implicit-GEMM tiles
     // Winograd F(2x2,3x3) kernel (3x3 stride-1 convs), 32 tiles x BN channels
-    kTileWino64 = 13,
-    kTileWino32 = 14,
-    kNumConvShapes = 15,
+    kTileWino64 = 14,
+    kTileWino32 = 15,
+    kNumConvShapes = 16,
 };
 inline bool is_wino_tile(int tile) { return tile == kTileWino64 || tile == kTileWino32; }
 ConvTileShape conv_tile_shape(int tile);

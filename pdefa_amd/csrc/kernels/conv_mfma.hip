@@ -586,11 +586,11 @@ constexpr ConvTileShape kShapes[kNumConvTiles] = {
     {128, 128, 64, 64, 1}, {128, 64, 64, 32, 1}, {64, 128, 32, 64, 1}, {64, 64, 32, 32, 1},
     {128, 32, 32, 32, 1},  {64, 32, 32, 32, 2},  {32, 64, 32, 32, 2},  {32, 32, 32, 32, 4},
     {128, 64, 32, 32, 1},  {64, 64, 32, 32, 2},  {128, 128, 64, 32, 1}, {64, 128, 32, 32, 1},
-    {32, 64, 32, 32, 4},
+    {32, 64, 32, 32, 4},   {32, 32, 32, 32, 8},
 };
 constexpr const char* kNames[kNumConvTiles] = {"128x128",  "128x64",     "64x128",    "64x64",    "128x32",
                                                "64x32k2",  "32x64k2",    "32x32k4",   "128x64w8", "64x64k2w8",
-                                               "128x128w8", "64x128w8", "32x64k4w8"};
+                                               "128x128w8", "64x128w8", "32x64k4w8", "32x32k8w8"};
 
 template <int BM, int BN, int WM, int WN, int KG, int PF, bool VEC, bool UPK>
 void launch_one(const ConvArgs& a, dim3 grid, hipStream_t s) {
@@ -682,9 +682,9 @@ double conv_cost(int64_t M, int Cout, int ktiles, int t, int splits, int steps) 
     constexpr double kWgCycles = 1500.0;       // workgroup start-up (first loads)
     constexpr double kStepFloor = 2200.0;      // latency floor of one pipeline step
     constexpr double kEff[kNumConvTiles] = {1.0, 0.8, 0.8, 0.85, 0.8, 0.75, 0.75, 0.7,
-                                            0.85, 0.85, 0.9, 0.85, 0.75};
+                                            0.85, 0.85, 0.9, 0.85, 0.75, 0.65};
     // 8-wave tiles hide part of a step's latency behind the other wave of the SIMD
-    constexpr double kFloorScale[kNumConvTiles] = {1, 1, 1, 1, 1, 1, 1, 1, 0.75, 0.75, 0.75, 0.75, 0.75};
+    constexpr double kFloorScale[kNumConvTiles] = {1, 1, 1, 1, 1, 1, 1, 1, 0.75, 0.75, 0.75, 0.75, 0.75, 0.8};
     const ConvTileShape& sh = kShapes[t];
     const int64_t wgs0 = ((M + sh.bm - 1) / sh.bm) * ((Cout + sh.bn - 1) / sh.bn);
     const double c = std::ceil(static_cast<double>(wgs0 * splits) / kCus);
@@ -796,6 +796,7 @@ void launch_conv_mfma(const ConvArgs& a, int tile, bool vec, hipStream_t s) {
         case kTile128x128W8: launch_tile<128, 128, 64, 32, 1>(a, vec, grid, s); break;
         case kTile64x128W8: launch_tile<64, 128, 32, 32, 1>(a, vec, grid, s); break;
         case kTile32x64K4W8: launch_tile<32, 64, 32, 32, 4>(a, vec, grid, s); break;
+        case kTile32x32K8W8: launch_tile<32, 32, 32, 32, 8>(a, vec, grid, s); break;
     }
     if (a.splits > 1) {
         const int64_t total = M * a.Cout * a.groups;
@@ -839,6 +840,7 @@ void launch_conv_mfma_group(const ConvArgs* probs, int count, int tile, hipStrea
         case kTile128x128W8: launch_group<128, 128, 64, 32, 1, kPrefetch>(g, s); break;
         case kTile64x128W8: launch_group<64, 128, 32, 32, 1, kPrefetch>(g, s); break;
         case kTile32x64K4W8: launch_group<32, 64, 32, 32, 4, kPrefetch>(g, s); break;
+        case kTile32x32K8W8: launch_group<32, 32, 32, 32, 8, kPrefetch>(g, s); break;
     }
 }
 

@@ -134,7 +134,7 @@ def test_single_conv(tmp_path, cin, cout, k, s, hw):
 
 
 TILES = ["128x128", "128x64", "64x128", "64x64", "128x32", "64x32k2", "32x64k2", "32x32k4",
-         "128x64w8", "64x64k2w8", "128x128w8", "64x128w8", "32x64k4w8"]
+         "128x64w8", "64x64k2w8", "128x128w8", "64x128w8", "32x64k4w8", "32x32k8w8"]
 
 
 @pytest.mark.parametrize("tile", TILES)
