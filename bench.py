@@ -3,7 +3,7 @@ the conv roofline and the reference CPU engine timed on the host.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W]
     python bench.py --only roofline [--calib-copy]   # the roofline layer alone (profiling runs)
-    python bench.py --ingest-pmc FETCH.csv WRITE.csv  # HBM traffic of the roofline launch -> profiles/
+    python bench.py --ingest-pmc FETCH.csv WRITE.csv TILE  # HBM traffic of the roofline launch -> profiles/
 
 A step is one forward of the whole YOLOv8n device program over one batch of
 synthetic letterboxed input already resident in HBM: the session's captured
@@ -111,11 +111,14 @@ def roofline(tmp: str, iters: int):
     finally:
         eng.close()
     achieved = CONV_ROOF_FLOPS / (ms * 1e-3) / 1e12
+    shape = line.split("(")[1].split(")")[0]
+    tile = shape.split(",")[0].split("=")[1]
+    # HBM bytes per launch measured for this launch shape (the measured choice
+    # between close shapes can differ from run to run)
     traffic = None
     if os.path.exists(TRAFFIC_FILE):
         with open(TRAFFIC_FILE) as f:
-            traffic = json.load(f).get("hbm_bytes_per_launch")
-    shape = line.split("(")[1].split(")")[0]
+            traffic = json.load(f).get("tiles", {}).get(tile, {}).get("hbm_bytes_per_launch")
     wino = "tile=wino" in shape
     out = dict(bound="mfma", achieved=round(achieved, 3), peak=MFMA_FP32_PEAK_TFLOPS, unit="TFLOP/s",
                frac=round(achieved / MFMA_FP32_PEAK_TFLOPS, 4), traffic=traffic,
@@ -149,9 +152,10 @@ def calibration_copy(tmp: str, iters: int = 5):
         f"({2 * CALIB_BYTES / (ms * 1e-3) / 1e9:.0f} GB/s)")
 
 
-def ingest_pmc(fetch_csv: str, write_csv: str):
+def ingest_pmc(fetch_csv: str, write_csv: str, tile: str):
     """FETCH_SIZE / WRITE_SIZE (KiB per dispatch) of the roofline conv launches
-    and of the calibration copy -> profiles/conv3x3s1_64x64_160_traffic.json."""
+    (run with PDEFA_CONV_TILE=tile) and of the calibration copy -> the entry
+    for `tile` in profiles/conv3x3s1_64x64_160_traffic.json."""
     def read(path, counter):
         convs, calib = {}, []
         with open(path) as f:
@@ -177,12 +181,17 @@ def ingest_pmc(fetch_csv: str, write_csv: str):
     read_b = fc * 1024.0 * f_scale
     write_b = wc * 1024.0 * w_scale
     algo = 4 * (64 * 160 * 160 * 2 + 64 * 64 * 9 + 64)  # input + output + weights + bias
-    out = dict(kernel=kname, layer="conv 3x3 s1 p1 64->64, 1x64x160x160",
-               fetch_kib_per_dispatch=fc, write_kib_per_dispatch=wc, conv_dispatches=[nfc, nwc],
-               calib_fetch_kib=fk, calib_write_kib=wk, calib_dispatches=[nfk, nwk],
-               calib_bytes_each_way=CALIB_BYTES, fetch_scale=round(f_scale, 4), write_scale=round(w_scale, 4),
-               hbm_read_bytes_per_launch=round(read_b), hbm_write_bytes_per_launch=round(write_b),
-               hbm_bytes_per_launch=round(read_b + write_b), algorithmic_bytes_per_launch=algo)
+    entry = dict(kernel=kname, fetch_kib_per_dispatch=fc, write_kib_per_dispatch=wc, conv_dispatches=[nfc, nwc],
+                 calib_fetch_kib=fk, calib_write_kib=wk, calib_dispatches=[nfk, nwk],
+                 calib_bytes_each_way=CALIB_BYTES, fetch_scale=round(f_scale, 4), write_scale=round(w_scale, 4),
+                 hbm_read_bytes_per_launch=round(read_b), hbm_write_bytes_per_launch=round(write_b),
+                 hbm_bytes_per_launch=round(read_b + write_b))
+    out = {"layer": "conv 3x3 s1 p1 64->64, 1x64x160x160", "algorithmic_bytes_per_launch": algo, "tiles": {}}
+    if os.path.exists(TRAFFIC_FILE):
+        with open(TRAFFIC_FILE) as f:
+            old = json.load(f)
+        out["tiles"] = old.get("tiles", {})
+    out["tiles"][tile] = entry
     with open(TRAFFIC_FILE, "w") as f:
         json.dump(out, f, indent=1)
     print(json.dumps(out))
@@ -272,7 +281,7 @@ def main():
                          "(a kernel trace's last steps x launches dispatches are the timed forwards)")
     ap.add_argument("--batch", type=int, default=1, help="with --only program: the batch size")
     ap.add_argument("--calib-copy", action="store_true", help="with --only roofline: also run the PMC calibration copy")
-    ap.add_argument("--ingest-pmc", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"))
+    ap.add_argument("--ingest-pmc", nargs=3, metavar=("FETCH_CSV", "WRITE_CSV", "TILE"))
     args = ap.parse_args()
     if args.ingest_pmc:
         ingest_pmc(*args.ingest_pmc)
