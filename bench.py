@@ -24,6 +24,7 @@ import csv
 import json
 import os
 import statistics
+import subprocess
 import sys
 import tempfile
 import time
@@ -245,23 +246,26 @@ def pipeline(path: str, batch: int = 8, iters: int = 20):
 
 def cpu_baseline(path: str, x: np.ndarray, budget_s: float = 12.0):
     """The reference CPU engine (oracle/_ref, built from the reference sources)
-    on the same YOLOv8n b1 workload: median Session::run over a bounded sample."""
+    on the same YOLOv8n b1 workload: median Session::run over a bounded sample,
+    timed in a child process (oracle/ref_bench.py) so that the reference's
+    worker threads begin and end there."""
     from oracle import ref_lib  # checker / baseline only
 
     if not ref_lib.available():
         return None
     threads = max(1, min(16, os.cpu_count() or 1))
-    ref_lib.set_threads(threads)
-    r = ref_lib.RefSession(path)
-    r.run(x)
-    for _ in range(2):
-        r.rerun()
-    times = []
-    t_end = time.perf_counter() + budget_s
-    while time.perf_counter() < t_end and len(times) < 30:
-        r.rerun()
-        times.append(r.last_ms())
-    r.close()
+    npy = os.path.join(os.path.dirname(path), "cpu_baseline_input.npy")
+    np.save(npy, x)
+    try:
+        r = subprocess.run([sys.executable, "-m", "oracle.ref_bench", path, npy, str(budget_s), str(threads)],
+                           cwd=ROOT, capture_output=True, text=True, timeout=budget_s + 120)
+    except subprocess.TimeoutExpired:
+        log("cpu baseline: the reference run did not finish")
+        return None
+    if r.returncode != 0 or not r.stdout.strip():
+        log(f"cpu baseline: the reference run failed ({r.returncode}): {r.stderr[-400:]}")
+        return None
+    times = json.loads(r.stdout.strip().splitlines()[-1])["ms"]
     med = statistics.median(times)
     return dict(value=round(1000.0 / med, 3), unit="images/s", cores=threads, kind="reference",
                 sample=f"YOLOv8n b1 640x640, median of {len(times)} Session::run after 3 warm-ups "
