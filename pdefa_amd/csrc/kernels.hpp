@@ -146,6 +146,7 @@ struct ConvGroupArgs {
     int32_t m_tiles[kMaxConvGroup] = {};         // m blocks of each problem
     ConvArgs p[kMaxConvGroup];
 };
+static_assert(sizeof(ConvGroupArgs) <= 4096, "grouped launch arguments must fit the 4 KiB kernel-argument segment");
 void launch_conv_mfma_group(const ConvArgs* probs, int count, int tile, hipStream_t s);
 
 // Winograd F(2x2,3x3) on MFMA for 3x3 / stride 1 / dilation 1 convs with
