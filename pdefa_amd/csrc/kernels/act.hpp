@@ -17,23 +17,30 @@ namespace k {
 // the polynomial below.  The reference applies it on 3x3/s1 layers with
 // 16 < Cin <= 512, and its outputs are matched only with the same function.
 __device__ __forceinline__ float silu_winograd_form(float x) {
+    // The product -x log2 e is rounded before it is used, as in the reference:
+    // no contraction into the rounding add or the remainder.
+#pragma clang fp contract(off)
     const float neg_x = -x;
     const float fx = neg_x * 1.44269504088896341f;
-    const float n = roundf(fx);
+    // round half away from zero: for every float |fx| < 2^23,
+    // trunc(fx + copysign(0.49999997, fx)) rounds fx that way (an exhaustive
+    // check over all such floats agrees); the add is the only rounding step
+    const float n = __builtin_truncf(fx + __builtin_copysignf(0.49999997f, fx));
     const float f = fx - n;
     float p = 1.9875691500e-4f;
-    p = p * f + 1.3981999507e-3f;
-    p = p * f + 8.3334519073e-3f;
-    p = p * f + 4.1665795894e-2f;
-    p = p * f + 1.6666665459e-1f;
-    p = p * f + 5.0000001201e-1f;
-    p = p * f + 1.0f;
+    p = __builtin_fmaf(p, f, 1.3981999507e-3f);
+    p = __builtin_fmaf(p, f, 8.3334519073e-3f);
+    p = __builtin_fmaf(p, f, 4.1665795894e-2f);
+    p = __builtin_fmaf(p, f, 1.6666665459e-1f);
+    p = __builtin_fmaf(p, f, 5.0000001201e-1f);
+    p = __builtin_fmaf(p, f, 1.0f);
     const int32_t e = (static_cast<int32_t>(n) + 127) << 23;
     // x / d as x * (1/d) with the hardware reciprocal (1 ulp)
-    const float r = x * __builtin_amdgcn_rcpf(1.0f + p * __int_as_float(e));
+    const float r = x * __builtin_amdgcn_rcpf(__builtin_fmaf(p, __int_as_float(e), 1.0f));
     // the range cut-offs are selects, not branches (the polynomial result of
     // an out-of-range x is discarded)
-    return neg_x < -88.37626f ? x : (neg_x > 88.37626f ? 0.0f : r);
+    const float lo = __builtin_unpredictable(neg_x > 88.37626f) ? 0.0f : r;
+    return __builtin_unpredictable(neg_x < -88.37626f) ? x : lo;
 }
 
 // SiLU for the fused conv epilogues: x * 1/(1 + 2^(-x log2 e)) with the

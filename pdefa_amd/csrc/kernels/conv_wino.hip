@@ -48,11 +48,22 @@ constexpr int kCK = 8;   // input channels per K step (4 per lane half)
 constexpr int kXcds = 8;
 constexpr int kMaxCin = 4096;
 constexpr int kXchRow = kWT + 4;  // exchange rows: 32 tiles + 4 floats of padding
+// Output and residual views are addressed by 32-bit byte offsets from their
+// base; views must span less than kWinoMaxViewBytes, and kWinoNoPixel (added
+// to a valid offset, or to itself) always lands at or past the range.
+constexpr int32_t kWinoMaxViewBytes = 1 << 30;
+constexpr int32_t kWinoNoPixel = 1 << 30;
+// buffer resource word 3 for raw 32-bit buffer access
+constexpr int kWinoBufferFlags = 0x00020000;
 
 int wino_cin_pad(int Cin) { return (Cin + kCK - 1) / kCK * kCK; }
 int wino_cout_pad(int Cout) { return (Cout + 63) / 64 * 64; }
 
 void fail(const std::string& m) { throw std::runtime_error("conv_wino: " + m); }
+// Bytes from a view's base to the end of its last element.
+int64_t view_bytes(int N, int H, int W, int C, int64_t sn, int64_t sh, int64_t sw) {
+    return 4 * ((N - 1) * sn + (H - 1) * sh + (W - 1) * sw + C);
+}
 
 }  // namespace
 
@@ -63,6 +74,12 @@ __device__ __attribute__((aligned(16))) float g_wino_zero[kMaxCin];
 bool wino_eligible(int KH, int KW, int sh, int sw, int dh, int dw, int Cin) {
     return KH == 3 && KW == 3 && sh == 1 && sw == 1 && dh == 1 && dw == 1 && Cin % 4 == 0 && Cin >= 8 &&
            Cin <= kMaxCin;
+}
+
+bool wino_views_fit(const ConvArgs& a) {
+    const int64_t yb = view_bytes(a.N, a.Ho, a.Wo, a.Cout, a.y_sn, a.y_sh, a.y_sw);
+    const int64_t rb = a.res ? view_bytes(a.N, a.Ho, a.Wo, a.Cout, a.r_sn, a.r_sh, a.r_sw) : 0;
+    return yb < kWinoMaxViewBytes && rb < kWinoMaxViewBytes;
 }
 
 int64_t wino_packed_elems(int Cout, int Cin) {
@@ -109,13 +126,15 @@ __global__ void pack_wino_weights_kernel(float* dst, const float* w, int Cout, i
 }
 
 template <int BN, int ACT, bool RES>
-__global__ __launch_bounds__(256) void conv_wino_kernel(ConvArgs a, int tiles_h, int tiles_w) {
+__global__ __launch_bounds__(256) void conv_wino_kernel(ConvArgs a, int tiles_h, int tiles_w, int y_bytes,
+                                                        int r_bytes) {
     constexpr int CB = BN / 32;  // 32-wide channel blocks per wave
     __shared__ __attribute__((aligned(16))) float xch[4 * 2 * BN * kXchRow];  // [row i][column c][channel][tile]
-    // per tile of the workgroup: output / residual offset of its (0, 0) pixel
-    // and which of its four pixels exist (bit 0: the tile, 1: column 1, 2: row 1)
-    __shared__ int64_t s_yoff[kWT], s_roff[kWT];
-    __shared__ int s_vm[kWT];
+    // per tile of the workgroup: byte offsets of its four output (and
+    // residual) pixels (r, c) at [2r + c], kWinoNoPixel for pixels outside
+    // the output (or past the last tile)
+    __shared__ __attribute__((aligned(16))) int32_t s_yo4[kWT][4];
+    __shared__ __attribute__((aligned(16))) int32_t s_ro4[RES ? kWT : 1][4];
 
     const int tid = threadIdx.x;
     const int lane = tid & 63;
@@ -144,22 +163,23 @@ __global__ __launch_bounds__(256) void conv_wino_kernel(ConvArgs a, int tiles_h,
     const float bias_v = n0 + e_col < a.Cout ? a.bias[n0 + e_col] : 0.0f;
     if (tid < kWT) {  // read after the barrier that precedes the epilogue
         const int tg = t0 + tid;
-        int vm = 0;
-        int64_t yo = 0, ro = 0;
-        if (tg < T) {
-            const int nn = tg / tiles_img;
-            const int rr = tg - nn * tiles_img;
-            const int oh0 = 2 * (rr / tiles_w);
-            const int ow0 = 2 * (rr - (rr / tiles_w) * tiles_w);
-            vm = 1 | (ow0 + 1 < a.Wo ? 2 : 0) | (oh0 + 1 < a.Ho ? 4 : 0);
-            yo = static_cast<int64_t>(nn) * a.y_sn + static_cast<int64_t>(oh0) * a.y_sh +
-                 static_cast<int64_t>(ow0) * a.y_sw;
-            ro = static_cast<int64_t>(nn) * a.r_sn + static_cast<int64_t>(oh0) * a.r_sh +
-                 static_cast<int64_t>(ow0) * a.r_sw;
+        const int nn = tg / tiles_img;
+        const int rr = tg - nn * tiles_img;
+        const int oh0 = 2 * (rr / tiles_w);
+        const int ow0 = 2 * (rr - (rr / tiles_w) * tiles_w);
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const int oh = oh0 + (q >> 1), ow = ow0 + (q & 1);
+            const bool ok = tg < T && oh < a.Ho && ow < a.Wo;
+            const int64_t yo = static_cast<int64_t>(nn) * a.y_sn + static_cast<int64_t>(oh) * a.y_sh +
+                               static_cast<int64_t>(ow) * a.y_sw;
+            s_yo4[tid][q] = ok ? static_cast<int32_t>(yo * 4) : kWinoNoPixel;
+            if constexpr (RES) {
+                const int64_t ro = static_cast<int64_t>(nn) * a.r_sn + static_cast<int64_t>(oh) * a.r_sh +
+                                   static_cast<int64_t>(ow) * a.r_sw;
+                s_ro4[tid][q] = ok ? static_cast<int32_t>(ro * 4) : kWinoNoPixel;
+            }
         }
-        s_yoff[tid] = yo;
-        s_roff[tid] = ro;
-        s_vm[tid] = vm;
     }
 
     // this lane's tile and the two patch rows that row i of B^T combines:
@@ -295,10 +315,11 @@ __global__ __launch_bounds__(256) void conv_wino_kernel(ConvArgs a, int tiles_h,
     constexpr int NB = RPT / 4;          // blocks of 4 tile rows per lane
     constexpr int GSTEP = 256 / BN;      // lanes per channel
     const int co = n0 + e_col;
-    const bool co_ok = co < a.Cout;
+    // byte offset of this lane's channel; kWinoNoPixel past Cout, so that its
+    // stores fall outside the buffer range and are dropped
+    const int32_t co_b = co < a.Cout ? co * 4 : kWinoNoPixel;
     float yv[RPT][4];
-    int64_t yo[RPT], ro[RPT];
-    int vm[RPT];
+    int32_t yo[RPT][4], ro[RPT][4];
 #pragma unroll
     for (int bk = 0; bk < NB; ++bk) {
         const int trow0 = 4 * (tid / BN + bk * GSTEP);
@@ -316,24 +337,33 @@ __global__ __launch_bounds__(256) void conv_wino_kernel(ConvArgs a, int tiles_h,
                 yv[rk][c] = p[0][c][k] + p[1][c][k] + p[2][c][k];      // output row 0, column c
                 yv[rk][2 + c] = p[1][c][k] - p[2][c][k] - p[3][c][k];  // output row 1, column c
             }
-            yo[rk] = s_yoff[trow0 + k];
-            ro[rk] = s_roff[trow0 + k];
-            vm[rk] = co_ok ? s_vm[trow0 + k] : 0;
+            const int4 y4 = *reinterpret_cast<const int4*>(&s_yo4[trow0 + k][0]);
+            yo[rk][0] = y4.x;
+            yo[rk][1] = y4.y;
+            yo[rk][2] = y4.z;
+            yo[rk][3] = y4.w;
+            if constexpr (RES) {
+                const int4 r4 = *reinterpret_cast<const int4*>(&s_ro4[trow0 + k][0]);
+                ro[rk][0] = r4.x;
+                ro[rk][1] = r4.y;
+                ro[rk][2] = r4.z;
+                ro[rk][3] = r4.w;
+            }
         }
     }
-    // pixel q = (r, c) = (q / 2, q % 2) exists when bit 0, and bit 1 for c = 1, bit 2 for r = 1
-    auto pix_ok = [](int m, int q) { return (m & 1) && (!(q & 1) || (m & 2)) && (!(q & 2) || (m & 4)); };
+    // Buffer-range checked stores and loads: an offset at or past the view's
+    // byte extent stores nothing and loads zero, so pixels outside the output
+    // need no branch.
+    const __amdgpu_buffer_rsrc_t ybuf = __builtin_amdgcn_make_buffer_rsrc(a.y, 0, y_bytes, kWinoBufferFlags);
     float rv[RPT][4];
     if constexpr (RES) {
+        const __amdgpu_buffer_rsrc_t rbuf =
+            __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(a.res), 0, r_bytes, kWinoBufferFlags);
 #pragma unroll
         for (int k = 0; k < RPT; ++k)
 #pragma unroll
-            for (int q = 0; q < 4; ++q) {
-                const bool ok = pix_ok(vm[k], q);
-                const int64_t o = ro[k] + (q >> 1) * a.r_sh + (q & 1) * a.r_sw + co;
-                const float r = a.res[ok ? o : 0];
-                rv[k][q] = ok ? r : 0.0f;
-            }
+            for (int q = 0; q < 4; ++q)
+                rv[k][q] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rbuf, ro[k][q] + co_b, 0, 0));
     }
 #pragma unroll
     for (int k = 0; k < RPT; ++k)
@@ -341,29 +371,30 @@ __global__ __launch_bounds__(256) void conv_wino_kernel(ConvArgs a, int tiles_h,
         for (int q = 0; q < 4; ++q) {
             float v = act_fixed<ACT>(yv[k][q] + bias_v, a.act, a.slope);
             if (RES) v += rv[k][q];
-            if (pix_ok(vm[k], q)) a.y[yo[k] + (q >> 1) * a.y_sh + (q & 1) * a.y_sw + co] = v;
+            __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v), ybuf, yo[k][q] + co_b, 0, 0);
         }
 }
 
 namespace {
 
 template <int BN, int ACT>
-void launch_act(const ConvArgs& a, dim3 grid, int th, int tw, hipStream_t s) {
+void launch_act(const ConvArgs& a, dim3 grid, int th, int tw, int yb, int rb, hipStream_t s) {
     if (a.res)
-        hipLaunchKernelGGL((conv_wino_kernel<BN, ACT, true>), grid, dim3(256), 0, s, a, th, tw);
+        hipLaunchKernelGGL((conv_wino_kernel<BN, ACT, true>), grid, dim3(256), 0, s, a, th, tw, yb, rb);
     else
-        hipLaunchKernelGGL((conv_wino_kernel<BN, ACT, false>), grid, dim3(256), 0, s, a, th, tw);
+        hipLaunchKernelGGL((conv_wino_kernel<BN, ACT, false>), grid, dim3(256), 0, s, a, th, tw, yb, rb);
 }
 
 template <int BN>
-void launch_bn(const ConvArgs& a, dim3 grid, int th, int tw, hipStream_t s) {
+void launch_bn(const ConvArgs& a, dim3 grid, int th, int tw, int yb, int rb, hipStream_t s) {
     switch (a.act) {
-        case kActSilu: launch_act<BN, kActSilu>(a, grid, th, tw, s); break;
-        case kActSiluWinogradForm: launch_act<BN, kActSiluWinogradForm>(a, grid, th, tw, s); break;
-        case kActNone: launch_act<BN, kActNone>(a, grid, th, tw, s); break;
-        default: launch_act<BN, kActGeneric>(a, grid, th, tw, s); break;
+        case kActSilu: launch_act<BN, kActSilu>(a, grid, th, tw, yb, rb, s); break;
+        case kActSiluWinogradForm: launch_act<BN, kActSiluWinogradForm>(a, grid, th, tw, yb, rb, s); break;
+        case kActNone: launch_act<BN, kActNone>(a, grid, th, tw, yb, rb, s); break;
+        default: launch_act<BN, kActGeneric>(a, grid, th, tw, yb, rb, s); break;
     }
 }
+
 
 }  // namespace
 
@@ -385,10 +416,15 @@ void launch_conv_wino(const ConvArgs& a, int bn, hipStream_t s) {
     if (T >= (int64_t{1} << 31)) fail("too many tiles");
     const dim3 grid(static_cast<unsigned>((T + kWT - 1) / kWT), static_cast<unsigned>((a.Cout + bn - 1) / bn));
     if (grid.y > 65535) fail("grid");
+    if (a.y_sn < 0 || a.y_sh < 0 || a.y_sw < 0 || (a.res && (a.r_sn < 0 || a.r_sh < 0 || a.r_sw < 0)))
+        fail("negative output strides");
+    if (!wino_views_fit(a)) fail("output or residual view spans 1 GiB or more");
+    const int yb = static_cast<int>(view_bytes(a.N, a.Ho, a.Wo, a.Cout, a.y_sn, a.y_sh, a.y_sw));
+    const int rb = a.res ? static_cast<int>(view_bytes(a.N, a.Ho, a.Wo, a.Cout, a.r_sn, a.r_sh, a.r_sw)) : 0;
     if (bn == 64)
-        launch_bn<64>(a, grid, static_cast<int>(tiles_h), static_cast<int>(tiles_w), s);
+        launch_bn<64>(a, grid, static_cast<int>(tiles_h), static_cast<int>(tiles_w), yb, rb, s);
     else
-        launch_bn<32>(a, grid, static_cast<int>(tiles_h), static_cast<int>(tiles_w), s);
+        launch_bn<32>(a, grid, static_cast<int>(tiles_h), static_cast<int>(tiles_w), yb, rb, s);
 }
 
 void launch_pack_wino_weights(float* dst, const float* w, int Cout, int Cin, hipStream_t s) {

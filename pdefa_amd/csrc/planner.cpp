@@ -208,6 +208,20 @@ struct Val {
     VRef nhwc_view;
 };
 
+// Bytes from a view's first element to the end of its last one.
+int64_t view_span_bytes(const VRef& v) {
+    int64_t last = 0;
+    for (int d = 0; d < v.rank; ++d) last += (v.dims[d] - 1) * v.str[d];
+    return 4 * (last + 1);
+}
+
+// The Winograd kernel addresses its output and residual views with 32-bit
+// byte offsets (spans under 1 GiB).
+bool wino_views_ok(const Step& s) {
+    constexpr int64_t kMax = int64_t{1} << 30;
+    return view_span_bytes(s.out) < kMax && (!s.has_res || view_span_bytes(s.res) < kMax);
+}
+
 // Launch-shape query of an implicit-GEMM conv step.
 ConvQuery conv_query(const Step& s) {
     ConvQuery q;
@@ -230,7 +244,8 @@ ConvQuery conv_query(const Step& s) {
     q.has_res = s.has_res;
     q.vec = s.vec;
     q.groups = s.groups;
-    q.wino = s.vec && s.groups == 1 && k::wino_eligible(s.KH, s.KW, s.sh, s.sw, s.dh, s.dw, q.Cin);
+    q.wino = s.vec && s.groups == 1 && k::wino_eligible(s.KH, s.KW, s.sh, s.sw, s.dh, s.dw, q.Cin) &&
+             wino_views_ok(s);
     return q;
 }
 
@@ -925,7 +940,9 @@ class Planner {
             const int64_t K = cin * s.KH * s.KW;
             // The Winograd kernel needs the transformed weights packed at model
             // load for exactly these layers, and 16-byte aligned input pixels.
-            const bool wino = s.vec && G == 1 && k::wino_eligible(s.KH, s.KW, s.sh, s.sw, s.dh, s.dw, static_cast<int>(cin));
+            const bool wino = s.vec && G == 1 &&
+                              k::wino_eligible(s.KH, s.KW, s.sh, s.sw, s.dh, s.dw, static_cast<int>(cin)) &&
+                              wino_views_ok(s);
             k::ConvLaunchShape ls;
             if (opt_.tune_conv && opt_.force_tile < 0 && opt_.split_k) {
                 ls = opt_.tune_conv(conv_query(s));
