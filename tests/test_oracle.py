@@ -86,6 +86,27 @@ def test_winograd_form_silu_shape():
     assert graph_ref.silu_winograd_compat(np.array([-100.0], np.float32))[0] == 0.0
 
 
+def test_round_half_away_by_biased_truncation():
+    """The device form of the reference's std::round: trunc(x + copysign(
+    0.49999997, x)) in float32 equals rounding half away from zero, checked on
+    every half-integer tie in the SiLU's range, the floats on either side of
+    each, and 2^20 random floats (float64 rounding is the independent side)."""
+    f32 = np.float32
+    k = np.arange(-130, 131, dtype=np.float64)
+    ties = (k + 0.5).astype(np.float32)
+    ints = k.astype(np.float32)
+    base = np.concatenate([ties, ints, np.float32([0.5, -0.5, 0.49999997, -0.49999997])])
+    near = np.concatenate([base, np.nextafter(base, f32(np.inf)), np.nextafter(base, f32(-np.inf))])
+    rnd = np.random.default_rng(3).uniform(-128, 128, 1 << 20).astype(np.float32)
+    x = np.concatenate([near, rnd])
+    got = np.trunc((x + np.copysign(f32(0.49999997), x)).astype(np.float32))
+    want = np.trunc(x.astype(np.float64) + np.copysign(0.5, x.astype(np.float64)))
+    np.testing.assert_array_equal(got, want)
+    # the oracle's own rounding agrees on the ties
+    fx_ties = np.where(ties >= 0, np.floor(ties + f32(0.5)), np.ceil(ties - f32(0.5)))
+    np.testing.assert_array_equal(fx_ties, np.trunc(ties.astype(np.float64) + np.copysign(0.5, ties)))
+
+
 def test_winograd_dispatch_rule():
     assert graph_ref.winograd_path(64, 3, 3, (1, 1), (1, 1), 1)
     assert not graph_ref.winograd_path(16, 3, 3, (1, 1), (1, 1), 1)   # direct kernel
