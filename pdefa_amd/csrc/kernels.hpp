@@ -153,9 +153,9 @@ void launch_conv_mfma_group(const ConvArgs* probs, int count, int tile, hipStrea
 // Cin % 4 == 0 and Cin >= 8 (any padding).  a.wpk holds the transformed
 // weights U = G g G^T as [16][ceil(Cin/8)*2][ceil(Cout/64)*64][4]
 // (launch_pack_wino_weights from the OIHW weights); splits must be 1.
-// bn = 32 or 64 output channels per workgroup.  The output and residual
-// views are addressed by 32-bit byte offsets: each must span less than 1 GiB
-// (wino_views_fit), non-negative strides.
+// bn = 32 or 64 output channels per workgroup.  Input, transformed weights,
+// output and residual are addressed by 32-bit byte offsets: each must span
+// less than 1 GiB - 4 KiB (wino_views_fit), with non-negative strides.
 bool wino_eligible(int KH, int KW, int sh, int sw, int dh, int dw, int Cin);
 bool wino_views_fit(const ConvArgs& a);
 int64_t wino_packed_elems(int Cout, int Cin);

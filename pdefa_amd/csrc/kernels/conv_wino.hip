@@ -48,11 +48,12 @@ constexpr int kCK = 8;   // input channels per K step (4 per lane half)
 constexpr int kXcds = 8;
 constexpr int kMaxCin = 4096;
 constexpr int kXchRow = kWT + 4;  // exchange rows: 32 tiles + 4 floats of padding
-// Output and residual views are addressed by 32-bit byte offsets from their
-// base; views must span less than kWinoMaxViewBytes, and kWinoNoPixel (added
-// to a valid offset, or to itself) always lands at or past the range.
-constexpr int32_t kWinoMaxViewBytes = 1 << 30;
+// Input, weights, output and residual are addressed by 32-bit byte offsets
+// from their base.  Their spans stay under kWinoMaxViewBytes, so an offset
+// derived from kWinoNoPixel (less up to 16 bytes, or plus a valid offset, or
+// plus itself) always lands past the buffer range.
 constexpr int32_t kWinoNoPixel = 1 << 30;
+constexpr int32_t kWinoMaxViewBytes = kWinoNoPixel - 4096;
 // buffer resource word 3 for raw 32-bit buffer access
 constexpr int kWinoBufferFlags = 0x00020000;
 
@@ -67,19 +68,17 @@ int64_t view_bytes(int N, int H, int W, int C, int64_t sn, int64_t sh, int64_t s
 
 }  // namespace
 
-// Patch positions outside the image read this instead of the input (their
-// lanes then need no per-element mask): zeros, one channel run of any Cin.
-__device__ __attribute__((aligned(16))) float g_wino_zero[kMaxCin];
-
 bool wino_eligible(int KH, int KW, int sh, int sw, int dh, int dw, int Cin) {
     return KH == 3 && KW == 3 && sh == 1 && sw == 1 && dh == 1 && dw == 1 && Cin % 4 == 0 && Cin >= 8 &&
            Cin <= kMaxCin;
 }
 
 bool wino_views_fit(const ConvArgs& a) {
+    const int64_t xb = view_bytes(a.N, a.H, a.W, a.Cin, a.x_sn, a.x_sh, a.x_sw);
+    const int64_t ub = wino_packed_elems(a.Cout, a.Cin) * 4;
     const int64_t yb = view_bytes(a.N, a.Ho, a.Wo, a.Cout, a.y_sn, a.y_sh, a.y_sw);
     const int64_t rb = a.res ? view_bytes(a.N, a.Ho, a.Wo, a.Cout, a.r_sn, a.r_sh, a.r_sw) : 0;
-    return yb < kWinoMaxViewBytes && rb < kWinoMaxViewBytes;
+    return xb < kWinoMaxViewBytes && ub < kWinoMaxViewBytes && yb < kWinoMaxViewBytes && rb < kWinoMaxViewBytes;
 }
 
 int64_t wino_packed_elems(int Cout, int Cin) {
@@ -126,8 +125,8 @@ __global__ void pack_wino_weights_kernel(float* dst, const float* w, int Cout, i
 }
 
 template <int BN, int ACT, bool RES>
-__global__ __launch_bounds__(256) void conv_wino_kernel(ConvArgs a, int tiles_h, int tiles_w, int y_bytes,
-                                                        int r_bytes) {
+__global__ __launch_bounds__(256) void conv_wino_kernel(ConvArgs a, int tiles_h, int tiles_w, int x_bytes,
+                                                        int u_bytes, int y_bytes, int r_bytes) {
     constexpr int CB = BN / 32;  // 32-wide channel blocks per wave
     __shared__ __attribute__((aligned(16))) float xch[4 * 2 * BN * kXchRow];  // [row i][column c][channel][tile]
     // per tile of the workgroup: byte offsets of its four output (and
@@ -194,9 +193,15 @@ __global__ __launch_bounds__(256) void conv_wino_kernel(ConvArgs a, int tiles_h,
     const int ra = wi_row == 2 ? 2 : (wi_row == 0 ? 0 : 1);
     const int rb = wi_row == 0 ? 2 : (wi_row == 2 ? 1 : (wi_row == 1 ? 2 : 3));
     const float sg = wi_row == 1 ? 1.0f : -1.0f;
-    const float* xb = a.x + static_cast<int64_t>(n) * a.x_sn;  // offsets within one image fit int32
-    // channel-0 address of each patch position, the zero run outside the image
-    const float* pp[2][4];
+    // Patch and weight loads are buffer loads: a per-lane 32-bit byte offset,
+    // the K step's advance in a scalar offset, the channel block in the
+    // immediate.  Patch positions outside the image get kWinoNoPixel, past
+    // the input's buffer range, and load zeros.
+    const __amdgpu_buffer_rsrc_t xbuf =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(a.x), 0, x_bytes, kWinoBufferFlags);
+    const __amdgpu_buffer_rsrc_t ubuf = __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(a.wpk), 0, u_bytes, kWinoBufferFlags);
+    // byte offset of channel 4*half of each patch position
+    int32_t doff[2][4];
 #pragma unroll
     for (int r = 0; r < 2; ++r) {
         const int hi = 2 * th - a.ph + (r == 0 ? ra : rb);
@@ -205,28 +210,39 @@ __global__ __launch_bounds__(256) void conv_wino_kernel(ConvArgs a, int tiles_h,
             const int wi = 2 * tw - a.pw + b;
             const bool ok = t_ok & (static_cast<unsigned>(hi) < static_cast<unsigned>(a.H)) &
                             (static_cast<unsigned>(wi) < static_cast<unsigned>(a.W));
-            pp[r][b] = ok ? xb + (hi * static_cast<int>(a.x_sh) + wi * static_cast<int>(a.x_sw)) : g_wino_zero;
+            const int64_t o = static_cast<int64_t>(n) * a.x_sn + static_cast<int64_t>(hi) * a.x_sh +
+                              static_cast<int64_t>(wi) * a.x_sw;
+            doff[r][b] = ok ? static_cast<int32_t>(o * 4) + half * 16 : kWinoNoPixel;
         }
     }
-    // U float4 of (position (i, j), channel group, this lane's output channel of block cb)
-    const floatx4* up = reinterpret_cast<const floatx4*>(a.wpk) + n0 + l32;
+    // byte offset of the U float4 of (position (i, j), channel group `half`,
+    // this lane's output channel of block 0); block cb adds cb * 512 bytes,
+    // K step s adds s * 2 * cop float4s
+    int32_t uoff[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) uoff[j] = ((((wi_row * 4 + j) * cq + half) * cop) + n0 + l32) * 16;
+    const int32_t d_step = kCK * 4;      // bytes per K step of patch channels
+    const int32_t u_step = 2 * cop * 16;  // bytes per K step of U
 
     floatx4 dreg[2][2][4];
     floatx4 ureg[2][4][CB];
-    // Channels past Cin (the last step's upper half when Cin % 8 == 4) read the
-    // last 4 channels again; their U rows are zero, so they add nothing.
-    auto load = [&](int s, floatx4 (&d)[2][4], floatx4 (&u)[4][CB]) {
-        const int c = min(s * kCK + half * 4, a.Cin - 4);
+    // Channels past Cin (the upper half of the last step when Cin % 8 == 4)
+    // read the last 4 channels again (`back` = 16 bytes on that half of the
+    // last step); their U rows are zero, so they add nothing.
+    const int32_t last_back = (a.Cin & 4) && half ? 16 : 0;
+    auto load = [&](int s, floatx4 (&d)[2][4], floatx4 (&u)[4][CB], int32_t back) {
 #pragma unroll
         for (int r = 0; r < 2; ++r)
 #pragma unroll
-            for (int b = 0; b < 4; ++b) d[r][b] = *reinterpret_cast<const floatx4*>(pp[r][b] + c);
-        const int cg = s * (kCK / 4) + half;
+            for (int b = 0; b < 4; ++b)
+                d[r][b] = __builtin_bit_cast(
+                    floatx4, __builtin_amdgcn_raw_buffer_load_b128(xbuf, doff[r][b] - back, s * d_step, 0));
 #pragma unroll
         for (int j = 0; j < 4; ++j)
 #pragma unroll
             for (int cb = 0; cb < CB; ++cb)
-                u[j][cb] = up[(static_cast<int64_t>(wi_row * 4 + j) * cq + cg) * cop + cb * 32];
+                u[j][cb] = __builtin_bit_cast(
+                    floatx4, __builtin_amdgcn_raw_buffer_load_b128(ubuf, uoff[j] + cb * 512, s * u_step, 0));
     };
 
     floatx16 acc[4][CB];
@@ -264,20 +280,21 @@ __global__ __launch_bounds__(256) void conv_wino_kernel(ConvArgs a, int tiles_h,
     // step then waits a full L2 round trip); BN = 32 keeps two waves per SIMD
     // without them, which hides that wait instead.
     const int ns = (a.Cin + kCK - 1) / kCK;  // K steps
-    load(0, dreg[0], ureg[0]);
+    auto back_of = [&](int t) { return t == ns - 1 ? last_back : 0; };
+    load(0, dreg[0], ureg[0], back_of(0));
     int s = 0;
     for (; s + 2 < ns; s += 2) {
-        load(s + 1, dreg[1], ureg[1]);
+        load(s + 1, dreg[1], ureg[1], back_of(s + 1));
         if constexpr (BN == 64) __builtin_amdgcn_sched_barrier(0);
         compute(s, dreg[0], ureg[0]);
         if constexpr (BN == 64) __builtin_amdgcn_sched_barrier(0);
-        load(s + 2, dreg[0], ureg[0]);
+        load(s + 2, dreg[0], ureg[0], back_of(s + 2));
         if constexpr (BN == 64) __builtin_amdgcn_sched_barrier(0);
         compute(s + 1, dreg[1], ureg[1]);
         if constexpr (BN == 64) __builtin_amdgcn_sched_barrier(0);
     }
     if (s + 1 < ns) {
-        load(s + 1, dreg[1], ureg[1]);
+        load(s + 1, dreg[1], ureg[1], back_of(s + 1));
         if constexpr (BN == 64) __builtin_amdgcn_sched_barrier(0);
         compute(s, dreg[0], ureg[0]);
         compute(s + 1, dreg[1], ureg[1]);
@@ -377,21 +394,26 @@ __global__ __launch_bounds__(256) void conv_wino_kernel(ConvArgs a, int tiles_h,
 
 namespace {
 
+// Byte extents of the input, transformed weights, output and residual.
+struct WinoBytes {
+    int x, u, y, r;
+};
+
 template <int BN, int ACT>
-void launch_act(const ConvArgs& a, dim3 grid, int th, int tw, int yb, int rb, hipStream_t s) {
+void launch_act(const ConvArgs& a, dim3 grid, int th, int tw, WinoBytes b, hipStream_t s) {
     if (a.res)
-        hipLaunchKernelGGL((conv_wino_kernel<BN, ACT, true>), grid, dim3(256), 0, s, a, th, tw, yb, rb);
+        hipLaunchKernelGGL((conv_wino_kernel<BN, ACT, true>), grid, dim3(256), 0, s, a, th, tw, b.x, b.u, b.y, b.r);
     else
-        hipLaunchKernelGGL((conv_wino_kernel<BN, ACT, false>), grid, dim3(256), 0, s, a, th, tw, yb, rb);
+        hipLaunchKernelGGL((conv_wino_kernel<BN, ACT, false>), grid, dim3(256), 0, s, a, th, tw, b.x, b.u, b.y, b.r);
 }
 
 template <int BN>
-void launch_bn(const ConvArgs& a, dim3 grid, int th, int tw, int yb, int rb, hipStream_t s) {
+void launch_bn(const ConvArgs& a, dim3 grid, int th, int tw, WinoBytes b, hipStream_t s) {
     switch (a.act) {
-        case kActSilu: launch_act<BN, kActSilu>(a, grid, th, tw, yb, rb, s); break;
-        case kActSiluWinogradForm: launch_act<BN, kActSiluWinogradForm>(a, grid, th, tw, yb, rb, s); break;
-        case kActNone: launch_act<BN, kActNone>(a, grid, th, tw, yb, rb, s); break;
-        default: launch_act<BN, kActGeneric>(a, grid, th, tw, yb, rb, s); break;
+        case kActSilu: launch_act<BN, kActSilu>(a, grid, th, tw, b, s); break;
+        case kActSiluWinogradForm: launch_act<BN, kActSiluWinogradForm>(a, grid, th, tw, b, s); break;
+        case kActNone: launch_act<BN, kActNone>(a, grid, th, tw, b, s); break;
+        default: launch_act<BN, kActGeneric>(a, grid, th, tw, b, s); break;
     }
 }
 
@@ -408,23 +430,24 @@ void launch_conv_wino(const ConvArgs& a, int bn, hipStream_t s) {
     if (a.Ho != a.H + 2 * a.ph - 2 || a.Wo != a.W + 2 * a.pw - 2 || a.Ho <= 0 || a.Wo <= 0) fail("output size");
     if (a.x_sw % 4 != 0 || a.x_sh % 4 != 0 || a.x_sn % 4 != 0 || reinterpret_cast<uintptr_t>(a.x) % 16 != 0)
         fail("input rows must be 16-byte aligned");
-    // per-image input offsets (and the largest patch read) in int32
-    const int64_t img_extent = static_cast<int64_t>(a.H) * a.x_sh + static_cast<int64_t>(a.W) * a.x_sw + a.Cin;
-    if (img_extent >= (int64_t{1} << 31)) fail("image too large for int32 offsets");
     const int64_t tiles_h = (a.Ho + 1) / 2, tiles_w = (a.Wo + 1) / 2;
     const int64_t T = a.N * tiles_h * tiles_w;
     if (T >= (int64_t{1} << 31)) fail("too many tiles");
     const dim3 grid(static_cast<unsigned>((T + kWT - 1) / kWT), static_cast<unsigned>((a.Cout + bn - 1) / bn));
     if (grid.y > 65535) fail("grid");
-    if (a.y_sn < 0 || a.y_sh < 0 || a.y_sw < 0 || (a.res && (a.r_sn < 0 || a.r_sh < 0 || a.r_sw < 0)))
-        fail("negative output strides");
-    if (!wino_views_fit(a)) fail("output or residual view spans 1 GiB or more");
-    const int yb = static_cast<int>(view_bytes(a.N, a.Ho, a.Wo, a.Cout, a.y_sn, a.y_sh, a.y_sw));
-    const int rb = a.res ? static_cast<int>(view_bytes(a.N, a.Ho, a.Wo, a.Cout, a.r_sn, a.r_sh, a.r_sw)) : 0;
+    if (a.x_sn < 0 || a.x_sh < 0 || a.x_sw < 0 || a.y_sn < 0 || a.y_sh < 0 || a.y_sw < 0 ||
+        (a.res && (a.r_sn < 0 || a.r_sh < 0 || a.r_sw < 0)))
+        fail("negative strides");
+    if (!wino_views_fit(a)) fail("input, weights, output or residual span 1 GiB - 4 KiB or more");
+    WinoBytes b;
+    b.x = static_cast<int>(view_bytes(a.N, a.H, a.W, a.Cin, a.x_sn, a.x_sh, a.x_sw));
+    b.u = static_cast<int>(wino_packed_elems(a.Cout, a.Cin) * 4);
+    b.y = static_cast<int>(view_bytes(a.N, a.Ho, a.Wo, a.Cout, a.y_sn, a.y_sh, a.y_sw));
+    b.r = a.res ? static_cast<int>(view_bytes(a.N, a.Ho, a.Wo, a.Cout, a.r_sn, a.r_sh, a.r_sw)) : 0;
     if (bn == 64)
-        launch_bn<64>(a, grid, static_cast<int>(tiles_h), static_cast<int>(tiles_w), yb, rb, s);
+        launch_bn<64>(a, grid, static_cast<int>(tiles_h), static_cast<int>(tiles_w), b, s);
     else
-        launch_bn<32>(a, grid, static_cast<int>(tiles_h), static_cast<int>(tiles_w), yb, rb, s);
+        launch_bn<32>(a, grid, static_cast<int>(tiles_h), static_cast<int>(tiles_w), b, s);
 }
 
 void launch_pack_wino_weights(float* dst, const float* w, int Cout, int Cin, hipStream_t s) {

@@ -215,11 +215,13 @@ int64_t view_span_bytes(const VRef& v) {
     return 4 * (last + 1);
 }
 
-// The Winograd kernel addresses its output and residual views with 32-bit
-// byte offsets (spans under 1 GiB).
+// The Winograd kernel addresses its input, transformed weights, output and
+// residual with 32-bit byte offsets (spans under 1 GiB less 4 KiB).
 bool wino_views_ok(const Step& s) {
-    constexpr int64_t kMax = int64_t{1} << 30;
-    return view_span_bytes(s.out) < kMax && (!s.has_res || view_span_bytes(s.res) < kMax);
+    constexpr int64_t kMax = (int64_t{1} << 30) - 4096;
+    const int64_t u_bytes = 4 * k::wino_packed_elems(static_cast<int>(s.out.dims[1]), static_cast<int>(s.a.dims[1]));
+    return view_span_bytes(s.a) < kMax && u_bytes < kMax && view_span_bytes(s.out) < kMax &&
+           (!s.has_res || view_span_bytes(s.res) < kMax);
 }
 
 // Launch-shape query of an implicit-GEMM conv step.

@@ -168,10 +168,11 @@ def test_conv_every_tile(tmp_path, monkeypatch, tile, splits, cin, cout, k, s, h
 
 @pytest.mark.parametrize("tile", ["wino64", "wino32"])
 @pytest.mark.parametrize("cin,cout,hw", [(64, 64, 160), (32, 32, 17), (48, 80, 31), (12, 20, 9), (256, 256, 20),
-                                         (8, 136, 6)])
+                                         (8, 136, 6), (20, 24, 11), (28, 40, 13)])
 def test_winograd_conv(tmp_path, monkeypatch, tile, cin, cout, hw):
     """The Winograd F(2x2,3x3) kernel, forced, against the oracle (odd sizes
-    leave partial 2x2 tiles; Cin = 12 and 8 leave half-empty 8-channel steps)."""
+    leave partial 2x2 tiles; Cin = 8, 12, 20 and 28 leave a half-empty last
+    8-channel step after 0 to 3 full ones)."""
     print(f"[case] winograd tile={tile} cin={cin} cout={cout} hw={hw}", flush=True)
     monkeypatch.setenv("PDEFA_CONV_TILE", tile)
     monkeypatch.setenv("PDEFA_SILU", "exact")
