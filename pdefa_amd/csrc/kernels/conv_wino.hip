@@ -281,22 +281,35 @@ __global__ __launch_bounds__(256) void conv_wino_kernel(ConvArgs a, int tiles_h,
     // without them, which hides that wait instead.
     const int ns = (a.Cin + kCK - 1) / kCK;  // K steps
     auto back_of = [&](int t) { return t == ns - 1 ? last_back : 0; };
+    // BN = 64: one wave per SIMD, so a load instruction's issue must not
+    // leave the matrix core idle: the next step's loads go one after each of
+    // the step's first MFMAs (after the transform that feeds them).
+    auto interleave = [&] {
+        if constexpr (BN == 64) {
+            __builtin_amdgcn_sched_group_barrier(0x002, 64, 0);  // vector ALU (the transform)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+                __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // global load
+            }
+            __builtin_amdgcn_sched_group_barrier(0x008, 16, 0);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    };
     load(0, dreg[0], ureg[0], back_of(0));
     int s = 0;
     for (; s + 2 < ns; s += 2) {
         load(s + 1, dreg[1], ureg[1], back_of(s + 1));
-        if constexpr (BN == 64) __builtin_amdgcn_sched_barrier(0);
         compute(s, dreg[0], ureg[0]);
-        if constexpr (BN == 64) __builtin_amdgcn_sched_barrier(0);
+        interleave();
         load(s + 2, dreg[0], ureg[0], back_of(s + 2));
-        if constexpr (BN == 64) __builtin_amdgcn_sched_barrier(0);
         compute(s + 1, dreg[1], ureg[1]);
-        if constexpr (BN == 64) __builtin_amdgcn_sched_barrier(0);
+        interleave();
     }
     if (s + 1 < ns) {
         load(s + 1, dreg[1], ureg[1], back_of(s + 1));
-        if constexpr (BN == 64) __builtin_amdgcn_sched_barrier(0);
         compute(s, dreg[0], ureg[0]);
+        interleave();
         compute(s + 1, dreg[1], ureg[1]);
     } else {
         compute(s, dreg[0], ureg[0]);
