@@ -274,25 +274,26 @@ __global__ __launch_bounds__(256) void conv_wino_kernel(ConvArgs a, int tiles_h,
                     acc[j][cb] = __builtin_amdgcn_mfma_f32_32x32x2f32(v[j][m], u[j][cb][m], acc[j][cb], 0, 0, 0);
     };
 
-    // Loads run one K step (8 channels) ahead.  With BN = 64 scheduling
-    // barriers keep each step's loads ahead of the previous step's MFMAs
-    // (left alone, the scheduler sinks them below to save registers, and every
-    // step then waits a full L2 round trip); BN = 32 keeps two waves per SIMD
-    // without them, which hides that wait instead.
+    // Loads run one K step (8 channels) ahead.  Scheduling barriers keep each
+    // step's loads among the previous step's MFMAs (left alone, the scheduler
+    // sinks them below to save registers, and every step then waits a full L2
+    // round trip).
     const int ns = (a.Cin + kCK - 1) / kCK;  // K steps
     auto back_of = [&](int t) { return t == ns - 1 ? last_back : 0; };
-    // BN = 64: one wave per SIMD, so a load instruction's issue must not
-    // leave the matrix core idle: the next step's loads go one after each of
-    // the step's first MFMAs (after the transform that feeds them).
+    // A load instruction's issue must not leave the matrix core idle (one
+    // wave per SIMD with BN = 64, two with BN = 32): the next step's loads go
+    // one after each of the step's first MFMAs (after the transform that
+    // feeds them).
     auto interleave = [&] {
-        if constexpr (BN == 64) {
+        {
+            constexpr int kLoads = 8 + 4 * CB, kMfma = 16 * CB;
             __builtin_amdgcn_sched_group_barrier(0x002, 64, 0);  // vector ALU (the transform)
 #pragma unroll
-            for (int i = 0; i < 16; ++i) {
+            for (int i = 0; i < kLoads; ++i) {
                 __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
                 __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // global load
             }
-            __builtin_amdgcn_sched_group_barrier(0x008, 16, 0);
+            __builtin_amdgcn_sched_group_barrier(0x008, kMfma - kLoads, 0);
             __builtin_amdgcn_sched_barrier(0);
         }
     };
