@@ -93,6 +93,29 @@ def test_single_conv_plan(tmp_path):
     assert "act=6" in lines[1] and "vec=1" in lines[1]
 
 
+def test_winograd_needs_views_under_one_gib(tmp_path):
+    """The Winograd kernel addresses its views with 32-bit byte offsets: the
+    planner's cost model takes a Winograd shape for a 64->64 3x3 layer at
+    160x160 at batch 1 and at the largest batch whose input and output span
+    under 1 GiB - 4 KiB, and the implicit GEMM one image later."""
+    model, x = ys.build_single_conv(64, 64, 3, 1, 160)
+    path = str(tmp_path / "c.engine")
+    ys.save(model, path)
+    per_image = 64 * 160 * 160 * 4
+    fit = ((1 << 30) - 4096 - 1) // per_image
+
+    def conv_line(n):
+        _, lines = parse(native.plan_text(path, [n] + list(x.shape[1:])))
+        conv = [l for l in lines if " conv_mfma(" in l]
+        assert len(conv) == 1
+        return conv[0]
+
+    assert "tile=wino" in conv_line(1)
+    assert "tile=wino" in conv_line(fit)
+    big = conv_line(fit + 1)
+    assert "tile=wino" not in big and "tile=" in big
+
+
 def test_unsupported_op_is_reported(tmp_path):
     from pdefa_amd.engine_format import Node
     model, x = ys.build_single_conv(4, 4, 1, 1, 8, silu=False)
