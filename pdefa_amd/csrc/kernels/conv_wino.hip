@@ -21,11 +21,12 @@
 // (16-byte runs of 4 channels, half h taking channels 4h..4h+3 of each 8-wide
 // K step), forms V_(i,0..3) in registers, and pairs them with U_(i,j) float4s
 // of the same 4 channels; MFMA m of a step uses channel 4h+m on half h, the
-// same k for A and B.  Loads run one K step ahead.  At the end each wave
-// applies the column transform (A^T over j) in registers, the 4 waves exchange
-// those rows through LDS, and the row transform (A^T over i), bias,
-// activation and residual produce each tile's 2x2 outputs, stored through the
-// output view's strides.
+// same k for A and B.  Loads (range-checked buffer loads) run one K step
+// ahead, issued between the step's MFMAs.  At the end each wave applies the
+// column transform (A^T over j) in registers, the 4 waves exchange those rows
+// through LDS, and the row transform (A^T over i), bias, activation and
+// residual produce each tile's 2x2 outputs, written with range-checked buffer
+// stores at per-pixel offsets of the output view.
 #include "../kernels.hpp"
 #include "act.hpp"
 
@@ -199,7 +200,8 @@ __global__ __launch_bounds__(256) void conv_wino_kernel(ConvArgs a, int tiles_h,
     // the input's buffer range, and load zeros.
     const __amdgpu_buffer_rsrc_t xbuf =
         __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(a.x), 0, x_bytes, kWinoBufferFlags);
-    const __amdgpu_buffer_rsrc_t ubuf = __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(a.wpk), 0, u_bytes, kWinoBufferFlags);
+    const __amdgpu_buffer_rsrc_t ubuf =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(a.wpk), 0, u_bytes, kWinoBufferFlags);
     // byte offset of channel 4*half of each patch position
     int32_t doff[2][4];
 #pragma unroll
