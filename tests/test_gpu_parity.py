@@ -104,6 +104,8 @@ CONV_CASES = [
     (64, 80, 3, 1, 20),    # Cout not a multiple of the tile
     (8, 200, 1, 1, 9),
     (5, 7, 3, 1, 11),      # odd Cin, Cout < 8 (direct kernel)
+    (4, 6, 3, 1, 13),      # direct kernel, 4 input channels all loaded up front
+    (1, 8, 3, 2, 17),      # direct kernel, one input channel
     (256, 256, 3, 1, 20),  # deep layer: split-K
     (96, 144, 3, 2, 33),
     (576, 64, 3, 1, 10),   # Cin > 512: GEMM-path SiLU in the reference
