@@ -506,9 +506,9 @@ __global__ __launch_bounds__(256) void detect_decode_kernel(DetectDecodeArgs a, 
 // class scores (row stride S floats, the Detect head's [anchor][144] concat):
 // the rows are read once, coalesced, into LDS (row pitch S + 1 floats, so the
 // per-anchor reads below hit distinct banks); lane (side, anchor) takes one
-// side's DFL expectation, 64 lanes decode the boxes, and the class sigmoids
+// side's DFL expectation, kHeadAnchors lanes decode the boxes, and the class sigmoids
 // are written class-major with consecutive lanes on consecutive anchors.
-constexpr int kHeadAnchors = 64;
+constexpr int kHeadAnchors = 32;
 template <int R>
 __global__ __launch_bounds__(256) void detect_head_kernel(DetectDecodeArgs a, int32_t A, int32_t C, int32_t S) {
     extern __shared__ __attribute__((aligned(16))) float rows[];
@@ -532,7 +532,7 @@ __global__ __launch_bounds__(256) void detect_head_kernel(DetectDecodeArgs a, in
         dst[3] = v.w;
     }
     __syncthreads();
-    {
+    if (tid < 4 * kHeadAnchors) {
         const int an = tid % kHeadAnchors, side = tid / kHeadAnchors;
         float d = 0.0f;
         if (an < cnt) {
