@@ -13,8 +13,10 @@ semantics, which is what this module evaluates in NCHW:
   Conv      session_ops_nn.inc:2-65 -> ops::conv2d (conv2d.cpp:484-651);
             output size (H + 2p - ((k-1)d + 1)) / s + 1 (conv2d.cpp:442-446);
             fused activation codes 1 relu, 2 leaky, 3 sigmoid, 4 tanh, 5 silu
-            (session_fusion.inc:33-107, conv2d.hpp:16-24); groups > 1 per
-            group (depthwise conv2d.cpp:576-586, grouped 342-392)
+            (session_fusion.inc:33-107, conv2d.hpp:16-24), as the reference's
+            kernel for the conv evaluates them (reference_conv_path,
+            fused_activation); groups > 1 per group (depthwise
+            conv2d.cpp:576-586, grouped 342-392)
   MaxPool   session_ops_nn.inc:267-347 -> pooling.cpp:35-101 (padding never wins)
   Resize    session_ops_shape.inc:96-202: nearest, target = in * scale
             (+0.5 truncation), source index floor(out * in/out)
@@ -24,7 +26,8 @@ semantics, which is what this module evaluates in NCHW:
   Transpose session_ops_shape.inc:946-1096
   Softmax   session_ops_math.inc:223-318 (max-subtracted exp, / sum)
   Add/Sub/Mul/Div  session_ops_math.inc:4-220 (numpy broadcasting)
-  Sigmoid   activation_avx2.cpp:110-121 (1 / (1 + e^-x))
+  Sigmoid   activation_avx2.cpp:110-121 (1 / (1 + e^-x)); Relu, LeakyRelu,
+            Tanh, SiLU: session_ops_nn.inc:210-231 -> activation.cpp:28-70
 
 Pins (tests/test_oracle.py): the compiled reference (oracle/_ref) on the same
 `.engine` files and inputs; closed-form conv known answers from
@@ -82,6 +85,8 @@ def conv2d(x, w, b=None, stride=(1, 1), pad=(0, 0), dil=(1, 1), act=0, slope=0.0
 
 
 def activation(x, act, slope=0.01):
+    """The plain functions behind the fused codes (conv2d.cpp:131-139,
+    conv2d_gemm.cpp:55-64): 1 relu, 2 leaky relu, 3 sigmoid, 4 tanh, 5 silu."""
     if act == 0:
         return x
     if act == 1:
@@ -95,6 +100,47 @@ def activation(x, act, slope=0.01):
     if act == 5:
         return x / (1.0 + np.exp(-x))
     raise ValueError(f"activation code {act}")
+
+
+def gelu_tanh(x):
+    """Tanh-form GELU, 0.5 x (1 + tanh(0.7978845608 (x + 0.044715 x^3)))
+    (conv2d_winograd.cpp:108-111, conv2d_avx2.cpp:109-112)."""
+    return 0.5 * x * (1.0 + np.tanh(0.7978845608 * (x + 0.044715 * x * x * x)))
+
+
+def reference_conv_path(cin, kh, kw, stride, pad, dil, groups):
+    """The kernel the reference conv dispatcher (PDEFA1.0/src/ops/conv2d.cpp:484-651)
+    sends a conv to, as far as it changes the fused activations: "direct"
+    (groups 1, Cin <= 16, KH, KW <= 7 and not a plain 1x1 with stride 1 and
+    no padding; conv2d.cpp:599-611), "winograd" (3x3, stride 1, dilation 1,
+    groups 1, Cin <= 512; conv2d.cpp:616-629) or "other" (DFL, depthwise,
+    grouped GEMM, GEMM)."""
+    if groups != 1:
+        return "other"
+    pure_1x1 = (kh == 1 and kw == 1 and tuple(pad) == (0, 0) and tuple(stride) == (1, 1)
+                and tuple(dil) == (1, 1))
+    if not pure_1x1 and cin <= 16 and kh <= 7 and kw <= 7:
+        return "direct"
+    if kh == 3 and kw == 3 and tuple(stride) == (1, 1) and tuple(dil) == (1, 1) and cin <= 512:
+        return "winograd"
+    return "other"
+
+
+def fused_activation(y, act, path, slope=0.01, compat_silu=True):
+    """A fused code as the reference's kernel on `path` evaluates it:
+    code 3 on the direct kernel is 1 / (1 + v) (conv2d_avx2.cpp:99-103),
+    code 4 on the direct and Winograd kernels is tanh-form GELU
+    (conv2d_avx2.cpp:109-112, conv2d_winograd.cpp:108-111), code 5 on the
+    Winograd kernel the polynomial SiLU form (conv2d_winograd.cpp:81-101,
+    evaluated in float32; compat_silu=False takes the true SiLU); everything
+    else the plain function."""
+    if path == "direct" and act == 3:
+        return 1.0 / (1.0 + y)
+    if path in ("direct", "winograd") and act == 4:
+        return gelu_tanh(y)
+    if path == "winograd" and act == 5 and compat_silu:
+        return silu_winograd_compat(np.asarray(y, np.float32)).astype(np.asarray(y).dtype)
+    return activation(y, act, slope)
 
 
 def silu_winograd_compat(x):
@@ -160,8 +206,7 @@ def winograd_path(cin, kh, kw, stride, dil, groups):
     """True when the reference conv dispatcher routes a conv to its Winograd
     kernel (PDEFA1.0/src/ops/conv2d.cpp:602-631): 3x3, stride 1, dilation 1,
     groups 1, and 16 < Cin <= 512 (Cin <= 16 goes to the direct kernel)."""
-    return (kh == 3 and kw == 3 and tuple(stride) == (1, 1) and tuple(dil) == (1, 1)
-            and groups == 1 and 16 < cin <= 512)
+    return reference_conv_path(cin, kh, kw, stride, (1, 1), dil, groups) == "winograd"
 
 
 def conv2d_direct(x, w, b=None, stride=(1, 1), pad=(0, 0)):
@@ -247,8 +292,26 @@ def reshape(x, shape):
 
 
 def _consumers(model, ref):
-    return [n for n in model.nodes if ref in n.inputs] + \
+    """One entry per use of `ref`: a node for each of its inputs that reads
+    it, None for each graph output (session_fusion.inc:20-30 counts so)."""
+    return [n for n in model.nodes for i in n.inputs if i == ref] + \
         [None for o in model.graph_outputs if o == ref]
+
+
+_FUSABLE = {"Relu": 1, "LeakyRelu": 2, "Sigmoid": 3, "Tanh": 4}
+
+
+def _single_act_consumer(model, conv):
+    """(node, code) when conv's output has exactly one use and it is a
+    one-input ReLU / LeakyReLU / Sigmoid / Tanh (session_fusion.inc:85-107)."""
+    out = conv.outputs[0]
+    cons = _consumers(model, out)
+    if len(cons) != 1 or cons[0] is None:
+        return None
+    n = cons[0]
+    if n.inputs == [out] and n.op_name in _FUSABLE:
+        return n, _FUSABLE[n.op_name]
+    return None
 
 
 def _silu_nodes(model, conv):
@@ -307,14 +370,18 @@ def run_graph(model: EngineModel, inputs, dtype=np.float64, compat_silu=True, fl
             groups = max(1, int(p.get("groups", 1)))
             x, w = get(ins[0]), get(ins[1])
             stride, dil = (p["stride_h"], p["stride_w"]), (p["dil_h"], p["dil_w"])
-            y = conv2d(x, w, b, stride, (p["pad_h"], p["pad_w"]), dil, groups=groups)
+            pad = (p["pad_h"], p["pad_w"])
+            y = conv2d(x, w, b, stride, pad, dil, groups=groups)
+            path = reference_conv_path(x.shape[1], w.shape[2], w.shape[3], stride, pad, dil, groups)
+            slope = float(p.get("leaky_slope", 0.01))
             # Conv -> Sigmoid -> Mul is fused into the conv by the reference
-            # session (session_fusion.inc:33-81); on Winograd layers the fused
-            # SiLU is the compat form above.
+            # session (session_fusion.inc:33-81), a single-consumer
+            # ReLU / LeakyReLU / Sigmoid / Tanh too (85-107); on the reference's
+            # Winograd and direct kernels some fused codes are other functions
+            # (fused_activation).
             silu = _silu_consumer(model, node)
             if silu is not None:
-                if compat_silu and winograd_path(x.shape[1], w.shape[2], w.shape[3],
-                                                 stride, dil, groups):
+                if compat_silu and path == "winograd":
                     y32 = y.astype(np.float32)
                     straight = silu_winograd_compat(y32)
                     if flip is not None and flip(node.name):
@@ -328,8 +395,24 @@ def run_graph(model: EngineModel, inputs, dtype=np.float64, compat_silu=True, fl
                 inter[silu] = y
                 skip.update(_silu_nodes(model, node))
                 continue
+            single = _single_act_consumer(model, node)
+            code = int(p.get("fused_activation", 0))
+            if single is not None:
+                act_node, code = single
+                if code == 2:
+                    slope = float(act_node.params.get("leaky_slope", 0.01))
+                y = fused_activation(y, code, path, slope, compat_silu)
+                inter[node.outputs[0]] = y
+                inter[act_node.outputs[0]] = y
+                skip.add(act_node.name)
+                continue
+            y = fused_activation(y, code, path, slope, compat_silu)
         elif op == "Sigmoid":
             y = 1.0 / (1.0 + np.exp(-get(ins[0])))
+        elif op in ("Relu", "Tanh", "SiLU"):
+            y = activation(get(ins[0]), {"Relu": 1, "Tanh": 4, "SiLU": 5}[op])
+        elif op == "LeakyRelu":
+            y = activation(get(ins[0]), 2, float(p.get("leaky_slope", 0.01)))
         elif op in ("Add", "Sub", "Mul", "Div"):
             a, b = get(ins[0]), get(ins[1])
             y = {"Add": np.add, "Sub": np.subtract, "Mul": np.multiply,

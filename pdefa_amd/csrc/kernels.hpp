@@ -24,9 +24,16 @@ struct View {
 };
 
 // Fused epilogue activation codes.  1-5 follow the reference's
-// Conv2dConfig::FusedActivation numbering (PDEFA1.0/include/engine/ops/conv2d.hpp:16-24);
-// 6 is the SiLU form the reference's Winograd epilogue evaluates
-// (PDEFA1.0/src/kernels/simd/avx2/conv2d_winograd.cpp:81-101).
+// Conv2dConfig::FusedActivation numbering (PDEFA1.0/include/engine/ops/conv2d.hpp:16-24).
+// 6-8 are what some of the reference's conv kernels evaluate for codes 5, 4
+// and 3 (the planner picks them by the reference's dispatch rule):
+//   6  the SiLU form of its Winograd epilogue
+//      (PDEFA1.0/src/kernels/simd/avx2/conv2d_winograd.cpp:81-101);
+//   7  tanh-form GELU, 0.5 v (1 + tanh(0.7978845608 (v + 0.044715 v^3))),
+//      which its Winograd and direct kernels apply for code 4
+//      (conv2d_winograd.cpp:108-111, conv2d_avx2.cpp:109-112);
+//   8  1 / (1 + v), which its direct kernel applies for code 3
+//      (PDEFA1.0/src/kernels/simd/avx2/conv2d_avx2.cpp:99-103).
 enum Act : int32_t {
     kActNone = 0,
     kActRelu = 1,
@@ -35,6 +42,8 @@ enum Act : int32_t {
     kActTanh = 4,
     kActSilu = 5,
     kActSiluWinogradForm = 6,
+    kActGeluTanh = 7,
+    kActRecip1p = 8,
 };
 
 // Implicit-GEMM convolution tile configurations.  A workgroup is 4 or 8 waves

@@ -58,6 +58,11 @@ __device__ __forceinline__ float apply_act(float v, int act, float slope) {
         case kActTanh: return tanhf(v);
         case kActSilu: return v * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(v * -1.44269504088896341f));
         case kActSiluWinogradForm: return silu_winograd_form(v);
+        case kActGeluTanh: {
+            const float inner = 0.7978845608f * (v + 0.044715f * v * v * v);
+            return 0.5f * v * (1.0f + tanhf(inner));
+        }
+        case kActRecip1p: return 1.0f / (1.0f + v);
         default: return v;
     }
 }

@@ -224,6 +224,43 @@ bool wino_views_ok(const Step& s) {
            (!s.has_res || view_span_bytes(s.res) < kMax);
 }
 
+// The kernel the reference's conv dispatcher (PDEFA1.0/src/ops/conv2d.cpp:484-651)
+// sends a conv to, as far as it changes what a fused activation code computes:
+// its direct kernel (groups 1, Cin <= 16, KH, KW <= 7, not a plain 1x1 with
+// stride 1 and no padding; conv2d.cpp:599-611), its Winograd kernel (3x3,
+// stride 1, dilation 1, groups 1, Cin <= 512; conv2d.cpp:616-629), or one of
+// the others (DFL, depthwise, grouped GEMM, GEMM), which all apply the plain
+// functions.
+enum class RefConvPath { Direct, Winograd, Other };
+
+RefConvPath reference_conv_path(const Step& s, int64_t cin_per_group) {
+    if (s.groups != 1) return RefConvPath::Other;
+    const bool pure_1x1 = s.KH == 1 && s.KW == 1 && s.ph == 0 && s.pw == 0 && s.sh == 1 && s.sw == 1 && s.dh == 1 &&
+                          s.dw == 1;
+    if (!pure_1x1 && cin_per_group <= 16 && s.KH <= 7 && s.KW <= 7) return RefConvPath::Direct;
+    if (s.KH == 3 && s.KW == 3 && s.sh == 1 && s.sw == 1 && s.dh == 1 && s.dw == 1 && cin_per_group <= 512)
+        return RefConvPath::Winograd;
+    return RefConvPath::Other;
+}
+
+// The function a fused activation code stands for on the reference's path:
+// code 5 on its Winograd kernel is the polynomial SiLU form
+// (conv2d_winograd.cpp:81-101, unless `winograd_form_silu` is off), code 4 on
+// its Winograd and direct kernels is tanh-form GELU (conv2d_winograd.cpp:108-111,
+// conv2d_avx2.cpp:109-112), code 3 on its direct kernel is 1 / (1 + v)
+// (conv2d_avx2.cpp:99-103).  Results equal the reference's only with the
+// same functions.
+int32_t reference_activation(int32_t code, RefConvPath path, bool winograd_form_silu) {
+    if (path == RefConvPath::Direct) {
+        if (code == k::kActSigmoid) return k::kActRecip1p;
+        if (code == k::kActTanh) return k::kActGeluTanh;
+    } else if (path == RefConvPath::Winograd) {
+        if (code == k::kActTanh) return k::kActGeluTanh;
+        if (code == k::kActSilu && winograd_form_silu) return k::kActSiluWinogradForm;
+    }
+    return code;
+}
+
 // Launch-shape query of an implicit-GEMM conv step.
 ConvQuery conv_query(const Step& s) {
     ConvQuery q;
@@ -925,11 +962,7 @@ class Planner {
         const int64_t cin = wd[1], cout = wd[0];  // input channels per group, all output channels
         s.act = e.act;
         s.slope = e.slope;
-        // The reference routes 3x3/s1/d1 convs with 16 < Cin <= 512 to its Winograd
-        // kernel (conv2d.cpp:602-631), whose fused SiLU is the polynomial form.
-        const bool winograd = s.KH == 3 && s.KW == 3 && s.sh == 1 && s.sw == 1 && s.dh == 1 && s.dw == 1 && cin > 16 &&
-                              cin <= 512 && G == 1;
-        if (s.act == k::kActSilu && winograd && opt_.winograd_form_silu) s.act = k::kActSiluWinogradForm;
+        s.act = reference_activation(s.act, reference_conv_path(s, cin), opt_.winograd_form_silu);
         if (e.res != INT32_MIN) {
             s.has_res = true;
             s.res = input_view(e.res);

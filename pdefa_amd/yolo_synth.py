@@ -245,15 +245,24 @@ def build_yolov8(scale: str = "n", seed: int = 0, nc: int = 80, imgsz: int = 640
 
 
 def build_single_conv(cin: int, cout: int, k: int, stride: int, hw: int, seed: int = 7,
-                      silu: bool = True, groups: int = 1) -> Tuple[EngineModel, np.ndarray]:
+                      silu: bool = True, groups: int = 1, act: Optional[str] = None,
+                      leaky_slope: float = 0.1, centered: bool = False) -> Tuple[EngineModel, np.ndarray]:
     """One Conv2d(k, stride, pad k//2, groups) + bias (+ SiLU as Sigmoid*Mul)
     graph.
 
-    Returns the model and its seeded input x ~ U[0,1) of shape [1,cin,hw,hw].
+    act: instead of the SiLU, one single-consumer activation node after the
+    conv ("Relu", "LeakyRelu" with leaky_slope, "Sigmoid" or "Tanh"), which
+    the reference session fuses into the conv (session_fusion.inc:85-107).
+    centered: the input is U[-1,1) instead of U[0,1) (pre-activations of
+    both signs).
+
+    Returns the model and its seeded input x of shape [1,cin,hw,hw].
     Seed stream: x, then W [cout, cin/groups, k, k] (Kaiming-uniform, bound
     sqrt(6/fan_in)), then b ~ U[-0.1, 0.1]."""
     rng = np.random.default_rng(seed)
     x = rng.random((1, cin, hw, hw), dtype=np.float32)
+    if centered:
+        x = (x * np.float32(2.0) - np.float32(1.0)).astype(np.float32)
     w = kaiming_uniform(rng, (cout, cin // groups, k, k))
     bias = rng.uniform(-0.1, 0.1, size=cout).astype(np.float32)
     b = GraphBuilder()
@@ -261,7 +270,10 @@ def build_single_conv(cin: int, cout: int, k: int, stride: int, hw: int, seed: i
     p = k // 2
     y = b.node("Conv", "/conv/Conv", [-1, wi, bi], stride_h=stride, stride_w=stride,
                pad_h=p, pad_w=p, dil_h=1, dil_w=1, groups=groups)
-    if silu:
+    if act is not None:
+        params = {"leaky_slope": leaky_slope} if act == "LeakyRelu" else {}
+        y = b.node(act, f"/act/{act}", [y], **params)
+    elif silu:
         sg = b.node("Sigmoid", "/act/Sigmoid", [y])
         y = b.node("Mul", "/act/Mul", [y, sg])
     ho = (hw + 2 * p - k) // stride + 1

@@ -379,3 +379,123 @@ def test_flip_takes_the_other_side_of_each_jump():
     assert not np.array_equal(lo, hi)
     # no flip predicate: the straight compat form
     np.testing.assert_array_equal(graph_ref.run_graph(model, [x])[0], straight)
+
+
+# ------------------------------------------------ decode / NMS known answers
+
+from tests import decode_kats  # noqa: E402
+
+
+def _decode_kat(fn, name):
+    boxes, nc, kw, want = decode_kats.CASES[name]
+    h = decode_kats.head(boxes, nc)
+    kw = dict(kw)
+    meta = kw.pop("meta", None)
+    return fn(h, meta, **kw), want
+
+
+@pytest.mark.parametrize("name", sorted(decode_kats.CASES))
+def test_decode_restatement_known_answers(name):
+    got, want = _decode_kat(lambda h, meta, **kw: decode_ref.decode(h.tolist(), meta, **kw), name)
+    assert got == want
+
+
+@pytest.mark.parametrize("name", sorted(decode_kats.CASES))
+def test_decode_yolo_known_answers(name):
+    got, want = _decode_kat(lambda h, meta, **kw: postprocess.decode_yolo(h[None], meta, with_anchor=True, **kw),
+                            name)
+    assert got == want
+
+
+def test_decode_known_answers_catch_rule_changes(monkeypatch):
+    """Each rule the known answers pin, changed in a copy of the restatement,
+    makes at least one of them fail: '<' for '<=' at the IoU threshold, '<='
+    for '<' at conf_thres, '>=' for '>' in the class scan, clamps dropped,
+    sorting by anchor instead of by class order."""
+    import inspect
+    src = inspect.getsource(decode_ref)
+    mutants = {
+        "iou <= thr": ("iou(boxes[cur], boxes[j]) <= iou_thres", "iou(boxes[cur], boxes[j]) < iou_thres"),
+        "conf <": ("if best_s < conf_thres:", "if best_s <= conf_thres:"),
+        "strict >": ("if s > best_s:", "if s >= best_s:"),
+        "clamp": ("x1 = 0.0 if x1 < 0 else (ow if x1 > ow else x1)", "pass"),
+        "class order": ("keep.sort(key=lambda i: boxes[i][4], reverse=True)",
+                        "keep.sort(key=lambda i: (-boxes[i][4], boxes[i][6]))"),
+        "max_det": ("keep = keep[:max_det]", "keep = keep[:max_det + 1]"),
+        "iou guard": ("- inter + 1e-9)", "- inter + 1e-3)"),
+    }
+    for what, (a, b) in mutants.items():
+        assert a in src, what
+        ns = {}
+        exec(compile(src.replace(a, b), "decode_mutant", "exec"), ns)
+        failed = []
+        for name in decode_kats.CASES:
+            got, want = _decode_kat(lambda h, meta, **kw: ns["decode"](h.tolist(), meta, **kw), name)
+            if got != want:
+                failed.append(name)
+        assert failed, f"no known answer catches the change '{what}'"
+
+
+# ---------------------------- fused single-consumer activations, by path
+
+ACT_CONV_CASES = [
+    # cin, cout, k, stride, hw: the reference's direct kernel (Cin <= 16),
+    # its Winograd kernel (3x3 s1, 16 < Cin <= 512), its GEMM (1x1, 3x3 s2,
+    # Cin > 512) and a direct-kernel 5x5
+    (3, 16, 3, 1, 20), (12, 20, 5, 1, 11), (32, 24, 3, 1, 18), (576, 40, 3, 1, 8), (64, 48, 3, 2, 17),
+    (24, 32, 1, 1, 13),
+]
+
+
+def _pole_safe_close(o, r, pre, act, path):
+    """|o - r| <= 2e-5 (1 + |r|), except where the reference's direct-kernel
+    sigmoid 1 / (1 + v) is near its pole (|1 + v| < 0.1), where fp32 is
+    ill-conditioned (relative error amplified by |v / (1 + v)|): there the
+    relative bound is 1e-3."""
+    err = np.abs(o.astype(np.float64) - r.astype(np.float64))
+    ok = err <= 2e-5 * (1 + np.abs(r))
+    if act == "Sigmoid" and path == "direct":
+        near = np.abs(1.0 + pre) < 0.1
+        ok |= near & (err <= 1e-3 * np.abs(r))
+    assert ok.all(), f"{int((~ok).sum())} elements differ, max {err.max():.3e}"
+
+
+@needs_ref
+@pytest.mark.parametrize("act", ["Relu", "LeakyRelu", "Sigmoid", "Tanh"])
+@pytest.mark.parametrize("cin,cout,k,s,hw", ACT_CONV_CASES)
+def test_oracle_fused_activation_vs_compiled_reference(tmp_path, act, cin, cout, k, s, hw):
+    """Conv -> ReLU / LeakyReLU(0.1) / Sigmoid / Tanh, fused by the reference
+    session (session_fusion.inc:85-107) and evaluated by the kernel its
+    dispatcher picks.  On the Winograd and direct kernels a fused Tanh is
+    tanh-form GELU and on the direct kernel a fused Sigmoid is 1 / (1 + v):
+    the plain functions differ from the reference there (checked), the
+    oracle's per-path functions do not."""
+    model, x = ys.build_single_conv(cin, cout, k, s, hw, seed=5, act=act, centered=True)
+    path = str(tmp_path / "a.engine")
+    ys.save(model, path)
+    r = ref_lib.RefSession(path).run(x)[0]
+    o = graph_ref.run_graph(model, [x])[0]
+    pre_model, _ = ys.build_single_conv(cin, cout, k, s, hw, seed=5, silu=False, centered=True)
+    pre = graph_ref.run_graph(pre_model, [x])[0].astype(np.float64)
+    kpath = graph_ref.reference_conv_path(cin, k, k, (s, s), (k // 2, k // 2), (1, 1), 1)
+    _pole_safe_close(o, r, pre, act, kpath)
+    code = {"Relu": 1, "LeakyRelu": 2, "Sigmoid": 3, "Tanh": 4}[act]
+    plain = graph_ref.activation(pre, code, 0.1)
+    quirk = (act == "Tanh" and kpath in ("direct", "winograd")) or (act == "Sigmoid" and kpath == "direct")
+    assert quirk == (not np.allclose(plain, r, atol=1e-3, rtol=1e-3)), (act, kpath)
+
+
+def test_reference_conv_path_rule():
+    p = graph_ref.reference_conv_path
+    assert p(3, 3, 3, (2, 2), (1, 1), (1, 1), 1) == "direct"
+    assert p(16, 3, 3, (1, 1), (1, 1), (1, 1), 1) == "direct"
+    assert p(16, 1, 1, (1, 1), (0, 0), (1, 1), 1) == "other"     # plain 1x1
+    assert p(16, 1, 1, (2, 2), (0, 0), (1, 1), 1) == "direct"    # strided 1x1
+    assert p(16, 9, 9, (1, 1), (4, 4), (1, 1), 1) == "other"     # kernel > 7
+    assert p(17, 3, 3, (1, 1), (1, 1), (1, 1), 1) == "winograd"
+    assert p(512, 3, 3, (1, 1), (1, 1), (1, 1), 1) == "winograd"
+    assert p(513, 3, 3, (1, 1), (1, 1), (1, 1), 1) == "other"
+    assert p(64, 3, 3, (2, 2), (1, 1), (1, 1), 1) == "other"
+    assert p(64, 3, 3, (1, 1), (1, 1), (2, 2), 1) == "other"
+    assert p(64, 3, 3, (1, 1), (1, 1), (1, 1), 4) == "other"
+    assert p(8, 3, 3, (1, 1), (1, 1), (1, 1), 8) == "other"      # depthwise
