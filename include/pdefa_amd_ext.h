@@ -100,8 +100,17 @@ PDEFA_EXPORT EngineStatus pdefa_amd_session_plan(const EngineSession* sess, char
 PDEFA_EXPORT EngineStatus pdefa_amd_plan_model(const EngineModel* m, const int64_t* shape, int32_t ndim, char* buf,
                                                size_t cap, size_t* out_len);
 
-/* "<name> (<gcnArch>)" of HIP device 0, or "none". */
+/* "<name> (<gcnArch>, <compute units> CUs, <memory> GiB)" of HIP device 0
+ * ("AMD GPU" when the driver reports no marketing name), or "none". */
 PDEFA_EXPORT const char* pdefa_amd_device_name(void);
+
+/* Conv launch-shape choices made so far in this process: *measured = timed
+ * on the device while planning, *from_table = read from the device kind's
+ * launch-shape table (tuning/<arch>.txt beside the library directory, or
+ * PDEFA_TUNE_TABLE).  A process whose choices all come from the table plans
+ * the same launch shapes, hence the same results, as every other such
+ * process. */
+PDEFA_EXPORT EngineStatus pdefa_amd_tune_stats(int64_t* measured, int64_t* from_table);
 
 #ifdef __cplusplus
 }

@@ -11,7 +11,11 @@ carries the anchor index it came from.
 from collections import defaultdict
 
 
-def decode(arr, meta=None, conf_thres=0.25, iou_thres=0.45, max_det=300):
+def decode(arr, meta=None, conf_thres=0.25, iou_thres=0.45, max_det=300, iou_log=None):
+    """Detections of one [4 + classes, A] head (nested lists, batch dims of 1
+    unwrapped), as the reference's decode_yolo returns them plus the anchor.
+    iou_log: optional list that receives every IoU the NMS compares with
+    iou_thres (for robustness margins of test fixtures)."""
     while isinstance(arr, list) and len(arr) == 1 and isinstance(arr[0], list) and len(arr[0]) > 4:
         arr = arr[0]
     n_classes = len(arr) - 4
@@ -66,8 +70,38 @@ def decode(arr, meta=None, conf_thres=0.25, iou_thres=0.45, max_det=300):
             keep.append(cur)
             if not idxs:
                 break
-            idxs = [j for j in idxs if iou(boxes[cur], boxes[j]) <= iou_thres]
+            ious = [iou(boxes[cur], boxes[j]) for j in idxs]
+            if iou_log is not None:
+                iou_log.extend(ious)
+            idxs = [j for j, v in zip(idxs, ious) if v <= iou_thres]
     keep.sort(key=lambda i: boxes[i][4], reverse=True)
     keep = keep[:max_det]
     return [{"x1": boxes[i][0], "y1": boxes[i][1], "x2": boxes[i][2], "y2": boxes[i][3],
              "conf": boxes[i][4], "cls": boxes[i][5], "anchor": boxes[i][6]} for i in keep]
+
+
+def robust_conf(arr, start=0.25, min_gap=1e-2, min_candidates=5, step=0.0025, stop=0.9):
+    """The smallest conf_thres >= start on a `step` grid such that no anchor's
+    best class score lies within min_gap of it and at least min_candidates
+    anchors score above it (a threshold at which outputs within the parity
+    tolerance select the same candidates), with that gap; (None, None) when
+    there is none.  arr: [4 + classes, A] (numpy or nested lists)."""
+    import numpy as np
+    a = np.asarray(arr, np.float64)
+    while a.ndim > 2:
+        a = a[0]
+    best = np.sort(a[4:].max(axis=0))
+    for i in range(int(round((stop - start) / step)) + 1):
+        t = round(start + i * step, 6)
+        gap = float(np.abs(best - t).min())
+        if gap >= min_gap and int((best > t).sum()) >= min_candidates:
+            return t, gap
+    return None, None
+
+
+def min_iou_gap(arr, meta=None, conf_thres=0.25, iou_thres=0.45):
+    """The smallest |IoU - iou_thres| over the comparisons the NMS makes
+    (inf when it makes none)."""
+    log = []
+    decode(arr, meta, conf_thres, iou_thres, max_det=1 << 30, iou_log=log)
+    return min((abs(v - iou_thres) for v in log), default=float("inf"))

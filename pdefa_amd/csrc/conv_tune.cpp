@@ -1,11 +1,19 @@
 #include "conv_tune.hpp"
 
+#include <dlfcn.h>
+
 #include <algorithm>
 #include <array>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <fstream>
 #include <map>
 #include <memory>
 #include <mutex>
+#include <sstream>
 #include <stdexcept>
+#include <string>
 
 #include "runtime.hpp"
 
@@ -18,17 +26,120 @@ constexpr int64_t kMaxWorkspaceBytes = 256LL << 20;  // split-K partials of one 
 constexpr double kKeepModelChoice = 0.97;      // another shape must beat the model's by 3%
 constexpr int kTimingPasses = 2;                // timing passes over the candidates
 
-using Key = std::array<int32_t, 21>;
+constexpr size_t kKeyInts = 21;  // device, then the 20 shape fields of a ConvQuery
+using Key = std::array<int32_t, kKeyInts>;
 
 using GroupKey = std::vector<int32_t>;
 
 std::mutex g_mu;
 std::map<Key, k::ConvLaunchShape> g_cache;
 std::map<GroupKey, ConvGroupTiming> g_group_cache;
+size_t g_measured = 0, g_from_table = 0;
 
 Key make_key(const ConvQuery& q, int device) {
     return {device, q.N,  q.H,  q.W,  q.Cin, q.Ho, q.Wo, q.Cout, q.KH, q.KW, q.sh,
             q.sw,   q.ph, q.pw, q.dh, q.dw,  q.act, q.has_res ? 1 : 0, q.vec ? 1 : 0, q.wino ? 1 : 0, q.groups};
+}
+
+// ---- persisted choices
+//
+// A launch-shape table holds measured choices for one kind of device (its
+// architecture name and compute-unit count), so that a process plans the
+// same launch shapes as the one that measured them, without timing:
+//
+//   device gfx950 256
+//   conv <20 shape ints> <tile> <splits> <k steps per split>
+//   group <members> {<20 shape ints> <tile> <splits> <k steps per split>}... <tile> <group ms> <separate ms>
+//
+// The table is read once per process from PDEFA_TUNE_TABLE, or by default
+// from tuning/<arch>.txt beside the library's directory; PDEFA_TUNE_TABLE=0
+// disables it.  With PDEFA_TUNE_RECORD=<file> every choice measured in this
+// process is appended to that file in the same format.
+
+struct Table {
+    bool loaded = false;
+    std::string arch;
+    int cus = 0;
+    std::map<std::vector<int32_t>, k::ConvLaunchShape> conv;  // shape ints (no device)
+    std::map<std::vector<int32_t>, ConvGroupTiming> group;     // members' ints (no device)
+};
+std::map<int, Table> g_tables;  // per device
+
+void device_kind(int device, std::string& arch, int& cus) {
+    hipDeviceProp_t p;
+    PDEFA_HIP(hipGetDeviceProperties(&p, device));
+    arch = p.gcnArchName;
+    arch = arch.substr(0, arch.find(':'));
+    cus = p.multiProcessorCount;
+}
+
+std::string default_table_path(const std::string& arch) {
+    Dl_info info;
+    if (!dladdr(reinterpret_cast<void*>(&tune_conv), &info) || !info.dli_fname) return {};
+    std::string lib = info.dli_fname;
+    const size_t slash = lib.rfind('/');
+    const std::string dir = slash == std::string::npos ? std::string(".") : lib.substr(0, slash);
+    return dir + "/../tuning/" + arch + ".txt";
+}
+
+std::vector<int32_t> shape_ints(const Key& k) { return std::vector<int32_t>(k.begin() + 1, k.end()); }
+
+Table& table_for(int device) {
+    Table& t = g_tables[device];
+    if (t.loaded) return t;
+    t.loaded = true;
+    device_kind(device, t.arch, t.cus);
+    const char* env = std::getenv("PDEFA_TUNE_TABLE");
+    std::string path = env ? std::string(env) : default_table_path(t.arch);
+    if (path.empty() || path == "0") return t;
+    std::ifstream f(path);
+    if (!f) return t;
+    std::string line, tag;
+    bool match = false;
+    while (std::getline(f, line)) {
+        std::istringstream is(line);
+        if (!(is >> tag) || tag[0] == '#') continue;
+        if (tag == "device") {
+            std::string arch;
+            int cus = 0;
+            is >> arch >> cus;
+            match = arch == t.arch && cus == t.cus;
+            continue;
+        }
+        if (!match) continue;
+        if (tag == "conv") {
+            std::vector<int32_t> key(kKeyInts - 1);
+            k::ConvLaunchShape ls{};
+            for (auto& v : key) is >> v;
+            is >> ls.tile >> ls.splits >> ls.kt_per_split;
+            if (is && ls.tile >= 0 && ls.tile < k::kNumConvShapes && ls.splits >= 1) t.conv[key] = ls;
+        } else if (tag == "group") {
+            int n = 0;
+            is >> n;
+            if (n < 2 || n > k::kMaxConvGroup) continue;
+            std::vector<int32_t> key(static_cast<size_t>(n) * (kKeyInts - 1 + 3));
+            for (auto& v : key) is >> v;
+            ConvGroupTiming g;
+            is >> g.tile >> g.group_ms >> g.separate_ms;
+            if (is && g.tile >= 0 && g.tile < k::kNumConvTiles) t.group[key] = g;
+        }
+    }
+    return t;
+}
+
+void record_line(const Table& t, const std::string& body) {
+    const char* path = std::getenv("PDEFA_TUNE_RECORD");
+    if (!path || !*path) return;
+    if (std::FILE* f = std::fopen(path, "a")) {
+        std::fprintf(f, "device %s %d\n%s\n", t.arch.c_str(), t.cus, body.c_str());
+        std::fclose(f);
+    }
+}
+
+std::string ints_text(const std::vector<int32_t>& v) {
+    std::ostringstream os;
+    for (size_t i = 0; i < v.size(); ++i) os << (i ? " " : "") << v[i];
+    return os.str();
 }
 
 struct DeviceBuffer {
@@ -151,6 +262,12 @@ k::ConvLaunchShape tune_conv(const ConvQuery& q, hipStream_t s) {
     const Key key = make_key(q, device);
     std::lock_guard<std::mutex> lock(g_mu);
     if (auto it = g_cache.find(key); it != g_cache.end()) return it->second;
+    Table& table = table_for(device);
+    if (auto it = table.conv.find(shape_ints(key)); it != table.conv.end()) {
+        ++g_from_table;
+        g_cache.emplace(key, it->second);
+        return it->second;
+    }
 
     const int64_t M = static_cast<int64_t>(q.N) * q.Ho * q.Wo;
     const int K = q.KH * q.KW * (q.Cin / q.groups);  // per group
@@ -192,7 +309,10 @@ k::ConvLaunchShape tune_conv(const ConvQuery& q, hipStream_t s) {
             }
         PDEFA_HIP(hipStreamSynchronize(s));
     }
+    ++g_measured;
     g_cache.emplace(key, best);
+    record_line(table, "conv " + ints_text(shape_ints(key)) + " " + std::to_string(best.tile) + " " +
+                           std::to_string(best.splits) + " " + std::to_string(best.kt_per_split));
     return best;
 }
 
@@ -202,16 +322,24 @@ ConvGroupTiming tune_conv_group(const std::vector<ConvQuery>& qs, const std::vec
         throw std::runtime_error("tune_conv_group: bad group");
     int device = 0;
     PDEFA_HIP(hipGetDevice(&device));
-    GroupKey key;
+    GroupKey key;  // device, then per member its shape ints and solo launch shape
+    key.push_back(device);
     for (size_t i = 0; i < qs.size(); ++i) {
         const Key k1 = make_key(qs[i], device);
-        key.insert(key.end(), k1.begin(), k1.end());
+        key.insert(key.end(), k1.begin() + 1, k1.end());
         key.push_back(solo[i].tile);
         key.push_back(solo[i].splits);
         key.push_back(solo[i].kt_per_split);
     }
     std::lock_guard<std::mutex> lock(g_mu);
     if (auto it = g_group_cache.find(key); it != g_group_cache.end()) return it->second;
+    Table& table = table_for(device);
+    const std::vector<int32_t> tkey(key.begin() + 1, key.end());
+    if (auto it = table.group.find(tkey); it != table.group.end()) {
+        ++g_from_table;
+        g_group_cache.emplace(key, it->second);
+        return it->second;
+    }
 
     std::vector<std::unique_ptr<LayerScratch>> L;
     for (size_t i = 0; i < qs.size(); ++i) {
@@ -252,13 +380,23 @@ ConvGroupTiming tune_conv_group(const std::vector<ConvQuery>& qs, const std::vec
             r.group_ms = ms[t];
         }
     PDEFA_HIP(hipStreamSynchronize(s));
+    ++g_measured;
     g_group_cache.emplace(std::move(key), r);
+    char times[64];
+    std::snprintf(times, sizeof(times), " %d %.17g %.17g", r.tile, r.group_ms, r.separate_ms);
+    record_line(table, "group " + std::to_string(qs.size()) + " " + ints_text(tkey) + times);
     return r;
 }
 
 size_t conv_tune_cache_size() {
     std::lock_guard<std::mutex> lock(g_mu);
     return g_cache.size();
+}
+
+void conv_tune_stats(size_t& measured, size_t& from_table) {
+    std::lock_guard<std::mutex> lock(g_mu);
+    measured = g_measured;
+    from_table = g_from_table;
 }
 
 }  // namespace pdefa

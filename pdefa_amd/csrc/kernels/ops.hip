@@ -5,6 +5,7 @@
 // All kernels walk the logical output index with the innermost logical
 // dimension fastest, except the NCHW-logical spatial kernels which walk
 // (n, h, w, c) so that channels-last outputs are written contiguously.
+#include "../letterbox.hpp"
 #include "../kernels.hpp"
 #include "act.hpp"
 
@@ -609,9 +610,10 @@ void launch_detect_decode(const DetectDecodeArgs& a, hipStream_t s) {
 // three channels.  Pixels outside the scaled window take the pad value as
 // is; inside, source x = dx * (1/ratio) truncated, x0 clamped to w-2, and
 // (p00*w0 + p10*w1)*wy0 + (p01*w0 + p11*w1)*wy1 with the scale folded into
-// the row weights, every product and sum rounded separately (contraction
-// into fused multiply-adds is off here: it would also take fx = sx - x0
-// from the unrounded product), as the host path computes it.
+// the row weights, with the fused multiply-adds of letterbox_blend and
+// every other product and sum rounded separately (contraction is off here:
+// it would also take fx = sx - x0 from the unrounded product), as the host
+// path computes it.
 __global__ __launch_bounds__(256) void letterbox_kernel(LetterboxArgs a) {
 #pragma clang fp contract(off)
     const int idx = blockIdx.x * 256 + threadIdx.x;
@@ -638,11 +640,8 @@ __global__ __launch_bounds__(256) void letterbox_kernel(LetterboxArgs a) {
 #pragma unroll
         for (int c = 0; c < 3; ++c) {
             const int sc = a.ch == 1 ? 0 : c;
-            const float p00 = r0[x0 * a.ch + sc], p10 = r0[x1 * a.ch + sc];
-            const float p01 = r1[x0 * a.ch + sc], p11 = r1[x1 * a.ch + sc];
-            const float top = p00 * w0 + p10 * w1;
-            const float bot = p01 * w0 + p11 * w1;
-            v[c] = top * wy0 + bot * wy1;
+            v[c] = letterbox_blend(r0[x0 * a.ch + sc], r0[x1 * a.ch + sc], r1[x0 * a.ch + sc], r1[x1 * a.ch + sc],
+                                   w0, w1, wy0, wy1);
         }
     }
 #pragma unroll

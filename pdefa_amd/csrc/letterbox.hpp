@@ -27,6 +27,23 @@ inline LetterboxGeometry letterbox_geometry(int32_t src_w, int32_t src_h, int32_
     return g;
 }
 
+// One output value of the bilinear blend
+// (p00 w0 + p10 w1) wy0 + (p01 w0 + p11 w1) wy1 of preprocess.cpp:106-120,
+// rounded as the reference's own build evaluates it: GCC contracts each
+// a * b + c * d there into fma(a, b, c * d) (imageloader/CMakeLists.txt:41
+// compiles with -mfma, and GCC's default contraction fuses the first product
+// of each sum).  Host and device use this one function, so the device tensor
+// equals pdefa_preprocess_letterbox's, and the reference's, bit for bit.
+#if defined(__HIPCC__) || defined(__HIP__)
+__host__ __device__
+#endif
+inline float letterbox_blend(float p00, float p10, float p01, float p11, float w0, float w1, float wy0, float wy1) {
+#pragma clang fp contract(off)
+    const float top = std::fma(p00, w0, p10 * w1);
+    const float bot = std::fma(p01, w0, p11 * w1);
+    return std::fma(top, wy0, bot * wy1);
+}
+
 // One interleaved 8-bit image (1, 3 or 4 channels; channels 0..2 are used).
 struct ImageRef {
     const uint8_t* pixels = nullptr;

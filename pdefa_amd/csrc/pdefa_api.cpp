@@ -14,6 +14,7 @@
 
 #include "letterbox.hpp"
 #include "../../include/pdefa_amd_ext.h"
+#include "conv_tune.hpp"
 #include "../../include/pdefa_c_api.h"
 #include "api_internal.hpp"
 
@@ -83,7 +84,8 @@ std::unique_ptr<PdefaImage> load_pnm(const std::string& path, std::string* why) 
 // Letterbox restated from imageloader/src/preprocess.cpp:15-144: ratio =
 // min(tw/w, th/h); scaled = clamp(round(src*ratio), 1, target); centred
 // integer pads; source x = dx/ratio truncated, x0 clamped to w-2; bilinear
-// with the scale folded into the row weights; pad value written raw; NCHW.
+// with the scale folded into the row weights (letterbox_blend); pad value
+// written raw; NCHW.
 void letterbox(const PdefaImage& img, int tw, int th, float scale, float pad, float* out, PdefaPreprocessMeta* m) {
     const int sw_src = img.width, sh_src = img.height, ch = img.channels;
     const pdefa::LetterboxGeometry g = pdefa::letterbox_geometry(sw_src, sh_src, tw, th);
@@ -118,9 +120,9 @@ void letterbox(const PdefaImage& img, int tw, int th, float scale, float pad, fl
             const float w1 = fxv[dx], w0 = 1.0f - w1;
             for (int c = 0; c < 3; ++c) {
                 const int sc = ch == 1 ? 0 : c;
-                const float v = (r0[a * ch + sc] * w0 + r0[b * ch + sc] * w1) * wy0 +
-                                (r1[a * ch + sc] * w0 + r1[b * ch + sc] * w1) * wy1;
-                out[c * plane + row + dx] = v;
+                out[c * plane + row + dx] =
+                    pdefa::letterbox_blend(r0[a * ch + sc], r0[b * ch + sc], r1[a * ch + sc], r1[b * ch + sc], w0, w1,
+                                           wy0, wy1);
             }
         }
     }
@@ -468,9 +470,25 @@ PDEFA_EXPORT const char* pdefa_amd_device_name(void) {
         if (!pdefa::device_available()) return std::string("none");
         hipDeviceProp_t p;
         if (hipGetDeviceProperties(&p, 0) != hipSuccess) return std::string("unknown");
-        return std::string(p.name) + " (" + p.gcnArchName + ")";
+        // the marketing name can be empty (it is on some drivers): then the
+        // architecture, compute units and memory identify the device
+        std::string n = p.name;
+        if (n.find_first_not_of(' ') == std::string::npos) n = "AMD GPU";
+        std::ostringstream os;
+        os << n << " (" << p.gcnArchName << ", " << p.multiProcessorCount << " CUs, "
+           << (p.totalGlobalMem >> 30) << " GiB)";
+        return os.str();
     }();
     return name.c_str();
+}
+
+PDEFA_EXPORT EngineStatus pdefa_amd_tune_stats(int64_t* measured, int64_t* from_table) {
+    if (!measured || !from_table) return ENGINE_ERR_NULL_PTR;
+    size_t m = 0, t = 0;
+    pdefa::conv_tune_stats(m, t);
+    *measured = static_cast<int64_t>(m);
+    *from_table = static_cast<int64_t>(t);
+    return ENGINE_OK;
 }
 
 }  // extern "C"

@@ -196,8 +196,10 @@ Session::~Session() {
     }
     for (hipStream_t s : side_streams_) (void)hipStreamDestroy(s);
     if (stream_) (void)hipStreamDestroy(stream_);
-    if (dev_px_) (void)hipFree(dev_px_);
-    if (host_px_) (void)hipHostFree(host_px_);
+    for (StagedInput& st : staged_) {
+        if (st.dev_px) (void)hipFree(st.dev_px);
+        if (st.host_px) (void)hipHostFree(st.host_px);
+    }
     if (dec_ws_) (void)hipFree(dec_ws_);
     if (dec_host_) (void)hipHostFree(dec_host_);
 }
@@ -319,16 +321,16 @@ std::vector<LetterboxGeometry> Session::set_images(int32_t idx, const std::vecto
     }
     // the previous run's upload has finished reading the pinned staging
     if (stream_) PDEFA_HIP(hipStreamSynchronize(stream_));
-    if (total > host_px_cap_) {
-        if (host_px_) (void)hipHostFree(host_px_);
-        host_px_ = nullptr;
-        host_px_cap_ = 0;
-        PDEFA_HIP(hipHostMalloc(reinterpret_cast<void**>(&host_px_), total, hipHostMallocDefault));
-        host_px_cap_ = total;
-    }
     if (staged_.size() < inputs_.size()) staged_.resize(inputs_.size());
     StagedInput& st = staged_[idx];
     st.images.clear();
+    if (total > st.host_cap) {
+        if (st.host_px) (void)hipHostFree(st.host_px);
+        st.host_px = nullptr;
+        st.host_cap = 0;
+        PDEFA_HIP(hipHostMalloc(reinterpret_cast<void**>(&st.host_px), total, hipHostMallocDefault));
+        st.host_cap = total;
+    }
     st.tw = tw;
     st.th = th;
     st.scale = scale;
@@ -337,7 +339,7 @@ std::vector<LetterboxGeometry> Session::set_images(int32_t idx, const std::vecto
     size_t off = 0;
     for (const ImageRef& im : images) {
         const size_t n = static_cast<size_t>(im.width) * im.height * im.channels;
-        std::memcpy(host_px_ + off, im.pixels, n);
+        std::memcpy(st.host_px + off, im.pixels, n);
         StagedImage si;
         si.offset = off;
         si.img = im;
@@ -718,23 +720,23 @@ void Session::upload_inputs() {
     for (size_t i = 0; i < inputs_.size(); ++i) {
         float* dst = prep_->arena + plan.bufs.at(plan.input_bufs[i]).offset;
         if (i < staged_.size() && !staged_[i].images.empty()) {
-            const StagedInput& st = staged_[i];
+            StagedInput& st = staged_[i];
             const StagedImage& last = st.images.back();
             const size_t bytes = last.offset + static_cast<size_t>(last.img.width) * last.img.height * last.img.channels;
-            if (bytes > dev_px_cap_) {
+            if (bytes > st.dev_cap) {
                 PDEFA_HIP(hipStreamSynchronize(stream_));
-                if (dev_px_) (void)hipFree(dev_px_);
-                dev_px_ = nullptr;
-                dev_px_cap_ = 0;
-                PDEFA_HIP(hipMalloc(reinterpret_cast<void**>(&dev_px_), bytes));
-                dev_px_cap_ = bytes;
+                if (st.dev_px) (void)hipFree(st.dev_px);
+                st.dev_px = nullptr;
+                st.dev_cap = 0;
+                PDEFA_HIP(hipMalloc(reinterpret_cast<void**>(&st.dev_px), bytes));
+                st.dev_cap = bytes;
             }
-            PDEFA_HIP(hipMemcpyAsync(dev_px_, host_px_, bytes, hipMemcpyHostToDevice, stream_));
+            PDEFA_HIP(hipMemcpyAsync(st.dev_px, st.host_px, bytes, hipMemcpyHostToDevice, stream_));
             const size_t plane = static_cast<size_t>(st.tw) * st.th;
             for (size_t b = 0; b < st.images.size(); ++b) {
                 const StagedImage& si = st.images[b];
                 k::LetterboxArgs la;
-                la.src = dev_px_ + si.offset;
+                la.src = st.dev_px + si.offset;
                 la.w = si.img.width;
                 la.h = si.img.height;
                 la.ch = si.img.channels;

@@ -145,13 +145,19 @@ class Session {
     // device buffer they are uploaded to, and per image its geometry.
     struct StagedImage {
         size_t offset = 0;
-        ImageRef img;  // pixels unused (they live in host_px_ at offset)
+        ImageRef img;  // pixels unused (they live in the input's host_px at offset)
         LetterboxGeometry g;
     };
+    // Each input has its own staging buffers (grow-only), so that images
+    // staged for one input never overwrite another's.
     struct StagedInput {
         std::vector<StagedImage> images;
         int32_t tw = 0, th = 0;
         float scale = 1.0f, pad = 0.0f;
+        uint8_t* host_px = nullptr;  // pinned
+        size_t host_cap = 0;
+        uint8_t* dev_px = nullptr;
+        size_t dev_cap = 0;
     };
     std::vector<StagedInput> staged_;  // per input; empty images = host tensor input
     // decode workspace (device, grow-only) and its pinned result staging
@@ -159,10 +165,6 @@ class Session {
     size_t dec_ws_bytes_ = 0;
     void* dec_host_ = nullptr;
     size_t dec_host_bytes_ = 0;
-    uint8_t* host_px_ = nullptr;       // pinned
-    size_t host_px_cap_ = 0;
-    uint8_t* dev_px_ = nullptr;
-    size_t dev_px_cap_ = 0;
 
     Model* model_;
     std::shared_ptr<DeviceModel> dev_;

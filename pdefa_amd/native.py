@@ -70,6 +70,7 @@ def lib() -> C.CDLL:
                                                        C.POINTER(i64), i32, C.POINTER(i32)]),
             "pdefa_amd_plan_model": (C.c_int, [vp, C.POINTER(i64), i32, C.c_char_p, sz, C.POINTER(sz)]),
             "pdefa_amd_device_name": (C.c_char_p, []),
+            "pdefa_amd_tune_stats": (C.c_int, [C.POINTER(i64), C.POINTER(i64)]),
         }
         for name, (res, args) in sig.items():
             f = getattr(L, name)
@@ -195,6 +196,14 @@ class Engine:
             pass
 
 
+def tune_stats():
+    """(measured, from_table): conv launch-shape choices of this process
+    timed on the device, and read from the launch-shape table."""
+    m, t = C.c_int64(), C.c_int64()
+    check(lib().pdefa_amd_tune_stats(C.byref(m), C.byref(t)), "pdefa_amd_tune_stats")
+    return m.value, t.value
+
+
 def plan_text(path: str, shape: Sequence[int]) -> str:
     """Device program for `path` at input `shape`, planned on the host."""
     L = lib()
@@ -212,6 +221,21 @@ def plan_text(path: str, shape: Sequence[int]) -> str:
         if model:
             L.engine_model_destroy(model)
         L.engine_context_destroy(ctx)
+
+
+def matmul_into(a: np.ndarray, b: np.ndarray, out: np.ndarray) -> np.ndarray:
+    """engine_ops_matmul(a, b, out) with `out` a pre-filled tensor of any
+    shape; returns what the call left in it (the call returns ENGINE_OK also
+    when it leaves `out` untouched for mismatched shapes, as the reference's
+    ops::matmul does)."""
+    L = lib()
+    ha, hb, hc = tensor_from_numpy(a), tensor_from_numpy(b), tensor_from_numpy(out)
+    try:
+        check(L.engine_ops_matmul(ha, hb, hc), "engine_ops_matmul")
+        return tensor_to_numpy(hc)
+    finally:
+        for h in (ha, hb, hc):
+            L.engine_tensor_destroy(h)
 
 
 def matmul(a: np.ndarray, b: np.ndarray) -> np.ndarray:

@@ -141,14 +141,20 @@ class _Yolo:
         return self.b.node("Resize", f"/{name}/Resize", [x, sc])
 
 
-# Class-head bias per scale: the spread of the random-weight class logits
-# grows with model width, so wider models need a lower bias for a few to a
-# hundred candidates above 0.25 on the synthetic images.
-CLS_BIAS = {"n": -6.0, "s": -6.0, "m": -7.75, "l": -7.75, "x": -7.75}
+# Class-head gain and bias per scale.  The random-weight class logits of
+# the unscaled head are tightly clustered (spread ~0.01), so the gain spreads
+# them out: at 300 the best-class scores of the synthetic images are sparse
+# enough above 0.25 that thresholds with no score within 1e-2 exist (a parity
+# test's detection lists then cannot flip on a tolerance-sized difference);
+# the bias puts 15 to 150 candidates above 0.25 on each synthetic image (the
+# spread of the logits grows with model width, hence a lower bias for wider
+# models).
+CLS_GAIN = 300.0
+CLS_BIAS = {"n": -50.0, "s": -50.0, "m": -66.0, "l": -66.0, "x": -66.0}
 
 
 def build_yolov8(scale: str = "n", seed: int = 0, nc: int = 80, imgsz: int = 640,
-                 cls_bias: Optional[float] = None, cls_gain: float = 30.0) -> EngineModel:
+                 cls_bias: Optional[float] = None, cls_gain: float = CLS_GAIN) -> EngineModel:
     """YOLOv8{scale} detection graph with seeded random weights (BN folded).
 
     The class head's last conv has its Kaiming weights scaled by cls_gain and
@@ -357,7 +363,10 @@ def letterbox(img: np.ndarray, target_w: int = 640, target_h: int = 640,
     scaled size = clamp(round(src*ratio), 1, target), centred pads (integer
     halves), sample positions s = d * (1/ratio) truncated to int, x0/y0
     clamped to src-2, bilinear weights with the scale folded into the row
-    weights, and the pad value written raw (not scaled).
+    weights, and the pad value written raw (not scaled).  The blend rounds as
+    the reference's own build computes it (imageloader/CMakeLists.txt:41
+    compiles with -mfma and GCC contracts (p00 w0 + p10 w1) into
+    fma(p00, w0, p10 w1), and so on).
     Returns (tensor, meta dict)."""
     h, w = img.shape[:2]
     ch = 1 if img.ndim == 2 else img.shape[2]
@@ -390,11 +399,19 @@ def letterbox(img: np.ndarray, target_w: int = 640, target_h: int = 640,
     w1 = fx[None, :]
     src = img.astype(np.float32)
     chans = [0, 0, 0] if ch == 1 else [0, 1, 2]
+
+    def fma(a, b, c):
+        # one rounding of a * b + c: the exact value fits the 64-bit
+        # significand of long double for these operands (8-bit pixels and
+        # float32 weights)
+        return (a.astype(np.longdouble) * b + c).astype(np.float32)
+
     for c in range(3):
         p = src[:, :, chans[c]]
-        r0 = p[y0][:, x0] * w0 + p[y0][:, x1] * w1
-        r1 = p[y1][:, x0] * w0 + p[y1][:, x1] * w1
-        out[c, py:py + sh, px:px + sw] = r0 * wy0 + r1 * wy1
+        # the reference's GCC build computes a * b + c * d as fma(a, b, c * d)
+        r0 = fma(p[y0][:, x0], w0, (p[y0][:, x1] * w1).astype(np.float32))
+        r1 = fma(p[y1][:, x0], w0, (p[y1][:, x1] * w1).astype(np.float32))
+        out[c, py:py + sh, px:px + sw] = fma(r0, wy0, (r1 * wy1).astype(np.float32))
     meta = dict(target_w=target_w, target_h=target_h, orig_w=w, orig_h=h, pad_x=px,
                 pad_y=py, scaled_w=sw, scaled_h=sh, ratio=float(ratio))
     return out[None], meta

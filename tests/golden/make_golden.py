@@ -64,12 +64,17 @@ def yolo_case(tmp, scale, seed, batch_index=0, imgsz=640):
     x, metas = ys.yolo_inputs(batch_index + 1, imgsz=imgsz)
     x = x[batch_index:batch_index + 1]
     out = ref_lib.RefSession(path).run(x)[0]
-    dets = decode_ref.decode(out.tolist(), metas[batch_index])
-    scores = np.sort(out[0, 4:].max(axis=0))
+    # a conf_thres with no best-class score within 1e-2 of it, so that outputs
+    # within the parity tolerance select the same candidates
+    conf, gap = decode_ref.robust_conf(out)
+    if conf is None:
+        raise SystemExit(f"yolov8{scale} image {batch_index}: no conf_thres with a 1e-2 score gap")
+    dets = decode_ref.decode(out.tolist(), metas[batch_index], conf)
     return {"scale": scale, "weight_seed": seed, "image_index": batch_index, "imgsz": imgsz,
             "engine_sha256": file_sha(path), "input_sha256": sha(x.tobytes()), "meta": metas[batch_index],
             "shape": list(out.shape), "samples": samples(out), "channel_means": channel_means(out),
-            "min_score_gap_to_threshold": float(np.abs(scores - 0.25).min()),
+            "conf_thres": conf, "iou_thres": 0.45, "min_score_gap_to_threshold": gap,
+            "min_iou_gap_to_threshold": decode_ref.min_iou_gap(out.tolist(), metas[batch_index], conf),
             "detections": dets}
 
 

@@ -12,6 +12,8 @@ Differences, all from what this build ships:
 """
 import re
 
+import os
+
 import numpy as np
 import pytest
 
@@ -406,6 +408,30 @@ def test_device_letterbox_bit_exact(tmp_path, tw, th):
     s.set_input(0, host[0][0])
     s.run()
     np.testing.assert_array_equal(s.output(0).to_numpy(), host[0][0].to_numpy())
+
+
+@pytest.mark.gpu
+def test_device_letterbox_matches_reference_fixture(tmp_path):
+    """The device letterbox of the synthetic 1280x720 image (seed 0) hashes
+    to the reference's pdefa_preprocess_letterbox output recorded in
+    tests/golden/letterbox_1280x720.json (imageloader/src/preprocess.cpp:15-144),
+    and its meta equals the recorded one."""
+    import hashlib
+    import json
+    with open(os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "letterbox_1280x720.json")) as f:
+        g = json.load(f)
+    raw = ys.synth_image(0, 1280, 720)
+    assert hashlib.sha256(raw.tobytes()).hexdigest() == g["image_sha256"]
+    ctx = pdefa.Context()
+    model = pdefa.Model(ctx, _identity_engine(tmp_path))
+    s = pdefa.Session(ctx, model)
+    metas = s.set_images(0, [pdefa.Image.from_array(raw)], 640, 640, 1 / 255, 114 / 255)
+    s.run()
+    got = np.ascontiguousarray(s.output(0).to_numpy(), np.float32)
+    assert hashlib.sha256(got.tobytes()).hexdigest() == g["output_sha256"]
+    for k in ("pad_x", "pad_y", "scaled_w", "scaled_h"):
+        assert getattr(metas[0], k) == g["meta"][k]
+    assert metas[0].ratio == np.float32(g["meta"]["ratio"])
 
 
 @pytest.mark.gpu

@@ -35,7 +35,7 @@ engine_ops_concat engine_ops_stack engine_random_randn engine_random_rand
 EXTENSIONS = ["pdefa_amd_session_replay", "pdefa_amd_session_step_times", "pdefa_amd_session_step_repeat",
               "pdefa_amd_session_plan", "pdefa_amd_session_set_images", "pdefa_amd_image_from_pixels",
               "pdefa_amd_session_decode",
-              "pdefa_amd_plan_model", "pdefa_amd_device_name"]
+              "pdefa_amd_plan_model", "pdefa_amd_device_name", "pdefa_amd_tune_stats"]
 
 
 def test_def_list_complete():
@@ -276,3 +276,22 @@ def test_engine_file_roundtrip_and_reference_parse(tmp_path):
     if ref_lib.available():
         r = ref_lib.RefSession(path)  # the reference loader parses the same bytes
         r.close()
+
+
+@pytest.mark.parametrize("a_shape,b_shape,out_shape", [
+    ((4, 5), (6, 3), (4, 3)),          # inner dimensions differ
+    ((4, 5), (5, 3), (4, 4)),          # out has the wrong shape
+    ((4, 5), (5, 3), (12,)),           # out is 1-D
+    ((2, 4, 5), (2, 6, 3), (2, 4, 3)),  # batched, inner dimensions differ
+    ((2, 4, 5), (5, 3), (4, 3)),       # batched, out too small for the batch
+])
+def test_matmul_shape_mismatch_is_a_silent_no_op(a_shape, b_shape, out_shape):
+    """engine_ops_matmul with mismatched shapes returns ENGINE_OK and leaves
+    `out` untouched (PDEFA1.0/src/ops/matmul.cpp:59-66,113-126); the checks
+    come before any device work, so this runs without a GPU."""
+    rng = np.random.default_rng(1)
+    a = rng.standard_normal(a_shape).astype(np.float32)
+    b = rng.standard_normal(b_shape).astype(np.float32)
+    sentinel = np.full(out_shape, -7.25, np.float32)
+    got = native.matmul_into(a, b, sentinel)
+    np.testing.assert_array_equal(got, sentinel)

@@ -1,9 +1,21 @@
-"""GPU parity: the HIP path through the C ABI against the oracle.
+"""GPU parity: the HIP path through the C ABI against the reference engine
+(compiled from its own sources, oracle/_ref, run on the host) and the float64
+oracle.
 
-Tolerance: every output element satisfies
-|gpu - ref| <= 1e-3 + 1e-3 * |ref| (numpy allclose with atol = rtol = 1e-3),
-and the post-NMS detection lists are identical (same anchors, classes and
-order; coordinates and scores within the same tolerance).
+Tolerance: every output element within max abs err 1e-3 AND max rel err
+1e-3, checked separately (relative error over every element whose reference
+value is a normal float, |ref| >= FLT_MIN); post-NMS detection lists
+identical (same anchors, classes and order; coordinates and scores within
+the same bounds), at a conf_thres with no best-class score within 1e-2 of it.
+
+The reference's Winograd-layer SiLU jumps by ~2% of |x| where -x log2 e
+crosses a half-integer, so an fp32 conv whose rounding lands on the other
+side of a jump than the reference's moves that activation, and what follows
+from it, beyond the tolerance.  Launch shapes come from the launch-shape
+table (every process plans the same launches and computes the same bits),
+so where this happens it happens reproducibly: each test lists the anchors
+(or elements) where it does, and each listed one must match the oracle
+evaluated with its near-jump activations on the other side.
 """
 import os
 import re
@@ -11,14 +23,92 @@ import re
 import numpy as np
 import pytest
 
-from oracle import decode_ref, graph_ref
+from oracle import decode_ref, graph_ref, ref_lib
 from pdefa_amd import native, yolo_synth as ys
 from pdefa_amd.postprocess import decode_yolo
 
 ATOL = 1e-3
 RTOL = 1e-3
+FLT_MIN = float(np.finfo(np.float32).tiny)
 
 pytestmark = pytest.mark.gpu
+
+
+def errors(got, want):
+    """(max abs err over all elements, max rel err over elements with
+    |want| >= FLT_MIN, mask of elements over either bound)."""
+    g = got.astype(np.float64)
+    w = want.astype(np.float64)
+    err = np.abs(g - w)
+    normal = np.abs(w) >= FLT_MIN
+    rel = np.where(normal, err / np.where(normal, np.abs(w), 1.0), 0.0)
+    bad = (err > ATOL) | (rel > RTOL)
+    return float(err.max(initial=0.0)), float(rel.max(initial=0.0)), bad
+
+
+def reference_outputs(path, x):
+    """The reference engine's output for each image of x (it has no batch
+    path: BatchInference runs one session per image), stacked."""
+    if not ref_lib.available():
+        pytest.fail("oracle/_ref/libpdefa_ref.so is missing: build it with __graft_entry__.build()")
+    ref_lib.set_threads(min(16, os.cpu_count() or 1))
+    r = ref_lib.RefSession(path)
+    try:
+        return np.concatenate([r.run(x[i:i + 1])[0] for i in range(x.shape[0])], axis=0)
+    finally:
+        r.close()
+
+
+def assert_matches_reference(got, want, what, model=None, x=None, jump_anchors=()):
+    """Every element of `got` within ATOL and RTOL of the reference output
+    `want`, except for the listed (image, anchor) pairs of a [N, C, A] head,
+    which must each hold an element out of bounds and must match the oracle
+    with its near-jump compat-SiLU activations on the other side."""
+    assert got.shape == want.shape, (what, got.shape, want.shape)
+    assert np.isfinite(got).all(), f"{what}: non-finite values"
+    mx_abs, mx_rel, bad = errors(got, want)
+    listed = sorted(tuple(a) for a in jump_anchors)
+    if got.ndim == 3:
+        where = sorted({(int(n), int(a)) for n, _, a in zip(*np.nonzero(bad))})
+        ok = ~bad
+        for n, a in listed:
+            ok[n, :, a] = True
+        o_abs, o_rel, _ = errors(np.where(ok, got, 0), np.where(ok, want, 0))
+        print(f"{what}: max abs err {o_abs:.3e}, max rel err {o_rel:.3e} (all elements: {mx_abs:.3e}, "
+              f"{mx_rel:.3e}); out of bounds at (image, anchor) {where}", flush=True)
+        assert where == listed, (f"{what}: elements out of bounds at (image, anchor) {where}, listed {listed}; "
+                                 f"max abs err {mx_abs:.3e}, max rel err {mx_rel:.3e}")
+        if listed:
+            for n, a in listed:
+                alt = graph_ref.run_graph(model, [x[n:n + 1]], flip=lambda name: True, flip_tol=1e-5)[0]
+                a_abs, a_rel, _ = errors(got[n:n + 1, :, a], alt[0:1, :, a])
+                assert a_abs <= ATOL and a_rel <= RTOL, (f"{what}: image {n} anchor {a} is not explained by "
+                                                         f"the SiLU jumps (abs {a_abs:.3e}, rel {a_rel:.3e})")
+    else:
+        print(f"{what}: max abs err {mx_abs:.3e}, max rel err {mx_rel:.3e}", flush=True)
+        assert not bad.any(), (f"{what}: {int(bad.sum())} elements out of bounds, max abs err {mx_abs:.3e}, "
+                               f"max rel err {mx_rel:.3e}")
+    return mx_abs, mx_rel
+
+
+def assert_same_detections_as_reference(got, want, meta, what, conf=None, iou=0.45):
+    """decode_yolo of the GPU output equals the oracle's restatement of the
+    reference decode on the reference output, at a conf_thres with a 1e-2
+    score margin (found on the reference output when not given): same
+    anchors, classes and order, box corners within 1e-3 pixels, scores
+    within abs and rel 1e-3."""
+    if conf is None:
+        conf, gap = decode_ref.robust_conf(want)
+        assert conf is not None, f"{what}: no conf_thres with a 1e-2 score margin"
+    dg = decode_yolo(got, meta, conf_thres=conf, iou_thres=iou, with_anchor=True)
+    dw = decode_ref.decode(want.tolist(), meta, conf, iou)
+    assert [(d["anchor"], d["cls"]) for d in dg] == [(d["anchor"], d["cls"]) for d in dw], what
+    for a, b in zip(dg, dw):
+        for k in ("x1", "y1", "x2", "y2"):
+            assert abs(a[k] - b[k]) <= ATOL, (what, k, a, b)
+        assert abs(a["conf"] - b["conf"]) <= ATOL and abs(a["conf"] - b["conf"]) <= RTOL * b["conf"], (what, a, b)
+    print(f"{what}: {len(dg)} detections identical at conf_thres {conf}", flush=True)
+    return dg
 
 
 def assert_close(got, want, what):
@@ -467,6 +557,20 @@ def test_matmul_shapes(m, k, n):
     b = rng.standard_normal((k, n), dtype=np.float32)
     c = native.matmul(a, b)
     assert_close(c, (a.astype(np.float64) @ b.astype(np.float64)).astype(np.float32), "sgemm")
+
+
+@pytest.mark.parametrize("a_shape,b_shape", [((3, 37, 64), (3, 64, 29)), ((2, 2, 50, 33), (33, 70)),
+                                             ((4, 1, 8), (4, 8, 1))])
+def test_matmul_batched(a_shape, b_shape):
+    """Batched ops_matmul: [..., M, K] x [..., K, N], or a 2-D B shared by
+    every batch (PDEFA1.0/src/ops/matmul.cpp:59-101), against float64."""
+    print(f"[case] batched ops_matmul {a_shape} x {b_shape}", flush=True)
+    rng = np.random.default_rng(sum(a_shape))
+    a = rng.standard_normal(a_shape, dtype=np.float32)
+    b = rng.standard_normal(b_shape, dtype=np.float32)
+    out = native.matmul_into(a, b, np.zeros(a_shape[:-1] + (b_shape[-1],), np.float32))
+    want = np.matmul(a.astype(np.float64), b.astype(np.float64))
+    assert_close(out, want.astype(np.float32), "batched sgemm")
 
 
 def test_graph_and_eager_agree(tmp_path, monkeypatch):
