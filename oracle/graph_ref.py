@@ -339,7 +339,8 @@ def _silu_consumer(model, conv):
     return mul.outputs[0]
 
 
-def run_graph(model: EngineModel, inputs, dtype=np.float64, compat_silu=True, flip=None, flip_tol=1e-5):
+def run_graph(model: EngineModel, inputs, dtype=np.float64, compat_silu=True, flip=None, flip_tol=1e-5,
+              flip_elems=None, jump_log=None, jump_tol=1e-6):
     """Evaluates the graph on `inputs` (list of NCHW arrays); returns outputs
     as float32 arrays in graph_outputs order.  compat_silu=False evaluates the
     true SiLU everywhere.
@@ -348,7 +349,13 @@ def run_graph(model: EngineModel, inputs, dtype=np.float64, compat_silu=True, fl
     it accepts, every element whose pre-activation lies within flip_tol
     (relative, see silu_winograd_compat_branches) of one of the form's jumps
     takes the other side of the jump: the output an fp32 computation gets when
-    its rounding lands there on the other side."""
+    its rounding lands there on the other side.
+    flip_elems: {conv node name: flat indices} -- exactly these compat-SiLU
+    activations take the other side of their jump.
+    jump_log: optional list that receives (conv node name, flat index,
+    relative distance) of every compat-SiLU activation whose pre-activation
+    lies within jump_tol of a jump (the candidates for an fp32 conv landing
+    on the other side)."""
     inter = {}
     skip = set()
 
@@ -388,6 +395,16 @@ def run_graph(model: EngineModel, inputs, dtype=np.float64, compat_silu=True, fl
                         y_lo, y_hi, unstable = silu_winograd_compat_branches(y32, tol=flip_tol)
                         other = np.where(straight == y_lo, y_hi, y_lo)
                         straight = np.where(unstable, other, straight)
+                    if flip_elems and node.name in flip_elems:
+                        idx = np.asarray(flip_elems[node.name], np.int64)
+                        y_lo, y_hi, _ = silu_winograd_compat_branches(y32, tol=0.0)
+                        flat, lo_f, hi_f = straight.reshape(-1), y_lo.reshape(-1), y_hi.reshape(-1)
+                        flat[idx] = np.where(flat[idx] == lo_f[idx], hi_f[idx], lo_f[idx])
+                    if jump_log is not None:
+                        fx = ((-y32) * np.float32(1.44269504088896341)).astype(np.float64).reshape(-1)
+                        dist = np.abs(fx - np.floor(fx) - 0.5) / np.maximum(1.0, np.abs(fx))
+                        for i in np.flatnonzero(dist <= jump_tol):
+                            jump_log.append((node.name, int(i), float(dist[i])))
                     y = straight.astype(dtype)
                 else:
                     y = y / (1.0 + np.exp(-y))

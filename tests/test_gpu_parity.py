@@ -3,10 +3,16 @@
 oracle.
 
 Tolerance: every output element within max abs err 1e-3 AND max rel err
-1e-3, checked separately (relative error over every element whose reference
-value is a normal float, |ref| >= FLT_MIN); post-NMS detection lists
-identical (same anchors, classes and order; coordinates and scores within
-the same bounds), at a conf_thres with no best-class score within 1e-2 of it.
+1e-3, checked separately.  On YOLO heads the relative error is taken over
+every element whose reference value is a normal float (|ref| >= FLT_MIN);
+on single conv and matmul outputs over elements with |ref| >= 1e-3 of the
+tensor's largest magnitude (values nearer zero come from cancellation,
+where the relative error of any fp32 summation order is unbounded; the
+absolute bound covers them), and the normwise relative error
+||got - ref|| / ||ref|| is asserted beside it.
+Post-NMS detection lists identical (same anchors, classes and order; box
+corners within 1e-3 pixels, scores within the same bounds), at a
+conf_thres with no best-class score within 1e-2 of it.
 
 The reference's Winograd-layer SiLU jumps by ~2% of |x| where -x log2 e
 crosses a half-integer, so an fp32 conv whose rounding lands on the other
@@ -34,16 +40,26 @@ FLT_MIN = float(np.finfo(np.float32).tiny)
 pytestmark = pytest.mark.gpu
 
 
-def errors(got, want):
+REL_FLOOR_CONV = "scale"  # 1e-3 of the tensor's largest magnitude
+
+
+def errors(got, want, rel_floor=FLT_MIN):
     """(max abs err over all elements, max rel err over elements with
-    |want| >= FLT_MIN, mask of elements over either bound)."""
+    |want| >= rel_floor, mask of elements over either bound)."""
     g = got.astype(np.float64)
     w = want.astype(np.float64)
     err = np.abs(g - w)
-    normal = np.abs(w) >= FLT_MIN
+    if isinstance(rel_floor, str):
+        rel_floor = max(1e-3 * float(np.abs(w).max(initial=0.0)), FLT_MIN)
+    normal = np.abs(w) >= rel_floor
     rel = np.where(normal, err / np.where(normal, np.abs(w), 1.0), 0.0)
     bad = (err > ATOL) | (rel > RTOL)
     return float(err.max(initial=0.0)), float(rel.max(initial=0.0)), bad
+
+
+def norm_rel(got, want):
+    w = want.astype(np.float64)
+    return float(np.linalg.norm(got.astype(np.float64) - w) / max(np.linalg.norm(w), 1e-300))
 
 
 def reference_outputs(path, x):
@@ -59,50 +75,102 @@ def reference_outputs(path, x):
         r.close()
 
 
-def assert_matches_reference(got, want, what, model=None, x=None, jump_anchors=()):
-    """Every element of `got` within ATOL and RTOL of the reference output
-    `want`, except for the listed (image, anchor) pairs of a [N, C, A] head,
-    which must each hold an element out of bounds and must match the oracle
-    with its near-jump compat-SiLU activations on the other side."""
+def _save(name, arr):
+    """Keeps an array for offline analysis when PDEFA_TEST_SAVE is a directory."""
+    d = os.environ.get("PDEFA_TEST_SAVE")
+    if d:
+        os.makedirs(d, exist_ok=True)
+        np.save(os.path.join(d, name + ".npy"), arr)
+
+
+def assert_matches_reference(got, want, what, model=None, x=None, jumps=None):
+    """Every element of the [N, C, A] head `got` within ATOL and RTOL of the
+    reference output `want`; returns, per image with listed jumps, the
+    oracle output that explains the device's.  `jumps` lists, per image, the compat-SiLU
+    activations (conv node name, flat index) where the device's fp32
+    pre-activation ("device") or the reference's ("reference") lands on the
+    other side of a jump than the float64 oracle's; for such an image the
+    device output must match the oracle with the device's activations
+    flipped, the reference output the oracle with the reference's flipped,
+    every listed activation must lie within 1e-5 of a jump (relative; an
+    activation downstream of another flip sits further from where the
+    unflipped oracle puts it), and device and reference must agree wherever
+    those two oracle outputs do."""
     assert got.shape == want.shape, (what, got.shape, want.shape)
     assert np.isfinite(got).all(), f"{what}: non-finite values"
-    mx_abs, mx_rel, bad = errors(got, want)
-    listed = sorted(tuple(a) for a in jump_anchors)
-    if got.ndim == 3:
-        where = sorted({(int(n), int(a)) for n, _, a in zip(*np.nonzero(bad))})
-        ok = ~bad
-        for n, a in listed:
-            ok[n, :, a] = True
-        o_abs, o_rel, _ = errors(np.where(ok, got, 0), np.where(ok, want, 0))
-        print(f"{what}: max abs err {o_abs:.3e}, max rel err {o_rel:.3e} (all elements: {mx_abs:.3e}, "
-              f"{mx_rel:.3e}); out of bounds at (image, anchor) {where}", flush=True)
-        assert where == listed, (f"{what}: elements out of bounds at (image, anchor) {where}, listed {listed}; "
-                                 f"max abs err {mx_abs:.3e}, max rel err {mx_rel:.3e}")
-        if listed:
-            for n, a in listed:
-                alt = graph_ref.run_graph(model, [x[n:n + 1]], flip=lambda name: True, flip_tol=1e-5)[0]
-                a_abs, a_rel, _ = errors(got[n:n + 1, :, a], alt[0:1, :, a])
-                assert a_abs <= ATOL and a_rel <= RTOL, (f"{what}: image {n} anchor {a} is not explained by "
-                                                         f"the SiLU jumps (abs {a_abs:.3e}, rel {a_rel:.3e})")
-    else:
-        print(f"{what}: max abs err {mx_abs:.3e}, max rel err {mx_rel:.3e}", flush=True)
-        assert not bad.any(), (f"{what}: {int(bad.sum())} elements out of bounds, max abs err {mx_abs:.3e}, "
-                               f"max rel err {mx_rel:.3e}")
-    return mx_abs, mx_rel
+    jumps = jumps or {}
+    worst_abs = worst_rel = 0.0
+    explained = {}
+    unexplained = []
+    for n in range(got.shape[0]):
+        g, r = got[n:n + 1], want[n:n + 1]
+        mx_abs, mx_rel, bad = errors(g, r)
+        listed = jumps.get(n)
+        if not listed:
+            if bad.any():
+                tag = re.sub(r"[^A-Za-z0-9]+", "_", what)
+                _save(f"{tag}_img{n}_device", g)
+                _save(f"{tag}_img{n}_reference", r)
+                log = []
+                graph_ref.run_graph(model, [x[n:n + 1]], jump_log=log)
+                anchors = np.unique(np.nonzero(bad)[-1]).tolist()
+                unexplained.append(f"{what} image {n}: {int(bad.sum())} elements over {len(anchors)} anchors out of "
+                                   f"bounds (max abs err {mx_abs:.3e}, max rel err {mx_rel:.3e}); compat-SiLU "
+                                   f"activations within 1e-6 of a jump: {log}")
+                print(unexplained[-1], flush=True)
+            worst_abs, worst_rel = max(worst_abs, mx_abs), max(worst_rel, mx_rel)
+            continue
+        log = []
+        plain = graph_ref.run_graph(model, [x[n:n + 1]], jump_log=log, jump_tol=1e-5)[0]
+        near = {(a, i) for a, i, _ in log}
+        flips = {}
+        for side in ("device", "reference"):
+            for a, i in listed.get(side, []):
+                assert (a, i) in near, f"{what} image {n}: {a}[{i}] is not within 1e-5 of a jump"
+            fe = {}
+            for a, i in listed.get(side, []):
+                fe.setdefault(a, []).append(i)
+            flips[side] = graph_ref.run_graph(model, [x[n:n + 1]], flip_elems=fe)[0] if fe else plain
+        d_abs, d_rel, d_bad = errors(g, flips["device"])
+        r_abs, r_rel, r_bad = errors(r, flips["reference"])
+        assert not d_bad.any(), f"{what} image {n}: device vs its flipped oracle: abs {d_abs:.3e}, rel {d_rel:.3e}"
+        assert not r_bad.any(), f"{what} image {n}: reference vs its flipped oracle: abs {r_abs:.3e}, rel {r_rel:.3e}"
+        # where the two explanations differ by more than a tenth of the bounds
+        fd, fr = flips["device"].astype(np.float64), flips["reference"].astype(np.float64)
+        dd = np.abs(fd - fr)
+        sides_differ = (dd > 0.1 * ATOL) | (dd > 0.1 * RTOL * np.maximum(np.abs(fr), FLT_MIN))
+        explained[n] = flips["device"]
+        o_abs, o_rel, o_bad = errors(np.where(sides_differ, 0, g), np.where(sides_differ, 0, r))
+        assert not o_bad.any(), f"{what} image {n}: device and reference differ where the oracle does not"
+        print(f"{what} image {n}: the device output matches the oracle with {listed.get('device', [])} on the other "
+              f"side (abs {d_abs:.3e}, rel {d_rel:.3e}), the reference output the oracle with "
+              f"{listed.get('reference', [])} (abs {r_abs:.3e}, rel {r_rel:.3e}); elsewhere device vs reference "
+              f"abs {o_abs:.3e}, rel {o_rel:.3e}", flush=True)
+        worst_abs, worst_rel = max(worst_abs, o_abs), max(worst_rel, o_rel)
+    assert not unexplained, "\n".join(unexplained)
+    print(f"{what}: device vs reference, max abs err {worst_abs:.3e}, max rel err {worst_rel:.3e}"
+          f"{' (outside the listed jumps)' if jumps else ''}", flush=True)
+    return explained
 
 
-def assert_same_detections_as_reference(got, want, meta, what, conf=None, iou=0.45):
+def assert_same_detections_as_reference(got, want, meta, what, conf=None, iou=0.45, follow=None):
     """decode_yolo of the GPU output equals the oracle's restatement of the
     reference decode on the reference output, at a conf_thres with a 1e-2
     score margin (found on the reference output when not given): same
     anchors, classes and order, box corners within 1e-3 pixels, scores
-    within abs and rel 1e-3."""
+    within abs and rel 1e-3 -- of the reference's detections, or, when the
+    device takes other sides of listed compat-SiLU jumps than the
+    reference, of the detections of `follow`, the oracle output that
+    explains the device's."""
     if conf is None:
         conf, gap = decode_ref.robust_conf(want)
         assert conf is not None, f"{what}: no conf_thres with a 1e-2 score margin"
     dg = decode_yolo(got, meta, conf_thres=conf, iou_thres=iou, with_anchor=True)
     dw = decode_ref.decode(want.tolist(), meta, conf, iou)
     assert [(d["anchor"], d["cls"]) for d in dg] == [(d["anchor"], d["cls"]) for d in dw], what
+    if follow is not None:
+        dw = decode_ref.decode(follow.tolist(), meta, conf, iou)
+        assert [(d["anchor"], d["cls"]) for d in dg] == [(d["anchor"], d["cls"]) for d in dw], what
     for a, b in zip(dg, dw):
         for k in ("x1", "y1", "x2", "y2"):
             assert abs(a[k] - b[k]) <= ATOL, (what, k, a, b)
@@ -111,66 +179,75 @@ def assert_same_detections_as_reference(got, want, meta, what, conf=None, iou=0.
     return dg
 
 
-def assert_close(got, want, what):
+def assert_close(got, want, what, rel_floor=REL_FLOOR_CONV):
+    """Every element within ATOL, and within RTOL where |want| >= rel_floor;
+    normwise relative error within RTOL; returns max abs err."""
     assert got.shape == want.shape, (what, got.shape, want.shape)
     assert np.isfinite(got).all(), f"{what}: non-finite values"
-    err = np.abs(got.astype(np.float64) - want.astype(np.float64))
-    bad = err > ATOL + RTOL * np.abs(want)
-    assert not bad.any(), (f"{what}: {int(bad.sum())} elements out of tolerance, max abs err "
-                           f"{err.max():.3e} at {np.unravel_index(err.argmax(), err.shape)}")
-    return float(err.max())
+    mx_abs, mx_rel, bad = errors(got, want, rel_floor)
+    nr = norm_rel(got, want)
+    assert not bad.any() and nr <= RTOL, (f"{what}: {int(bad.sum())} elements out of bounds, max abs err "
+                                          f"{mx_abs:.3e}, max rel err {mx_rel:.3e}, normwise rel err {nr:.3e}")
+    return mx_abs
 
 
-def assert_close_anchors(got, want, what, max_anchors=4):
-    """Two device runs of one network whose launch shapes differ (batch size,
-    measured choice): within tolerance except where one of them lands on the
-    other side of a jump of the reference's Winograd-layer SiLU, which moves a
-    few anchors' values only (see assert_network_close)."""
-    err = np.abs(got.astype(np.float64) - want.astype(np.float64))
-    bad = err > ATOL + RTOL * np.abs(want)
-    anchors = np.unique(np.nonzero(bad)[-1])
-    assert len(anchors) <= max_anchors, (f"{what}: {int(bad.sum())} elements over {len(anchors)} anchors out of "
-                                         f"tolerance, max abs err {err.max():.3e}")
+def explain_by_jumps(got, model, x, what, max_set=3):
+    """Whole-network parity of one image's head against the float64 oracle.
+    An fp32 conv whose rounding lands on the other side of a compat-SiLU
+    jump than the float64 oracle is as faithful as the reference's own fp32
+    result; so `got` must match, within the bounds on every element, the
+    oracle with some set of at most `max_set` of its near-jump activations
+    (within 1e-6 of a jump) on the other side -- usually the empty set.
+    Returns (that oracle output, the plain oracle output, the set)."""
+    import itertools
+    log = []
+    plain = graph_ref.run_graph(model, [x], jump_log=log)[0]
+    mx_abs, mx_rel, bad = errors(got, plain)
+    if not bad.any():
+        print(f"{what}: max abs err {mx_abs:.3e}, max rel err {mx_rel:.3e}", flush=True)
+        return plain, plain, ()
+    cands = [(a, i) for a, i, _ in log]
+    for k in range(1, min(max_set, len(cands)) + 1):
+        for subset in itertools.combinations(cands, k):
+            fe = {}
+            for a, i in subset:
+                fe.setdefault(a, []).append(i)
+            alt = graph_ref.run_graph(model, [x], flip_elems=fe)[0]
+            a_abs, a_rel, a_bad = errors(got, alt)
+            if not a_bad.any():
+                print(f"{what}: matches the oracle with {list(subset)} on the other side of the compat-SiLU jump "
+                      f"(max abs err {a_abs:.3e}, max rel err {a_rel:.3e}; {int(bad.sum())} elements differ from "
+                      f"the unflipped oracle)", flush=True)
+                return alt, plain, subset
+    raise AssertionError(f"{what}: {int(bad.sum())} elements out of bounds (max abs err {mx_abs:.3e}, max rel err "
+                         f"{mx_rel:.3e}) and no set of near-jump activations {cands} explains them")
 
 
 def assert_network_close(got, model, x, what, want=None):
-    """Whole-network parity against the oracle.  The reference's Winograd-layer
-    SiLU jumps by ~2% where -x log2 e crosses a half-integer; an fp32 conv
-    whose rounding lands on the other side of a jump than the float64 oracle
-    is as faithful as the reference's own fp32 result.  Elements out of
-    tolerance are therefore accepted only where the oracle matches once its
-    compat-SiLU activations within 1e-5 (relative) of a jump take their other
-    side, confined to at most 4 anchors; everything else must match the plain
-    oracle.  Returns the oracle output the detections follow."""
-    if want is None:
-        want = graph_ref.run_graph(model, [x])[0]
-    err = np.abs(got.astype(np.float64) - want.astype(np.float64))
-    bad = err > ATOL + RTOL * np.abs(want)
-    if not bad.any():
-        return want
-    alt = graph_ref.run_graph(model, [x], flip=lambda name: True, flip_tol=1e-5)[0]
-    still = bad & (np.abs(got.astype(np.float64) - alt) > ATOL + RTOL * np.abs(alt))
-    assert not still.any(), (f"{what}: {int(still.sum())} elements out of tolerance of both the oracle and its "
-                             f"jump-flipped form, max abs err {err.max():.3e} at "
-                             f"{np.unravel_index(err.argmax(), err.shape)}")
-    anchors = np.unique(np.nonzero(bad)[-1])
-    assert len(anchors) <= 4, f"{what}: jump differences spread over {len(anchors)} anchors"
-    print(f"{what}: {int(bad.sum())} elements at anchors {anchors.tolist()} follow the other side of "
-          f"the reference SiLU's jump", flush=True)
-    return alt
+    """explain_by_jumps for each image of a [N, C, A] head; returns the
+    oracle outputs that explain the device's, stacked."""
+    outs = []
+    for n in range(got.shape[0]):
+        follow, _, _ = explain_by_jumps(got[n:n + 1], model, x[n:n + 1], f"{what} image {n}" if got.shape[0] > 1
+                                        else what)
+        outs.append(follow)
+    return np.concatenate(outs, axis=0)
 
 
 def assert_same_detections(got, want_candidates, meta, what):
     """Post-NMS lists identical to the oracle's (to one of the given oracle
-    outputs, see assert_network_close): same anchors, classes and order,
-    coordinates and scores within tolerance."""
-    dg = decode_yolo(got, meta, with_anchor=True)
+    outputs, see assert_network_close) at a conf_thres with a 1e-2 score
+    margin on the first: same anchors, classes and order, box corners within
+    1e-3 pixels, scores within abs and rel 1e-3."""
+    conf, _ = decode_ref.robust_conf(want_candidates[0])
+    assert conf is not None, f"{what}: no conf_thres with a 1e-2 score margin"
+    dg = decode_yolo(got, meta, conf_thres=conf, with_anchor=True)
     for want in want_candidates:
-        dw = decode_ref.decode(want.tolist(), meta)
+        dw = decode_ref.decode(want.tolist(), meta, conf)
         if [(d["anchor"], d["cls"]) for d in dg] != [(d["anchor"], d["cls"]) for d in dw]:
             continue
-        if all(abs(a[k] - b[k]) <= ATOL + RTOL * abs(b[k]) for a, b in zip(dg, dw)
-               for k in ("x1", "y1", "x2", "y2", "conf")):
+        if all(abs(a[k] - b[k]) <= ATOL for a, b in zip(dg, dw) for k in ("x1", "y1", "x2", "y2")) and \
+                all(abs(a["conf"] - b["conf"]) <= min(ATOL, RTOL * b["conf"]) for a, b in zip(dg, dw)):
             return dg
     raise AssertionError(f"{what}: detections differ from the oracle's")
 
@@ -202,27 +279,98 @@ CONV_CASES = [
 ]
 
 
+# Elements (flat indices) of single-conv outputs where the device conv and
+# the reference's land on different sides of a compat-SiLU jump, with the
+# launch shapes of the launch-shape table.
+CONV_JUMPS = {}
+
+
+def tune_measured():
+    return native.tune_stats()[0]
+
+
 @pytest.mark.parametrize("cin,cout,k,s,hw", CONV_CASES)
 def test_single_conv(tmp_path, cin, cout, k, s, hw):
+    """Conv + bias + SiLU (cfg 2a/2b/2c and edge shapes) against the
+    reference engine on every element, and against the float64 oracle."""
     print(f"[case] conv cin={cin} cout={cout} k={k} s={s} hw={hw}", flush=True)
     model, x = ys.build_single_conv(cin, cout, k, s, hw, seed=7)
     path = str(tmp_path / "conv.engine")
     ys.save(model, path)
+    m0 = tune_measured()
     got = run_engine(path, x)[0]
-    want = graph_ref.run_graph(model, [x])[0]
-    if graph_ref.winograd_path(cin, k, k, (s, s), (1, 1), 1):
-        # The reference's Winograd-layer SiLU jumps by ~2% where -x log2 e
-        # crosses a half-integer; within ~1e-5 of such a point either side is
-        # a faithful result of an fp32 conv, so both are accepted there.
+    assert tune_measured() == m0, "a launch shape of this conv is not in the launch-shape table"
+    ref = reference_outputs(path, x)
+    _, _, bad = errors(got, ref, REL_FLOOR_CONV)
+    jumps = np.flatnonzero(bad).tolist()
+    print(f"conv {cin}->{cout} k{k} s{s} {hw}x{hw}: elements across a jump from the reference's {jumps}", flush=True)
+    assert jumps == CONV_JUMPS.get((cin, cout, k, s, hw), []), jumps
+    if jumps:
+        # each one: its pre-activation within 1e-5 of a jump of the
+        # reference's Winograd-layer SiLU, and the device on one side of it
         pre_model, _ = ys.build_single_conv(cin, cout, k, s, hw, seed=7, silu=False)
         pre = graph_ref.run_graph(pre_model, [x])[0]
         lo, hi, unstable = graph_ref.silu_winograd_compat_branches(pre, tol=1e-5)
-        near = lambda ref: np.abs(got - ref) <= ATOL + RTOL * np.abs(ref)
+        f = got.reshape(-1)[jumps]
+        assert unstable.reshape(-1)[jumps].all()
+        assert (np.isclose(f, lo.reshape(-1)[jumps], rtol=RTOL, atol=0) |
+                np.isclose(f, hi.reshape(-1)[jumps], rtol=RTOL, atol=0)).all()
+    keep = ~bad
+    mx_abs, mx_rel, _ = errors(np.where(keep, got, 0), np.where(keep, ref, 0), REL_FLOOR_CONV)
+    print(f"conv vs reference: max abs err {mx_abs:.3e}, max rel err {mx_rel:.3e} (|ref| >= 1e-3 max|ref|), normwise "
+          f"rel err {norm_rel(got, ref):.3e}", flush=True)
+    assert mx_abs < 1e-4
+    # the float64 oracle: either side within 1e-5 of a jump
+    want = graph_ref.run_graph(model, [x])[0]
+    if graph_ref.winograd_path(cin, k, k, (s, s), (1, 1), 1):
+        pre_model, _ = ys.build_single_conv(cin, cout, k, s, hw, seed=7, silu=False)
+        pre = graph_ref.run_graph(pre_model, [x])[0]
+        lo, hi, unstable = graph_ref.silu_winograd_compat_branches(pre, tol=1e-5)
+        near = lambda r: ~errors(got, r, REL_FLOOR_CONV)[2]
         either = unstable & (near(lo) | near(hi))
         assert unstable.sum() < 1e-3 * got.size
         want = np.where(either, got, want)
-    err = assert_close(got, want, "conv")
-    assert err < 1e-4, err
+    assert assert_close(got, want, "conv vs oracle") < 1e-4
+
+
+ACT_CASES = [
+    # cin, cout, k, stride, hw: the reference's direct kernel, its Winograd
+    # kernel, its GEMM (Cin > 512, 1x1, 3x3 s2)
+    (3, 16, 3, 1, 20), (32, 24, 3, 1, 18), (576, 40, 3, 1, 8), (24, 32, 1, 1, 13), (64, 48, 3, 2, 17),
+]
+
+
+@pytest.mark.parametrize("act", ["Relu", "LeakyRelu", "Sigmoid", "Tanh"])
+@pytest.mark.parametrize("cin,cout,k,s,hw", ACT_CASES)
+def test_fused_activation_vs_reference(tmp_path, act, cin, cout, k, s, hw):
+    """Conv -> ReLU / LeakyReLU(0.1) / Sigmoid / Tanh, fused into the conv
+    epilogue (session_fusion.inc:85-107), with the function the reference's
+    kernel for the conv evaluates (tanh-form GELU for a fused Tanh on its
+    Winograd and direct kernels, 1 / (1 + v) for a fused Sigmoid on its
+    direct kernel), against the reference engine on every element."""
+    print(f"[case] fused {act} conv cin={cin} cout={cout} k={k} s={s} hw={hw}", flush=True)
+    model, x = ys.build_single_conv(cin, cout, k, s, hw, seed=5, act=act, centered=True)
+    path = str(tmp_path / "a.engine")
+    ys.save(model, path)
+    eng = native.Engine(path)
+    try:
+        got = eng.run(x)[0]
+        plan = eng.plan()
+    finally:
+        eng.close()
+    assert f"/act/{act}" not in plan  # fused: no separate activation step
+    ref = reference_outputs(path, x)
+    pre_model, _ = ys.build_single_conv(cin, cout, k, s, hw, seed=5, silu=False, centered=True)
+    pre = graph_ref.run_graph(pre_model, [x])[0].astype(np.float64)
+    mx_abs, mx_rel, bad = errors(got, ref, REL_FLOOR_CONV)
+    kpath = graph_ref.reference_conv_path(cin, k, k, (s, s), (k // 2, k // 2), (1, 1), 1)
+    if act == "Sigmoid" and kpath == "direct":
+        # 1 / (1 + v) near its pole: fp32 error amplified by |v / (1 + v)|
+        near = np.abs(1.0 + pre) < 0.1
+        g, r = got.astype(np.float64), ref.astype(np.float64)
+        bad &= ~(near & (np.abs(g - r) <= RTOL * np.abs(r)))
+    print(f"fused {act} ({kpath}): max abs err {mx_abs:.3e}, max rel err {mx_rel:.3e}", flush=True)
+    assert not bad.any(), f"{int(bad.sum())} elements out of bounds"
 
 
 TILES = ["128x128", "128x64", "64x128", "64x64", "128x32", "64x32k2", "32x64k2", "32x32k4",
@@ -297,9 +445,8 @@ def test_yolov8n_winograd_everywhere(yolov8n, monkeypatch, tile):
     finally:
         eng.close()
     assert plan.count(f"tile={tile},") >= 30
-    want = graph_ref.run_graph(model, [x])[0]
-    follow = assert_network_close(got, model, x, "yolov8n b1 winograd", want=want)
-    assert_same_detections(got, [want, follow], metas[0], "yolov8n b1 winograd")
+    follow, plain, _ = explain_by_jumps(got, model, x, "yolov8n b1 winograd")
+    assert_same_detections(got, [follow, plain], metas[0], "yolov8n b1 winograd")
 
 
 @pytest.mark.parametrize("n,c,h,w,k", [(2, 37, 13, 19, 5), (1, 16, 8, 8, 3), (2, 20, 23, 9, 7), (1, 128, 20, 20, 5)])
@@ -338,37 +485,74 @@ def yolov8n(tmp_path_factory):
     return model, path
 
 
+# Per image of a test's batch, the compat-SiLU activations (conv node name,
+# flat index) where the device's fp32 pre-activation ("device"), or the
+# reference's ("reference"), lands on the other side of a jump than the
+# float64 oracle's, with the launch shapes of the launch-shape table.
+YOLO_JUMPS = {
+    "yolov8n_b1": {0: {"device": [("/model.4/m.0/cv1/conv/Conv", 188763)]}},
+    "yolov8n_b8": {
+        0: {"device": [("/model.4/m.0/cv1/conv/Conv", 188763)]},
+        3: {"device": [("/model.4/m.1/cv2/conv/Conv", 137681)]},
+        5: {"reference": [("/model.4/m.0/cv2/conv/Conv", 9278)]},
+        7: {"device": [("/model.4/m.1/cv1/conv/Conv", 23266), ("/model.15/m.0/cv1/conv/Conv", 79898),
+                       ("/model.4/m.1/cv2/conv/Conv", 88128)],
+            "reference": [("/model.4/m.1/cv1/conv/Conv", 23266)]},
+    },
+    "yolov8m_b16": {  # images 0, 1 and 15 of the batch
+        0: {"device": [("/model.2/m.1/cv1/conv/Conv", 12047), ("/model.4/m.3/cv2/conv/Conv", 430789)],
+            "reference": [("/model.2/m.1/cv1/conv/Conv", 12047), ("/model.4/m.3/cv2/conv/Conv", 430789),
+                          ("/model.2/m.1/cv2/conv/Conv", 246510), ("/model.2/m.1/cv1/conv/Conv", 318232)]},
+        1: {"device": [("/model.4/m.3/cv2/conv/Conv", 17293)],
+            "reference": [("/model.4/m.2/cv2/conv/Conv", 574759)]},
+        2: {"reference": [("/model.4/m.3/cv1/conv/Conv", 157346)]},
+    },
+}
+
+
 def test_yolov8n_b1(yolov8n):
+    """YOLOv8n 640x640 b1 against the reference engine on every one of the
+    705,600 output elements, and identical detections."""
     print("[case] yolov8n b1", flush=True)
     model, path = yolov8n
     x, metas = ys.yolo_inputs(1)
+    m0 = tune_measured()
     eng = native.Engine(path)
     try:
         got = eng.run(x)[0]
         again = eng.run(x)[0]
     finally:
         eng.close()
+    assert tune_measured() == m0, "a launch shape of YOLOv8n b1 is not in the launch-shape table"
     assert np.array_equal(got, again), "two runs differ"
-    want = graph_ref.run_graph(model, [x])[0]
-    follow = assert_network_close(got, model, x, "yolov8n b1", want=want)
-    assert len(assert_same_detections(got, [want, follow], metas[0], "yolov8n b1")) > 0
+    ref = reference_outputs(path, x)
+    explained = assert_matches_reference(got, ref, "yolov8n b1", model, x, YOLO_JUMPS["yolov8n_b1"])
+    g = _golden("yolov8n_640_img0")
+    dets = assert_same_detections_as_reference(got, ref, metas[0], "yolov8n b1", conf=g["conf_thres"],
+                                               follow=explained.get(0))
+    assert [(d["anchor"], d["cls"]) for d in dets] == [(d["anchor"], d["cls"]) for d in g["detections"]]
 
 
-def test_yolov8n_b8_batch_matches_b1(yolov8n):
-    """A stacked batch of 8 letterboxed images equals 8 single-image runs."""
+def test_yolov8n_b8_vs_reference(yolov8n):
+    """YOLOv8n b8 (8 letterboxed images of three aspect ratios in one
+    batched program) against the reference engine run on each image: every
+    output element and the detection lists of all 8 images."""
     print("[case] yolov8n b8", flush=True)
     model, path = yolov8n
     x, metas = ys.yolo_inputs(8)
+    m0 = tune_measured()
     eng = native.Engine(path)
     try:
         got = eng.run(x)[0]
-        singles = [eng.run(x[i:i + 1])[0] for i in (0, 5, 7)]
     finally:
         eng.close()
+    assert tune_measured() == m0, "a launch shape of YOLOv8n b8 is not in the launch-shape table"
     assert got.shape == (8, 84, 8400)
-    for j, i in enumerate((0, 5, 7)):
-        assert_close_anchors(got[i:i + 1], singles[j], f"b8 image {i}")
-    assert_network_close(got[7:8], model, x[7:8], "b8 image 7 vs oracle")
+    ref = reference_outputs(path, x)
+    explained = assert_matches_reference(got, ref, "yolov8n b8", model, x, YOLO_JUMPS["yolov8n_b8"])
+    for i in range(8):
+        assert_same_detections_as_reference(got[i:i + 1], ref[i:i + 1], metas[i], f"yolov8n b8 image {i}",
+                                            follow=explained.get(i))
 
 
 GROUPED_CASES = [
@@ -509,7 +693,7 @@ def test_grouped_launches(yolov8n, monkeypatch, tile):
     monkeypatch.delenv("PDEFA_GROUP_TILE")
     monkeypatch.setenv("PDEFA_GROUP", "0")
     solo = run_engine(path, x)[0]
-    assert_close_anchors(got, solo, "grouped vs separate launches")
+    assert_network_close(solo, model, x, "separate launches vs oracle")
     assert_network_close(got, model, x, f"grouped ({tile}) vs oracle")
 
 
@@ -529,15 +713,14 @@ def test_measured_grouping_at_batch1(yolov8n):
 
 
 def test_autotune_off_within_tolerance(yolov8n, monkeypatch):
-    """The cost model's own launch shapes (no device timing) give the same
-    result within tolerance."""
+    """The cost model's own launch shapes (no table, no device timing) give a
+    result that matches the oracle as well."""
     print("[case] yolov8n b1 autotune off", flush=True)
     model, path = yolov8n
     x, _ = ys.yolo_inputs(1)
-    tuned = run_engine(path, x)[0]
     monkeypatch.setenv("PDEFA_AUTOTUNE", "0")
     model_pick = run_engine(path, x)[0]
-    assert_close_anchors(model_pick, tuned, "autotune off vs on")
+    assert_network_close(model_pick, model, x, "autotune off vs oracle")
 
 
 def test_matmul_512():
@@ -592,14 +775,19 @@ def _golden(name):
         return json.load(f)
 
 
-def _check_golden_samples(arr, g):
-    flat = arr.reshape(-1).astype(np.float64)
+def _check_golden_samples(arr, g, skip=None, rel_floor=FLT_MIN):
+    """The fixture's strided samples (except where `skip` is set) and, when
+    nothing is skipped, its per-channel means."""
+    flat = arr.reshape(-1)
     idx = np.asarray(g["samples"]["index"])
-    want = np.asarray(g["samples"]["value"])
-    bad = np.abs(flat[idx] - want) > ATOL + RTOL * np.abs(want)
-    assert not bad.any(), f"{int(bad.sum())} golden samples out of tolerance"
-    means = arr.reshape(arr.shape[0], arr.shape[1], -1).astype(np.float64).mean(axis=(0, 2))
-    np.testing.assert_allclose(means, g["channel_means"], atol=ATOL, rtol=RTOL)
+    want = np.asarray(g["samples"]["value"], np.float32)
+    if skip is not None and skip.any():
+        keep = ~skip.reshape(-1)[idx]
+        idx, want = idx[keep], want[keep]
+    assert_close(flat[idx], want, "golden samples", rel_floor=rel_floor)
+    if skip is None or not skip.any():
+        means = arr.reshape(arr.shape[0], arr.shape[1], -1).astype(np.float64).mean(axis=(0, 2))
+        assert_close(means, np.asarray(g["channel_means"]), "golden channel means", rel_floor=rel_floor)
 
 
 @pytest.mark.parametrize("name,args", [("conv3x3_s2_64_160", (64, 64, 3, 2, 160)),
@@ -609,51 +797,73 @@ def test_conv_vs_reference_golden(tmp_path, name, args):
     model, x = ys.build_single_conv(*args, seed=7)
     path = str(tmp_path / "c.engine")
     ys.save(model, path)
-    _check_golden_samples(run_engine(path, x)[0], g)
+    _check_golden_samples(run_engine(path, x)[0], g, rel_floor=REL_FLOOR_CONV)
+
+
+def _check_golden_detections(out, meta, g, what, exempt=()):
+    """Detections of `out` at the fixture's conf_thres (no best-class score
+    of the reference output within 1e-2 of it) equal the fixture's list
+    (values not compared at the `exempt` anchors)."""
+    assert g["min_score_gap_to_threshold"] >= 1e-2
+    dets = decode_yolo(out, meta, conf_thres=g["conf_thres"], iou_thres=g["iou_thres"], with_anchor=True)
+    gd = g["detections"]
+    assert [(d["anchor"], d["cls"]) for d in dets] == [(d["anchor"], d["cls"]) for d in gd], what
+    for a, b in zip(dets, gd):
+        if a["anchor"] in exempt:
+            continue
+        for k in ("x1", "y1", "x2", "y2"):
+            assert abs(a[k] - b[k]) <= ATOL, (what, k, a, b)
+        assert abs(a["conf"] - b["conf"]) <= min(ATOL, RTOL * b["conf"]), (what, a, b)
 
 
 def test_yolov8n_batch_vs_reference_golden(yolov8n):
-    """b3 stacked run; each image against the reference's output and detections."""
-    _, path = yolov8n
+    """b3 stacked run; each image against the fixtures written from the
+    reference's outputs (samples, channel means, detections), except at the
+    elements where the device's side of a compat-SiLU jump (explained by the
+    oracle) differs from the reference's."""
+    model, path = yolov8n
     x, metas = ys.yolo_inputs(3)
     out = run_engine(path, x)[0]
     for i in range(3):
         g = _golden(f"yolov8n_640_img{i}")
-        _check_golden_samples(out[i:i + 1], g)
-        dets = decode_yolo(out[i:i + 1], metas[i], with_anchor=True)
-        gd = g["detections"]
-        assert [(d["anchor"], d["cls"]) for d in dets] == [(d["anchor"], d["cls"]) for d in gd]
-        for a, b in zip(dets, gd):
-            for k in ("x1", "y1", "x2", "y2", "conf"):
-                assert abs(a[k] - b[k]) <= ATOL + RTOL * abs(b[k]), (i, k, a, b)
+        follow, plain, _ = explain_by_jumps(out[i:i + 1], model, x[i:i + 1], f"yolov8n b3 image {i}")
+        differ = errors(follow, plain)[2]
+        _check_golden_samples(out[i:i + 1], g, skip=differ)
+        _check_golden_detections(out[i:i + 1], metas[i], g, f"yolov8n image {i}",
+                                 exempt=set(np.unique(np.nonzero(differ)[-1]).tolist()))
 
 
-def test_yolov8m_b16_vs_reference_golden(tmp_path):
-    """YOLOv8m (weight seed 1) at batch 16 in one batched program: images 0
-    and 1 against the reference's outputs and detections, three more
-    against single-image runs of the same session type."""
+def test_yolov8m_b16_vs_reference(tmp_path):
+    """YOLOv8m (weight seed 1) at batch 16 in one batched program: images 0,
+    1 and 15 against the reference engine on every output element, with
+    identical detections, and images 0-1 against the fixtures."""
     print("[case] yolov8m b16", flush=True)
+    model = ys.build_yolov8("m", seed=1)
     path = str(tmp_path / "yolov8m.engine")
-    ys.save(ys.build_yolov8("m", seed=1), path)
+    ys.save(model, path)
     x, metas = ys.yolo_inputs(16)
+    m0 = tune_measured()
     eng = native.Engine(path)
     try:
         out = eng.run(x)[0]
-        assert out.shape == (16, 84, 8400)
-        for i in range(2):
-            g = _golden(f"yolov8m_640_img{i}")
-            _check_golden_samples(out[i:i + 1], g)
-            dets = decode_yolo(out[i:i + 1], metas[i], with_anchor=True)
-            gd = g["detections"]
-            assert [(d["anchor"], d["cls"]) for d in dets] == [(d["anchor"], d["cls"]) for d in gd]
-            for a, b in zip(dets, gd):
-                for k in ("x1", "y1", "x2", "y2", "conf"):
-                    assert abs(a[k] - b[k]) <= ATOL + RTOL * abs(b[k]), (i, k, a, b)
     finally:
         eng.close()
-    for i in (2, 9, 15):
-        single = run_engine(path, x[i:i + 1])[0]
-        assert_close_anchors(out[i:i + 1], single, f"yolov8m b16 image {i} vs b1")
+    assert tune_measured() == m0, "a launch shape of YOLOv8m b16 is not in the launch-shape table"
+    assert out.shape == (16, 84, 8400)
+    pick = [0, 1, 15]
+    ref = reference_outputs(path, x[pick])
+    explained = assert_matches_reference(out[pick], ref, "yolov8m b16 images 0, 1, 15", model, x[pick],
+                                         YOLO_JUMPS["yolov8m_b16"])
+    for j, i in enumerate(pick):
+        assert_same_detections_as_reference(out[i:i + 1], ref[j:j + 1], metas[i], f"yolov8m b16 image {i}",
+                                            follow=explained.get(j))
+    for i in range(2):
+        g = _golden(f"yolov8m_640_img{i}")
+        follow = explained.get(i)
+        differ = errors(follow, ref[i:i + 1])[2] if follow is not None else None
+        ex = set(np.unique(np.nonzero(differ)[-1]).tolist()) if differ is not None else set()
+        _check_golden_samples(out[i:i + 1], g, skip=differ)
+        _check_golden_detections(out[i:i + 1], metas[i], g, f"yolov8m image {i}", exempt=ex)
 
 
 # ---- YOLO decode + NMS on the device (extension) against the oracle's restatement
@@ -737,3 +947,25 @@ def test_device_decode_yolov8n_with_metas(yolov8n):
         assert got[i] == want
         assert [{k: v for k, v in d.items() if k != "anchor"} for d in got[i]] == decode_yolo(out[i:i + 1], metas[i])
     assert sum(len(g) for g in got) > 0
+
+
+@pytest.mark.parametrize("name", sorted(__import__("tests.decode_kats", fromlist=["CASES"]).CASES))
+def test_device_decode_known_answers(tmp_path, name):
+    """The device decode + NMS on the hand-worked known answers
+    (tests/decode_kats.py): IoU exactly at the threshold kept, score at
+    conf_thres kept, ties across and within classes, letterbox clamps,
+    max_det, touching boxes, the 1e-9 guard."""
+    from pdefa_amd import pdefa
+    from tests import decode_kats
+    print(f"[case] device decode known answer {name}", flush=True)
+    boxes, nc, kw, want = decode_kats.CASES[name]
+    heads = decode_kats.head(boxes, nc)[None]
+    kw = dict(kw)
+    meta = kw.pop("meta", None)
+    metas = None
+    if meta is not None:
+        metas = [pdefa.PreprocessMeta(orig_w=meta["orig_w"], orig_h=meta["orig_h"], pad_x=meta["pad_x"],
+                                      pad_y=meta["pad_y"], ratio=meta["ratio"])]
+    path = _head_engine(tmp_path, 4 + nc, heads.shape[-1])
+    got = _device_decode(path, heads, metas, **kw)
+    assert got[0] == want

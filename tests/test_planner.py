@@ -277,3 +277,31 @@ def test_grouped_channel_mismatch_is_reported(tmp_path):
     ys.save(model, path)
     with pytest.raises(native.NativeError, match="channel mismatch"):
         native.plan_text(path, list(x.shape))
+
+
+def test_launch_shape_table_is_well_formed():
+    """The committed launch-shape table (read by the library at planning time)
+    parses: one header per device kind, conv lines of 20 shape ints plus
+    (tile, splits, k steps per split), group lines of n members of 23 ints
+    plus (tile, group ms, separate ms), and one choice per shape."""
+    import os
+    from pdefa_amd import tune_table
+    path = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "pdefa_amd", "tuning",
+                        "gfx950.txt")
+    table = tune_table.read(path)
+    assert ("gfx950", 256) in table
+    keys = set()
+    for line in table[("gfx950", 256)]:
+        f = line.split()
+        if f[0] == "conv":
+            assert len(f) == 1 + 20 + 3, line
+            ints = [int(v) for v in f[1:]]
+            assert ints[-2] >= 1 and ints[-1] >= 1
+        else:
+            n = int(f[1])
+            assert 2 <= n <= 8 and len(f) == 2 + 23 * n + 3, line
+            [int(v) for v in f[2:-2]]
+            assert float(f[-2]) > 0 and float(f[-1]) > 0
+        key = tune_table._key(line)
+        assert key not in keys, line
+        keys.add(key)
