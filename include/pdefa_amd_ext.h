@@ -104,6 +104,23 @@ PDEFA_EXPORT EngineStatus pdefa_amd_plan_model(const EngineModel* m, const int64
  * ("AMD GPU" when the driver reports no marketing name), or "none". */
 PDEFA_EXPORT const char* pdefa_amd_device_name(void);
 
+/* engine_ops_matmul (same arguments, shape rules, results and error
+ * behaviour) for callers that cannot allocate device memory (tight serving
+ * loops, harnesses that forbid hipMalloc); it has no counterpart in the
+ * reference.  Its device buffers
+ * (A, B, B packed for the MFMA core, a zero bias, C and split-K partials)
+ * live in a static 32 MiB scratch array that each GPU holds from the
+ * library's load until the process ends: no hipMalloc, hipFree or other
+ * allocating routine is called, and work is issued on the null stream.
+ * A product whose buffers exceed the array (roughly 4 (MK + KN + MN)
+ * bytes plus padding and partials > 32 MiB) returns ENGINE_ERR_INVALID_ARG
+ * with a message saying so.  Every call on a GPU shares that GPU's array,
+ * which keeps the last call's contents; calls in one process are
+ * serialized by a lock, since overlapping calls on one GPU would race on
+ * the array. */
+PDEFA_EXPORT EngineStatus pdefa_amd_ops_matmul_noalloc(const EngineTensor* a, const EngineTensor* b,
+                                                       EngineTensor* out);
+
 /* Conv launch-shape choices made so far in this process: *measured = timed
  * on the device while planning, *from_table = read from the device kind's
  * launch-shape table (tuning/<arch>.txt beside the library directory, or

@@ -24,6 +24,7 @@ SOURCES = [
     "kernels/conv_wino.hip",
     "kernels/ops.hip",
     "kernels/yolo_decode.hip",
+    "kernels/noalloc.hip",
     "model.cpp",
     "planner.cpp",
     "runtime.cpp",

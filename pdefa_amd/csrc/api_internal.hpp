@@ -62,6 +62,9 @@ EngineStatus guarded(Fn&& fn) noexcept {
     } catch (const HipError& e) {
         set_error(e.what());
         return e.code == hipErrorOutOfMemory ? ENGINE_ERR_OUT_OF_MEMORY : ENGINE_ERR_RUNTIME;
+    } catch (const std::invalid_argument& e) {
+        set_error(e.what());
+        return ENGINE_ERR_INVALID_ARG;
     } catch (const std::exception& e) {
         set_error(e.what());
         return ENGINE_ERR_RUNTIME;

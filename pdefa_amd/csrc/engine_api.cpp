@@ -491,8 +491,17 @@ PDEFA_EXPORT EngineStatus engine_run_simple(const char* model_path, const Engine
 }
 
 // ---------------------------------------------------------------- matmul
-// engine_api.cpp:898-914 -> ops::matmul (matmul.cpp:59-135), on the GPU.
-PDEFA_EXPORT EngineStatus engine_ops_matmul(const EngineTensor* a, const EngineTensor* b, EngineTensor* out) {
+
+namespace {
+
+using GemmFn = void (*)(const float*, const float*, float*, int64_t, int64_t, int64_t);
+
+// The shape rules of ops::matmul (matmul.cpp:59-135): F32 only; rank > 2
+// on either side is batched [..., M, K] x [..., K, N] (or a 2-D B shared by
+// every batch), one GEMM per batch; mismatched shapes leave `out` untouched
+// and still return ENGINE_OK.  (The reference does not check that `out` or
+// a batched B hold the whole batch; here such calls are no-ops too.)
+EngineStatus matmul_front(const EngineTensor* a, const EngineTensor* b, EngineTensor* out, GemmFn gemm) {
     if (!valid(a) || !valid(b) || !valid(out)) return ENGINE_ERR_INVALID_HANDLE;
     if (out->is_borrowed()) {
         set_error("cannot write to borrowed tensor");
@@ -505,7 +514,6 @@ PDEFA_EXPORT EngineStatus engine_ops_matmul(const EngineTensor* a, const EngineT
         HostTensor& Cc = *out->ptr();
         if (A.dtype != pdefa::kF32 || B.dtype != pdefa::kF32 || Cc.dtype != pdefa::kF32) return ENGINE_OK;
         if (A.rank > 2 || B.rank > 2) {
-            // batched: [..., M, K] x [..., K, N] (or a shared 2-D B), one GEMM per batch
             if (A.rank < 2 || B.rank < 2 || Cc.rank < 2) return ENGINE_OK;
             if (A.dim(A.rank - 1) != B.dim(B.rank - 2)) return ENGINE_OK;
             const int64_t M = A.dim(A.rank - 2), K = A.dim(A.rank - 1), N = B.dim(B.rank - 1);
@@ -515,15 +523,28 @@ PDEFA_EXPORT EngineStatus engine_ops_matmul(const EngineTensor* a, const EngineT
             const int64_t bstride = B.rank == 2 ? 0 : K * N;
             if (bstride && B.numel() < batch * K * N) return ENGINE_OK;
             for (int64_t i = 0; i < batch; ++i)
-                pdefa::device_matmul(A.f32() + i * M * K, B.f32() + i * bstride, Cc.f32() + i * M * N, M, K, N);
+                gemm(A.f32() + i * M * K, B.f32() + i * bstride, Cc.f32() + i * M * N, M, K, N);
             return ENGINE_OK;
         }
         if (A.rank != 2 || B.rank != 2 || Cc.rank != 2) return ENGINE_OK;
         const int64_t M = A.dims[0], K = A.dims[1], N = B.dims[1];
         if (B.dims[0] != K || Cc.dims[0] != M || Cc.dims[1] != N) return ENGINE_OK;
-        pdefa::device_matmul(A.f32(), B.f32(), Cc.f32(), M, K, N);
+        gemm(A.f32(), B.f32(), Cc.f32(), M, K, N);
         return ENGINE_OK;
     });
+}
+
+}  // namespace
+
+// engine_api.cpp:898-914 -> ops::matmul (matmul.cpp:59-135), on the GPU.
+PDEFA_EXPORT EngineStatus engine_ops_matmul(const EngineTensor* a, const EngineTensor* b, EngineTensor* out) {
+    return matmul_front(a, b, out, &pdefa::device_matmul);
+}
+
+// engine_ops_matmul with its device buffers in the static scratch array.
+PDEFA_EXPORT EngineStatus pdefa_amd_ops_matmul_noalloc(const EngineTensor* a, const EngineTensor* b,
+                                                       EngineTensor* out) {
+    return matmul_front(a, b, out, &pdefa::device_matmul_noalloc);
 }
 
 }  // extern "C"

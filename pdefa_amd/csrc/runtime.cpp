@@ -943,43 +943,41 @@ MatmulScratch& matmul_scratch() {
     return s;
 }
 
-}  // namespace
+// Device buffers of one C = A @ B (floats, each 64-aligned): A, B, B packed
+// K-major for the MFMA conv core, a zero bias, C, and the split-K partials.
+struct MatmulLayout {
+    size_t nA = 0, nB = 0, nP = 0, nBias = 0, nC = 0, nW = 0;
+    k::ConvLaunchShape ls;
+    size_t total() const { return nA + nB + nP + nBias + nC + nW; }
+};
 
-void device_matmul(const float* A, const float* B, float* C, int64_t M, int64_t K, int64_t N) {
-    if (!device_available()) throw std::runtime_error("no HIP device available for ops_matmul");
-    if (M <= 0 || K <= 0 || N <= 0) return;
+MatmulLayout matmul_layout(int64_t M, int64_t K, int64_t N) {
     if (M >= (int64_t{1} << 31) || K >= (int64_t{1} << 30) || N >= (int64_t{1} << 30))
         throw std::runtime_error("ops_matmul: shape too large");
-    MatmulScratch& sc = matmul_scratch();
-    std::lock_guard<std::mutex> g(sc.mu);
-    if (!sc.stream) PDEFA_HIP(hipStreamCreateWithFlags(&sc.stream, hipStreamNonBlocking));
-    const size_t nA = align_up(static_cast<size_t>(M * K));
-    const size_t nB = align_up(static_cast<size_t>(K * N));
-    const size_t nP = align_up(static_cast<size_t>(k::packed_weight_elems(static_cast<int>(N), static_cast<int>(K))));
-    const size_t nBias = align_up(static_cast<size_t>(N));
-    const size_t nC = align_up(static_cast<size_t>(M * N));
-    const int ktiles = static_cast<int>((K + k::kConvBK - 1) / k::kConvBK);
-    const k::ConvLaunchShape ls = k::conv_select(M, static_cast<int>(N), static_cast<int>(K), true);
-    const int tile = ls.tile, splits = ls.splits, kps = ls.kt_per_split;
-    const size_t nW = splits > 1 ? align_up(static_cast<size_t>(splits) * M * N) : 0;
-    const size_t need = nA + nB + nP + nBias + nC + nW;
-    if (need > sc.cap) {
-        if (sc.buf) PDEFA_HIP(hipFree(sc.buf));
-        sc.buf = nullptr;
-        sc.cap = 0;
-        PDEFA_HIP(hipMalloc(&sc.buf, need * sizeof(float)));
-        sc.cap = need;
-    }
-    float* dA = sc.buf;
-    float* dB = dA + nA;
-    float* dP = dB + nB;
-    float* dBias = dP + nP;
-    float* dC = dBias + nBias;
-    float* dW = dC + nC;
-    PDEFA_HIP(hipMemcpyAsync(dA, A, sizeof(float) * M * K, hipMemcpyHostToDevice, sc.stream));
-    PDEFA_HIP(hipMemcpyAsync(dB, B, sizeof(float) * K * N, hipMemcpyHostToDevice, sc.stream));
-    PDEFA_HIP(hipMemsetAsync(dBias, 0, nBias * sizeof(float), sc.stream));
-    k::launch_pack_gemm_b(dP, dB, static_cast<int>(K), static_cast<int>(N), sc.stream);
+    MatmulLayout L;
+    L.nA = align_up(static_cast<size_t>(M * K));
+    L.nB = align_up(static_cast<size_t>(K * N));
+    L.nP = align_up(static_cast<size_t>(k::packed_weight_elems(static_cast<int>(N), static_cast<int>(K))));
+    L.nBias = align_up(static_cast<size_t>(N));
+    L.nC = align_up(static_cast<size_t>(M * N));
+    L.ls = k::conv_select(M, static_cast<int>(N), static_cast<int>(K), true);
+    L.nW = L.ls.splits > 1 ? align_up(static_cast<size_t>(L.ls.splits) * M * N) : 0;
+    return L;
+}
+
+// Host A, B in; host C out; the device buffers at `base` (L.total() floats).
+void matmul_on(const MatmulLayout& L, float* base, const float* A, const float* B, float* C, int64_t M, int64_t K,
+               int64_t N, hipStream_t s) {
+    float* dA = base;
+    float* dB = dA + L.nA;
+    float* dP = dB + L.nB;
+    float* dBias = dP + L.nP;
+    float* dC = dBias + L.nBias;
+    float* dW = dC + L.nC;
+    PDEFA_HIP(hipMemcpyAsync(dA, A, sizeof(float) * M * K, hipMemcpyHostToDevice, s));
+    PDEFA_HIP(hipMemcpyAsync(dB, B, sizeof(float) * K * N, hipMemcpyHostToDevice, s));
+    PDEFA_HIP(hipMemsetAsync(dBias, 0, L.nBias * sizeof(float), s));
+    k::launch_pack_gemm_b(dP, dB, static_cast<int>(K), static_cast<int>(N), s);
     k::ConvArgs c;
     c.x = dA;
     c.N = 1;
@@ -999,14 +997,52 @@ void device_matmul(const float* A, const float* B, float* C, int64_t M, int64_t 
     c.wpk = dP;
     c.bias = dBias;
     c.K = static_cast<int32_t>(K);
-    c.ktiles = ktiles;
-    c.splits = splits;
-    c.kt_per_split = kps;
-    c.ws = splits > 1 ? dW : nullptr;
-    k::launch_conv_mfma(c, tile, K % 4 == 0, sc.stream);
+    c.ktiles = static_cast<int>((K + k::kConvBK - 1) / k::kConvBK);
+    c.splits = L.ls.splits;
+    c.kt_per_split = L.ls.kt_per_split;
+    c.ws = L.ls.splits > 1 ? dW : nullptr;
+    k::launch_conv_mfma(c, L.ls.tile, K % 4 == 0, s);
     PDEFA_HIP(hipGetLastError());
-    PDEFA_HIP(hipMemcpyAsync(C, dC, sizeof(float) * M * N, hipMemcpyDeviceToHost, sc.stream));
-    PDEFA_HIP(hipStreamSynchronize(sc.stream));
+    PDEFA_HIP(hipMemcpyAsync(C, dC, sizeof(float) * M * N, hipMemcpyDeviceToHost, s));
+    PDEFA_HIP(hipStreamSynchronize(s));
+}
+
+}  // namespace
+
+void device_matmul(const float* A, const float* B, float* C, int64_t M, int64_t K, int64_t N) {
+    if (!device_available()) throw std::runtime_error("no HIP device available for ops_matmul");
+    if (M <= 0 || K <= 0 || N <= 0) return;
+    const MatmulLayout L = matmul_layout(M, K, N);
+    MatmulScratch& sc = matmul_scratch();
+    std::lock_guard<std::mutex> g(sc.mu);
+    if (!sc.stream) PDEFA_HIP(hipStreamCreateWithFlags(&sc.stream, hipStreamNonBlocking));
+    if (L.total() > sc.cap) {
+        if (sc.buf) PDEFA_HIP(hipFree(sc.buf));
+        sc.buf = nullptr;
+        sc.cap = 0;
+        PDEFA_HIP(hipMalloc(&sc.buf, L.total() * sizeof(float)));
+        sc.cap = L.total();
+    }
+    matmul_on(L, sc.buf, A, B, C, M, K, N, sc.stream);
+}
+
+void device_matmul_noalloc(const float* A, const float* B, float* C, int64_t M, int64_t K, int64_t N) {
+    if (!device_available()) throw std::runtime_error("no HIP device available for ops_matmul");
+    if (M <= 0 || K <= 0 || N <= 0) return;
+    const MatmulLayout L = matmul_layout(M, K, N);
+    static std::mutex mu;  // calls share this device's scratch array: one at a time
+    std::lock_guard<std::mutex> g(mu);
+    size_t cap = 0;
+    float* base = noalloc_scratch(cap);
+    if (L.total() > cap) {
+        std::ostringstream os;
+        os << "ops_matmul_noalloc: a " << M << "x" << K << " @ " << K << "x" << N << " product needs "
+           << L.total() * sizeof(float) << " bytes of device scratch, more than the " << cap * sizeof(float)
+           << " bytes of the static scratch array";
+        throw std::invalid_argument(os.str());
+    }
+    // the null stream: nothing is created
+    matmul_on(L, base, A, B, C, M, K, N, nullptr);
 }
 
 }  // namespace pdefa

@@ -185,4 +185,14 @@ class Session {
 // C = A[M,K] @ B[K,N] on the device (the ops_matmul path); host pointers.
 void device_matmul(const float* A, const float* B, float* C, int64_t M, int64_t K, int64_t N);
 
+// The same product with its device buffers (A, B, packed B, bias, C, split-K
+// partials) in the static scratch array instead of allocated memory; throws
+// std::invalid_argument when they do not fit it.  Calls in one process are
+// serialized (they share the array).
+void device_matmul_noalloc(const float* A, const float* B, float* C, int64_t M, int64_t K, int64_t N);
+
+// Address of the current device's static scratch array (kernels/noalloc.hip)
+// and its size in floats; looked up once per device.
+float* noalloc_scratch(size_t& floats);
+
 }  // namespace pdefa

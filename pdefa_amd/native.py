@@ -15,6 +15,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "lib", "libpdefa_native.so")
 
 ENGINE_OK = 0
+ENGINE_ERR_INVALID_ARG = 7
 STATUS = {0: "OK", 1: "NULL_PTR", 2: "INVALID_HANDLE", 3: "OUT_OF_MEMORY", 4: "FILE_NOT_FOUND",
           5: "INVALID_FORMAT", 6: "INVALID_SHAPE", 7: "INVALID_ARG", 8: "RUNTIME", 9: "NOT_IMPL",
           99: "UNKNOWN"}
@@ -71,6 +72,7 @@ def lib() -> C.CDLL:
             "pdefa_amd_plan_model": (C.c_int, [vp, C.POINTER(i64), i32, C.c_char_p, sz, C.POINTER(sz)]),
             "pdefa_amd_device_name": (C.c_char_p, []),
             "pdefa_amd_tune_stats": (C.c_int, [C.POINTER(i64), C.POINTER(i64)]),
+            "pdefa_amd_ops_matmul_noalloc": (C.c_int, [vp, vp, vp]),
         }
         for name, (res, args) in sig.items():
             f = getattr(L, name)
@@ -223,15 +225,18 @@ def plan_text(path: str, shape: Sequence[int]) -> str:
         L.engine_context_destroy(ctx)
 
 
-def matmul_into(a: np.ndarray, b: np.ndarray, out: np.ndarray) -> np.ndarray:
-    """engine_ops_matmul(a, b, out) with `out` a pre-filled tensor of any
-    shape; returns what the call left in it (the call returns ENGINE_OK also
-    when it leaves `out` untouched for mismatched shapes, as the reference's
-    ops::matmul does)."""
+def matmul_into(a: np.ndarray, b: np.ndarray, out: np.ndarray, noalloc: bool = False) -> np.ndarray:
+    """engine_ops_matmul(a, b, out) (or, with noalloc, its variant
+    pdefa_amd_ops_matmul_noalloc, which allocates no device memory) with
+    `out` a pre-filled tensor of any shape; returns what the call left in it
+    (the call returns ENGINE_OK also when it leaves `out` untouched for
+    mismatched shapes, as the reference's ops::matmul does)."""
     L = lib()
+    fn, name = ((L.pdefa_amd_ops_matmul_noalloc, "pdefa_amd_ops_matmul_noalloc") if noalloc
+                else (L.engine_ops_matmul, "engine_ops_matmul"))
     ha, hb, hc = tensor_from_numpy(a), tensor_from_numpy(b), tensor_from_numpy(out)
     try:
-        check(L.engine_ops_matmul(ha, hb, hc), "engine_ops_matmul")
+        check(fn(ha, hb, hc), name)
         return tensor_to_numpy(hc)
     finally:
         for h in (ha, hb, hc):
