@@ -3,10 +3,13 @@
 bench.py's cpu_baseline leg starts this as a child process, so the reference
 engine's worker threads live and end in their own process:
 
-    python -m oracle.ref_bench MODEL.engine INPUT.npy BUDGET_S THREADS
+    python -m oracle.ref_bench MODEL.engine INPUT.npy THREADS [RUNS] [WARMUP]
 
-Runs Session::run once, two warm-up reruns, then reruns for up to BUDGET_S
-seconds (at most 30) and prints one JSON line {"ms": [...], "threads": n}.
+The protocol of the reference's own benchmark (pdefa/benchmarks/
+bench_models.py:61-62,226-241): one untimed Session::run, WARMUP (5) more,
+then RUNS (30) timed with the host clock; prints one JSON line
+{"ms": [...], "threads": n} (the caller takes the median as the reference
+does, the upper one of an even count).
 """
 from __future__ import annotations
 
@@ -21,18 +24,20 @@ from oracle import ref_lib
 
 
 def main() -> None:
-    path, npy, budget_s, threads = sys.argv[1], sys.argv[2], float(sys.argv[3]), int(sys.argv[4])
+    path, npy, threads = sys.argv[1], sys.argv[2], int(sys.argv[3])
+    runs = int(sys.argv[4]) if len(sys.argv) > 4 else 30
+    warmup = int(sys.argv[5]) if len(sys.argv) > 5 else 5
     x = np.load(npy)  # written by bench.py (no pickled objects)
     ref_lib.set_threads(threads)
     r = ref_lib.RefSession(path)
     r.run(x)
-    for _ in range(2):
+    for _ in range(warmup):
         r.rerun()
     times = []
-    t_end = time.perf_counter() + budget_s
-    while time.perf_counter() < t_end and len(times) < 30:
+    for _ in range(runs):
+        t0 = time.perf_counter()
         r.rerun()
-        times.append(r.last_ms())
+        times.append((time.perf_counter() - t0) * 1e3)
     r.close()
     sys.stdout.write(json.dumps({"ms": times, "threads": threads}) + "\n")
     sys.stdout.flush()

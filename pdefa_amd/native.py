@@ -146,6 +146,24 @@ class Engine:
             i += 1
         return outs
 
+    def session_run_times(self, warmup: int, runs: int) -> List[float]:
+        """Wall ms of each of `runs` engine_session_run calls on the inputs of
+        the last run() (host input uploaded, program launched, output
+        downloaded and synchronised), after one untimed call and `warmup`
+        more -- the protocol of the reference's bench_models.py:226-241."""
+        import time
+        L = lib()
+        check(L.engine_session_run(self.sess), "engine_session_run")
+        for _ in range(warmup):
+            check(L.engine_session_run(self.sess), "engine_session_run")
+        ts = []
+        for _ in range(runs):
+            t0 = time.perf_counter()
+            st = L.engine_session_run(self.sess)
+            ts.append((time.perf_counter() - t0) * 1e3)
+            check(st, "engine_session_run")
+        return ts
+
     def replay(self, iters: int) -> float:
         ms = C.c_double()
         check(lib().pdefa_amd_session_replay(self.sess, iters, C.byref(ms)), "pdefa_amd_session_replay")
