@@ -26,6 +26,8 @@ semantics, which is what this module evaluates in NCHW:
   Transpose session_ops_shape.inc:946-1096
   Softmax   session_ops_math.inc:223-318 (max-subtracted exp, / sum)
   Add/Sub/Mul/Div  session_ops_math.inc:4-220 (numpy broadcasting)
+  TopK      session_ops_math.inc:321-395 (values, then indices)
+  GatherElements  session_ops_math.inc:397-432
   Sigmoid   activation_avx2.cpp:110-121 (1 / (1 + e^-x)); Relu, LeakyRelu,
             Tanh, SiLU: session_ops_nn.inc:210-231 -> activation.cpp:28-70
 
@@ -459,6 +461,38 @@ def run_graph(model: EngineModel, inputs, dtype=np.float64, compat_silu=True, fl
             y = np.transpose(get(ins[0]), _ints(get(ins[1])))
         elif op == "Softmax":
             y = softmax(get(ins[0]), int(p["axis"]))
+        elif op == "TopK":
+            # session_ops_math.inc:321-395: the k largest along the axis
+            # (k <= 0 or > the axis length: all of it), values then indices;
+            # ties go to the lower index here (the reference's partial_sort
+            # leaves their order open)
+            x = get(ins[0])
+            kt = model.weights[-1000 - ins[1]] if ins[1] <= -1000 else get(ins[1])
+            kk = int(np.asarray(kt).reshape(-1)[0])
+            ax = int(p["axis"])
+            ax = ax + x.ndim if ax < 0 else ax
+            if x.ndim == 4:
+                raise NotImplementedError("TopK on rank-4 tensors (the reference sorts its channels-last storage)")
+            n_ax = x.shape[ax]
+            if kk <= 0 or kk > n_ax:
+                kk = n_ax
+            order = np.take(np.argsort(-x, axis=ax, kind="stable"), np.arange(kk), axis=ax)
+            if node.outputs[0] >= 0:
+                inter[node.outputs[0]] = np.take_along_axis(x, order, axis=ax)
+            if len(node.outputs) > 1 and node.outputs[1] >= 0:
+                inter[node.outputs[1]] = order.astype(np.float64)
+            continue
+        elif op == "GatherElements":
+            # session_ops_math.inc:397-432: indices truncated toward zero,
+            # negative ones from the end, the rest out of range read element 0
+            data, idx = get(ins[0]), get(ins[1])
+            ax = int(p["axis"])
+            ax = ax + data.ndim if ax < 0 else ax
+            n_ax = data.shape[ax]
+            g = np.trunc(np.asarray(idx, np.float64)).astype(np.int64)
+            g = np.where(g < 0, g + n_ax, g)
+            g = np.where((g < 0) | (g >= n_ax), 0, g)
+            y = np.take_along_axis(data, g, axis=ax)
         elif op in ("Input", "Output"):
             continue
         else:

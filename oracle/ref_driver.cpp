@@ -106,13 +106,29 @@ __attribute__((visibility("default"))) int ref_output_shape(void* sp, int idx, i
     return t->rank();
 }
 
+/* Output idx as float values (I32 / I64 outputs, such as TopK indices, are
+ * converted value by value). */
 __attribute__((visibility("default"))) int ref_output_copy(void* sp, int idx, float* dst, int64_t n) {
     auto* s = static_cast<RefSession*>(sp);
     if (!s || !dst) return -1;
     const engine::Tensor* t = s->sess->output(idx);
     if (!t || t->numel() != n) return -1;
-    std::memcpy(dst, t->data(), t->nbytes());
+    if (t->dtype() == engine::DType::I32) {
+        for (int64_t i = 0; i < n; ++i) dst[i] = static_cast<float>(t->data<int32_t>()[i]);
+    } else if (t->dtype() == engine::DType::I64) {
+        for (int64_t i = 0; i < n; ++i) dst[i] = static_cast<float>(t->data<int64_t>()[i]);
+    } else {
+        std::memcpy(dst, t->data(), t->nbytes());
+    }
     return 0;
+}
+
+/* Element type of output idx (the engine's DType code), or -1. */
+__attribute__((visibility("default"))) int ref_output_dtype(void* sp, int idx) {
+    auto* s = static_cast<RefSession*>(sp);
+    if (!s) return -1;
+    const engine::Tensor* t = s->sess->output(idx);
+    return t ? static_cast<int>(t->dtype()) : -1;
 }
 
 __attribute__((visibility("default"))) void ref_set_threads(int n) {

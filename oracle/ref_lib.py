@@ -41,6 +41,7 @@ def lib() -> C.CDLL:
         L.ref_output_count.argtypes = [vp]
         L.ref_output_shape.argtypes = [vp, C.c_int, i64p]
         L.ref_output_copy.argtypes = [vp, C.c_int, f32p, C.c_int64]
+        L.ref_output_dtype.argtypes = [vp, C.c_int]
         L.ref_set_threads.argtypes = [C.c_int]
         L.ref_matmul.argtypes = [f32p, f32p, f32p, C.c_int64, C.c_int64, C.c_int64]
         L.ref_letterbox.argtypes = [C.POINTER(C.c_uint8), C.c_int, C.c_int, C.c_int, C.c_int,
@@ -84,7 +85,13 @@ class RefSession:
     def last_ms(self) -> float:
         return lib().ref_session_last_ms(self.sess)
 
+    def output_dtypes(self) -> List[int]:
+        """The engine's DType code of each output (12 F32, 6 I32, 8 I64)."""
+        L = lib()
+        return [L.ref_output_dtype(self.sess, i) for i in range(L.ref_output_count(self.sess))]
+
     def outputs(self) -> List[np.ndarray]:
+        """Every output as float32 values (integer outputs converted)."""
         L = lib()
         outs = []
         for i in range(L.ref_output_count(self.sess)):

@@ -266,6 +266,21 @@ void launch_resize_nearest(const View& out, const View& in, hipStream_t s);
 // Softmax along `axis` of the logical shape.
 void launch_softmax(const View& out, const View& in, int axis, hipStream_t s);
 
+// TopK along `axis` (PDEFA1.0/src/core/session_parts/session_ops_math.inc:321-395):
+// the k largest values of each row in descending order, ties broken by the
+// lower index; `out` receives the values, or with `indices` the indices as
+// float values (exact: the axis is at most kTopKMaxAxis long).  One
+// workgroup sorts one row in LDS.
+constexpr int64_t kTopKMaxAxis = 16384;
+void launch_topk(const View& out, const View& in, int axis, int64_t k, bool indices, hipStream_t s);
+
+// GatherElements along `axis` (session_ops_math.inc:397-432): out[...] =
+// data[... with the axis coordinate replaced by idx[...]]; indices are read
+// as float values truncated toward zero, negative ones count from the end,
+// and ones still out of range read element 0 of the axis.  idx and out have
+// the data's extents off the axis.
+void launch_gather_elements(const View& out, const View& data, const View& idx, int axis, hipStream_t s);
+
 // Three chained stride-1 "same" max pools of kernel k (the SPPF block) in one
 // pass: out0 = pool_k(in), out1 = pool_k(out0) = pool_{2k-1}(in),
 // out2 = pool_k(out1) = pool_{3k-2}(in) (max composes exactly; padding never

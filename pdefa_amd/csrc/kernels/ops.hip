@@ -605,6 +605,127 @@ void launch_detect_decode(const DetectDecodeArgs& a, hipStream_t s) {
     if (C > 0) launch_eltwise(kEltSigmoid, a.cls_out, a.cls, a.cls, 0.0f, s);
 }
 
+// ---- TopK -------------------------------------------------------------------
+
+namespace {
+
+// Offset of row `r` of a view with the axis dimension left out.
+__device__ __forceinline__ int64_t row_offset(const View& v, int axis, int64_t r) {
+    int64_t off = 0;
+    for (int d = v.rank - 1; d >= 0; --d) {
+        if (d == axis) continue;
+        const int64_t c = r % v.dims[d];
+        r /= v.dims[d];
+        off += c * v.str[d];
+    }
+    return off;
+}
+
+// Sort key: ascending keys = descending values, then ascending index.
+__device__ __forceinline__ unsigned long long topk_key(float v, int32_t i) {
+    uint32_t u = __float_as_uint(v);
+    u = (u & 0x80000000u) ? ~u : (u | 0x80000000u);  // order-preserving
+    return (static_cast<unsigned long long>(~u) << 32) | static_cast<uint32_t>(i);
+}
+
+// One workgroup per row: the row's keys in LDS (padded to a power of two
+// P with keys that sort last), a bitonic sort, the first k written.
+__global__ __launch_bounds__(1024) void topk_kernel(View out, View in, int axis, int64_t k, int P, bool indices) {
+    extern __shared__ unsigned long long keys[];
+    const int64_t r = blockIdx.x;
+    const int64_t L = in.dims[axis];
+    const float* src = in.ptr + row_offset(in, axis, r);
+    const int64_t sa = in.str[axis];
+    for (int i = threadIdx.x; i < P; i += blockDim.x)
+        keys[i] = i < L ? topk_key(src[i * sa], i) : ~0ull;
+    __syncthreads();
+    for (int size = 2; size <= P; size <<= 1) {
+        for (int j = size >> 1; j > 0; j >>= 1) {
+            for (int i = threadIdx.x; i < P; i += blockDim.x) {
+                const int ij = i ^ j;
+                if (ij > i) {
+                    const unsigned long long a = keys[i], b = keys[ij];
+                    const bool up = (i & size) == 0;
+                    if ((a > b) == up) {
+                        keys[i] = b;
+                        keys[ij] = a;
+                    }
+                }
+            }
+            __syncthreads();
+        }
+    }
+    float* dst = out.ptr + row_offset(out, axis, r);
+    const int64_t so = out.str[axis];
+    for (int64_t j = threadIdx.x; j < k; j += blockDim.x) {
+        const int32_t idx = static_cast<int32_t>(keys[j] & 0xffffffffull);
+        dst[j * so] = indices ? static_cast<float>(idx) : src[idx * sa];
+    }
+}
+
+// One lane per output element.
+__global__ __launch_bounds__(256) void gather_elements_kernel(View out, View data, View idx, int axis, int64_t total) {
+    for (int64_t e = blockIdx.x * 256ll + threadIdx.x; e < total; e += static_cast<int64_t>(gridDim.x) * 256) {
+        int64_t rem = e, o_off = 0, i_off = 0, d_off = 0, ca = 0;
+        for (int d = out.rank - 1; d >= 0; --d) {
+            const int64_t c = rem % out.dims[d];
+            rem /= out.dims[d];
+            o_off += c * out.str[d];
+            i_off += c * idx.str[d];
+            if (d == axis) ca = c;
+            else d_off += c * data.str[d];
+        }
+        (void)ca;
+        const int64_t n = data.dims[axis];
+        int64_t g = static_cast<int64_t>(idx.ptr[i_off]);  // toward zero
+        if (g < 0) g += n;
+        if (g < 0 || g >= n) g = 0;
+        out.ptr[o_off] = data.ptr[d_off + g * data.str[axis]];
+    }
+}
+
+}  // namespace
+
+void launch_topk(const View& out, const View& in, int axis, int64_t k, bool indices, hipStream_t s) {
+    check_view(out, "topk out");
+    check_view(in, "topk in");
+    if (out.rank != in.rank || axis < 0 || axis >= in.rank) throw std::runtime_error("topk: bad axis/rank");
+    const int64_t L = in.dims[axis];
+    if (L < 1 || L > kTopKMaxAxis) throw std::runtime_error("topk: axis length out of range");
+    if (k < 1 || k > L || out.dims[axis] != k) throw std::runtime_error("topk: bad k");
+    for (int d = 0; d < in.rank; ++d)
+        if (d != axis && out.dims[d] != in.dims[d]) throw std::runtime_error("topk: shape mismatch");
+    const int64_t rows = numel(in) / L;
+    if (rows == 0) return;
+    if (rows >= (int64_t{1} << 31)) throw std::runtime_error("topk: too many rows");
+    int P = 2;
+    while (P < L) P <<= 1;
+    const size_t lds = sizeof(unsigned long long) * static_cast<size_t>(P);
+    static std::once_flag once;
+    std::call_once(once, [] {
+        (void)hipFuncSetAttribute(reinterpret_cast<const void*>(&topk_kernel), hipFuncAttributeMaxDynamicSharedMemorySize,
+                                  static_cast<int>(sizeof(unsigned long long) * kTopKMaxAxis));
+    });
+    hipLaunchKernelGGL(topk_kernel, dim3(static_cast<unsigned>(rows)), dim3(1024), lds, s, out, in, axis, k, P,
+                       indices);
+}
+
+void launch_gather_elements(const View& out, const View& data, const View& idx, int axis, hipStream_t s) {
+    check_view(out, "gather out");
+    check_view(data, "gather data");
+    check_view(idx, "gather indices");
+    if (out.rank != data.rank || idx.rank != data.rank || axis < 0 || axis >= data.rank)
+        throw std::runtime_error("gather_elements: bad axis/rank");
+    for (int d = 0; d < data.rank; ++d) {
+        if (out.dims[d] != idx.dims[d]) throw std::runtime_error("gather_elements: out and indices differ");
+        if (d != axis && idx.dims[d] != data.dims[d]) throw std::runtime_error("gather_elements: shape mismatch");
+    }
+    if (data.dims[axis] < 1) throw std::runtime_error("gather_elements: empty axis");
+    const int64_t total = numel(out);
+    if (total == 0) return;
+    hipLaunchKernelGGL(gather_elements_kernel, dim3(grid_for(total)), dim3(256), 0, s, out, data, idx, axis, total);
+}
+
 // Letterbox of one interleaved 8-bit image into a planar fp32 [3, th, tw]
 // tensor (imageloader/src/preprocess.cpp:15-144): lane = one output pixel,
 // three channels.  Pixels outside the scaled window take the pad value as

@@ -31,6 +31,8 @@ const char* op_name(int32_t op) {
         case kOpReshape: return "Reshape";
         case kOpTranspose: return "Transpose";
         case kOpSlice: return "Slice";
+        case kOpTopK: return "TopK";
+        case kOpGatherElements: return "GatherElements";
         default: return "Unknown";
     }
 }
@@ -197,8 +199,12 @@ bool load_engine_file(const std::string& path, Model& m, std::string* why) {
     std::vector<std::string> names;
     weights.reserve(nw);
     for (auto& w : wm) {
-        if (w.dtype != 12) return fail("only F32 weights are supported");
-        HostTensor t = HostTensor::empty(w.dims, w.rank, kF32);
+        // F32 weights (all the reference converter writes, onnx_to_engine.py:428),
+        // and I64 / I32 constants, which the reference loads typed
+        // (custom_loader.cpp:87-101) and reads with get_tensor_int.
+        if (w.dtype != 12 && w.dtype != 8 && w.dtype != 6)
+            return fail(("weight '" + w.name + "': only F32, I64 and I32 weights are supported").c_str());
+        HostTensor t = HostTensor::empty(w.dims, w.rank, public_dtype(w.dtype));
         if (t.nbytes != w.size && !(t.nbytes == 0 && w.size == 0)) {
             if (t.nbytes > w.size) return fail("weight blob smaller than its shape");
         }

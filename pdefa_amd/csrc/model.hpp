@@ -18,7 +18,7 @@ enum Op : int32_t {
     kOpRelu = 10, kOpLeaky = 11, kOpSigmoid = 12, kOpTanh = 13, kOpSilu = 14, kOpGelu = 15,
     kOpMaxPool = 20, kOpAvgPool = 21, kOpBatchNorm = 22, kOpSoftmax = 30, kOpConcat = 31,
     kOpUpsample = 32, kOpResize = 33, kOpInput = 40, kOpOutput = 41, kOpReshape = 42,
-    kOpTranspose = 43, kOpSlice = 44,
+    kOpTranspose = 43, kOpSlice = 44, kOpTopK = 50, kOpGatherElements = 51,
 };
 const char* op_name(int32_t op);
 

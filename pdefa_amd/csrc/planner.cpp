@@ -170,7 +170,7 @@ VRef broadcast_view(const VRef& a, const Dims& dims) {
 }
 
 // ------------------------------------------------------------ graph ops ----
-enum class EK { Conv, Elt, MaxPool, Resize, Softmax, Concat, Slice, Reshape, Transpose };
+enum class EK { Conv, Elt, MaxPool, Resize, Softmax, Concat, Slice, Reshape, Transpose, TopK, GatherElements };
 
 struct EOp {
     EK k = EK::Elt;
@@ -187,6 +187,9 @@ struct EOp {
     std::vector<int64_t> sl_start, sl_step;  // per dim (slice)
     std::vector<int32_t> perm;                // transpose
     Dims target;                              // reshape
+    int32_t kref = 0;                         // topk: the k constant
+    int64_t topk = 0;
+    bool topk_indices = false;
     // concat slots (reverse pass) and which inputs need copies
     std::vector<VRef> slots;
     std::vector<bool> copy;
@@ -298,7 +301,8 @@ void step_views(const Step& s, std::vector<VRef>& rd, std::vector<VRef>& wr) {
     if (s.has_res) rd.push_back(s.res);
     if (s.kind == StepKind::ConvMfma && s.up.buf != -1) wr.push_back(s.up);
     switch (s.kind) {
-        case StepKind::Elt: rd.push_back(s.b); break;
+        case StepKind::Elt:
+        case StepKind::GatherElements: rd.push_back(s.b); break;
         case StepKind::MaxPoolChain:
             wr.push_back(s.b);
             wr.push_back(s.c);
@@ -401,9 +405,13 @@ class Planner {
     std::vector<int64_t> const_ints(int32_t ref, int node) {
         const HostTensor& t = weight_tensor(ref, node);
         std::vector<int64_t> v(static_cast<size_t>(t.numel()));
-        // F32 constants are truncated toward zero, as get_tensor_int does
-        // (session_helpers.inc:156-170).
-        for (size_t i = 0; i < v.size(); ++i) v[i] = static_cast<int64_t>(t.f32()[i]);
+        // I64 / I32 as stored; F32 constants are truncated toward zero, as
+        // get_tensor_int does (session_helpers.inc:156-170).
+        for (size_t i = 0; i < v.size(); ++i) {
+            if (t.dtype == kI64) v[i] = static_cast<const int64_t*>(t.data)[i];
+            else if (t.dtype == kI32) v[i] = static_cast<const int32_t*>(t.data)[i];
+            else v[i] = static_cast<int64_t>(t.f32()[i]);
+        }
         return v;
     }
 
@@ -519,6 +527,27 @@ class Planner {
                 case kOpSlice: e.k = EK::Slice; break;
                 case kOpReshape: e.k = EK::Reshape; break;
                 case kOpTranspose: e.k = EK::Transpose; break;
+                case kOpTopK: {
+                    // one step per used output (values, indices), each from the
+                    // same sort (session_ops_math.inc:321-395)
+                    if (n.inputs.size() < 2) fail(m_, e.node, "TopK needs the input and k");
+                    e.k = EK::TopK;
+                    e.kref = n.inputs[1];
+                    e.in.resize(1);
+                    if (n.outputs[0] >= 0) eops_.push_back(e);
+                    if (n.outputs.size() >= 2 && n.outputs[1] >= 0) {
+                        EOp ei = e;
+                        ei.out = n.outputs[1];
+                        ei.topk_indices = true;
+                        eops_.push_back(std::move(ei));
+                    }
+                    continue;
+                }
+                case kOpGatherElements:
+                    if (n.inputs.size() < 2) fail(m_, e.node, "GatherElements needs data and indices");
+                    e.k = EK::GatherElements;
+                    e.in.resize(2);
+                    break;
                 default:
                     fail(m_, e.node, "op not supported by the device executor");
             }
@@ -710,6 +739,41 @@ class Planner {
                     if (prod(t) != prod(x)) fail(m_, e.node, "reshape element count mismatch");
                     e.target = t;
                     out = t;
+                    break;
+                }
+                case EK::TopK: {
+                    const Dims x = dims(e.in[0], e.node);
+                    const int r = static_cast<int>(x.size());
+                    // The reference applies the axis to its storage, which is
+                    // channels-last for rank 4 and logical otherwise.
+                    if (r == 4 || r < 1) fail(m_, e.node, "TopK is supported on tensors of rank 1-3 and 5-6");
+                    const int ax = p.axis < 0 ? p.axis + r : p.axis;
+                    if (ax < 0 || ax >= r) fail(m_, e.node, "TopK axis out of range");
+                    if (!val(e.kref).is_weight) fail(m_, e.node, "TopK k must be a constant");
+                    const auto kv = const_ints(e.kref, e.node);
+                    int64_t kk = kv.empty() ? 0 : kv[0];
+                    if (kk <= 0 || kk > x[ax]) kk = x[ax];
+                    if (x[ax] > k::kTopKMaxAxis) fail(m_, e.node, "TopK axis longer than 16384");
+                    e.axis = ax;
+                    e.topk = kk;
+                    out = x;
+                    out[ax] = kk;
+                    break;
+                }
+                case EK::GatherElements: {
+                    const Dims d = dims(e.in[0], e.node);
+                    const Dims ix = dims(e.in[1], e.node);
+                    const int r = static_cast<int>(d.size());
+                    if (r == 4 || r < 1) fail(m_, e.node, "GatherElements is supported on tensors of rank 1-3 and 5-6");
+                    if (static_cast<int>(ix.size()) != r) fail(m_, e.node, "GatherElements rank mismatch");
+                    const int ax = p.axis < 0 ? p.axis + r : p.axis;
+                    if (ax < 0 || ax >= r) fail(m_, e.node, "GatherElements axis out of range");
+                    // the reference walks the indices with the data's outer and
+                    // inner extents (session_ops_math.inc:414-427)
+                    for (int q = 0; q < r; ++q)
+                        if (q != ax && ix[q] != d[q]) fail(m_, e.node, "GatherElements: indices and data differ off the axis");
+                    e.axis = ax;
+                    out = ix;
                     break;
                 }
                 case EK::Transpose: {
@@ -1067,6 +1131,29 @@ class Planner {
                     for (size_t j = 0; j < e.in.size(); ++j)
                         if (e.copy[j]) emit_copy(e.node, e.slots[j], input_view(e.in[j]));
                     break;
+                case EK::TopK: {
+                    Step s;
+                    s.kind = StepKind::TopK;
+                    s.node = e.node;
+                    s.out = o.view;
+                    s.a = input_view(e.in[0]);
+                    s.axis = e.axis;
+                    s.topk = e.topk;
+                    s.topk_indices = e.topk_indices;
+                    plan_.steps.push_back(s);
+                    break;
+                }
+                case EK::GatherElements: {
+                    Step s;
+                    s.kind = StepKind::GatherElements;
+                    s.node = e.node;
+                    s.out = o.view;
+                    s.a = input_view(e.in[0]);
+                    s.b = input_view(e.in[1]);
+                    s.axis = e.axis;
+                    plan_.steps.push_back(s);
+                    break;
+                }
                 case EK::Slice:
                 case EK::Reshape:
                 case EK::Transpose: {
@@ -1108,6 +1195,8 @@ class Planner {
             }
             plan_.outputs.push_back(ov);
             plan_.output_dims.push_back(v.dims);
+            plan_.output_int32.push_back(v.producer >= 0 && eops_[v.producer].k == EK::TopK &&
+                                         eops_[v.producer].topk_indices);
         }
     }
 
@@ -1120,7 +1209,7 @@ class Planner {
     bool reads_buf(const Step& s, int32_t buf) const {
         auto uses = [&](const VRef& v) { return v.buf == buf; };
         if (uses(s.a) || (s.has_res && uses(s.res))) return true;
-        if ((s.kind == StepKind::Elt || s.kind == StepKind::DetectDecode) && (uses(s.b) || uses(s.c))) return true;
+        if ((reads_second_input(s.kind) || s.kind == StepKind::DetectDecode) && (uses(s.b) || uses(s.c))) return true;
         if (s.kind == StepKind::DetectDecode && s.cls_in.buf != -1 && uses(s.cls_in)) return true;
         return false;
     }
@@ -1388,7 +1477,7 @@ class Planner {
             for (int t : {lo[i], hi[i]}) {
                 touch(s.out, t);
                 touch(s.a, t);
-                if (s.kind == StepKind::Elt) touch(s.b, t);
+                if (reads_second_input(s.kind)) touch(s.b, t);
                 if (s.kind == StepKind::MaxPoolChain) {
                     touch(s.b, t);
                     touch(s.c, t);
@@ -1458,6 +1547,8 @@ const char* step_kind_name(StepKind k) {
         case StepKind::Softmax: return "softmax";
         case StepKind::MaxPoolChain: return "maxpool_chain";
         case StepKind::DetectDecode: return "detect_decode";
+        case StepKind::TopK: return "topk";
+        case StepKind::GatherElements: return "gather_elements";
     }
     return "?";
 }
@@ -1507,7 +1598,7 @@ Schedule schedule_plan(const Plan& p, int max_streams) {
         const Step& s = p.steps[i];
         wr[i].push_back(view_range(p, s.out));
         rd[i].push_back(view_range(p, s.a));
-        if (s.kind == StepKind::Elt) rd[i].push_back(view_range(p, s.b));
+        if (reads_second_input(s.kind)) rd[i].push_back(view_range(p, s.b));
         if (s.has_res) rd[i].push_back(view_range(p, s.res));
         if (s.kind == StepKind::MaxPoolChain) {
             wr[i].push_back(view_range(p, s.b));
@@ -1602,7 +1693,11 @@ std::string describe_plan(const Model& m, const Plan& p) {
         os << " node=" << s.node;
         if (s.node >= 0) os << " '" << m.nodes[s.node].name << "'";
         os << " out=" << fmt_view(s.out) << " a=" << fmt_view(s.a);
-        if (s.kind == StepKind::Elt && s.elt >= k::kEltAdd && s.elt <= k::kEltDiv) os << " b=" << fmt_view(s.b);
+        if ((s.kind == StepKind::Elt && s.elt >= k::kEltAdd && s.elt <= k::kEltDiv) || s.kind == StepKind::GatherElements)
+            os << " b=" << fmt_view(s.b);
+        if (s.kind == StepKind::TopK)
+            os << " axis=" << s.axis << " k=" << s.topk << (s.topk_indices ? " indices" : " values");
+        if (s.kind == StepKind::GatherElements) os << " axis=" << s.axis;
         if (s.has_res) os << " res=" << fmt_view(s.res);
         if (s.kind == StepKind::ConvMfma && s.up.buf != -1) os << " up=" << fmt_view(s.up);
         if (s.kind == StepKind::DetectDecode && s.cls_in.buf != -1)

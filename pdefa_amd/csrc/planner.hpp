@@ -33,7 +33,12 @@ struct VRef {
     int64_t str[k::kMaxRank] = {0, 0, 0, 0, 0, 0};
 };
 
-enum class StepKind : int32_t { ConvMfma, ConvDirect, Elt, MaxPool, Resize, Softmax, MaxPoolChain, DetectDecode };
+enum class StepKind : int32_t {
+    ConvMfma, ConvDirect, Elt, MaxPool, Resize, Softmax, MaxPoolChain, DetectDecode, TopK, GatherElements
+};
+
+// Steps whose `b` view is a second input (read).
+inline bool reads_second_input(StepKind k) { return k == StepKind::Elt || k == StepKind::GatherElements; }
 
 struct Step {
     StepKind kind = StepKind::Elt;
@@ -59,8 +64,12 @@ struct Step {
     // eltwise
     int32_t elt = 0;
     float alpha = 0.0f;
-    // softmax
+    // softmax, topk, gather elements
     int32_t axis = 0;
+    // TopK: the k largest along `axis` (ties: lower index first); this step
+    // writes the values, or with topk_indices the indices (as float values)
+    int64_t topk = 0;
+    bool topk_indices = false;
     // DetectDecode: the DFL conv's weight (and bias) indices, number of bins,
     // and optionally (cls_in.buf != -1) the class scores whose sigmoid it
     // also writes to cls_out
@@ -82,6 +91,7 @@ struct Plan {
     std::vector<int32_t> input_bufs;          // contiguous NCHW staging, one per graph input
     std::vector<VRef> outputs;                // contiguous views, graph_outputs order
     std::vector<std::vector<int64_t>> output_dims;
+    std::vector<bool> output_int32;           // the output holds indices (TopK), returned as I32
     std::vector<Step> steps;
     std::vector<Buffer> bufs;
     int64_t arena_elems = 0;

@@ -105,8 +105,20 @@ std::shared_ptr<DeviceModel> upload_model(const Model& m) {
     }
     // host image of the uploaded part (alignment gaps and absent biases zero)
     std::vector<float> host(host_floats, 0.0f);
-    for (size_t i = 0; i < m.weights.size(); ++i)
-        if (m.weights[i].nbytes) std::memcpy(host.data() + woff[i], m.weights[i].data, m.weights[i].nbytes);
+    for (size_t i = 0; i < m.weights.size(); ++i) {
+        const HostTensor& t = m.weights[i];
+        if (!t.nbytes) continue;
+        if (t.dtype == kF32) {
+            std::memcpy(host.data() + woff[i], t.data, t.nbytes);
+        } else {
+            // integer constants reach the device as float values (exact
+            // below 2^24, which covers every index a kernel reads)
+            float* d = host.data() + woff[i];
+            for (int64_t j = 0; j < t.numel(); ++j)
+                d[j] = t.dtype == kI64 ? static_cast<float>(static_cast<const int64_t*>(t.data)[j])
+                                       : static_cast<float>(static_cast<const int32_t*>(t.data)[j]);
+        }
+    }
     for (const auto& p : pp)
         if (p.b >= 0) std::memcpy(host.data() + p.bias_off, m.weights[p.b].data, sizeof(float) * p.cout);
     dm->blob_bytes = total * sizeof(float);
@@ -608,6 +620,19 @@ void Session::prepare(const std::vector<std::vector<int64_t>>& dims) {
                 }
                 break;
             }
+            case StepKind::TopK:
+                l.out = V(s.out, "topk out", si);
+                l.a = V(s.a, "topk in", si);
+                l.axis = s.axis;
+                l.topk = s.topk;
+                l.topk_indices = s.topk_indices;
+                break;
+            case StepKind::GatherElements:
+                l.out = V(s.out, "gather out", si);
+                l.a = V(s.a, "gather data", si);
+                l.b = V(s.b, "gather indices", si);
+                l.axis = s.axis;
+                break;
             case StepKind::MaxPool:
             case StepKind::Resize:
             case StepKind::Softmax:
@@ -646,7 +671,9 @@ void Session::prepare(const std::vector<std::vector<int64_t>>& dims) {
                                 hipHostMallocDefault));
         prep_->host_out.push_back(h);
         HostTensor t;
-        t.dtype = kF32;
+        // TopK indices leave as I32, as the reference's indices tensor is
+        // (session_ops_math.inc:346); the device holds them as float values
+        t.dtype = (i < plan.output_int32.size() && plan.output_int32[i]) ? kI32 : kF32;
         t.rank = static_cast<int32_t>(plan.output_dims[i].size());
         for (int d = 0; d < t.rank; ++d) t.dims[d] = plan.output_dims[i][d];
         t.data = h;
@@ -673,6 +700,8 @@ void Session::launch_one(const Launch& l, hipStream_t s) {
         case StepKind::Softmax: k::launch_softmax(l.out, l.a, l.axis, s); break;
         case StepKind::MaxPoolChain: k::launch_maxpool_chain(l.out, l.b, l.c, l.a, l.kh, s); break;
         case StepKind::DetectDecode: k::launch_detect_decode(l.decode, s); break;
+        case StepKind::TopK: k::launch_topk(l.out, l.a, l.axis, l.topk, l.topk_indices, s); break;
+        case StepKind::GatherElements: k::launch_gather_elements(l.out, l.a, l.b, l.axis, s); break;
     }
 }
 
@@ -824,6 +853,14 @@ void Session::run() {
     }
     download_outputs();
     PDEFA_HIP(hipStreamSynchronize(stream_));
+    for (size_t i = 0; i < prep_->outputs.size(); ++i) {
+        HostTensor& t = prep_->outputs[i];
+        if (t.dtype != kI32) continue;
+        // float-valued indices (exact integers) -> int32, in place
+        float* f = prep_->host_out[i];
+        int32_t* d = reinterpret_cast<int32_t*>(f);
+        for (int64_t j = 0; j < t.numel(); ++j) d[j] = static_cast<int32_t>(f[j]);
+    }
     const auto t1 = std::chrono::high_resolution_clock::now();
     last_run_ms = std::chrono::duration<double, std::milli>(t1 - t0).count();
     ++runs;

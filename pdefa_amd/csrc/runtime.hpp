@@ -119,6 +119,8 @@ class Session {
         int elt = 0;
         float alpha = 0.0f;
         int kh = 0, kw = 0, sh = 1, sw = 1, ph = 0, pw = 0, axis = 0;
+        int64_t topk = 0;
+        bool topk_indices = false;
         std::string label;
     };
     struct Prepared {

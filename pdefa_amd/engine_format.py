@@ -6,7 +6,7 @@ The byte layout is the one the reference loader parses
 
 header   u32 magic 0x4E474E45 ("ENGN"), u32 version (1|2), u32 n_weights,
          u32 n_nodes, u32 n_inputs, u32 n_outputs, char brand[64]
-weights  n_weights x { u32 name_len, name, u8 dtype (12 = F32), u8 rank,
+weights  n_weights x { u32 name_len, name, u8 dtype (12 F32, 8 I64, 6 I32), u8 rank,
                        i64 dims[rank], u64 offset, u64 size }
 nodes    n_nodes x { u8 op, u32 name_len, name, u16 n_in, u16 n_out,
                      i32 in[n_in], i32 out[n_out], 128-byte OpParams }
@@ -34,7 +34,12 @@ import numpy as np
 
 MAGIC = 0x4E474E45
 DT_F32 = 12
+DT_I64 = 8
+DT_I32 = 6
 PARAMS_SIZE = 128
+# weight dtypes (PDEFA1.0/include/engine/dtype.hpp:36-53 codes) <-> numpy
+_NP_OF_DT = {DT_F32: np.float32, DT_I64: np.int64, DT_I32: np.int32}
+_DT_OF_NP = {np.dtype(np.int64): DT_I64, np.dtype(np.int32): DT_I32}
 
 # OpType codes (PDEFA1.0/include/engine/graph.hpp:20-73)
 OP = {
@@ -43,6 +48,7 @@ OP = {
     "MaxPool": 20, "AveragePool": 21, "BatchNormalization": 22,
     "Softmax": 30, "Concat": 31, "Upsample": 32, "Resize": 33,
     "Input": 40, "Output": 41, "Reshape": 42, "Transpose": 43, "Slice": 44,
+    "TopK": 50, "GatherElements": 51,
 }
 OP_NAME = {v: k for k, v in OP.items()}
 
@@ -124,10 +130,14 @@ def write_engine(path: str, m: EngineModel) -> None:
     cursor = 0
     blobs = []
     for name, arr in zip(m.weight_names, m.weights):
-        arr = np.ascontiguousarray(arr, dtype=np.float32)
+        # int64 / int32 arrays keep their type; everything else is F32, as the
+        # reference converter writes every initializer (onnx_to_engine.py:428)
+        arr = np.asarray(arr)
+        dt = _DT_OF_NP.get(arr.dtype, DT_F32)
+        arr = np.ascontiguousarray(arr, dtype=_NP_OF_DT[dt])
         nb = name.encode()
         out += struct.pack("<I", len(nb)) + nb
-        out += struct.pack("<BB", DT_F32, arr.ndim)
+        out += struct.pack("<BB", dt, arr.ndim)
         for d in arr.shape:
             out += struct.pack("<q", int(d))
         out += struct.pack("<QQ", cursor, arr.nbytes)
@@ -212,9 +222,10 @@ def read_engine(path: str) -> EngineModel:
     data_start = pos
     weights, names = [], []
     for name, dt, dims, off, size in wmeta:
-        if dt != DT_F32:
+        if dt not in _NP_OF_DT:
             raise FormatError(f"weight {name}: dtype {dt} unsupported")
-        a = np.frombuffer(raw, dtype=np.float32, count=size // 4, offset=data_start + off)
+        npdt = np.dtype(_NP_OF_DT[dt])
+        a = np.frombuffer(raw, dtype=npdt, count=size // npdt.itemsize, offset=data_start + off)
         weights.append(a.reshape(dims).copy())
         names.append(name)
     return EngineModel(weights, names, nodes, gin, gout, iinfo, oinfo, version, brand)

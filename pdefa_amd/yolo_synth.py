@@ -59,7 +59,10 @@ class GraphBuilder:
         self.n_inter = 0
 
     def const(self, name: str, arr) -> int:
-        self.weights.append(np.ascontiguousarray(np.asarray(arr, dtype=np.float32)))
+        a = np.asarray(arr)
+        # int64 / int32 constants keep their type (written as I64 / I32)
+        a = a if a.dtype in (np.int64, np.int32) else a.astype(np.float32)
+        self.weights.append(np.ascontiguousarray(a))
         self.wnames.append(name)
         return -1000 - (len(self.weights) - 1)
 
@@ -70,9 +73,13 @@ class GraphBuilder:
         return outs[0] if n_out == 1 else outs
 
     def model(self, in_shape, out_shape, outputs: List[int]) -> EngineModel:
+        """out_shape: the output's shape, or with several outputs a list of
+        shapes (the second and later ones may be None)."""
+        shapes = out_shape if len(outputs) > 1 else [out_shape]
+        infos = [TensorInfo(f"output{i}", list(sh) if sh is not None else []) for i, sh in enumerate(shapes)]
+        infos += [TensorInfo(f"output{i}", []) for i in range(len(infos), len(outputs))]
         return EngineModel(self.weights, self.wnames, self.nodes, [-1], outputs,
-                           [TensorInfo("images", list(in_shape))],
-                           [TensorInfo("output0", list(out_shape))])
+                           [TensorInfo("images", list(in_shape))], infos)
 
 
 def make_divisible(x: float, d: int = 8) -> int:
@@ -310,6 +317,54 @@ def build_scdown(cin: int, cout: int, hw: int, n: int = 1, seed: int = 11) -> Tu
     out = b.node("Add", "/add/Add", [y2, y3])
     ho = (hw - 1) // 2 + 1
     return b.model([n, cin, hw, hw], [n, cout, ho, ho], [out]), x
+
+
+def build_topk_head(anchors: int = 8400, nc: int = 80, k: int = 300, seed: int = 9,
+                    k_dtype=np.int64) -> Tuple[EngineModel, np.ndarray]:
+    """A YOLOv10-style selection of the best anchors from a [1, 4 + nc, A]
+    head: Transpose to [1, A, 4 + nc], Slice boxes [1, A, 4] and scores
+    [1, A, nc], TopK(k, axis 1) of the scores (values and indices), the
+    indices of the first four classes gather the boxes (GatherElements,
+    axis 1), and Concat(boxes, values of those classes) -> [1, k, 8]; the
+    indices [1, k, nc] are a second (I32) output.  k is an int64 constant.
+    Returns the model and a seeded head input (scores distinct)."""
+    rng = np.random.default_rng(seed)
+    x = np.empty((1, 4 + nc, anchors), np.float32)
+    x[0, :4] = rng.uniform(0, 640, (4, anchors)).astype(np.float32)
+    x[0, 4:] = rng.permutation(nc * anchors).reshape(nc, anchors).astype(np.float32) / np.float32(nc * anchors)
+    b = GraphBuilder()
+    perm = b.const("/head/perm", np.array([0, 2, 1], np.float32))
+    t = b.node("Transpose", "/head/Transpose", [-1, perm])
+    def sl(name, src, start, end):
+        return b.node("Slice", name, [src, b.const(name + "/starts", np.array([start], np.float32)),
+                                      b.const(name + "/ends", np.array([end], np.float32)),
+                                      b.const(name + "/axes", np.array([2], np.float32))])
+    boxes = sl("/head/boxes", t, 0, 4)
+    scores = sl("/head/scores", t, 4, 4 + nc)
+    kk = b.const("/head/k", np.array([k], k_dtype))
+    vals, idx = b.node("TopK", "/head/TopK", [scores, kk], n_out=2, axis=1)
+    idx4 = sl("/head/idx4", idx, 0, 4)
+    got = b.node("GatherElements", "/head/GatherElements", [boxes, idx4], axis=1)
+    v4 = sl("/head/vals4", vals, 0, 4)
+    out = b.node("Concat", "/head/Concat", [got, v4], axis=2)
+    return b.model([1, 4 + nc, anchors], [[1, k, 8], [1, k, nc]], [out, idx]), x
+
+
+def build_topk_gather(shape, axis: int, k: int, gather_idx=None, seed: int = 4) -> Tuple[EngineModel, np.ndarray]:
+    """TopK(k, axis) of a seeded input with distinct values (values and
+    indices as outputs 0 and 1) and, with `gather_idx` (an int64 array of
+    the input's rank), GatherElements(input, gather_idx constant, axis) as
+    output 2.  Returns the model and the input."""
+    rng = np.random.default_rng(seed)
+    n = int(np.prod(shape))
+    x = (rng.permutation(n).astype(np.float32) / np.float32(n) - np.float32(0.5)).reshape(shape)
+    b = GraphBuilder()
+    vals, idx = b.node("TopK", "/t/TopK", [-1, b.const("/t/k", np.array([k], np.int64))], n_out=2, axis=axis)
+    outs = [vals, idx]
+    if gather_idx is not None:
+        outs.append(b.node("GatherElements", "/t/GatherElements",
+                           [-1, b.const("/t/idx", np.asarray(gather_idx, np.int64))], axis=axis))
+    return b.model(list(shape), [None] * len(outs), outs), x
 
 
 def build_pool_chain(n: int, c: int, h: int, w: int, k: int, seed: int = 5) -> Tuple[EngineModel, np.ndarray]:

@@ -969,3 +969,59 @@ def test_device_decode_known_answers(tmp_path, name):
     path = _head_engine(tmp_path, 4 + nc, heads.shape[-1])
     got = _device_decode(path, heads, metas, **kw)
     assert got[0] == want
+
+
+@pytest.mark.parametrize("anchors,nc,k,k_dtype", [(8400, 80, 300, np.int64), (2100, 20, 100, np.float32),
+                                                  (700, 6, 5000, np.int64)])
+def test_topk_head_vs_reference(tmp_path, anchors, nc, k, k_dtype):
+    """The YOLOv10-style selection (TopK over anchors per class, indices
+    output, GatherElements of the boxes, Concat) on the device: both
+    outputs equal the compiled reference's and the oracle's exactly on a
+    tie-free head; the indices output is int32 as the reference's is."""
+    print(f"[case] topk head anchors={anchors} nc={nc} k={k} {np.dtype(k_dtype).name}", flush=True)
+    model, x = ys.build_topk_head(anchors, nc, k, k_dtype=k_dtype)
+    path = str(tmp_path / "h.engine")
+    ys.save(model, path)
+    plan = native.plan_text(path, list(x.shape))
+    assert " topk " in plan and " gather_elements " in plan
+    got = run_engine(path, x)
+    assert got[1].dtype == np.int32
+    want = graph_ref.run_graph(model, [x])
+    np.testing.assert_array_equal(got[0], want[0])
+    np.testing.assert_array_equal(got[1].astype(np.float32), want[1])
+    if not ref_lib.available():
+        pytest.fail("oracle/_ref/libpdefa_ref.so is missing: build it with __graft_entry__.build()")
+    r = ref_lib.RefSession(path)
+    try:
+        ref = r.run(x)
+    finally:
+        r.close()
+    np.testing.assert_array_equal(got[0], ref[0])
+    np.testing.assert_array_equal(got[1].astype(np.float32), ref[1])
+
+
+@pytest.mark.parametrize("shape,axis,k", [((5, 1000), 1, 7), ((1000, 3), 0, 10), ((2, 3, 50), -1, 50),
+                                          ((16384,), 0, 300), ((3, 700, 2), 1, 699)])
+def test_topk_gather_elements(tmp_path, shape, axis, k):
+    """TopK on every axis position up to the 16384-element limit, and
+    GatherElements whose constant indices hold negative and out-of-range
+    entries, against the oracle and the compiled reference."""
+    print(f"[case] topk/gather shape={shape} axis={axis} k={k}", flush=True)
+    ax = axis % len(shape)
+    rng = np.random.default_rng(len(shape) * 100 + k)
+    gi = rng.integers(-shape[ax] - 3, shape[ax] + 3, size=shape).astype(np.int64)
+    model, x = ys.build_topk_gather(shape, axis, k, gather_idx=gi)
+    path = str(tmp_path / "t.engine")
+    ys.save(model, path)
+    got = run_engine(path, x)
+    want = graph_ref.run_graph(model, [x])
+    assert got[1].dtype == np.int32
+    for g, w in zip(got, want):
+        np.testing.assert_array_equal(g.astype(np.float32), w)
+    r = ref_lib.RefSession(path)
+    try:
+        ref = r.run(x)
+    finally:
+        r.close()
+    for g, w in zip(got, ref):
+        np.testing.assert_array_equal(g.astype(np.float32), w)

@@ -508,3 +508,61 @@ def test_reference_conv_path_rule():
     assert p(64, 3, 3, (1, 1), (1, 1), (2, 2), 1) == "other"
     assert p(64, 3, 3, (1, 1), (1, 1), (1, 1), 4) == "other"
     assert p(8, 3, 3, (1, 1), (1, 1), (1, 1), 8) == "other"      # depthwise
+
+
+# --------------------------------------- TopK / GatherElements (YOLOv10 heads)
+
+@needs_ref
+@pytest.mark.parametrize("anchors,nc,k,k_dtype", [(8400, 80, 300, np.int64), (2100, 20, 100, np.float32),
+                                                  (1000, 5, 0, np.int64), (700, 6, 5000, np.int64)])
+def test_oracle_topk_head_vs_compiled_reference(tmp_path, anchors, nc, k, k_dtype):
+    """The YOLOv10-style selection (Transpose, Slice, TopK, GatherElements,
+    Concat) on a tie-free head: oracle = reference on every output element,
+    k from an int64 or float constant (k <= 0 or > the axis length: all of
+    it), the indices output typed I32 by the reference."""
+    model, x = ys.build_topk_head(anchors, nc, k, k_dtype=k_dtype)
+    path = str(tmp_path / "h.engine")
+    ys.save(model, path)
+    r = ref_lib.RefSession(path)
+    ro = r.run(x)
+    assert r.output_dtypes() == [12, 6]
+    oo = graph_ref.run_graph(model, [x])
+    kk = k if 0 < k <= anchors else anchors
+    assert ro[0].shape == (1, kk, 8) and ro[1].shape == (1, kk, nc)
+    for a, b in zip(ro, oo):
+        np.testing.assert_array_equal(a, b)
+
+
+@needs_ref
+@pytest.mark.parametrize("shape,axis,k", [((5, 1000), 1, 7), ((1000, 3), 0, 10), ((2, 3, 50), -1, 50),
+                                          ((4096,), 0, 1), ((3, 700, 2), 1, 699)])
+def test_oracle_topk_gather_vs_compiled_reference(tmp_path, shape, axis, k):
+    """TopK values and indices, and GatherElements with a constant int64
+    index tensor holding negative and out-of-range entries (the reference
+    wraps negatives once and reads element 0 for the rest)."""
+    ax = axis % len(shape)
+    rng = np.random.default_rng(len(shape) * 100 + k)
+    gi = rng.integers(-shape[ax] - 3, shape[ax] + 3, size=shape).astype(np.int64)
+    model, x = ys.build_topk_gather(shape, axis, k, gather_idx=gi)
+    path = str(tmp_path / "t.engine")
+    ys.save(model, path)
+    ro = ref_lib.RefSession(path).run(x)
+    oo = graph_ref.run_graph(model, [x])
+    for a, b in zip(ro, oo):
+        np.testing.assert_array_equal(a, b)
+    # the gather rule by hand on one row
+    flat_idx = np.moveaxis(gi, ax, 0).reshape(shape[ax], -1)[:, 0]
+    want = np.moveaxis(x, ax, 0).reshape(shape[ax], -1)[:, 0]
+    fixed = [v + shape[ax] if v < 0 else v for v in flat_idx]
+    fixed = [v if 0 <= v < shape[ax] else 0 for v in fixed]
+    np.testing.assert_array_equal(np.moveaxis(oo[2], ax, 0).reshape(shape[ax], -1)[:, 0], want[fixed])
+
+
+def test_engine_format_keeps_int64_constants(tmp_path):
+    from pdefa_amd import engine_format as ef
+    model, _ = ys.build_topk_head(300, 4, 10)
+    path = str(tmp_path / "h.engine")
+    ys.save(model, path)
+    back = ef.read_engine(path)
+    k = back.weights[back.weight_names.index("/head/k")]
+    assert k.dtype == np.int64 and k.tolist() == [10]

@@ -305,3 +305,26 @@ def test_launch_shape_table_is_well_formed():
         key = tune_table._key(line)
         assert key not in keys, line
         keys.add(key)
+
+
+def test_topk_gather_plan(tmp_path):
+    """TopK becomes a values launch and an indices launch over the same
+    sort; GatherElements reads its constant index tensor from the weights;
+    a rank-4 TopK and an axis over 16384 elements are refused."""
+    model, x = ys.build_topk_head(8400, 80, 300)
+    path = str(tmp_path / "h.engine")
+    ys.save(model, path)
+    info, lines = parse(native.plan_text(path, list(x.shape)))
+    kinds = [l.split()[1].split("(")[0] for l in lines]
+    assert kinds.count("topk") == 2 and kinds.count("gather_elements") == 1
+    assert any("k=300 values" in l for l in lines) and any("k=300 indices" in l for l in lines)
+    model, x = ys.build_topk_gather((2, 20000), 1, 5)
+    path = str(tmp_path / "big.engine")
+    ys.save(model, path)
+    with pytest.raises(native.NativeError, match="16384"):
+        native.plan_text(path, list(x.shape))
+    model, x = ys.build_topk_gather((1, 2, 3, 4), 3, 2)
+    path = str(tmp_path / "r4.engine")
+    ys.save(model, path)
+    with pytest.raises(native.NativeError):
+        native.plan_text(path, list(x.shape))
