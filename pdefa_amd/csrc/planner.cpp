@@ -364,6 +364,7 @@ class Planner {
         fuse_steps();
         group_convs();
         allocate();
+        check_bounds();
         return std::move(plan_);
     }
 
@@ -1450,6 +1451,36 @@ class Planner {
         Buffer& b = plan_.bufs[v.buf];
         b.first = std::min(b.first, step);
         b.last = std::max(b.last, step);
+    }
+
+    // Every element a step's views (and the graph's input and output views)
+    // can address lies inside the view's own buffer: a kernel indexes only
+    // through these views, so a plan that passes cannot send one outside
+    // its allocation.
+    void check_bounds() const {
+        auto check = [&](const VRef& v, int64_t step, const char* what) {
+            if (v.buf < 0) return;
+            if (v.buf >= static_cast<int32_t>(plan_.bufs.size()))
+                throw std::logic_error("plan: step " + std::to_string(step) + " " + what + " names no buffer");
+            int64_t lo = v.off, hi = v.off;
+            for (int d = 0; d < v.rank; ++d) {
+                if (v.dims[d] <= 0) return;
+                const int64_t span = (v.dims[d] - 1) * v.str[d];
+                if (span < 0) lo += span;
+                else hi += span;
+            }
+            if (lo < 0 || hi >= plan_.bufs[v.buf].elems)
+                throw std::logic_error("plan: step " + std::to_string(step) + " " + what + " view [" +
+                                       std::to_string(lo) + ", " + std::to_string(hi) + "] outside its buffer of " +
+                                       std::to_string(plan_.bufs[v.buf].elems) + " elements");
+        };
+        std::vector<VRef> rd, wr;
+        for (size_t i = 0; i < plan_.steps.size(); ++i) {
+            step_views(plan_.steps[i], rd, wr);
+            for (const VRef& v : rd) check(v, static_cast<int64_t>(i), "read");
+            for (const VRef& v : wr) check(v, static_cast<int64_t>(i), "write");
+        }
+        for (const VRef& v : plan_.outputs) check(v, -1, "graph output");
     }
 
     void allocate() {
