@@ -121,7 +121,7 @@ Table& table_for(int device) {
             for (auto& v : key) is >> v;
             ConvGroupTiming g;
             is >> g.tile >> g.group_ms >> g.separate_ms;
-            if (is && g.tile >= 0 && g.tile < k::kNumConvTiles) t.group[key] = g;
+            if (is && k::is_gemm_tile(g.tile)) t.group[key] = g;
         }
     }
     return t;
@@ -363,19 +363,20 @@ ConvGroupTiming tune_conv_group(const std::vector<ConvQuery>& qs, const std::vec
         }
     };
     // interleaved passes as in tune_conv, each time scored by its faster pass
-    std::vector<double> ms(k::kNumConvTiles, 0.0);
+    std::vector<double> ms(k::kNumConvShapes, 0.0);
     for (int pass = 0; pass < kTimingPasses; ++pass) {
         const double sep = time_reps(separate, s, ev, reps);
         r.separate_ms = pass == 0 ? sep : std::min(r.separate_ms, sep);
-        for (int t = 0; t < k::kNumConvTiles; ++t) {
+        for (int t = 0; t < k::kNumConvShapes; ++t) {
+            if (!k::is_gemm_tile(t)) continue;
             group_args(t);
             const double g = time_reps(
                 [&] { k::launch_conv_mfma_group(probs.data(), static_cast<int>(probs.size()), t, s); }, s, ev, reps);
             ms[t] = pass == 0 ? g : std::min(ms[t], g);
         }
     }
-    for (int t = 0; t < k::kNumConvTiles; ++t)
-        if (r.tile < 0 || ms[t] < r.group_ms) {
+    for (int t = 0; t < k::kNumConvShapes; ++t)
+        if (k::is_gemm_tile(t) && (r.tile < 0 || ms[t] < r.group_ms)) {
             r.tile = t;
             r.group_ms = ms[t];
         }

@@ -48,7 +48,8 @@ enum Act : int32_t {
 
 // Implicit-GEMM convolution tile configurations.  A workgroup is 4 or 8 waves
 // and computes a BM x BN output tile; each wave owns a WM x WN sub-tile of 32x32
-// MFMA blocks and one of KG interleaved K slices.  KG > 1 splits K across the
+// MFMA blocks (16x16 blocks where WM or WN is 16) and one of KG interleaved K
+// slices.  KG > 1 splits K across the
 // waves of one workgroup (partial tiles summed through LDS in slice order),
 // which multiplies the workgroup count of small layers without any
 // cross-workgroup traffic.
@@ -72,13 +73,23 @@ enum ConvTile : int32_t {
     kTile64x128W8 = 11,    // 2x4 waves of 32x32
     kTile32x64K4W8 = 12,   // 1x2 waves of 32x32, K split in 4
     kTile32x32K8W8 = 13,   // 1 wave tile of 32x32, K split in 8 (small-M, long-K layers)
-    kNumConvTiles = 14,    // implicit-GEMM tiles
     // Winograd F(2x2,3x3) kernel (3x3 stride-1 convs), 32 tiles x BN channels
     kTileWino64 = 14,
     kTileWino32 = 15,
-    kNumConvShapes = 16,
+    // Small tiles on the 16x16x4 MFMA (v_mfma_f32_16x16x4_f32) for layers
+    // whose 32x32 tile grid leaves most of the 256 CUs idle (batch 1 at
+    // 20x20 to 40x40): four times the workgroups of 32x32k4 at the same K
+    // split, a quarter of the MFMA chain per pipeline step.
+    kTile16x16K4 = 16,     // 1 wave tile of 16x16, K split in 4
+    kTile16x32K4 = 17,     // 1 wave tile of 16x32, K split in 4
+    kTile32x16K4 = 18,     // 1 wave tile of 32x16, K split in 4
+    kTile16x32K8W8 = 19,   // 1 wave tile of 16x32, K split in 8
+    kTile32x16K8W8 = 20,   // 1 wave tile of 32x16, K split in 8
+    kNumConvShapes = 21,   // tile ids (implicit-GEMM and Winograd)
 };
 inline bool is_wino_tile(int tile) { return tile == kTileWino64 || tile == kTileWino32; }
+// An implicit-GEMM tile id (conv_mfma_kernel).
+inline bool is_gemm_tile(int tile) { return tile >= 0 && tile < kNumConvShapes && !is_wino_tile(tile); }
 ConvTileShape conv_tile_shape(int tile);
 const char* conv_tile_name(int tile);
 

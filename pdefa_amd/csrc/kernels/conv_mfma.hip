@@ -1,17 +1,20 @@
-// Implicit-GEMM convolution on CDNA4 fp32 matrix cores (v_mfma_f32_32x32x2_f32).
+// Implicit-GEMM convolution on CDNA4 fp32 matrix cores (v_mfma_f32_32x32x2_f32,
+// and v_mfma_f32_16x16x4_f32 for the small tiles).
 //
 // GEMM view of an NHWC convolution: C[m, co] = sum_k A[m, k] * B[k, co] with
 // m = (n, ho, wo), k = (kh, kw, ci) and A gathered on the fly from the input
 // (no im2col buffer).  One workgroup = 4 or 8 waves computes a BM x BN
-// output tile.  Each wave owns a WM x WN sub-tile of 32x32 MFMA blocks and one
-// of KG K slices: a pipeline step advances K by BKT = 32*KG, slice g of the
+// output tile.  Each wave owns a WM x WN sub-tile of MB x MB MFMA blocks (MB =
+// 32, or 16 when WM or WN is 16) and one of KG K slices: a pipeline step advances K by BKT = 32*KG, slice g of the
 // step (32 k wide) feeding the waves of group g.  With KG > 1 the slices'
 // partial tiles are summed through LDS in slice order at the end.
 //
 // Global loads run two steps ahead of the MFMAs (two register stages) into two
 // LDS stages whose rows are padded to 36 floats; each lane feeds four MFMA
-// steps from one 16-byte LDS read: lane half h supplies k = 8q + 4h + j for
-// step (q, j), the same k for A and B, which covers the 32 k of a slice once.
+// steps from one 16-byte LDS read: with 32x32 blocks lane half h supplies
+// k = 8q + 4h + j for step (q, j), with 16x16 blocks lane quarter h supplies
+// k = 16q + 4h + j, the same k for A and B, which covers the 32 k of a slice
+// once.
 // Loads are issued unconditionally (out-of-range A rows read the tensor base,
 // out-of-range K blocks and N rows re-read the last valid block) and the
 // in-range mask is applied when a stage is written to LDS, so the loads of the
@@ -82,6 +85,13 @@ constexpr int tile_threads() {
     return 64 * (BM / WM) * (BN / WN) * KG;
 }
 
+// MFMA block edge of a wave tile: 32x32 blocks, or 16x16 where the wave tile
+// is 16 wide in either dimension.
+template <int WM, int WN>
+constexpr int mfma_block() {
+    return (WM % 32 == 0 && WN % 32 == 0) ? 32 : 16;
+}
+
 // XCD-aware tile order: dispatch slot `lin` (of `total`) runs on XCD lin % 8;
 // give each XCD a contiguous range of tile indices.
 __device__ __forceinline__ int xcd_tile(int lin, int total) {
@@ -99,14 +109,20 @@ __device__ __forceinline__ void conv_tile(const ConvArgs& a, const int bx, const
     constexpr int WAVES_N = BN / WN;
     constexpr int NT = tile_threads<BM, BN, WM, WN, KG>();  // 256 or 512 lanes
     static_assert(NT == 256 || NT == 512, "4 or 8 waves per workgroup");
-    constexpr int TM = WM / 32;
-    constexpr int TN = WN / 32;
+    constexpr int MB = mfma_block<WM, WN>();
+    constexpr int TM = WM / MB;
+    constexpr int TN = WN / MB;
+    // accumulator registers per lane and block: lane l, register e holds row
+    // acc_row(e) and column l % MB of its MFMA block
+    constexpr int NE = MB * MB / 64;
+    using AccT = std::conditional_t<MB == 32, floatx16, floatx4>;
     constexpr int BKT = BK * KG;            // K per pipeline step
     constexpr int CH = BKT / 4;             // float4 chunks per tile row per step
     constexpr int ROW_STEP = NT / CH;       // rows covered by one pass of all lanes
     constexpr int A_ROWS = BM / ROW_STEP;   // A float4 loads per lane per step
     constexpr int B_ROWS = BN / ROW_STEP;   // B float4 loads per lane per step
-    static_assert(WM % 32 == 0 && WN % 32 == 0 && BM % ROW_STEP == 0 && BN % ROW_STEP == 0, "tile");
+    static_assert(WM % MB == 0 && WN % MB == 0 && BM % ROW_STEP == 0 && BN % ROW_STEP == 0, "tile");
+    static_assert(BM * BN >= NT, "one reduced element per lane at least");
     static_assert(A_ROWS <= 32, "mask bits");
 
     extern __shared__ __attribute__((aligned(16))) float smem[];
@@ -168,12 +184,14 @@ __device__ __forceinline__ void conv_tile(const ConvArgs& a, const int bx, const
     // Bias of this lane's output columns, loaded now so its latency hides
     // behind the K loop (the epilogue only reads registers).
     const int half = lane >> 5;
-    const int l32 = lane & 31;
+    const int lcol = lane & (MB - 1);  // column of this lane in its MFMA blocks
+    // tile row of accumulator register e of this lane (within its MFMA block)
+    auto acc_row = [&](int e) { return MB == 32 ? (e >> 2) * 8 + half * 4 + (e & 3) : (lane >> 4) * 4 + e; };
     float bias_lane[KG == 1 ? TN : 1];
     if constexpr (KG == 1) {
 #pragma unroll
         for (int tn = 0; tn < TN; ++tn) {
-            const int co = n0 + wave_n * WN + tn * 32 + l32;
+            const int co = n0 + wave_n * WN + tn * MB + lcol;
             bias_lane[tn] = co < a.Cout ? a.bias[g_out + co] : 0.0f;
         }
     } else {
@@ -308,35 +326,46 @@ __device__ __forceinline__ void conv_tile(const ConvArgs& a, const int bx, const
             *reinterpret_cast<floatx4*>(&B[(r0 + ROW_STEP * i) * LDS_STRIDE + cc * 4]) = br[i];
     };
 
-    floatx16 acc[TM][TN];
+    AccT acc[TM][TN];
 #pragma unroll
     for (int i = 0; i < TM; ++i)
 #pragma unroll
         for (int j = 0; j < TN; ++j)
 #pragma unroll
-            for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.0f;
+            for (int e = 0; e < NE; ++e) acc[i][j][e] = 0.0f;
 
+    // 32x32 blocks: lane (half h, row l % 32) reads k = 8q + 4h .. +3 and feeds
+    // them to MFMA steps (q, 0..3) of 2 k each; 16x16 blocks: lane (quarter h,
+    // row l % 16) reads k = 16q + 4h .. +3 for steps (q, 0..3) of 4 k each.
+    constexpr int KQ = MB == 32 ? 8 : 16;  // k per quad of MFMA steps
+    const int krd = MB == 32 ? half * 4 : (lane >> 4) * 4;
     auto compute_step = [&](int st) {
         const float* Ab = As(st, wg);
         const float* Bb = Bs(st, wg);
 #pragma unroll
-        for (int qq = 0; qq < BK / 8; ++qq) {
+        for (int qq = 0; qq < BK / KQ; ++qq) {
             floatx4 av[TM], bv[TN];
 #pragma unroll
             for (int tm = 0; tm < TM; ++tm)
                 av[tm] = *reinterpret_cast<const floatx4*>(
-                    &Ab[(wave_m * WM + tm * 32 + l32) * LDS_STRIDE + qq * 8 + half * 4]);
+                    &Ab[(wave_m * WM + tm * MB + lcol) * LDS_STRIDE + qq * KQ + krd]);
 #pragma unroll
             for (int tn = 0; tn < TN; ++tn)
                 bv[tn] = *reinterpret_cast<const floatx4*>(
-                    &Bb[(wave_n * WN + tn * 32 + l32) * LDS_STRIDE + qq * 8 + half * 4]);
+                    &Bb[(wave_n * WN + tn * MB + lcol) * LDS_STRIDE + qq * KQ + krd]);
 #pragma unroll
             for (int j = 0; j < 4; ++j)
 #pragma unroll
                 for (int tm = 0; tm < TM; ++tm)
 #pragma unroll
-                    for (int tn = 0; tn < TN; ++tn)
-                        acc[tm][tn] = __builtin_amdgcn_mfma_f32_32x32x2f32(av[tm][j], bv[tn][j], acc[tm][tn], 0, 0, 0);
+                    for (int tn = 0; tn < TN; ++tn) {
+                        if constexpr (MB == 32)
+                            acc[tm][tn] =
+                                __builtin_amdgcn_mfma_f32_32x32x2f32(av[tm][j], bv[tn][j], acc[tm][tn], 0, 0, 0);
+                        else
+                            acc[tm][tn] =
+                                __builtin_amdgcn_mfma_f32_16x16x4f32(av[tm][j], bv[tn][j], acc[tm][tn], 0, 0, 0);
+                    }
         }
     };
 
@@ -396,30 +425,30 @@ __device__ __forceinline__ void conv_tile(const ConvArgs& a, const int bx, const
             u[a.u_sh + a.u_sw] = v;
         };
         if constexpr (KG == 1) {
-            // 32x32 block register e of lane l holds row 8*(e/4) + 4*(l/32) + e%4, column l%32.
+            // block register e of lane l holds row acc_row(e), column l % MB
             int co[TN];
             bool cok[TN];
             float bias_v[TN];
 #pragma unroll
             for (int tn = 0; tn < TN; ++tn) {
-                co[tn] = n0 + wave_n * WN + tn * 32 + l32;
+                co[tn] = n0 + wave_n * WN + tn * MB + lcol;
                 cok[tn] = co[tn] < a.Cout;
                 bias_v[tn] = PART ? 0.0f : bias_lane[tn];
             }
 #pragma unroll
             for (int tm = 0; tm < TM; ++tm) {
-                int64_t yo[16], ro[16], uo[16];
+                int64_t yo[NE], ro[NE], uo[NE];
 #pragma unroll
-                for (int e = 0; e < 16; ++e) {
-                    const int row = wave_m * WM + tm * 32 + (e >> 2) * 8 + half * 4 + (e & 3);
+                for (int e = 0; e < NE; ++e) {
+                    const int row = wave_m * WM + tm * MB + acc_row(e);
                     yo[e] = s_yoff[row];
                     if (RES) ro[e] = s_roff[row];
                     if (UP) uo[e] = s_uoff[row];
                 }
-                float rv[16][TN];
+                float rv[NE][TN];
                 if constexpr (RES) {
 #pragma unroll
-                    for (int e = 0; e < 16; ++e)
+                    for (int e = 0; e < NE; ++e)
 #pragma unroll
                         for (int tn = 0; tn < TN; ++tn) {
                             const bool ok = yo[e] >= 0 && cok[tn];
@@ -428,7 +457,7 @@ __device__ __forceinline__ void conv_tile(const ConvArgs& a, const int bx, const
                         }
                 }
 #pragma unroll
-                for (int e = 0; e < 16; ++e)
+                for (int e = 0; e < NE; ++e)
 #pragma unroll
                     for (int tn = 0; tn < TN; ++tn) {
                         float v = acc[tm][tn][e];
@@ -448,11 +477,11 @@ __device__ __forceinline__ void conv_tile(const ConvArgs& a, const int bx, const
 #pragma unroll
             for (int tm = 0; tm < TM; ++tm)
 #pragma unroll
-                for (int e = 0; e < 16; ++e)
+                for (int e = 0; e < NE; ++e)
 #pragma unroll
                     for (int tn = 0; tn < TN; ++tn) {
-                        const int row = wave_m * WM + tm * 32 + (e >> 2) * 8 + half * 4 + (e & 3);
-                        const int col = wave_n * WN + tn * 32 + l32;
+                        const int row = wave_m * WM + tm * MB + acc_row(e);
+                        const int col = wave_n * WN + tn * MB + lcol;
                         red[(wg * BM + row) * BN + col] = acc[tm][tn][e];
                     }
             __syncthreads();
@@ -582,15 +611,19 @@ __global__ __launch_bounds__(256) void conv_splitk_reduce(ConvArgs a) {
 
 namespace {
 
-constexpr ConvTileShape kShapes[kNumConvTiles] = {
+// indexed by tile id; the Winograd ids (14, 15) have no implicit-GEMM shape
+constexpr ConvTileShape kShapes[kNumConvShapes] = {
     {128, 128, 64, 64, 1}, {128, 64, 64, 32, 1}, {64, 128, 32, 64, 1}, {64, 64, 32, 32, 1},
     {128, 32, 32, 32, 1},  {64, 32, 32, 32, 2},  {32, 64, 32, 32, 2},  {32, 32, 32, 32, 4},
     {128, 64, 32, 32, 1},  {64, 64, 32, 32, 2},  {128, 128, 64, 32, 1}, {64, 128, 32, 32, 1},
-    {32, 64, 32, 32, 4},   {32, 32, 32, 32, 8},
+    {32, 64, 32, 32, 4},   {32, 32, 32, 32, 8},  {0, 0, 0, 0, 0},       {0, 0, 0, 0, 0},
+    {16, 16, 16, 16, 4},   {16, 32, 16, 32, 4},  {32, 16, 32, 16, 4},   {16, 32, 16, 32, 8},
+    {32, 16, 32, 16, 8},
 };
-constexpr const char* kNames[kNumConvTiles] = {"128x128",  "128x64",     "64x128",    "64x64",    "128x32",
-                                               "64x32k2",  "32x64k2",    "32x32k4",   "128x64w8", "64x64k2w8",
-                                               "128x128w8", "64x128w8", "32x64k4w8", "32x32k8w8"};
+constexpr const char* kNames[kNumConvShapes] = {
+    "128x128",  "128x64",    "64x128",    "64x64",     "128x32",    "64x32k2",   "32x64k2",
+    "32x32k4",  "128x64w8",  "64x64k2w8", "128x128w8", "64x128w8",  "32x64k4w8", "32x32k8w8",
+    "wino64",   "wino32",    "16x16k4",   "16x32k4",   "32x16k4",   "16x32k8w8", "32x16k8w8"};
 
 template <int BM, int BN, int WM, int WN, int KG, int PF, bool VEC, bool UPK>
 void launch_one(const ConvArgs& a, dim3 grid, hipStream_t s) {
@@ -652,14 +685,10 @@ void launch_tile(const ConvArgs& a, bool vec, dim3 grid, hipStream_t s) {
 }  // namespace
 
 ConvTileShape conv_tile_shape(int tile) {
-    if (tile < 0 || tile >= kNumConvTiles) return {0, 0, 0, 0, 0};
+    if (!is_gemm_tile(tile)) return {0, 0, 0, 0, 0};
     return kShapes[tile];
 }
-const char* conv_tile_name(int tile) {
-    if (tile == kTileWino64) return "wino64";
-    if (tile == kTileWino32) return "wino32";
-    return tile >= 0 && tile < kNumConvTiles ? kNames[tile] : "?";
-}
+const char* conv_tile_name(int tile) { return tile >= 0 && tile < kNumConvShapes ? kNames[tile] : "?"; }
 
 int64_t packed_weight_elems(int Cout, int K) {
     const int64_t cout_pad = (Cout + kConvBN - 1) / kConvBN * kConvBN;
@@ -681,10 +710,12 @@ double conv_cost(int64_t M, int Cout, int ktiles, int t, int splits, int steps) 
     constexpr double kKernelCycles = 10000.0;  // launch + completion of one kernel
     constexpr double kWgCycles = 1500.0;       // workgroup start-up (first loads)
     constexpr double kStepFloor = 2200.0;      // latency floor of one pipeline step
-    constexpr double kEff[kNumConvTiles] = {1.0, 0.8, 0.8, 0.85, 0.8, 0.75, 0.75, 0.7,
-                                            0.85, 0.85, 0.9, 0.85, 0.75, 0.65};
-    // 8-wave tiles hide part of a step's latency behind the other wave of the SIMD
-    constexpr double kFloorScale[kNumConvTiles] = {1, 1, 1, 1, 1, 1, 1, 1, 0.75, 0.75, 0.75, 0.75, 0.75, 0.8};
+    constexpr double kEff[kNumConvShapes] = {1.0, 0.8, 0.8, 0.85, 0.8, 0.75, 0.75, 0.7, 0.85, 0.85, 0.9,
+                                             0.85, 0.75, 0.65, 1.0, 1.0, 0.55, 0.6, 0.6, 0.55, 0.55};
+    // 8-wave tiles hide part of a step's latency behind the other wave of the
+    // SIMD; a 16x16 block's step runs a quarter of the MFMA chain
+    constexpr double kFloorScale[kNumConvShapes] = {1,    1,    1,    1,   1,   1,   1,   1,   0.75, 0.75, 0.75,
+                                                    0.75, 0.75, 0.8,  1,   1,   0.6, 0.7, 0.7, 0.55, 0.55};
     const ConvTileShape& sh = kShapes[t];
     const int64_t wgs0 = ((M + sh.bm - 1) / sh.bm) * ((Cout + sh.bn - 1) / sh.bn);
     const double c = std::ceil(static_cast<double>(wgs0 * splits) / kCus);
@@ -704,7 +735,8 @@ std::vector<ConvLaunchShape> conv_candidates(int64_t M, int Cout, int K, bool al
         ConvLaunchShape ls;
     };
     std::vector<Scored> out;
-    for (int t = 0; t < kNumConvTiles; ++t) {
+    for (int t = 0; t < kNumConvShapes; ++t) {
+        if (!is_gemm_tile(t)) continue;
         const ConvTileShape& sh = kShapes[t];
         const int steps_total = (ktiles + sh.kg - 1) / sh.kg;
         const int max_splits = allow_split ? std::min(16, std::max(1, steps_total / 2)) : 1;
@@ -797,6 +829,12 @@ void launch_conv_mfma(const ConvArgs& a, int tile, bool vec, hipStream_t s) {
         case kTile64x128W8: launch_tile<64, 128, 32, 32, 1>(a, vec, grid, s); break;
         case kTile32x64K4W8: launch_tile<32, 64, 32, 32, 4>(a, vec, grid, s); break;
         case kTile32x32K8W8: launch_tile<32, 32, 32, 32, 8>(a, vec, grid, s); break;
+        case kTile16x16K4: launch_tile<16, 16, 16, 16, 4>(a, vec, grid, s); break;
+        case kTile16x32K4: launch_tile<16, 32, 16, 32, 4>(a, vec, grid, s); break;
+        case kTile32x16K4: launch_tile<32, 16, 32, 16, 4>(a, vec, grid, s); break;
+        case kTile16x32K8W8: launch_tile<16, 32, 16, 32, 8>(a, vec, grid, s); break;
+        case kTile32x16K8W8: launch_tile<32, 16, 32, 16, 8>(a, vec, grid, s); break;
+        default: fail("unknown tile");
     }
     if (a.splits > 1) {
         const int64_t total = M * a.Cout * a.groups;
@@ -841,6 +879,12 @@ void launch_conv_mfma_group(const ConvArgs* probs, int count, int tile, hipStrea
         case kTile64x128W8: launch_group<64, 128, 32, 32, 1, kPrefetch>(g, s); break;
         case kTile32x64K4W8: launch_group<32, 64, 32, 32, 4, kPrefetch>(g, s); break;
         case kTile32x32K8W8: launch_group<32, 32, 32, 32, 8, kPrefetch>(g, s); break;
+        case kTile16x16K4: launch_group<16, 16, 16, 16, 4, kPrefetch>(g, s); break;
+        case kTile16x32K4: launch_group<16, 32, 16, 32, 4, kPrefetch>(g, s); break;
+        case kTile32x16K4: launch_group<32, 16, 32, 16, 4, kPrefetch>(g, s); break;
+        case kTile16x32K8W8: launch_group<16, 32, 16, 32, 8, kPrefetch>(g, s); break;
+        case kTile32x16K8W8: launch_group<32, 16, 32, 16, 8, kPrefetch>(g, s); break;
+        default: fail("unknown tile");
     }
 }
 

@@ -1052,7 +1052,7 @@ class Planner {
             }
             if (k::is_wino_tile(opt_.force_tile)) {
                 if (wino) ls = {opt_.force_tile, 1, static_cast<int>((K + k::kConvBK - 1) / k::kConvBK)};
-            } else if (opt_.force_tile >= 0 && opt_.force_tile < k::kNumConvTiles) {
+            } else if (k::is_gemm_tile(opt_.force_tile)) {
                 const int kg = k::conv_tile_shape(opt_.force_tile).kg;
                 const int steps_total = static_cast<int>((K + k::kConvBK - 1) / k::kConvBK + kg - 1) / kg;
                 const int want = std::max(1, std::min(opt_.force_splits, steps_total));

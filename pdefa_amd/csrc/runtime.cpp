@@ -195,8 +195,8 @@ Session::Session(Model& m) : model_(&m) {
     // PDEFA_GROUP_TILE=<tile>: take every group the planner offers, with this
     // implicit-GEMM tile (tests of the grouped kernel)
     if (const char* t = std::getenv("PDEFA_GROUP_TILE")) {
-        for (int i = 0; i < k::kNumConvTiles; ++i)
-            if (std::strcmp(t, k::conv_tile_name(i)) == 0) group_tile_ = i;
+        for (int i = 0; i < k::kNumConvShapes; ++i)
+            if (k::is_gemm_tile(i) && std::strcmp(t, k::conv_tile_name(i)) == 0) group_tile_ = i;
         if (group_tile_ < 0) throw std::runtime_error(std::string("PDEFA_GROUP_TILE: unknown tile ") + t);
     }
 }

@@ -374,15 +374,18 @@ def test_fused_activation_vs_reference(tmp_path, act, cin, cout, k, s, hw):
 
 
 TILES = ["128x128", "128x64", "64x128", "64x64", "128x32", "64x32k2", "32x64k2", "32x32k4",
-         "128x64w8", "64x64k2w8", "128x128w8", "64x128w8", "32x64k4w8", "32x32k8w8"]
+         "128x64w8", "64x64k2w8", "128x128w8", "64x128w8", "32x64k4w8", "32x32k8w8",
+         "16x16k4", "16x32k4", "32x16k4", "16x32k8w8", "32x16k8w8"]
 
 
 @pytest.mark.parametrize("tile", TILES)
 @pytest.mark.parametrize("splits", [1, 3])
-@pytest.mark.parametrize("cin,cout,k,s,hw", [(64, 64, 3, 1, 24), (48, 80, 3, 2, 31), (96, 40, 1, 1, 20)])
+@pytest.mark.parametrize("cin,cout,k,s,hw", [(64, 64, 3, 1, 24), (48, 80, 3, 2, 31), (96, 40, 1, 1, 20),
+                                             (12, 24, 3, 1, 15)])
 def test_conv_every_tile(tmp_path, monkeypatch, tile, splits, cin, cout, k, s, hw):
     """Each implicit-GEMM tile shape (and split-K across workgroups), forced,
-    against the oracle; exact SiLU so no compat-form branch points."""
+    against the oracle; exact SiLU so no compat-form branch points (Cin = 12:
+    4-channel vector loads that straddle a tap within a 32-k slice)."""
     print(f"[case] tile={tile} splits={splits} conv cin={cin} cout={cout} k={k} s={s} hw={hw}", flush=True)
     monkeypatch.setenv("PDEFA_CONV_TILE", tile)
     monkeypatch.setenv("PDEFA_CONV_SPLITS", str(splits))
@@ -566,6 +569,8 @@ GROUPED_CASES = [
     (256, 256, 3, 2, 20, 2, None),     # two groups of 128
     (256, 256, 3, 2, 20, 2, ("64x64", "3")),   # the same with K split across workgroups
     (64, 128, 3, 1, 30, 4, ("32x32k4", "2")),
+    (64, 128, 3, 1, 30, 4, ("16x32k4", "2")),
+    (256, 256, 3, 2, 20, 2, ("32x16k8w8", "2")),
 ]
 
 
@@ -669,7 +674,7 @@ def test_concurrent_capture_matches_serial(yolov8n, monkeypatch):
     assert np.array_equal(again, serial)
 
 
-@pytest.mark.parametrize("tile", ["32x32k4", "64x64", "32x64k2", "128x64w8", "32x64k4w8"])
+@pytest.mark.parametrize("tile", ["32x32k4", "64x64", "32x64k2", "128x64w8", "32x64k4w8", "16x16k4", "32x16k8w8"])
 def test_grouped_launches(yolov8n, monkeypatch, tile):
     """Every conv group the planner offers taken with one tile: independent
     convs of different shapes, activations and output slices (the Detect
