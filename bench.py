@@ -50,8 +50,12 @@ CONV_ROOF = dict(cin=64, cout=64, k=3, stride=1, hw=160)
 CONV_ROOF_FLOPS = 2 * 64 * 64 * 9 * 160 * 160
 KIND_CONV_MFMA, KIND_CONV_DIRECT = 0, 1
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "conv3x3s1_64x64_160_traffic.json")
-CALIB_SHAPE = (1, 16, 1024, 1024)  # 64 MiB in, 64 MiB out: larger than all L2s together
+CALIB_SHAPE = (4096, 4096)  # 64 MiB in, 64 MiB out, contiguous: larger than all L2s together
 CALIB_BYTES = 4 * 16 * 1024 * 1024
+# the calibration dispatch: an elementwise kernel with at least one lane per
+# 4 elements of the 64 MiB tensor (no other elementwise launch is as large)
+CALIB_GRID = CALIB_BYTES // 16
+CALIB_KEY = "calibration copy (eltwise, 64 MiB ReLU)"
 
 
 def log(*a):
@@ -171,7 +175,7 @@ def ingest_pmc(fetch_csv: str, write_csv: str, tile: str):
                 name, val = row["Kernel_Name"], float(row["Counter_Value"])
                 if "conv_mfma_kernel" in name or "conv_wino_kernel" in name:
                     convs.setdefault(name, []).append(val)
-                elif "eltwise_kernel" in name and int(row.get("Grid_Size", 0)) >= CALIB_BYTES // 4:
+                elif "eltwise" in name and int(row.get("Grid_Size", 0)) >= CALIB_GRID:
                     calib.append(val)
         if not convs or not calib:
             raise SystemExit(f"{path}: no {counter} rows for the conv or the calibration copy")
@@ -316,8 +320,9 @@ def session_run_stats(eng: native.Engine, batch: int, warmup: int = 5, runs: int
 
 
 COUNTER_DIR = os.path.join(ROOT, "profiles")
-BANDWIDTH_KERNELS = ("maxpool_chain_kernel", "detect_head_kernel", "detect_decode_kernel", "eltwise_kernel",
-                     "resize_nearest_kernel", "maxpool_kernel", "softmax_kernel", "letterbox_kernel")
+BANDWIDTH_KERNELS = ("maxpool_chain_kernel", "maxpool_chain_vec_kernel", "detect_head_kernel", "detect_decode_kernel",
+                     "eltwise_kernel", "eltwise_vec_kernel", "calibration copy", "resize_nearest_kernel",
+                     "maxpool_kernel", "softmax_kernel", "letterbox_kernel")
 
 
 def _kernel_key(name: str) -> str:
@@ -350,13 +355,13 @@ def ingest_counters(name: str, trace_csv: str, mfma_csv: str, fetch_csv: str = N
     SIMDs); the MOPS counter x 512 = fp32 MFMA flops executed);
     fetch_csv / write_csv: FETCH_SIZE and WRITE_SIZE (KiB per dispatch) runs
     with the 64 MiB calibration copy, which scales each counter to bytes."""
-    calib_grid = CALIB_BYTES // 4
+    calib_grid = CALIB_GRID
     dur, calls = {}, {}
     for r in _read_rows(trace_csv):
         k = _kernel_key(r["Kernel_Name"])
         grid = int(r.get("Grid_Size") or r.get("Grid_Size_X") or 0)
-        if "eltwise_kernel" in k and grid >= calib_grid:
-            k = "calibration copy (eltwise_kernel, 64 MiB ReLU)"
+        if "eltwise" in k and grid >= calib_grid:
+            k = CALIB_KEY
         dur.setdefault(k, []).append((int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) * 1e-3)
     def counter(path, cname):
         vals = {}
@@ -364,15 +369,15 @@ def ingest_counters(name: str, trace_csv: str, mfma_csv: str, fetch_csv: str = N
             if r.get("Counter_Name") != cname:
                 continue
             k = _kernel_key(r["Kernel_Name"])
-            if "eltwise_kernel" in k and int(r.get("Grid_Size", 0) or 0) >= calib_grid:
-                k = "calibration copy (eltwise_kernel, 64 MiB ReLU)"
+            if "eltwise" in k and int(r.get("Grid_Size", 0) or 0) >= calib_grid:
+                k = CALIB_KEY
             vals.setdefault(k, []).append(float(r["Counter_Value"]))
         return vals
     util = counter(mfma_csv, "MfmaUtil")
     mops = counter(mfma_csv, "SQ_INSTS_VALU_MFMA_MOPS_F32")
     fetch = counter(fetch_csv, "FETCH_SIZE") if fetch_csv else {}
     write = counter(write_csv, "WRITE_SIZE") if write_csv else {}
-    calib = "calibration copy (eltwise_kernel, 64 MiB ReLU)"
+    calib = CALIB_KEY
     f_scale = w_scale = None
     if calib in fetch and calib in write:
         f_scale = CALIB_BYTES / (statistics.median(fetch[calib]) * 1024.0)

@@ -10,6 +10,7 @@
 #include "act.hpp"
 
 #include <algorithm>
+#include <cstdlib>
 #include <mutex>
 #include <stdexcept>
 #include <string>
@@ -73,6 +74,22 @@ bool fits_i32(const View& v) {
 // Logistic sigmoid, as the Sigmoid operator evaluates it.
 __device__ __forceinline__ float sigmoid_elt(float x) { return 1.0f / (1.0f + expf(-x)); }
 
+// One element of an elementwise op (y: the second operand, unused by unary ops).
+__device__ __forceinline__ float elt_apply(int op, float x, float y, float alpha) {
+    switch (op) {
+        case kEltAdd: return x + y;
+        case kEltSub: return x - y;
+        case kEltMul: return x * y;
+        case kEltDiv: return x / y;
+        case kEltSigmoid: return sigmoid_elt(x);
+        case kEltRelu: return x > 0.0f ? x : 0.0f;
+        case kEltTanh: return tanhf(x);
+        case kEltLeaky: return x > 0.0f ? x : x * alpha;
+        case kEltSilu: return x / (1.0f + expf(-x));
+        default: return x;
+    }
+}
+
 template <typename I>
 __global__ __launch_bounds__(256) void eltwise_kernel(int op, IView<I> out, IView<I> a, IView<I> b, float alpha,
                                                       I total) {
@@ -87,23 +104,105 @@ __global__ __launch_bounds__(256) void eltwise_kernel(int op, IView<I> out, IVie
             ao += idx * a.str[d];
             bo += idx * b.str[d];
         }
-        const float x = a.ptr[ao];
-        float r;
-        switch (op) {
-            case kEltAdd: r = x + b.ptr[bo]; break;
-            case kEltSub: r = x - b.ptr[bo]; break;
-            case kEltMul: r = x * b.ptr[bo]; break;
-            case kEltDiv: r = x / b.ptr[bo]; break;
-            case kEltSigmoid: r = sigmoid_elt(x); break;
-            case kEltRelu: r = x > 0.0f ? x : 0.0f; break;
-            case kEltTanh: r = tanhf(x); break;
-            case kEltLeaky: r = x > 0.0f ? x : x * alpha; break;
-            case kEltSilu: r = x / (1.0f + expf(-x)); break;
-            default: r = x; break;
-        }
-        out.ptr[oo] = r;
+        out.ptr[oo] = elt_apply(op, a.ptr[ao], b.ptr[bo], alpha);
     }
 }
+
+// The three views of an elementwise op with adjacent dims merged wherever
+// every view is contiguous across them (and size-1 dims dropped), innermost
+// last: most graph tensors collapse to one or two dims.
+struct EltDims {
+    int32_t rank = 0;
+    int32_t dims[kMaxRank] = {};
+    int32_t so[kMaxRank] = {}, sa[kMaxRank] = {}, sb[kMaxRank] = {};
+};
+
+// Float4 form: the innermost collapsed dim is contiguous in out and a (and in
+// b, or b is constant along it: b_splat) and a multiple of 4 long, every
+// base and outer stride 16-byte aligned; one lane per 4 consecutive elements,
+// each computed exactly as eltwise_kernel computes it.
+__global__ __launch_bounds__(256) void eltwise_vec_kernel(int op, float* out, const float* a, const float* b,
+                                                          bool b_splat, EltDims d, float alpha, int32_t total4) {
+    const int32_t inner = d.dims[d.rank - 1];
+    for (int32_t i = blockIdx.x * 256 + threadIdx.x; i < total4; i += gridDim.x * 256) {
+        int32_t e = i * 4;
+        const int32_t ix = e % inner;
+        e /= inner;
+        int32_t oo = ix, ao = ix, bo = b_splat ? 0 : ix;
+        for (int k = d.rank - 2; k >= 0; --k) {
+            const int32_t idx = e % d.dims[k];
+            e /= d.dims[k];
+            oo += idx * d.so[k];
+            ao += idx * d.sa[k];
+            bo += idx * d.sb[k];
+        }
+        const float4 x = *reinterpret_cast<const float4*>(a + ao);
+        float4 y;
+        if (b_splat) {
+            const float v = b[bo];
+            y = make_float4(v, v, v, v);
+        } else {
+            y = *reinterpret_cast<const float4*>(b + bo);
+        }
+        float4 r;
+        r.x = elt_apply(op, x.x, y.x, alpha);
+        r.y = elt_apply(op, x.y, y.y, alpha);
+        r.z = elt_apply(op, x.z, y.z, alpha);
+        r.w = elt_apply(op, x.w, y.w, alpha);
+        *reinterpret_cast<float4*>(out + oo) = r;
+    }
+}
+
+namespace {
+
+// Collapsed dims of (out, a, b); false if some extent or stride exceeds int32.
+// An elementwise op may visit its elements in any order, so the dims are
+// first ordered by the output's stride (largest first): a channels-last
+// tensor then has its contiguous channel dim innermost.
+bool collapse_elt(const View& o, const View& a, const View& b, EltDims& c) {
+    int order[kMaxRank];
+    for (int k = 0; k < o.rank; ++k) order[k] = k;
+    std::stable_sort(order, order + o.rank,
+                     [&](int x, int y) { return std::abs(o.str[x]) > std::abs(o.str[y]); });
+    int64_t dims[kMaxRank], so[kMaxRank], sa[kMaxRank], sb[kMaxRank];
+    int r = 0;
+    for (int kk = 0; kk < o.rank; ++kk) {
+        const int k = order[kk];
+        if (o.dims[k] == 1) continue;
+        if (r > 0 && so[r - 1] == o.str[k] * o.dims[k] && sa[r - 1] == a.str[k] * o.dims[k] &&
+            sb[r - 1] == b.str[k] * o.dims[k]) {
+            dims[r - 1] *= o.dims[k];
+            so[r - 1] = o.str[k];
+            sa[r - 1] = a.str[k];
+            sb[r - 1] = b.str[k];
+            continue;
+        }
+        dims[r] = o.dims[k];
+        so[r] = o.str[k];
+        sa[r] = a.str[k];
+        sb[r] = b.str[k];
+        ++r;
+    }
+    if (r == 0) {
+        dims[0] = 1;
+        so[0] = sa[0] = sb[0] = 1;
+        r = 1;
+    }
+    c.rank = r;
+    for (int k = 0; k < r; ++k) {
+        const int64_t m = std::max({dims[k], std::abs(so[k]), std::abs(sa[k]), std::abs(sb[k])});
+        if (m >= (int64_t{1} << 31)) return false;
+        c.dims[k] = static_cast<int32_t>(dims[k]);
+        c.so[k] = static_cast<int32_t>(so[k]);
+        c.sa[k] = static_cast<int32_t>(sa[k]);
+        c.sb[k] = static_cast<int32_t>(sb[k]);
+    }
+    return true;
+}
+
+bool aligned16(const float* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
+
+}  // namespace
 
 void launch_eltwise(int op, const View& out, const View& a, const View& b, float alpha, hipStream_t s) {
     check_view(out, "eltwise out");
@@ -114,6 +213,22 @@ void launch_eltwise(int op, const View& out, const View& a, const View& b, float
     const int64_t total = numel(out);
     if (total == 0) return;
     const View& bb = binary ? b : a;
+    // float4 path (see eltwise_vec_kernel)
+    EltDims c;
+    if (total < (int64_t{1} << 31) && fits_i32(out) && fits_i32(a) && fits_i32(bb) && collapse_elt(out, a, bb, c)) {
+        const int in = c.rank - 1;
+        const bool b_splat = binary && c.sb[in] == 0;
+        bool vec = c.dims[in] % 4 == 0 && c.so[in] == 1 && c.sa[in] == 1 && (b_splat || c.sb[in] == 1) &&
+                   aligned16(out.ptr) && aligned16(a.ptr) && (b_splat || aligned16(bb.ptr));
+        // (a b constant along the inner dim is read one float at a time)
+        for (int k = 0; k < in; ++k) vec = vec && c.so[k] % 4 == 0 && c.sa[k] % 4 == 0 && (b_splat || c.sb[k] % 4 == 0);
+        if (vec) {
+            const int32_t total4 = static_cast<int32_t>(total / 4);
+            hipLaunchKernelGGL(eltwise_vec_kernel, dim3(grid_for(total4)), dim3(256), 0, s, op, out.ptr, a.ptr,
+                               bb.ptr, b_splat, c, alpha, total4);
+            return;
+        }
+    }
     if (fits_i32(out) && fits_i32(a) && fits_i32(bb))
         hipLaunchKernelGGL(eltwise_kernel<int32_t>, dim3(grid_for(total)), dim3(256), 0, s, op, iview<int32_t>(out),
                            iview<int32_t>(a), iview<int32_t>(bb), alpha, static_cast<int32_t>(total));
@@ -391,6 +506,102 @@ __global__ __launch_bounds__(256) void maxpool_chain_kernel(IView<int32_t> o0, I
     }
 }
 
+// The same three pools over channels-last views (channel stride 1, C and
+// every pixel stride a multiple of 4, 16-byte aligned bases): each lane
+// moves float4 runs of 4 channels, so a workgroup's T x T x CB tile (plus the
+// 3r halo) is staged, swept and stored with a quarter of the instructions.
+template <int r>
+__global__ __launch_bounds__(256) void maxpool_chain_vec_kernel(IView<int32_t> o0, IView<int32_t> o1, IView<int32_t> o2,
+                                                                IView<int32_t> in, int tiles_w) {
+    constexpr int T = kPoolTile, CB = kPoolCb, G = CB / 4;  // G float4 groups per pixel
+    constexpr int R3 = 3 * r;
+    constexpr int RH = T + 2 * R3;
+    constexpr int NL = (RH * RH * G + 255) / 256;
+    __shared__ float4 reg[RH * RH * G];    // [RH][RH][G]
+    __shared__ float4 hz[3 * RH * T * G];  // [3][RH][T][G]
+    const int C = o0.dims[1], H = in.dims[2], W = in.dims[3];
+    const int th = blockIdx.x / tiles_w, tw = blockIdx.x - th * tiles_w;
+    const int h0 = th * T, w0 = tw * T, c0 = blockIdx.y * CB, n = blockIdx.z;
+    const float* base = in.ptr + n * in.str[0];
+    const float4 lowest = make_float4(-3.402823466e+38f, -3.402823466e+38f, -3.402823466e+38f, -3.402823466e+38f);
+    auto vmax = [](float4 a, float4 b) {
+        return make_float4(b.x > a.x ? b.x : a.x, b.y > a.y ? b.y : a.y, b.z > a.z ? b.z : a.z, b.w > a.w ? b.w : a.w);
+    };
+    float4 v[NL];
+#pragma unroll
+    for (int j = 0; j < NL; ++j) {
+        const int i = threadIdx.x + 256 * j;
+        const int g = i % G, p = i / G;
+        const int rx = p % RH, ry = p / RH;
+        const int h = h0 - R3 + ry, w = w0 - R3 + rx;
+        const bool ok = (i < RH * RH * G) & (h >= 0) & (h < H) & (w >= 0) & (w < W) & (c0 + 4 * g < C);
+        const float4 x = *reinterpret_cast<const float4*>(base + (ok ? c0 + 4 * g + h * in.str[2] + w * in.str[3] : 0));
+        // (a float4 select, written per component)
+        v[j].x = ok ? x.x : lowest.x;
+        v[j].y = ok ? x.y : lowest.y;
+        v[j].z = ok ? x.z : lowest.z;
+        v[j].w = ok ? x.w : lowest.w;
+    }
+#pragma unroll
+    for (int j = 0; j < NL; ++j) {
+        const int i = threadIdx.x + 256 * j;
+        if (i < RH * RH * G) reg[i] = v[j];
+    }
+    __syncthreads();
+    for (int i = threadIdx.x; i < RH * T * G; i += 256) {
+        const int g = i % G, p = i / G;
+        const int tx = p % T, ry = p / T;
+        const float4* row = reg + ry * RH * G + g;
+        const int x = R3 + tx;
+        // running maximum over radii 1..3r; the three widths are its values at r, 2r, 3r
+        float4 m = row[x * G], m1 = m, m2 = m;
+#pragma unroll
+        for (int d = 1; d <= R3; ++d) {
+            m = vmax(vmax(m, row[(x - d) * G]), row[(x + d) * G]);
+            if (d == r) m1 = m;
+            if (d == 2 * r) m2 = m;
+        }
+        hz[((0 * RH + ry) * T + tx) * G + g] = m1;
+        hz[((1 * RH + ry) * T + tx) * G + g] = m2;
+        hz[((2 * RH + ry) * T + tx) * G + g] = m;
+    }
+    __syncthreads();
+    for (int i = threadIdx.x; i < T * T * G; i += 256) {
+        const int g = i % G, p = i / G;
+        const int tx = p % T, ty = p / T;
+        const int h = h0 + ty, w = w0 + tx;
+        if (h >= H || w >= W || c0 + 4 * g >= C) continue;
+        const int y = R3 + ty;
+        // column maximum of row-maxima plane k over radius rad (row stride T*G)
+        auto colmax = [&](int k, auto rad_c) {
+            constexpr int rad = decltype(rad_c)::value;
+            const float4* col = hz + (k * RH * T + tx) * G + g;
+            float4 m = col[y * T * G];
+#pragma unroll
+            for (int d = 1; d <= rad; ++d) m = vmax(vmax(m, col[(y - d) * T * G]), col[(y + d) * T * G]);
+            return m;
+        };
+        const float4 r0 = colmax(0, std::integral_constant<int, r>{});
+        const float4 r1 = colmax(1, std::integral_constant<int, 2 * r>{});
+        const float4 r2 = colmax(2, std::integral_constant<int, 3 * r>{});
+        const int cc = c0 + 4 * g;
+        *reinterpret_cast<float4*>(o0.ptr + n * o0.str[0] + cc + h * o0.str[2] + w * o0.str[3]) = r0;
+        *reinterpret_cast<float4*>(o1.ptr + n * o1.str[0] + cc + h * o1.str[2] + w * o1.str[3]) = r1;
+        *reinterpret_cast<float4*>(o2.ptr + n * o2.str[0] + cc + h * o2.str[2] + w * o2.str[3]) = r2;
+    }
+}
+
+namespace {
+
+// Channels-last float4 form applies: channel stride 1, C and the pixel
+// strides multiples of 4 floats, 16-byte aligned bases.
+bool pool_vec_ok(const View& v) {
+    return v.str[1] == 1 && v.dims[1] % 4 == 0 && v.str[0] % 4 == 0 && v.str[2] % 4 == 0 && v.str[3] % 4 == 0 &&
+           (reinterpret_cast<uintptr_t>(v.ptr) & 15) == 0;
+}
+
+}  // namespace
+
 void launch_maxpool_chain(const View& out0, const View& out1, const View& out2, const View& in, int k,
                           hipStream_t s) {
     check_view(out0, "maxpool_chain out0");
@@ -415,6 +626,15 @@ void launch_maxpool_chain(const View& out0, const View& out1, const View& out2, 
     const auto o0 = iview<int32_t>(out0), o1 = iview<int32_t>(out1), o2 = iview<int32_t>(out2);
     const auto x = iview<int32_t>(in);
     const int tw = static_cast<int>(tiles_w);
+    if (pool_vec_ok(out0) && pool_vec_ok(out1) && pool_vec_ok(out2) && pool_vec_ok(in)) {
+        switch (k / 2) {
+            case 0: hipLaunchKernelGGL(maxpool_chain_vec_kernel<0>, grid, dim3(256), 0, s, o0, o1, o2, x, tw); break;
+            case 1: hipLaunchKernelGGL(maxpool_chain_vec_kernel<1>, grid, dim3(256), 0, s, o0, o1, o2, x, tw); break;
+            case 2: hipLaunchKernelGGL(maxpool_chain_vec_kernel<2>, grid, dim3(256), 0, s, o0, o1, o2, x, tw); break;
+            default: hipLaunchKernelGGL(maxpool_chain_vec_kernel<3>, grid, dim3(256), 0, s, o0, o1, o2, x, tw); break;
+        }
+        return;
+    }
     switch (k / 2) {
         case 0: hipLaunchKernelGGL(maxpool_chain_kernel<0>, grid, dim3(256), 0, s, o0, o1, o2, x, tw); break;
         case 1: hipLaunchKernelGGL(maxpool_chain_kernel<1>, grid, dim3(256), 0, s, o0, o1, o2, x, tw); break;

@@ -367,6 +367,30 @@ def build_topk_gather(shape, axis: int, k: int, gather_idx=None, seed: int = 4) 
     return b.model(list(shape), [None] * len(outs), outs), x
 
 
+def build_eltwise_chain(n: int, c: int, h: int, w: int, seed: int = 6) -> Tuple[EngineModel, np.ndarray]:
+    """A chain of elementwise nodes over an [n, c, h, w] input: Add of a
+    per-channel constant, Mul by a per-pixel constant, Sub of a scalar, Div
+    by a full-shape constant, then Sigmoid, Relu, LeakyRelu (slope 0.1) and
+    Tanh, each node feeding the next (broadcast along every kind of dim)."""
+    rng = np.random.default_rng(seed)
+    b = GraphBuilder()
+    pc = b.const("per_channel", rng.uniform(-1, 1, (1, c, 1, 1)))
+    pp = b.const("per_pixel", rng.uniform(0.5, 1.5, (1, 1, h, w)))
+    sc = b.const("scalar", rng.uniform(-1, 1, (1,)))
+    full = b.const("full", rng.uniform(0.5, 2.0, (1, c, h, w)))
+    y = b.node("Add", "/add", [-1, pc])
+    y = b.node("Mul", "/mul", [y, pp])
+    y = b.node("Sub", "/sub", [y, sc])
+    y = b.node("Div", "/div", [y, full])
+    y = b.node("Sigmoid", "/sigmoid", [y])
+    y = b.node("Sub", "/center", [y, b.const("half", [0.5])])
+    y = b.node("Relu", "/relu", [y])
+    y = b.node("LeakyRelu", "/leaky", [b.node("Sub", "/shift", [y, b.const("q", [0.25])])], leaky_slope=0.1)
+    y = b.node("Tanh", "/tanh", [y])
+    x = rng.uniform(-3, 3, (n, c, h, w)).astype(np.float32)
+    return b.model([n, c, h, w], [n, c, h, w], [y]), x
+
+
 def build_pool_chain(n: int, c: int, h: int, w: int, k: int, seed: int = 5) -> Tuple[EngineModel, np.ndarray]:
     """SPPF's pooling part on its own: three chained MaxPool(k, stride 1,
     pad k//2) and the channel Concat of the input and the three results.
@@ -380,6 +404,18 @@ def build_pool_chain(n: int, c: int, h: int, w: int, k: int, seed: int = 5) -> T
                          pad_h=k // 2, pad_w=k // 2))
     cat = b.node("Concat", "/Concat", ys, axis=1)
     return b.model([n, c, h, w], [n, 4 * c, h, w], [cat]), x
+
+
+def build_sppf(n: int, c: int, h: int, w: int, k: int = 5, seed: int = 8) -> Tuple[EngineModel, np.ndarray]:
+    """The YOLOv8 SPPF block on its own (Conv1x1 -> three chained
+    MaxPool(k, stride 1, pad k//2) -> Concat of the four -> Conv1x1, both
+    convs with SiLU): the pools then run over channels-last conv outputs, as
+    in the network.  Returns the model and a seeded input ~ U[0, 1)."""
+    rng = np.random.default_rng(seed)
+    b = GraphBuilder()
+    y = _Yolo(b, rng, 0.0).sppf(-1, c, c, "sppf")
+    x = rng.uniform(0.0, 1.0, (n, c, h, w)).astype(np.float32)
+    return b.model([n, c, h, w], [n, c, h, w], [y]), x
 
 
 def build_tiny(seed: int = 3) -> EngineModel:

@@ -30,6 +30,8 @@ import numpy as np
 import pytest
 
 from oracle import decode_ref, graph_ref, ref_lib
+
+import ref_worker
 from pdefa_amd import native, yolo_synth as ys
 from pdefa_amd.postprocess import decode_yolo
 
@@ -62,17 +64,19 @@ def norm_rel(got, want):
     return float(np.linalg.norm(got.astype(np.float64) - w) / max(np.linalg.norm(w), 1e-300))
 
 
-def reference_outputs(path, x):
-    """The reference engine's output for each image of x (it has no batch
-    path: BatchInference runs one session per image), stacked."""
+def reference_runs(path, x, split=True):
+    """The reference engine's outputs for each image of x (a list over
+    images of that run's outputs; split=False: one run on all of x), from
+    the worker process of ref_worker."""
     if not ref_lib.available():
         pytest.fail("oracle/_ref/libpdefa_ref.so is missing: build it with __graft_entry__.build()")
-    ref_lib.set_threads(min(16, os.cpu_count() or 1))
-    r = ref_lib.RefSession(path)
-    try:
-        return np.concatenate([r.run(x[i:i + 1])[0] for i in range(x.shape[0])], axis=0)
-    finally:
-        r.close()
+    return ref_worker.run(path, x, split)
+
+
+def reference_outputs(path, x):
+    """The reference engine's first output for each image of x (it has no
+    batch path: BatchInference runs one session per image), stacked."""
+    return np.concatenate([outs[0] for outs in reference_runs(path, x)], axis=0)
 
 
 def _save(name, arr):
@@ -273,6 +277,9 @@ CONV_CASES = [
     (5, 7, 3, 1, 11),      # odd Cin, Cout < 8 (direct kernel)
     (4, 6, 3, 1, 13),      # direct kernel, 4 input channels all loaded up front
     (1, 8, 3, 2, 17),      # direct kernel, one input channel
+    (3, 48, 3, 2, 50),     # YOLOv8m stem: 48 output channels, partial pixel blocks
+    (1, 64, 5, 2, 23),     # 5x5 kernel
+    (3, 40, 3, 1, 37),     # stride 1, 40 output channels
     (256, 256, 3, 1, 20),  # deep layer: split-K
     (96, 144, 3, 2, 33),
     (576, 64, 3, 1, 10),   # Cin > 512: GEMM-path SiLU in the reference
@@ -468,6 +475,47 @@ def test_pool_chain(tmp_path, n, c, h, w, k):
     assert " maxpool_chain " in plan
     want = graph_ref.run_graph(model, [x])[0]
     np.testing.assert_array_equal(got, want)
+
+
+@pytest.mark.parametrize("n,c,h,w,k", [(1, 128, 20, 20, 5), (2, 40, 13, 11, 5), (1, 16, 9, 30, 3), (3, 24, 7, 7, 7)])
+def test_sppf_channels_last(tmp_path, n, c, h, w, k):
+    """The SPPF block (conv, three chained pools, concat, conv): the fused
+    pool step reads and writes channels-last conv outputs, which takes the
+    float4 pool kernel, against the oracle."""
+    print(f"[case] sppf n={n} c={c} h={h} w={w} k={k}", flush=True)
+    model, x = ys.build_sppf(n, c, h, w, k)
+    path = str(tmp_path / "sppf.engine")
+    ys.save(model, path)
+    eng = native.Engine(path)
+    try:
+        got = eng.run(x)[0]
+        plan = eng.plan()
+    finally:
+        eng.close()
+    assert " maxpool_chain " in plan
+    want = graph_ref.run_graph(model, [x])[0]
+    assert assert_close(got, want, "sppf") < 1e-4
+
+
+@pytest.mark.parametrize("n,c,h,w", [(2, 12, 7, 9), (1, 10, 5, 6), (3, 64, 20, 20)])
+def test_elementwise_chain(tmp_path, n, c, h, w):
+    """Elementwise nodes with every kind of broadcast (per channel, per
+    pixel, scalar, full shape) against the oracle: channel counts that are a
+    multiple of 4 take the float4 kernel on the channels-last layout, the
+    others the per-element kernel."""
+    print(f"[case] eltwise chain {n}x{c}x{h}x{w}", flush=True)
+    model, x = ys.build_eltwise_chain(n, c, h, w)
+    path = str(tmp_path / "elt.engine")
+    ys.save(model, path)
+    eng = native.Engine(path)
+    try:
+        got = eng.run(x)[0]
+    finally:
+        eng.close()
+    want = graph_ref.run_graph(model, [x])[0]
+    assert got.shape == want.shape
+    err = np.abs(got.astype(np.float64) - want)
+    assert err.max() <= 1e-6 + 1e-6 * np.abs(want).max(), err.max()
 
 
 def test_single_conv_no_act(tmp_path):
@@ -994,13 +1042,7 @@ def test_topk_head_vs_reference(tmp_path, anchors, nc, k, k_dtype):
     want = graph_ref.run_graph(model, [x])
     np.testing.assert_array_equal(got[0], want[0])
     np.testing.assert_array_equal(got[1].astype(np.float32), want[1])
-    if not ref_lib.available():
-        pytest.fail("oracle/_ref/libpdefa_ref.so is missing: build it with __graft_entry__.build()")
-    r = ref_lib.RefSession(path)
-    try:
-        ref = r.run(x)
-    finally:
-        r.close()
+    ref = reference_runs(path, x, split=False)[0]
     np.testing.assert_array_equal(got[0], ref[0])
     np.testing.assert_array_equal(got[1].astype(np.float32), ref[1])
 
@@ -1023,10 +1065,6 @@ def test_topk_gather_elements(tmp_path, shape, axis, k):
     assert got[1].dtype == np.int32
     for g, w in zip(got, want):
         np.testing.assert_array_equal(g.astype(np.float32), w)
-    r = ref_lib.RefSession(path)
-    try:
-        ref = r.run(x)
-    finally:
-        r.close()
+    ref = reference_runs(path, x, split=False)[0]
     for g, w in zip(got, ref):
         np.testing.assert_array_equal(g.astype(np.float32), w)
