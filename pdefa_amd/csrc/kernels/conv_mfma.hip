@@ -149,38 +149,6 @@ __device__ __forceinline__ void conv_tile(const ConvArgs& a, const int bx, const
     const int nk = (kb_end - kb_begin + KG - 1) / KG;  // pipeline steps
     const int taps = a.KH * a.KW;
 
-    // Epilogue row table: element offset of each tile row in the output (or in
-    // this split's partial slab) and in the residual; -1 past the last row.
-    // Built once here, read after the pipeline's barriers.
-    int64_t* s_yoff = reinterpret_cast<int64_t*>(reinterpret_cast<char*>(smem) + lds_stage_bytes<BM, BN, KG>());
-    int64_t* s_roff = s_yoff + BM;
-    int64_t* s_uoff = s_roff + BM;
-    if (tid < BM) {
-        const int m = m0 + tid;
-        int64_t yo = -1, ro = 0, uo = 0;
-        if (m < M) {
-            if (a.splits > 1) {
-                yo = ((static_cast<int64_t>(grp) * a.splits + bz) * M + m) * a.Cout;
-            } else {
-                const int n = m / HoWo;
-                const int rem = m - n * HoWo;
-                const int ho = rem / a.Wo;
-                const int wo = rem - ho * a.Wo;
-                yo = static_cast<int64_t>(n) * a.y_sn + static_cast<int64_t>(ho) * a.y_sh +
-                     static_cast<int64_t>(wo) * a.y_sw + g_out;
-                if (a.res)
-                    ro = static_cast<int64_t>(n) * a.r_sn + static_cast<int64_t>(ho) * a.r_sh +
-                         static_cast<int64_t>(wo) * a.r_sw + g_out;
-                if (a.up)
-                    uo = static_cast<int64_t>(n) * a.u_sn + static_cast<int64_t>(2 * ho) * a.u_sh +
-                         static_cast<int64_t>(2 * wo) * a.u_sw + g_out;
-            }
-        }
-        s_yoff[tid] = yo;
-        s_roff[tid] = ro;
-        s_uoff[tid] = uo;
-    }
-
     // Bias of this lane's output columns, loaded now so its latency hides
     // behind the K loop (the epilogue only reads registers).
     const int half = lane >> 5;
@@ -381,6 +349,39 @@ __device__ __forceinline__ void conv_tile(const ConvArgs& a, const int bx, const
         constexpr int J = decltype(jc)::value + 1;
         if (J < nk) load_step(kb_begin + J * KG, areg[J], breg[J], amask[J]);
     });
+    // Epilogue row table: element offset of each tile row in the output (or in
+    // this split's partial slab) and in the residual; -1 past the last row.
+    // Built while the first steps' loads are in flight, read after the
+    // pipeline's barriers.
+    int64_t* s_yoff = reinterpret_cast<int64_t*>(reinterpret_cast<char*>(smem) + lds_stage_bytes<BM, BN, KG>());
+    int64_t* s_roff = s_yoff + BM;
+    int64_t* s_uoff = s_roff + BM;
+    if (tid < BM) {
+        const int m = m0 + tid;
+        int64_t yo = -1, ro = 0, uo = 0;
+        if (m < M) {
+            if (a.splits > 1) {
+                yo = ((static_cast<int64_t>(grp) * a.splits + bz) * M + m) * a.Cout;
+            } else {
+                const int n = m / HoWo;
+                const int rem = m - n * HoWo;
+                const int ho = rem / a.Wo;
+                const int wo = rem - ho * a.Wo;
+                yo = static_cast<int64_t>(n) * a.y_sn + static_cast<int64_t>(ho) * a.y_sh +
+                     static_cast<int64_t>(wo) * a.y_sw + g_out;
+                if (a.res)
+                    ro = static_cast<int64_t>(n) * a.r_sn + static_cast<int64_t>(ho) * a.r_sh +
+                         static_cast<int64_t>(wo) * a.r_sw + g_out;
+                if (a.up)
+                    uo = static_cast<int64_t>(n) * a.u_sn + static_cast<int64_t>(2 * ho) * a.u_sh +
+                         static_cast<int64_t>(2 * wo) * a.u_sw + g_out;
+            }
+        }
+        s_yoff[tid] = yo;
+        s_roff[tid] = ro;
+        s_uoff[tid] = uo;
+    }
+
     store_step(0, areg[0], breg[0], amask[0]);
     __syncthreads();
     // In the main loop both the load and the store happen unconditionally, so

@@ -41,6 +41,7 @@ namespace k {
 
 typedef float floatx4 __attribute__((ext_vector_type(4)));
 typedef float floatx16 __attribute__((ext_vector_type(16)));
+typedef unsigned int uintx4 __attribute__((ext_vector_type(4)));
 
 namespace {
 
@@ -48,7 +49,6 @@ constexpr int kWT = 32;  // tiles per workgroup (GEMM rows)
 constexpr int kCK = 8;   // input channels per K step (4 per lane half)
 constexpr int kXcds = 8;
 constexpr int kMaxCin = 4096;
-constexpr int kXchRow = kWT + 4;  // exchange rows: 32 tiles + 4 floats of padding
 // Input, weights, output and residual are addressed by 32-bit byte offsets
 // from their base.  Their spans stay under kWinoMaxViewBytes, so an offset
 // derived from kWinoNoPixel (less up to 16 bytes, or plus a valid offset, or
@@ -127,9 +127,13 @@ __global__ void pack_wino_weights_kernel(float* dst, const float* w, int Cout, i
 
 template <int BN, int ACT, bool RES>
 __global__ __launch_bounds__(256) void conv_wino_kernel(ConvArgs a, int tiles_h, int tiles_w, int x_bytes,
-                                                        int u_bytes, int y_bytes, int r_bytes) {
+                                                        int u_bytes, int y_bytes, int r_bytes, int vec_out) {
     constexpr int CB = BN / 32;  // 32-wide channel blocks per wave
-    __shared__ __attribute__((aligned(16))) float xch[4 * 2 * BN * kXchRow];  // [row i][column c][channel][tile]
+    // Exchange rows [row i][column c][tile] hold BN channels and 8 floats of
+    // padding: the two lane halves of a column-transform write (tiles 4
+    // apart) then fall on disjoint LDS banks.
+    constexpr int kXchRow = BN + 8;
+    __shared__ __attribute__((aligned(16))) float xch[4 * 2 * kWT * kXchRow];
     // per tile of the workgroup: byte offsets of its four output (and
     // residual) pixels (r, c) at [2r + c], kWinoNoPixel for pixels outside
     // the output (or past the last tile)
@@ -158,9 +162,20 @@ __global__ __launch_bounds__(256) void conv_wino_kernel(ConvArgs a, int tiles_h,
     const int cop = (a.Cout + 63) / 64 * 64;
     const int cq = (a.Cin + kCK - 1) / kCK * (kCK / 4);
 
-    // bias of this lane's epilogue channel (read now, used after the K loop)
-    const int e_col = tid % BN;
-    const float bias_v = n0 + e_col < a.Cout ? a.bias[n0 + e_col] : 0.0f;
+    // The epilogue's lane = (tile, 4 consecutive channels), channels fastest:
+    // the lane's channels are the same for each of its CB tiles.  Their biases
+    // are read now, used after the K loop.
+    constexpr int G4 = BN / 4;  // channel groups per tile
+    const int c4 = (tid % G4) * 4;
+    int32_t cob[4];  // byte offset of each channel, kWinoNoPixel past Cout
+    floatx4 bias4;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        const int co = n0 + c4 + k;
+        cob[k] = co < a.Cout ? co * 4 : kWinoNoPixel;
+        bias4[k] = co < a.Cout ? a.bias[co] : 0.0f;
+    }
+
     if (tid < kWT) {  // read after the barrier that precedes the epilogue
         const int tg = t0 + tid;
         const int nn = tg / tiles_img;
@@ -320,92 +335,103 @@ __global__ __launch_bounds__(256) void conv_wino_kernel(ConvArgs a, int tiles_h,
 
     // column transform in registers: P[i][0] = M0 + M1 + M2, P[i][1] = M1 - M2 - M3.
     // 32x32 block register e of lane l holds tile row 8*(e/4) + 4*(l/32) + e%4,
-    // column l%32: registers 4q..4q+3 are four consecutive tiles, stored as one
-    // 16-byte run of the [channel][tile] exchange (rows padded to 36 floats).
+    // column (channel) l%32, written to the channel-fastest exchange.
 #pragma unroll
     for (int cb = 0; cb < CB; ++cb)
 #pragma unroll
-        for (int qd = 0; qd < 4; ++qd) {
+        for (int e = 0; e < 16; ++e) {
             const int col = cb * 32 + l32;
-            const int trow = 8 * qd + 4 * half;
-            floatx4 p0, p1;
-#pragma unroll
-            for (int k = 0; k < 4; ++k) {
-                const int e = 4 * qd + k;
-                const float m0 = acc[0][cb][e], m1 = acc[1][cb][e], m2 = acc[2][cb][e], m3 = acc[3][cb][e];
-                p0[k] = m0 + m1 + m2;
-                p1[k] = m1 - m2 - m3;
-            }
-            *reinterpret_cast<floatx4*>(&xch[((wi_row * 2 + 0) * BN + col) * kXchRow + trow]) = p0;
-            *reinterpret_cast<floatx4*>(&xch[((wi_row * 2 + 1) * BN + col) * kXchRow + trow]) = p1;
+            const int trow = 8 * (e / 4) + 4 * half + e % 4;
+            const float m0 = acc[0][cb][e], m1 = acc[1][cb][e], m2 = acc[2][cb][e], m3 = acc[3][cb][e];
+            xch[((wi_row * 2 + 0) * kWT + trow) * kXchRow + col] = m0 + m1 + m2;
+            xch[((wi_row * 2 + 1) * kWT + trow) * kXchRow + col] = m1 - m2 - m3;
         }
     __syncthreads();
 
-    // row transform, bias, activation, residual: lane = (channel, blocks of 4
-    // tile rows), channel fastest; every LDS read, then every residual load,
-    // then every store of the lane in flight together (straight-line, predicated)
-    constexpr int RPT = kWT * BN / 256;  // tile rows per lane
-    constexpr int NB = RPT / 4;          // blocks of 4 tile rows per lane
-    constexpr int GSTEP = 256 / BN;      // lanes per channel
-    const int co = n0 + e_col;
-    // byte offset of this lane's channel; kWinoNoPixel past Cout, so that its
-    // stores fall outside the buffer range and are dropped
-    const int32_t co_b = co < a.Cout ? co * 4 : kWinoNoPixel;
-    float yv[RPT][4];
-    int32_t yo[RPT][4], ro[RPT][4];
+    // row transform, bias, activation, residual: lane = (tile, 4 consecutive
+    // channels), CB tiles per lane.  Outputs and residuals move as 16-byte
+    // runs when vec_out is set (output and residual rows 16-byte aligned,
+    // Cout % 4 == 0), else as single floats, channels past Cout skipped.
+    // Buffer-range checks drop stores (and zero loads) at kWinoNoPixel
+    // offsets, so pixels outside the output need no branch.
+    const __amdgpu_buffer_rsrc_t ybuf = __builtin_amdgcn_make_buffer_rsrc(a.y, 0, y_bytes, kWinoBufferFlags);
+    const __amdgpu_buffer_rsrc_t rbuf =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(RES ? a.res : a.y), 0, RES ? r_bytes : 0,
+                                          kWinoBufferFlags);
+    floatx4 yv[CB][4];
+    int32_t yo[CB][4], ro[CB][4];
 #pragma unroll
-    for (int bk = 0; bk < NB; ++bk) {
-        const int trow0 = 4 * (tid / BN + bk * GSTEP);
+    for (int r = 0; r < CB; ++r) {
+        const int tl = tid / G4 + r * (256 / G4);
         floatx4 p[4][2];
 #pragma unroll
         for (int i = 0; i < 4; ++i)
 #pragma unroll
             for (int c = 0; c < 2; ++c)
-                p[i][c] = *reinterpret_cast<const floatx4*>(&xch[((i * 2 + c) * BN + e_col) * kXchRow + trow0]);
+                p[i][c] = *reinterpret_cast<const floatx4*>(&xch[((i * 2 + c) * kWT + tl) * kXchRow + c4]);
 #pragma unroll
-        for (int k = 0; k < 4; ++k) {
-            const int rk = bk * 4 + k;
-#pragma unroll
-            for (int c = 0; c < 2; ++c) {
-                yv[rk][c] = p[0][c][k] + p[1][c][k] + p[2][c][k];      // output row 0, column c
-                yv[rk][2 + c] = p[1][c][k] - p[2][c][k] - p[3][c][k];  // output row 1, column c
-            }
-            const int4 y4 = *reinterpret_cast<const int4*>(&s_yo4[trow0 + k][0]);
-            yo[rk][0] = y4.x;
-            yo[rk][1] = y4.y;
-            yo[rk][2] = y4.z;
-            yo[rk][3] = y4.w;
-            if constexpr (RES) {
-                const int4 r4 = *reinterpret_cast<const int4*>(&s_ro4[trow0 + k][0]);
-                ro[rk][0] = r4.x;
-                ro[rk][1] = r4.y;
-                ro[rk][2] = r4.z;
-                ro[rk][3] = r4.w;
-            }
+        for (int c = 0; c < 2; ++c) {
+            yv[r][c] = p[0][c] + p[1][c] + p[2][c];      // output row 0, column c
+            yv[r][2 + c] = p[1][c] - p[2][c] - p[3][c];  // output row 1, column c
+        }
+        const int4 y4 = *reinterpret_cast<const int4*>(&s_yo4[tl][0]);
+        yo[r][0] = y4.x;
+        yo[r][1] = y4.y;
+        yo[r][2] = y4.z;
+        yo[r][3] = y4.w;
+        if constexpr (RES) {
+            const int4 r4 = *reinterpret_cast<const int4*>(&s_ro4[tl][0]);
+            ro[r][0] = r4.x;
+            ro[r][1] = r4.y;
+            ro[r][2] = r4.z;
+            ro[r][3] = r4.w;
         }
     }
-    // Buffer-range checked stores and loads: an offset at or past the view's
-    // byte extent stores nothing and loads zero, so pixels outside the output
-    // need no branch.
-    const __amdgpu_buffer_rsrc_t ybuf = __builtin_amdgcn_make_buffer_rsrc(a.y, 0, y_bytes, kWinoBufferFlags);
-    float rv[RPT][4];
-    if constexpr (RES) {
-        const __amdgpu_buffer_rsrc_t rbuf =
-            __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(a.res), 0, r_bytes, kWinoBufferFlags);
+    if (vec_out) {
+        floatx4 rv[CB][4];
+        if constexpr (RES) {
 #pragma unroll
-        for (int k = 0; k < RPT; ++k)
+            for (int r = 0; r < CB; ++r)
+#pragma unroll
+                for (int q = 0; q < 4; ++q)
+                    rv[r][q] = __builtin_bit_cast(
+                        floatx4, __builtin_amdgcn_raw_buffer_load_b128(rbuf, ro[r][q] + cob[0], 0, 0));
+        }
+#pragma unroll
+        for (int r = 0; r < CB; ++r)
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                floatx4 v;
+#pragma unroll
+                for (int k = 0; k < 4; ++k) {
+                    v[k] = act_fixed<ACT>(yv[r][q][k] + bias4[k], a.act, a.slope);
+                    if (RES) v[k] += rv[r][q][k];
+                }
+                __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(uintx4, v), ybuf, yo[r][q] + cob[0], 0, 0);
+            }
+    } else {
+        float rv[CB][4][4];
+        if constexpr (RES) {
+#pragma unroll
+            for (int r = 0; r < CB; ++r)
+#pragma unroll
+                for (int q = 0; q < 4; ++q)
+#pragma unroll
+                    for (int k = 0; k < 4; ++k)
+                        rv[r][q][k] =
+                            __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rbuf, ro[r][q] + cob[k], 0, 0));
+        }
+#pragma unroll
+        for (int r = 0; r < CB; ++r)
 #pragma unroll
             for (int q = 0; q < 4; ++q)
-                rv[k][q] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rbuf, ro[k][q] + co_b, 0, 0));
+#pragma unroll
+                for (int k = 0; k < 4; ++k) {
+                    float v = act_fixed<ACT>(yv[r][q][k] + bias4[k], a.act, a.slope);
+                    if (RES) v += rv[r][q][k];
+                    __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v), ybuf, yo[r][q] + cob[k], 0, 0);
+                }
     }
-#pragma unroll
-    for (int k = 0; k < RPT; ++k)
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-            float v = act_fixed<ACT>(yv[k][q] + bias_v, a.act, a.slope);
-            if (RES) v += rv[k][q];
-            __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v), ybuf, yo[k][q] + co_b, 0, 0);
-        }
 }
 
 namespace {
@@ -413,14 +439,15 @@ namespace {
 // Byte extents of the input, transformed weights, output and residual.
 struct WinoBytes {
     int x, u, y, r;
+    int vec;  // outputs (and residuals) as 16-byte runs
 };
 
 template <int BN, int ACT>
 void launch_act(const ConvArgs& a, dim3 grid, int th, int tw, WinoBytes b, hipStream_t s) {
     if (a.res)
-        hipLaunchKernelGGL((conv_wino_kernel<BN, ACT, true>), grid, dim3(256), 0, s, a, th, tw, b.x, b.u, b.y, b.r);
+        hipLaunchKernelGGL((conv_wino_kernel<BN, ACT, true>), grid, dim3(256), 0, s, a, th, tw, b.x, b.u, b.y, b.r, b.vec);
     else
-        hipLaunchKernelGGL((conv_wino_kernel<BN, ACT, false>), grid, dim3(256), 0, s, a, th, tw, b.x, b.u, b.y, b.r);
+        hipLaunchKernelGGL((conv_wino_kernel<BN, ACT, false>), grid, dim3(256), 0, s, a, th, tw, b.x, b.u, b.y, b.r, b.vec);
 }
 
 template <int BN>
@@ -460,6 +487,11 @@ void launch_conv_wino(const ConvArgs& a, int bn, hipStream_t s) {
     b.u = static_cast<int>(wino_packed_elems(a.Cout, a.Cin) * 4);
     b.y = static_cast<int>(view_bytes(a.N, a.Ho, a.Wo, a.Cout, a.y_sn, a.y_sh, a.y_sw));
     b.r = a.res ? static_cast<int>(view_bytes(a.N, a.Ho, a.Wo, a.Cout, a.r_sn, a.r_sh, a.r_sw)) : 0;
+    auto rows16 = [](const float* p, int64_t sn, int64_t sh, int64_t sw) {
+        return reinterpret_cast<uintptr_t>(p) % 16 == 0 && sn % 4 == 0 && sh % 4 == 0 && sw % 4 == 0;
+    };
+    b.vec = a.Cout % 4 == 0 && rows16(a.y, a.y_sn, a.y_sh, a.y_sw) &&
+            (!a.res || rows16(a.res, a.r_sn, a.r_sh, a.r_sw));
     if (bn == 64)
         launch_bn<64>(a, grid, static_cast<int>(tiles_h), static_cast<int>(tiles_w), b, s);
     else

@@ -418,6 +418,38 @@ def build_sppf(n: int, c: int, h: int, w: int, k: int = 5, seed: int = 8) -> Tup
     return b.model([n, c, h, w], [n, c, h, w], [y]), x
 
 
+def build_conv3x3_epilogue(cin: int, cout: int, hw: int, mode: str, side: int = 3,
+                           seed: int = 21) -> Tuple[EngineModel, np.ndarray]:
+    """A 3x3 stride-1 conv (+ SiLU) whose output either takes a residual or
+    lands inside a concat, for the output paths of the conv epilogues.
+
+    mode "add": Add(Conv1x1(x, cin->cout), Conv3x3(x, cin->cout)); the Add
+    becomes the 3x3 conv's residual.  mode "concat": Concat(Conv1x1(x,
+    cin->side), Conv3x3(x, cin->cout)) on channels; the 3x3 conv writes at
+    channel offset `side` of the (channels-last) concat buffer.  Either
+    result feeds a final Conv1x1 to 8 channels, the graph output, so that
+    the 3x3 conv's output stays an inner channels-last tensor.  Returns the
+    model and a seeded input ~ U[0, 1) of shape [1, cin, hw, hw]."""
+    rng = np.random.default_rng(seed)
+    b = GraphBuilder()
+    yb = _Yolo(b, rng, 0.0)
+    if mode == "add":
+        a = yb.conv(-1, cin, cout, 1, 1, "side")
+        c = yb.conv(-1, cin, cout, 3, 1, "main")
+        out = b.node("Add", "/add", [a, c])
+        oc = cout
+    elif mode == "concat":
+        a = yb.conv(-1, cin, side, 1, 1, "side")
+        c = yb.conv(-1, cin, cout, 3, 1, "main")
+        out = b.node("Concat", "/cat", [a, c], axis=1)
+        oc = side + cout
+    else:
+        raise ValueError(mode)
+    out = yb.conv(out, oc, 8, 1, 1, "head")
+    x = rng.uniform(0.0, 1.0, (1, cin, hw, hw)).astype(np.float32)
+    return b.model([1, cin, hw, hw], [1, 8, hw, hw], [out]), x
+
+
 def build_tiny(seed: int = 3) -> EngineModel:
     """A small stand-in for the reference tests' tiny.engine (a 64x64
     Conv -> AvgPool -> Linear to 4 outputs, pdefa/tests/README.md:13-39, not

@@ -441,6 +441,34 @@ def test_winograd_conv(tmp_path, monkeypatch, tile, cin, cout, hw):
 
 
 @pytest.mark.parametrize("tile", ["wino64", "wino32"])
+@pytest.mark.parametrize("mode,cin,cout,side,hw", [("add", 16, 18, 0, 13), ("add", 16, 24, 0, 11),
+                                                   ("concat", 16, 16, 3, 9), ("concat", 16, 20, 4, 10)])
+def test_winograd_epilogue_paths(tmp_path, monkeypatch, tile, mode, cin, cout, side, hw):
+    """The Winograd epilogue's two output paths: 16-byte runs (Cout % 4 == 0,
+    output and residual rows 16-byte aligned) and single floats (Cout = 18;
+    an output at channel offset 3 of a concat), each with and without a
+    fused residual."""
+    print(f"[case] winograd epilogue tile={tile} {mode} cin={cin} cout={cout} side={side} hw={hw}", flush=True)
+    monkeypatch.setenv("PDEFA_CONV_TILE", tile)
+    monkeypatch.setenv("PDEFA_SILU", "exact")
+    model, x = ys.build_conv3x3_epilogue(cin, cout, hw, mode, side=side)
+    path = str(tmp_path / "conv.engine")
+    ys.save(model, path)
+    eng = native.Engine(path)
+    try:
+        got = eng.run(x)[0]
+        plan = eng.plan()
+    finally:
+        eng.close()
+    wino = [l for l in plan.splitlines() if f"tile={tile}," in l]
+    assert len(wino) == 1, plan
+    if mode == "add":
+        assert " res=" in wino[0], plan
+    want = graph_ref.run_graph(model, [x], compat_silu=False)[0]
+    assert assert_close(got, want, "winograd epilogue") < 1e-4
+
+
+@pytest.mark.parametrize("tile", ["wino64", "wino32"])
 def test_yolov8n_winograd_everywhere(yolov8n, monkeypatch, tile):
     """Every eligible 3x3 stride-1 layer (incl. the residual bottlenecks) on the
     Winograd kernel: outputs and post-NMS lists match the oracle."""
