@@ -398,11 +398,26 @@ def ingest_counters(name: str, trace_csv: str, mfma_csv: str, fetch_csv: str = N
             e["hbm_gbs"] = round(b / (e["avg_us"] * 1e-6) / 1e9, 1)
             e["hbm_frac_of_peak"] = round(e["hbm_gbs"] / HBM_PEAK_GBS, 4)
         kernels.append(e)
+    # YOLO programs: one detect_head_kernel launch per forward, so its call
+    # count is the number of forwards in the trace; kernels launched a whole
+    # number of times per forward are the forward's (the weight packing and
+    # the calibration copy run once per process)
+    heads = [e["calls"] for e in kernels if e["kernel"].startswith("detect_head_kernel")]
+    forwards = heads[0] if len(heads) == 1 else None
+    if forwards:
+        for e in kernels:
+            if e["calls"] % forwards == 0:
+                e["per_forward"] = e["calls"] // forwards
+                e["us_per_forward"] = round(e["total_us"] / forwards, 2)
+    fw = [e for e in kernels if "per_forward" in e]
+    per_fw = dict(launches=sum(e["per_forward"] for e in fw),
+                  kernel_us=round(sum(e["us_per_forward"] for e in fw), 2)) if forwards else None
     conv = [e for e in kernels if e["kernel"].startswith("conv_")]
     conv_us = sum(e["total_us"] for e in conv)
     conv_fl = sum(e.get("mfma_gflop_per_call", 0.0) * 1e9 * e["calls"] for e in conv)
     util_w = sum(e.get("mfma_util_pct", 0.0) * e["total_us"] for e in conv)
     out = dict(workload=name, command=command, calibration=dict(fetch_scale=f_scale, write_scale=w_scale),
+               forwards=forwards, per_forward=per_fw,
                conv=dict(total_us=round(conv_us, 2),
                          mfma_tflops_executed=round(conv_fl / (conv_us * 1e-6) / 1e12, 3) if conv_us else None,
                          mfma_util_pct_time_weighted=round(util_w / conv_us, 2) if conv_us else None),
@@ -421,9 +436,16 @@ def ingest_counters(name: str, trace_csv: str, mfma_csv: str, fetch_csv: str = N
              f"({(out['conv']['mfma_tflops_executed'] or 0) / MFMA_FP32_PEAK_TFLOPS:.1%} of 157.3), "
              f"MfmaUtil {out['conv']['mfma_util_pct_time_weighted']}% (time-weighted)."
              + (f"  Calibration: FETCH_SIZE x {f_scale:.3f}, WRITE_SIZE x {w_scale:.3f}." if f_scale else ""),
-             "", "```"]
+             ""]
+    if forwards:
+        lines += [f"{forwards} forwards in the trace (detect_head_kernel calls): per forward "
+                  f"{per_fw['launches']} launches, {per_fw['kernel_us']:.1f} us of kernel time (`/fwd` launches and "
+                  f"`us/fwd` time per forward; the kernels without them run once per process).", ""]
+    lines.append("```")
     for e in kernels:
         parts = [f"{e['kernel'][:64]:64s}", f"x{e['calls']:5d}", f"{e['avg_us']:9.2f} us"]
+        if "per_forward" in e:
+            parts.append(f"{e['per_forward']:3d}/fwd {e['us_per_forward']:8.2f} us/fwd")
         if "mfma_util_pct" in e:
             parts.append(f"MfmaUtil {e['mfma_util_pct']:6.2f}%")
         if "mfma_tflops_executed" in e:
