@@ -124,6 +124,13 @@ __device__ __forceinline__ void conv_tile(const ConvArgs& a, const int bx, const
     static_assert(WM % MB == 0 && WN % MB == 0 && BM % ROW_STEP == 0 && BN % ROW_STEP == 0, "tile");
     static_assert(BM * BN >= NT, "one reduced element per lane at least");
     static_assert(A_ROWS <= 32, "mask bits");
+    // One wave per K slice (a single wave tile, KG > 1): each wave loads,
+    // stages and multiplies its own slice only, so the pipeline needs no
+    // workgroup barrier; LDS operations of one wave complete in issue order,
+    // so its stage writes are seen by its own later reads.  The slices meet
+    // once, in the epilogue's reduction.
+    constexpr bool WP = WAVES_M * WAVES_N == 1 && KG > 1;
+    static_assert(!WP || ROW_STEP == 8, "a wave covers 8 rows of its slice per pass");
 
     extern __shared__ __attribute__((aligned(16))) float smem[];
     // stage st, slice g: A tile at smem + (st*KG + g)*BM*LDS_STRIDE, B tiles after all A tiles
@@ -168,10 +175,11 @@ __device__ __forceinline__ void conv_tile(const ConvArgs& a, const int bx, const
     }
 
     // ---- loaders: this lane loads float4 chunk `chunk` (slice chunk / 8) of
-    // rows r0 + ROW_STEP*i of the A tile and of the B tile.
+    // rows r0 + ROW_STEP*i of the A tile and of the B tile (with one wave per
+    // slice: the chunks of the wave's own slice).
     // Offsets within one image fit in int32 (checked by the launcher).
-    const int chunk = tid % CH;
-    const int r0 = tid / CH;
+    const int chunk = WP ? wave * 8 + (lane & 7) : tid % CH;
+    const int r0 = WP ? lane >> 3 : tid / CH;
     const int cg = chunk / 8;  // slice of this chunk
     const int cc = chunk % 8;  // chunk within the slice
     int row_hi0[A_ROWS];
@@ -382,8 +390,19 @@ __device__ __forceinline__ void conv_tile(const ConvArgs& a, const int bx, const
         s_uoff[tid] = uo;
     }
 
+    // between a stage's LDS writes and its reads, and its reads and its next
+    // writes: a workgroup barrier, or with one wave per slice only a
+    // compiler fence (the wave's LDS operations stay in issue order)
+    auto stage_sync = [&] {
+        if constexpr (WP) {
+            __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+            __builtin_amdgcn_wave_barrier();
+        } else {
+            __syncthreads();
+        }
+    };
     store_step(0, areg[0], breg[0], amask[0]);
-    __syncthreads();
+    stage_sync();
     // In the main loop both the load and the store happen unconditionally, so
     // each iteration is one basic block and the scheduler can interleave the
     // loads' address arithmetic and the LDS stores with the MFMA chain.
@@ -394,7 +413,7 @@ __device__ __forceinline__ void conv_tile(const ConvArgs& a, const int bx, const
         if (load) load_step(kb_begin + (it + PF) * KG, areg[R], breg[R], amask[R]);
         compute_step(L);
         if (store) store_step(L ^ 1, areg[(R + 1) % PF], breg[(R + 1) % PF], amask[(R + 1) % PF]);
-        __syncthreads();
+        stage_sync();
     };
     int it = 0;
     for (; it + U + PF <= nk; it += U)
@@ -471,9 +490,11 @@ __device__ __forceinline__ void conv_tile(const ConvArgs& a, const int bx, const
                     }
             }
         } else {
-            // Slice partials -> LDS (the pipeline's last barrier has retired
-            // every LDS read of the stages), then each lane sums its elements
-            // (fixed column, rows tid/BN + i*256/BN) in slice order.
+            // Slice partials -> LDS (after a barrier that retires every LDS
+            // read of the stages: the pipeline's last one, or with one wave
+            // per slice this one), then each lane sums its elements (fixed
+            // column, rows tid/BN + i*256/BN) in slice order.
+            if constexpr (WP) __syncthreads();
             float* red = smem;  // [KG][BM][BN]
 #pragma unroll
             for (int tm = 0; tm < TM; ++tm)
