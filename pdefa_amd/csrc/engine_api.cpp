@@ -180,7 +180,7 @@ PDEFA_EXPORT EngineStatus engine_tensor_create(EngineTensor** out_t, const int64
     }
     return guarded([&] {
         clear_error();
-        *out_t = pdefa::api::wrap(HostTensor::empty(shape, ndim, dtype));
+        *out_t = pdefa::api::wrap(HostTensor::empty_pinned(shape, ndim, dtype));
         return ENGINE_OK;
     });
 }
@@ -198,7 +198,7 @@ PDEFA_EXPORT EngineStatus engine_tensor_create_from_data(EngineTensor** out_t, c
     }
     return guarded([&] {
         clear_error();
-        HostTensor t = HostTensor::empty(shape, ndim, dtype);
+        HostTensor t = HostTensor::empty_pinned(shape, ndim, dtype);
         if (bytes > t.nbytes) {
             set_error("data too large");
             return ENGINE_ERR_INVALID_ARG;

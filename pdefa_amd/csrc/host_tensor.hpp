@@ -13,6 +13,14 @@ namespace pdefa {
 
 constexpr int kMaxNdim = 8;
 
+// Page-locked host memory (defined by the device runtime): tensors created
+// through the public API from this size up live there, so that a session's
+// upload of them is a DMA transfer.  pinned_alloc returns nullptr when no
+// HIP device is available or the allocation fails.
+constexpr size_t kPinnedMinBytes = 256 * 1024;
+void* pinned_alloc(size_t bytes);
+void pinned_free(void* p);
+
 // Public EngineDType codes (PDEFA1.0/include/engine/engine_c_api.h:53-62).
 enum DT : int32_t { kF32 = 0, kF16 = 1, kBF16 = 2, kI8 = 3, kU8 = 4, kI32 = 5, kI64 = 6, kBool = 7 };
 
@@ -37,6 +45,7 @@ struct HostTensor {
     void* data = nullptr;
     size_t nbytes = 0;
     bool owns = false;
+    bool pinned = false;  // data from pinned_alloc
 
     HostTensor() = default;
     HostTensor(const HostTensor&) = delete;
@@ -51,18 +60,26 @@ struct HostTensor {
             data = o.data;
             nbytes = o.nbytes;
             owns = o.owns;
+            pinned = o.pinned;
             o.data = nullptr;
             o.nbytes = 0;
             o.owns = false;
+            o.pinned = false;
         }
         return *this;
     }
     ~HostTensor() { release(); }
 
     void release() {
-        if (owns && data) std::free(data);
+        if (owns && data) {
+            if (pinned)
+                pinned_free(data);
+            else
+                std::free(data);
+        }
         data = nullptr;
         owns = false;
+        pinned = false;
     }
 
     int64_t numel() const {
@@ -89,6 +106,27 @@ struct HostTensor {
             t.owns = true;
         }
         return t;
+    }
+
+    // empty(), in page-locked memory when the tensor is at least
+    // kPinnedMinBytes and a device is there (tensors of the public API)
+    static HostTensor empty_pinned(const int64_t* shape, int32_t ndim, int32_t dtype) {
+        HostTensor t;
+        t.dtype = dtype;
+        t.rank = ndim < 0 ? 0 : (ndim > kMaxNdim ? kMaxNdim : ndim);
+        for (int i = 0; i < t.rank; ++i) t.dims[i] = shape[i];
+        const int64_t n = t.numel();
+        const size_t nb = n > 0 ? static_cast<size_t>(n) * dt_size(dtype) : 0;
+        if (nb >= kPinnedMinBytes) {
+            if (void* p = pinned_alloc((nb + 63) / 64 * 64)) {
+                t.nbytes = nb;
+                t.data = p;
+                t.owns = true;
+                t.pinned = true;
+                return t;
+            }
+        }
+        return empty(shape, ndim, dtype);
     }
 
     HostTensor clone() const {

@@ -28,6 +28,18 @@ bool device_available() {
     return cached == 1;
 }
 
+void* pinned_alloc(size_t bytes) {
+    if (!device_available()) return nullptr;
+    void* p = nullptr;
+    if (hipHostMalloc(&p, bytes, hipHostMallocDefault) != hipSuccess) {
+        (void)hipGetLastError();
+        return nullptr;
+    }
+    return p;
+}
+
+void pinned_free(void* p) { (void)hipHostFree(p); }
+
 namespace {
 
 bool env_flag(const char* name, bool dflt) {

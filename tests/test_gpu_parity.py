@@ -277,6 +277,10 @@ CONV_CASES = [
     (5, 7, 3, 1, 11),      # odd Cin, Cout < 8 (direct kernel)
     (4, 6, 3, 1, 13),      # direct kernel, 4 input channels all loaded up front
     (1, 8, 3, 2, 17),      # direct kernel, one input channel
+    (3, 16, 3, 2, 33),     # few-channel direct kernel (the stem's shape), odd size
+    (1, 32, 3, 1, 9),      # few-channel direct kernel, 32-channel blocks
+    (2, 48, 3, 2, 20),     # few-channel direct kernel, 48-channel blocks
+    (3, 64, 3, 1, 15),     # few-channel direct kernel, 64-channel blocks
     (3, 48, 3, 2, 50),     # YOLOv8m stem: 48 output channels, partial pixel blocks
     (1, 64, 5, 2, 23),     # 5x5 kernel
     (3, 40, 3, 1, 37),     # stride 1, 40 output channels
