@@ -729,7 +729,7 @@ __global__ __launch_bounds__(256) void detect_decode_kernel(DetectDecodeArgs a, 
 // per-anchor reads below hit distinct banks); lane (side, anchor) takes one
 // side's DFL expectation, kHeadAnchors lanes decode the boxes, and the class sigmoids
 // are written class-major with consecutive lanes on consecutive anchors.
-constexpr int kHeadAnchors = 32;
+constexpr int kHeadAnchors = 16;
 template <int R>
 __global__ __launch_bounds__(256) void detect_head_kernel(DetectDecodeArgs a, int32_t A, int32_t C, int32_t S) {
     extern __shared__ __attribute__((aligned(16))) float rows[];
