@@ -6,8 +6,10 @@
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
+#include <map>
 #include <mutex>
 #include <sstream>
+#include <unordered_map>
 
 namespace pdefa {
 
@@ -28,17 +30,57 @@ bool device_available() {
     return cached == 1;
 }
 
+// Page-locking memory costs far more than a plain allocation, so freed
+// blocks go back to a pool (sizes rounded up to 64 KiB) and a later request
+// takes the smallest pooled block that holds it, at most twice its size.  The
+// pool keeps up to 1 GiB; blocks beyond that are released.  Pooled blocks
+// stay allocated until the process ends.
+namespace {
+constexpr size_t kPinnedGrain = 64 * 1024;
+constexpr size_t kPinnedPoolCap = size_t{1} << 30;
+std::mutex g_pinned_mu;
+std::multimap<size_t, void*> g_pinned_pool;          // size -> free block
+std::unordered_map<void*, size_t> g_pinned_size;      // every live or pooled block
+size_t g_pinned_pooled = 0;
+}  // namespace
+
 void* pinned_alloc(size_t bytes) {
     if (!device_available()) return nullptr;
+    const size_t sz = (bytes + kPinnedGrain - 1) / kPinnedGrain * kPinnedGrain;
+    {
+        std::lock_guard<std::mutex> lk(g_pinned_mu);
+        auto it = g_pinned_pool.lower_bound(sz);
+        if (it != g_pinned_pool.end() && it->first <= 2 * sz) {
+            void* p = it->second;
+            g_pinned_pooled -= it->first;
+            g_pinned_pool.erase(it);
+            return p;
+        }
+    }
     void* p = nullptr;
-    if (hipHostMalloc(&p, bytes, hipHostMallocDefault) != hipSuccess) {
+    if (hipHostMalloc(&p, sz, hipHostMallocDefault) != hipSuccess) {
         (void)hipGetLastError();
         return nullptr;
     }
+    std::lock_guard<std::mutex> lk(g_pinned_mu);
+    g_pinned_size[p] = sz;
     return p;
 }
 
-void pinned_free(void* p) { (void)hipHostFree(p); }
+void pinned_free(void* p) {
+    if (!p) return;
+    std::unique_lock<std::mutex> lk(g_pinned_mu);
+    auto it = g_pinned_size.find(p);
+    const size_t sz = it == g_pinned_size.end() ? 0 : it->second;
+    if (sz && g_pinned_pooled + sz <= kPinnedPoolCap) {
+        g_pinned_pool.emplace(sz, p);
+        g_pinned_pooled += sz;
+        return;
+    }
+    if (it != g_pinned_size.end()) g_pinned_size.erase(it);
+    lk.unlock();
+    (void)hipHostFree(p);
+}
 
 namespace {
 

@@ -318,6 +318,27 @@ def test_session_runs(tiny_engine):
 
 
 @pytest.mark.gpu
+def test_large_tensors_reused_blocks():
+    """Tensors of 256 KiB and up created through the C ABI live in page-locked
+    memory from a pool of freed blocks: contents survive creation and reuse
+    of a freed block of the same or a larger size, and a freed block handed
+    to a smaller tensor keeps that tensor's own size."""
+    from pdefa_amd import native
+    L = native.lib()
+    rng = np.random.default_rng(5)
+    for shape in [(1, 3, 200, 200), (1, 3, 200, 200), (1, 3, 180, 200), (2, 3, 200, 200), (1, 3, 200, 200)]:
+        a = rng.standard_normal(shape).astype(np.float32)
+        h = native.tensor_from_numpy(a)
+        keep = native.tensor_from_numpy(a[:, :1].copy())  # a small tensor alive across the loop
+        try:
+            assert np.array_equal(native.tensor_to_numpy(h), a)
+            assert np.array_equal(native.tensor_to_numpy(keep), a[:, :1])
+        finally:
+            L.engine_tensor_destroy(h)
+            L.engine_tensor_destroy(keep)
+
+
+@pytest.mark.gpu
 def test_batch_inference(tmp_path):
     """BatchInference (one batched GPU program per chunk) against single runs."""
     path = str(tmp_path / "y.engine")
