@@ -484,7 +484,7 @@ __device__ __forceinline__ void conv_tile(const ConvArgs& a, const int bx, const
                         if (!PART) v = act_fixed<ACT>(v + bias_v[tn], a.act, a.slope);
                         if (RES) v += rv[e][tn];
                         if (yo[e] >= 0 && cok[tn]) {
-                            dst[yo[e] + co[tn]] = v;
+                            __builtin_nontemporal_store(v, &dst[yo[e] + co[tn]]);
                             if (UP) store_up(uo[e], co[tn], v);
                         }
                     }
@@ -541,7 +541,7 @@ __device__ __forceinline__ void conv_tile(const ConvArgs& a, const int bx, const
                 if (!PART) r = act_fixed<ACT>(r + bias_v, a.act, a.slope);
                 if (RES) r += rv[i];
                 if (yo[i] >= 0 && cok) {
-                    dst[yo[i] + co] = r;
+                    __builtin_nontemporal_store(r, &dst[yo[i] + co]);
                     if (UP) store_up(uo[i], co, r);
                 }
             }

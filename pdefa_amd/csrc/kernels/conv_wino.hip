@@ -352,7 +352,7 @@ __global__ __launch_bounds__(256) void conv_wino_kernel(ConvArgs a, int tiles_h,
     // channels), CB tiles per lane.  Outputs and residuals move as 16-byte
     // runs when vec_out is set (output and residual rows 16-byte aligned,
     // Cout % 4 == 0), else as single floats, channels past Cout skipped.
-    // Buffer-range checks drop stores (and zero loads) at kWinoNoPixel
+    // Stores are non-temporal (cache policy 2).  Buffer-range checks drop stores (and zero loads) at kWinoNoPixel
     // offsets, so pixels outside the output need no branch.
     const __amdgpu_buffer_rsrc_t ybuf = __builtin_amdgcn_make_buffer_rsrc(a.y, 0, y_bytes, kWinoBufferFlags);
     const __amdgpu_buffer_rsrc_t rbuf =
@@ -407,7 +407,7 @@ __global__ __launch_bounds__(256) void conv_wino_kernel(ConvArgs a, int tiles_h,
                     v[k] = act_fixed<ACT>(yv[r][q][k] + bias4[k], a.act, a.slope);
                     if (RES) v[k] += rv[r][q][k];
                 }
-                __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(uintx4, v), ybuf, yo[r][q] + cob[0], 0, 0);
+                __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(uintx4, v), ybuf, yo[r][q] + cob[0], 0, 2);
             }
     } else {
         float rv[CB][4][4];
@@ -429,7 +429,7 @@ __global__ __launch_bounds__(256) void conv_wino_kernel(ConvArgs a, int tiles_h,
                 for (int k = 0; k < 4; ++k) {
                     float v = act_fixed<ACT>(yv[r][q][k] + bias4[k], a.act, a.slope);
                     if (RES) v += rv[r][q][k];
-                    __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v), ybuf, yo[r][q] + cob[k], 0, 0);
+                    __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v), ybuf, yo[r][q] + cob[k], 0, 2);
                 }
     }
 }
