@@ -352,8 +352,9 @@ __global__ __launch_bounds__(256) void conv_wino_kernel(ConvArgs a, int tiles_h,
     // channels), CB tiles per lane.  Outputs and residuals move as 16-byte
     // runs when vec_out is set (output and residual rows 16-byte aligned,
     // Cout % 4 == 0), else as single floats, channels past Cout skipped.
-    // Stores are non-temporal (cache policy 2).  Buffer-range checks drop stores (and zero loads) at kWinoNoPixel
-    // offsets, so pixels outside the output need no branch.
+    // Stores are non-temporal (cache policy 2).  Buffer-range checks drop
+    // stores (and zero loads) at kWinoNoPixel offsets, so pixels outside the
+    // output need no branch.
     const __amdgpu_buffer_rsrc_t ybuf = __builtin_amdgcn_make_buffer_rsrc(a.y, 0, y_bytes, kWinoBufferFlags);
     const __amdgpu_buffer_rsrc_t rbuf =
         __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(RES ? a.res : a.y), 0, RES ? r_bytes : 0,
