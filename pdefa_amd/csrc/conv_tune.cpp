@@ -51,13 +51,15 @@ Key make_key(const ConvQuery& q, int device) {
 //   conv <20 shape ints> <tile> <splits> <k steps per split>
 //   group <members> {<20 shape ints> <tile> <splits> <k steps per split>}... <tile> <group ms> <separate ms>
 //
-// The table is read once per process from PDEFA_TUNE_TABLE, or by default
-// from tuning/<arch>.txt beside the library's directory; PDEFA_TUNE_TABLE=0
-// disables it.  With PDEFA_TUNE_RECORD=<file> every choice measured in this
+// The table is read from PDEFA_TUNE_TABLE, or by default from
+// tuning/<arch>.txt beside the library's directory, when a plan first needs
+// it and again whenever PDEFA_TUNE_TABLE names another file;
+// PDEFA_TUNE_TABLE=0 disables it.  With PDEFA_TUNE_RECORD=<file> every choice measured in this
 // process is appended to that file in the same format.
 
 struct Table {
     bool loaded = false;
+    std::string path;  // the file it was read from
     std::string arch;
     int cus = 0;
     std::map<std::vector<int32_t>, k::ConvLaunchShape> conv;  // shape ints (no device)
@@ -86,11 +88,21 @@ std::vector<int32_t> shape_ints(const Key& k) { return std::vector<int32_t>(k.be
 
 Table& table_for(int device) {
     Table& t = g_tables[device];
+    const char* env = std::getenv("PDEFA_TUNE_TABLE");
+    if (t.loaded && env && t.path != env) {
+        // PDEFA_TUNE_TABLE names another file now: drop the old table and the
+        // choices this process took from it (or measured beside it)
+        t.conv.clear();
+        t.group.clear();
+        t.loaded = false;
+        g_cache.clear();
+        g_group_cache.clear();
+    }
     if (t.loaded) return t;
     t.loaded = true;
     device_kind(device, t.arch, t.cus);
-    const char* env = std::getenv("PDEFA_TUNE_TABLE");
     std::string path = env ? std::string(env) : default_table_path(t.arch);
+    t.path = path;
     if (path.empty() || path == "0") return t;
     std::ifstream f(path);
     if (!f) return t;
@@ -261,8 +273,8 @@ k::ConvLaunchShape tune_conv(const ConvQuery& q, hipStream_t s) {
     PDEFA_HIP(hipGetDevice(&device));
     const Key key = make_key(q, device);
     std::lock_guard<std::mutex> lock(g_mu);
-    if (auto it = g_cache.find(key); it != g_cache.end()) return it->second;
     Table& table = table_for(device);
+    if (auto it = g_cache.find(key); it != g_cache.end()) return it->second;
     if (auto it = table.conv.find(shape_ints(key)); it != table.conv.end()) {
         ++g_from_table;
         g_cache.emplace(key, it->second);
@@ -332,8 +344,8 @@ ConvGroupTiming tune_conv_group(const std::vector<ConvQuery>& qs, const std::vec
         key.push_back(solo[i].kt_per_split);
     }
     std::lock_guard<std::mutex> lock(g_mu);
-    if (auto it = g_group_cache.find(key); it != g_group_cache.end()) return it->second;
     Table& table = table_for(device);
+    if (auto it = g_group_cache.find(key); it != g_group_cache.end()) return it->second;
     const std::vector<int32_t> tkey(key.begin() + 1, key.end());
     if (auto it = table.group.find(tkey); it != table.group.end()) {
         ++g_from_table;
