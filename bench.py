@@ -321,8 +321,8 @@ def session_run_stats(eng: native.Engine, batch: int, warmup: int = 5, runs: int
 
 COUNTER_DIR = os.path.join(ROOT, "profiles")
 BANDWIDTH_KERNELS = ("maxpool_chain_kernel", "maxpool_chain_vec_kernel", "detect_head_kernel", "detect_decode_kernel",
-                     "eltwise_kernel", "eltwise_vec_kernel", "calibration copy", "resize_nearest_kernel",
-                     "maxpool_kernel", "softmax_kernel", "letterbox_kernel")
+                     "eltwise_kernel", "eltwise_vec_kernel", "transpose_elt_kernel", "calibration copy",
+                     "resize_nearest_kernel", "maxpool_kernel", "softmax_kernel", "letterbox_kernel")
 
 
 def _kernel_key(name: str) -> str:

@@ -153,6 +153,45 @@ __global__ __launch_bounds__(256) void eltwise_vec_kernel(int op, float* out, co
     }
 }
 
+// A unary op whose output is contiguous along one collapsed dim (Q) and
+// whose input along another (P), e.g. NCHW <-> NHWC at a graph's edges: per
+// index of the other (outer) dims, a P x Q transpose in 32 x 32 tiles through
+// LDS, so that both the reads (along P) and the writes (along Q) are
+// coalesced.  Each element is computed exactly as eltwise_kernel computes it.
+struct TransDims {
+    int32_t P = 0, Q = 0;
+    int32_t so_p = 0, sa_q = 0;  // output stride along P, input stride along Q
+    int32_t rank = 0;            // outer dims
+    int32_t dims[kMaxRank] = {}, so[kMaxRank] = {}, sa[kMaxRank] = {};
+};
+
+__global__ __launch_bounds__(256) void transpose_elt_kernel(int op, float* out, const float* a, TransDims d,
+                                                            float alpha) {
+    __shared__ float tile[32][33];
+    const int tiles_p = (d.P + 31) / 32;
+    const int p0 = (blockIdx.x % tiles_p) * 32;
+    const int q0 = (blockIdx.x / tiles_p) * 32;
+    int32_t o = blockIdx.y, ob = 0, ab = 0;
+    for (int k = d.rank - 1; k >= 0; --k) {
+        const int32_t idx = o % d.dims[k];
+        o /= d.dims[k];
+        ob += idx * d.so[k];
+        ab += idx * d.sa[k];
+    }
+    const int tx = threadIdx.x & 31, ty = threadIdx.x >> 5;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        const int q = q0 + ty + 8 * r, p = p0 + tx;
+        if (q < d.Q && p < d.P) tile[ty + 8 * r][tx] = a[ab + q * d.sa_q + p];
+    }
+    __syncthreads();
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        const int p = p0 + ty + 8 * r, q = q0 + tx;
+        if (p < d.P && q < d.Q) out[ob + p * d.so_p + q] = elt_apply(op, tile[tx][ty + 8 * r], 0.0f, alpha);
+    }
+}
+
 namespace {
 
 // Collapsed dims of (out, a, b); false if some extent or stride exceeds int32.
@@ -227,6 +266,33 @@ void launch_eltwise(int op, const View& out, const View& a, const View& b, float
             hipLaunchKernelGGL(eltwise_vec_kernel, dim3(grid_for(total4)), dim3(256), 0, s, op, out.ptr, a.ptr,
                                bb.ptr, b_splat, c, alpha, total4);
             return;
+        }
+        // tiled transpose (see transpose_elt_kernel): a unary op, the output
+        // contiguous along the inner collapsed dim Q, the input along dim P
+        int pj = -1;
+        for (int k = 0; k < in; ++k)
+            if (c.sa[k] == 1) pj = k;
+        if (!binary && c.so[in] == 1 && c.sa[in] != 1 && pj >= 0 && c.dims[in] >= 8 && c.dims[pj] >= 8) {
+            TransDims t;
+            t.P = c.dims[pj];
+            t.Q = c.dims[in];
+            t.so_p = c.so[pj];
+            t.sa_q = c.sa[in];
+            int64_t outer = 1;
+            for (int k = 0; k < in; ++k) {
+                if (k == pj) continue;
+                t.dims[t.rank] = c.dims[k];
+                t.so[t.rank] = c.so[k];
+                t.sa[t.rank] = c.sa[k];
+                ++t.rank;
+                outer *= c.dims[k];
+            }
+            const int64_t tiles = static_cast<int64_t>((t.P + 31) / 32) * ((t.Q + 31) / 32);
+            if (outer <= 65535 && tiles < (int64_t{1} << 31)) {
+                hipLaunchKernelGGL(transpose_elt_kernel, dim3(static_cast<unsigned>(tiles), static_cast<unsigned>(outer)),
+                                   dim3(256), 0, s, op, out.ptr, a.ptr, t, alpha);
+                return;
+            }
         }
     }
     if (fits_i32(out) && fits_i32(a) && fits_i32(bb))
