@@ -160,9 +160,11 @@ CLS_GAIN = 300.0
 CLS_BIAS = {"n": -50.0, "s": -50.0, "m": -66.0, "l": -66.0, "x": -66.0}
 
 
-def build_yolov8(scale: str = "n", seed: int = 0, nc: int = 80, imgsz: int = 640,
+def build_yolov8(scale: str = "n", seed: int = 0, nc: int = 80, imgsz=640,
                  cls_bias: Optional[float] = None, cls_gain: float = CLS_GAIN) -> EngineModel:
-    """YOLOv8{scale} detection graph with seeded random weights (BN folded).
+    """YOLOv8{scale} detection graph with seeded random weights (BN folded),
+    for square imgsz x imgsz inputs or, with imgsz = (h, w), h x w inputs
+    (both multiples of 32).
 
     The class head's last conv has its Kaiming weights scaled by cls_gain and
     a constant bias cls_bias (default CLS_BIAS[scale]), so that a random-weight
@@ -170,6 +172,7 @@ def build_yolov8(scale: str = "n", seed: int = 0, nc: int = 80, imgsz: int = 640
     unscaled head scores every anchor near sigmoid(cls_bias))."""
     if cls_bias is None:
         cls_bias = CLS_BIAS[scale]
+    ih, iw = (imgsz, imgsz) if isinstance(imgsz, int) else (int(imgsz[0]), int(imgsz[1]))
     depth, width, max_ch = SCALES[scale]
     ch = lambda c: make_divisible(min(c, max_ch) * width, 8)
     rep = lambda n: max(round(n * depth), 1)
@@ -220,11 +223,11 @@ def build_yolov8(scale: str = "n", seed: int = 0, nc: int = 80, imgsz: int = 640
         cat = b.node("Concat", f"/{n}/Concat_{i}", [a, c], axis=1)
         shp = b.const(f"/{n}/Reshape_{i}/shape::const", [1, no, -1])
         flat.append(b.node("Reshape", f"/{n}/Reshape_{i}", [cat, shp]))
-        hw = imgsz // s
-        sx = np.arange(hw, dtype=np.float32) + 0.5
-        gy, gx = np.meshgrid(sx, sx, indexing="ij")
+        fh, fw = ih // s, iw // s
+        gy, gx = np.meshgrid(np.arange(fh, dtype=np.float32) + 0.5, np.arange(fw, dtype=np.float32) + 0.5,
+                             indexing="ij")
         anchors.append(np.stack([gx.ravel(), gy.ravel()], 0))
-        strides.append(np.full(hw * hw, s, np.float32))
+        strides.append(np.full(fh * fw, s, np.float32))
     n_anchor = sum(a.shape[1] for a in anchors)
     xcat = b.node("Concat", "/model.22/Concat_3", flat, axis=2)
     box = y.slice(xcat, 0, 4 * reg, 1, "/model.22/Split_slice_0")
@@ -254,7 +257,7 @@ def build_yolov8(scale: str = "n", seed: int = 0, nc: int = 80, imgsz: int = 640
     dbox = b.node("Mul", "/model.22/Mul_2", [dbox, strd])
     sig = b.node("Sigmoid", "/model.22/Sigmoid", [cls])
     out = b.node("Concat", "/model.22/Concat_5", [dbox, sig], axis=1)
-    return b.model([1, 3, imgsz, imgsz], [1, 4 + nc, n_anchor], [out])
+    return b.model([1, 3, ih, iw], [1, 4 + nc, n_anchor], [out])
 
 
 def build_single_conv(cin: int, cout: int, k: int, stride: int, hw: int, seed: int = 7,
@@ -540,13 +543,15 @@ def letterbox(img: np.ndarray, target_w: int = 640, target_h: int = 640,
     return out[None], meta
 
 
-def yolo_inputs(batch: int, imgsz: int = 640) -> Tuple[np.ndarray, list]:
+def yolo_inputs(batch: int, imgsz=640) -> Tuple[np.ndarray, list]:
     """Letterboxed synthetic inputs: image i has seed i and the i-th size of the
-    16:9 / 4:3 / 1:1 cycle; pad 114/255, scale 1/255."""
+    16:9 / 4:3 / 1:1 cycle; pad 114/255, scale 1/255.  imgsz: the square side,
+    or (h, w)."""
+    th, tw = (imgsz, imgsz) if isinstance(imgsz, int) else (int(imgsz[0]), int(imgsz[1]))
     xs, metas = [], []
     for i in range(batch):
         w, h = ASPECT_SIZES[i % len(ASPECT_SIZES)]
-        t, m = letterbox(synth_image(i, w, h), imgsz, imgsz)
+        t, m = letterbox(synth_image(i, w, h), tw, th)
         xs.append(t)
         metas.append(m)
     return np.concatenate(xs, 0), metas

@@ -491,6 +491,31 @@ def test_yolov8n_winograd_everywhere(yolov8n, monkeypatch, tile):
     assert_same_detections(got, [follow, plain], metas[0], "yolov8n b1 winograd")
 
 
+@pytest.mark.parametrize("hw", [(384, 640), (640, 480)])
+def test_yolov8n_rectangular(tmp_path, hw):
+    """YOLOv8n built for a rectangular input (h x w, feature maps of unequal
+    sides at every scale), batch 2 (a 16:9 and a 4:3 image letterboxed into
+    it): every output element and the post-NMS lists of both images match
+    the oracle."""
+    print(f"[case] yolov8n {hw[0]}x{hw[1]} b2", flush=True)
+    model = ys.build_yolov8("n", seed=0, imgsz=hw)
+    path = str(tmp_path / "yolov8n_rect.engine")
+    ys.save(model, path)
+    x, metas = ys.yolo_inputs(2, hw)
+    m0 = tune_measured()
+    eng = native.Engine(path)
+    try:
+        got = eng.run(x)[0]
+    finally:
+        eng.close()
+    assert tune_measured() == m0, "a launch shape of this model is not in the launch-shape table"
+    n_anchor = sum((hw[0] // s) * (hw[1] // s) for s in (8, 16, 32))
+    assert got.shape == (2, 84, n_anchor)
+    for i in range(2):
+        follow, plain, _ = explain_by_jumps(got[i:i + 1], model, x[i:i + 1], f"yolov8n {hw} image {i}")
+        assert_same_detections(got[i:i + 1], [follow, plain], metas[i], f"yolov8n {hw} image {i}")
+
+
 @pytest.mark.parametrize("n,c,h,w,k", [(2, 37, 13, 19, 5), (1, 16, 8, 8, 3), (2, 20, 23, 9, 7), (1, 128, 20, 20, 5)])
 def test_pool_chain(tmp_path, n, c, h, w, k):
     """Three chained same-size max pools (SPPF) run as one fused step."""
