@@ -80,15 +80,7 @@ def time_program(eng: native.Engine, x: np.ndarray, steps: int, warmup: int):
 def launch_count(plan: str) -> int:
     """Launches of a prepared program: one per plan step, except that
     consecutive steps of one conv group share a grouped launch."""
-    n, prev = 0, None
-    for line in plan.splitlines()[1:]:
-        if line.startswith("arena"):
-            break
-        g = line.split(" group=")[1].split()[0] if " group=" in line else None
-        if g is None or g != prev:
-            n += 1
-        prev = g
-    return n
+    return len(plan_launches(plan))
 
 
 def conv_stats(eng: native.Engine, iters: int):
@@ -99,6 +91,63 @@ def conv_stats(eng: native.Engine, iters: int):
     return dict(conv_ms=conv_ms, conv_flops=conv_flops, step_ms=float(ms.sum()),
                 conv_tflops=(conv_flops / (conv_ms * 1e-3) / 1e12) if conv_ms > 0 else 0.0,
                 n_steps=int(len(ms)), n_conv=int(conv.sum()))
+
+
+def plan_launches(plan: str):
+    """The plan's step lines grouped by launch (consecutive steps of one conv
+    group share a grouped launch), in launch order."""
+    out, prev = [], None
+    for line in plan.splitlines()[1:]:
+        if line.startswith("arena"):
+            break
+        g = line.split(" group=")[1].split()[0] if " group=" in line else None
+        if g is None or g != prev:
+            out.append([])
+        out[-1].append(line)
+        prev = g
+    return out
+
+
+def conv3x3_layers(eng: native.Engine, iters: int = 20):
+    """Every launch of the forward whose convs are all 3x3, timed back to back
+    on the session stream (step_repeat: the launch boundary included, like
+    the roofline layer), in direct-conv flops (2*N*Ho*Wo*Cout*Cin*9) against
+    the fp32 MFMA peak.  MFMA launches (Winograd and implicit GEMM) are
+    summarised by stride; the direct-kernel stem (VALU) is listed apart."""
+    _, kind, flops = eng.step_times(1)
+    rows = []
+    for i, lines in enumerate(plan_launches(eng.plan())):
+        if not all(" k=3x3 " in l for l in lines):
+            continue
+        ms = eng.step_repeat(i, iters)
+        fl = int(flops[i])
+        tf = fl / (ms * 1e-3) / 1e12
+        first = lines[0]
+        rows.append(dict(launch=i, stride=int(first.split(" s=")[1].split("x")[0]),
+                         kernel="direct" if int(kind[i]) == KIND_CONV_DIRECT else
+                         ("wino" if "tile=wino" in first else "gemm"),
+                         tile=first.split("tile=")[1].split(",")[0] if "tile=" in first else "direct",
+                         convs=len(lines), names=[l.split("'")[1] for l in lines], us=round(ms * 1e3, 2),
+                         gflop=round(fl / 1e9, 4), tflops=round(tf, 2),
+                         frac=round(tf / MFMA_FP32_PEAK_TFLOPS, 4)))
+
+    def agg(rs):
+        if not rs:
+            return None
+        us = sum(r["us"] for r in rs)
+        gf = sum(r["gflop"] for r in rs)
+        tf = gf * 1e9 / (us * 1e-6) / 1e12
+        return dict(launches=len(rs), us=round(us, 2), gflop=round(gf, 3), tflops=round(tf, 2),
+                    frac=round(tf / MFMA_FP32_PEAK_TFLOPS, 4),
+                    launches_at_50pct=int(sum(r["frac"] >= 0.5 for r in rs)),
+                    min_frac=min(r["frac"] for r in rs), max_frac=max(r["frac"] for r in rs))
+
+    mf = [r for r in rows if r["kernel"] != "direct"]
+    summary = dict(mfma=agg(mf), s1=agg([r for r in mf if r["stride"] == 1]),
+                   s2=agg([r for r in mf if r["stride"] == 2]),
+                   direct=[{k: r[k] for k in ("names", "us", "tflops", "frac")} for r in rows
+                           if r["kernel"] == "direct"])
+    return summary, rows
 
 
 def roofline_engine(tmp: str):
@@ -556,9 +605,14 @@ def main():
                 ms, wall, first = time_program(eng, x, args.steps, args.warmup)
                 cs = conv_stats(eng, 20)
                 sr = session_run_stats(eng, batch)
+                c3, c3_rows = conv3x3_layers(eng)
             finally:
                 eng.close()
-            res[batch] = dict(ms=ms, wall=wall, first=first, ips=batch * 1000.0 / ms, session_run=sr, **cs)
+            for r in c3_rows:
+                log(f"  3x3 s{r['stride']} {r['kernel']:6s} {r['tile']:10s} {r['us']:8.2f} us {r['gflop']:8.4f} GFLOP "
+                    f"{r['tflops']:7.2f} TFLOP/s {r['frac']:6.1%}  {' + '.join(r['names'])}")
+            res[batch] = dict(ms=ms, wall=wall, first=first, ips=batch * 1000.0 / ms, session_run=sr, conv3x3=c3,
+                              **cs)
             log(f"  {res[batch]['ips']:.1f} images/s replayed from HBM, {ms:.4f} ms/step; engine_session_run "
                 f"(host input and output) median {sr['median_ms']:.4f} ms = {sr['images_per_s']} images/s; convs "
                 f"{cs['conv_ms']:.4f} ms launch by launch ({cs['n_conv']} convs, {cs['n_steps']} launches)")
@@ -623,6 +677,11 @@ def main():
         "first_run_ms": {"b1": round(b1["first"], 1), "b8": round(b8["first"], 1)},
         "pipeline_b8": pipe,
         "roofline": roof,
+        "conv3x3_layers": {
+            "note": ("every 3x3 conv launch of the YOLOv8n forward timed back to back, direct-conv flops "
+                     "(2*N*Ho*Wo*Cout*Cin*9) over the fp32 MFMA peak; Winograd and implicit-GEMM launches by stride, "
+                     "the VALU stem apart"),
+            "b1": b1["conv3x3"], "b8": b8["conv3x3"]},
         "counters": counters_summary(),
         "cpu_baseline": cpu,
     }

@@ -1720,6 +1720,8 @@ std::string describe_plan(const Model& m, const Plan& p) {
                << ")";
         if (s.group >= 0) os << " group=" << s.group;
         if (s.kind == StepKind::ConvDirect) os << "(act=" << s.act << ")";
+        if (s.kind == StepKind::ConvMfma || s.kind == StepKind::ConvDirect)
+            os << " k=" << s.KH << "x" << s.KW << " s=" << s.sh << "x" << s.sw;
         if ((s.kind == StepKind::ConvMfma || s.kind == StepKind::ConvDirect) && s.groups > 1) os << " groups=" << s.groups;
         os << " node=" << s.node;
         if (s.node >= 0) os << " '" << m.nodes[s.node].name << "'";
