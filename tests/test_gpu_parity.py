@@ -516,6 +516,35 @@ def test_yolov8n_rectangular(tmp_path, hw):
         assert_same_detections(got[i:i + 1], [follow, plain], metas[i], f"yolov8n {hw} image {i}")
 
 
+@pytest.mark.parametrize("scale,hw,seed,cls_bias,max_set", [("s", 640, 1, None, 2), ("l", 320, 2, -55.0, 2),
+                                                            ("x", 256, 4, -55.0, 3)])
+def test_yolov8_scales(tmp_path, scale, hw, seed, cls_bias, max_set):
+    """The other YOLOv8 scales at batch 1: s (width 0.50) at 640x640, l
+    (depth 1.0, width 1.0, 512 channels) at 320x320 and x (width 1.25, 640
+    channels) at 256x256: every output element and the post-NMS list match
+    the oracle.  Seeds and class-head bias give a well-conditioned
+    detection problem (a conf_thres with a 1e-2 score margin, every IoU the
+    NMS compares at least 1e-3 from its threshold) with few activations near
+    a compat-SiLU jump, so the search over flipped sets stays short."""
+    print(f"[case] yolov8{scale} {hw}x{hw} b1 seed {seed}", flush=True)
+    model = ys.build_yolov8(scale, seed=seed, imgsz=hw, cls_bias=cls_bias)
+    path = str(tmp_path / f"yolov8{scale}.engine")
+    ys.save(model, path)
+    x, metas = ys.yolo_inputs(1, hw)
+    m0 = tune_measured()
+    eng = native.Engine(path)
+    try:
+        got = eng.run(x)[0]
+    finally:
+        eng.close()
+    assert tune_measured() == m0, "a launch shape of this model is not in the launch-shape table"
+    assert got.shape == (1, 84, sum((hw // s) ** 2 for s in (8, 16, 32)))
+    follow, plain, _ = explain_by_jumps(got, model, x, f"yolov8{scale} {hw}", max_set=max_set)
+    conf, _ = decode_ref.robust_conf(plain)
+    assert conf is not None and decode_ref.min_iou_gap(plain.tolist(), metas[0], conf) >= 1e-3
+    assert_same_detections(got, [follow, plain], metas[0], f"yolov8{scale} {hw}")
+
+
 @pytest.mark.parametrize("n,c,h,w,k", [(2, 37, 13, 19, 5), (1, 16, 8, 8, 3), (2, 20, 23, 9, 7), (1, 128, 20, 20, 5)])
 def test_pool_chain(tmp_path, n, c, h, w, k):
     """Three chained same-size max pools (SPPF) run as one fused step."""
