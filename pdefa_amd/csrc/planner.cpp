@@ -326,6 +326,20 @@ void step_views(const Step& s, std::vector<VRef>& rd, std::vector<VRef>& wr) {
 // index ranges there (the producers of one concat buffer).
 bool views_may_overlap(const VRef& a, const VRef& b) {
     if (a.buf < 0 || b.buf < 0 || a.buf != b.buf) return false;
+    // disjoint element ranges (e.g. the slices of different scales in one
+    // concat buffer, whose strides differ)
+    auto range = [](const VRef& v, int64_t& lo, int64_t& hi) {
+        lo = hi = v.off;
+        for (int d = 0; d < v.rank; ++d) {
+            if (v.dims[d] <= 0) return false;
+            const int64_t e = (v.dims[d] - 1) * v.str[d];
+            (e < 0 ? lo : hi) += e;
+        }
+        return true;
+    };
+    int64_t alo, ahi, blo, bhi;
+    if (!range(a, alo, ahi) || !range(b, blo, bhi)) return false;  // an empty view touches nothing
+    if (ahi < blo || bhi < alo) return false;
     if (a.rank != b.rank) return true;
     for (int d = 0; d < a.rank; ++d)
         if (a.str[d] != b.str[d]) return true;
@@ -1382,6 +1396,21 @@ class Planner {
             for (int i = 0; i < j; ++i)
                 if (hit(wr[i], rd[j]) || hit(wr[i], wr[j]) || hit(rd[i], wr[j])) deps[j].push_back(i);
 
+        // Convs read only by the Detect decode (the head's last 1x1 convs of
+        // every scale) wait until nothing else is ready: they then become
+        // ready together, at the end, where they can share a launch.
+        std::vector<char> sink(n, 0);
+        for (int i = 0; i < n; ++i) {
+            if (!groupable(st[i])) continue;
+            bool any = false, only_decode = true;
+            for (int j = i + 1; j < n; ++j)
+                if (std::find(deps[j].begin(), deps[j].end(), i) != deps[j].end()) {
+                    any = true;
+                    only_decode = only_decode && st[j].kind == StepKind::DetectDecode;
+                }
+            sink[i] = any && only_decode;
+        }
+
         std::vector<char> done(n, 0);
         std::vector<Step> out;
         int32_t next_group = 0;
@@ -1397,6 +1426,11 @@ class Planner {
                     }
                 if (ok) ready.push_back(j);
             }
+            // waiting sinks go behind every other ready step
+            std::stable_partition(ready.begin(), ready.end(), [&](int j) { return !sink[j]; });
+            if (!sink[ready.front()])
+                ready.erase(std::remove_if(ready.begin(), ready.end(), [&](int j) { return sink[j] != 0; }),
+                            ready.end());
             std::vector<int> S = {ready.front()};
             int tile = -1;
             if (groupable(st[S[0]])) {
