@@ -326,11 +326,15 @@ void step_views(const Step& s, std::vector<VRef>& rd, std::vector<VRef>& wr) {
 // index ranges there (the producers of one concat buffer).
 bool views_may_overlap(const VRef& a, const VRef& b) {
     if (a.buf < 0 || b.buf < 0 || a.buf != b.buf) return false;
-    // disjoint element ranges (e.g. the slices of different scales in one
-    // concat buffer, whose strides differ)
-    auto range = [](const VRef& v, int64_t& lo, int64_t& hi) {
+    // Disjoint element ranges (e.g. the slices of different scales in one
+    // concat buffer, whose strides differ), over whole views or over one
+    // item of a common outer dim: with equal outer strides S whose items'
+    // ranges are disjoint and together span less than S, an element of one
+    // view and one of the other differ by less than S within an item, so
+    // they can only meet in the same item, where they do not.
+    auto range = [](const VRef& v, int first, int64_t& lo, int64_t& hi) {
         lo = hi = v.off;
-        for (int d = 0; d < v.rank; ++d) {
+        for (int d = first; d < v.rank; ++d) {
             if (v.dims[d] <= 0) return false;
             const int64_t e = (v.dims[d] - 1) * v.str[d];
             (e < 0 ? lo : hi) += e;
@@ -338,8 +342,11 @@ bool views_may_overlap(const VRef& a, const VRef& b) {
         return true;
     };
     int64_t alo, ahi, blo, bhi;
-    if (!range(a, alo, ahi) || !range(b, blo, bhi)) return false;  // an empty view touches nothing
+    if (!range(a, 0, alo, ahi) || !range(b, 0, blo, bhi)) return false;  // an empty view touches nothing
     if (ahi < blo || bhi < alo) return false;
+    if (a.rank == b.rank && a.rank > 1 && a.str[0] == b.str[0] && a.str[0] > 0 && range(a, 1, alo, ahi) &&
+        range(b, 1, blo, bhi) && (ahi < blo || bhi < alo) && std::max(ahi, bhi) - std::min(alo, blo) < a.str[0])
+        return false;
     if (a.rank != b.rank) return true;
     for (int d = 0; d < a.rank; ++d)
         if (a.str[d] != b.str[d]) return true;

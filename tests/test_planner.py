@@ -239,6 +239,13 @@ def test_grouped_plan_keeps_every_hazard_in_order(y8n_path, monkeypatch, shape):
         if m:
             groups.setdefault(int(m.group(1)), []).append(i)
     assert len(groups) >= 6  # the Detect head's convs ride along the neck
+    # the head's last 1x1 convs, read only by the decode, wait for the end of
+    # the program (their per-scale slices of the concat buffer are disjoint)
+    # and share the last launch before it
+    last = groups[max(groups)]
+    assert sorted(grouped[i].split("'")[1].split("/")[-2] for i in last) == \
+        sorted(f"cv{b}.{s}.2" for b in (2, 3) for s in range(3))
+    assert " detect_decode " in grouped[last[-1] + 1]
     arena = arena_offsets(text)
     for members in groups.values():
         assert members == list(range(members[0], members[0] + len(members))) and 2 <= len(members) <= 8
