@@ -335,3 +335,26 @@ def test_topk_gather_plan(tmp_path):
     ys.save(model, path)
     with pytest.raises(native.NativeError):
         native.plan_text(path, list(x.shape))
+
+
+def test_plan_launches_names_every_3x3_conv(y8n_path, monkeypatch):
+    """bench.py's launch list: one entry per launch (the members of a grouped
+    launch together), and every conv line names its kernel size and stride,
+    so the per-layer 3x3 report finds all 3x3 convs of YOLOv8n."""
+    import bench
+    monkeypatch.setenv("PDEFA_PLAN_GROUP_ALL", "1")
+    text = native.plan_text(y8n_path, [1, 3, 640, 640])
+    launches = bench.plan_launches(text)
+    _, lines = parse(text)
+    assert sum(len(l) for l in launches) == len(lines)
+    assert bench.launch_count(text) == len(launches) < len(lines)  # some groups formed
+    for members in launches:
+        groups = {re.search(r" group=(\d+)", l).group(1) if " group=" in l else None for l in members}
+        assert len(members) == 1 or (len(groups) == 1 and None not in groups)
+    convs = [l for l in lines if " conv_" in l]
+    assert all(re.search(r" k=\d+x\d+ s=\d+x\d+ ", l) for l in convs)
+    # YOLOv8n's 3x3 convs: the stem, 4 downsamples in the backbone and 2 in
+    # the neck, 2 in each of the 10 bottlenecks, 2 per branch of each of the
+    # Detect head's 3 scales (box and class)
+    k3 = [l for l in convs if " k=3x3 " in l]
+    assert len(k3) == 1 + 4 + 2 + 2 * 10 + 2 * 2 * 3
