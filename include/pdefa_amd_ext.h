@@ -92,6 +92,18 @@ PDEFA_EXPORT EngineStatus pdefa_amd_session_decode(EngineSession* sess, int32_t 
 /* Text dump of the session's current device program (one line per kernel). */
 PDEFA_EXPORT EngineStatus pdefa_amd_session_plan(const EngineSession* sess, char* buf, size_t cap, size_t* out_len);
 
+/* The logical [N, C, H, W] input of the conv step that implements graph node
+ * `node`, as the last run computed it, copied into dst (contiguous NCHW,
+ * N*C*H*W floats, at most `cap`); dims receives N, C, H, W.  Needs a session
+ * created with PDEFA_KEEP_TENSORS=1 in the environment, in which every
+ * tensor keeps its own device memory (the program and its launch shapes
+ * are the same as without it); ENGINE_ERR_INVALID_ARG otherwise or when no
+ * conv step implements the node.  No counterpart in the reference (its
+ * engine_session_debug_intermediate reads the NHWC tensors its own
+ * interpreter keeps); tests use it to inspect a conv's inputs. */
+PDEFA_EXPORT EngineStatus pdefa_amd_session_read_conv_input(EngineSession* sess, const char* node, float* dst,
+                                                           size_t cap, int64_t* dims);
+
 /* Plans `m` for inputs of the given shape without touching a GPU and returns
  * the program text (planner tests on hosts without a device).  With
  * PDEFA_PLAN_GROUP_ALL=1 in the environment, launch shapes come from the cost

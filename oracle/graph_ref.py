@@ -342,7 +342,7 @@ def _silu_consumer(model, conv):
 
 
 def run_graph(model: EngineModel, inputs, dtype=np.float64, compat_silu=True, flip=None, flip_tol=1e-5,
-              flip_elems=None, jump_log=None, jump_tol=1e-6):
+              flip_elems=None, jump_log=None, jump_tol=1e-6, jump_values=None):
     """Evaluates the graph on `inputs` (list of NCHW arrays); returns outputs
     as float32 arrays in graph_outputs order.  compat_silu=False evaluates the
     true SiLU everywhere.
@@ -357,7 +357,10 @@ def run_graph(model: EngineModel, inputs, dtype=np.float64, compat_silu=True, fl
     jump_log: optional list that receives (conv node name, flat index,
     relative distance) of every compat-SiLU activation whose pre-activation
     lies within jump_tol of a jump (the candidates for an fp32 conv landing
-    on the other side)."""
+    on the other side).
+    jump_values: optional dict that receives, for each jump_log entry
+    (conv node name, flat index), the activation on each side of the jump:
+    (the side the rounded float64 pre-activation takes, the other side)."""
     inter = {}
     skip = set()
 
@@ -405,8 +408,15 @@ def run_graph(model: EngineModel, inputs, dtype=np.float64, compat_silu=True, fl
                     if jump_log is not None:
                         fx = ((-y32) * np.float32(1.44269504088896341)).astype(np.float64).reshape(-1)
                         dist = np.abs(fx - np.floor(fx) - 0.5) / np.maximum(1.0, np.abs(fx))
-                        for i in np.flatnonzero(dist <= jump_tol):
+                        near = np.flatnonzero(dist <= jump_tol)
+                        if jump_values is not None and near.size:
+                            y_lo, y_hi, _ = silu_winograd_compat_branches(y32.reshape(-1)[near], tol=0.0)
+                            own = silu_winograd_compat(y32.reshape(-1)[near])
+                        for j, i in enumerate(near):
                             jump_log.append((node.name, int(i), float(dist[i])))
+                            if jump_values is not None:
+                                other = y_hi[j] if own[j] == y_lo[j] else y_lo[j]
+                                jump_values[(node.name, int(i))] = (float(own[j]), float(other))
                     y = straight.astype(dtype)
                 else:
                     y = y / (1.0 + np.exp(-y))

@@ -21,6 +21,11 @@ ARCH = os.environ.get("PDEFA_OFFLOAD_ARCH", "gfx950")
 
 SOURCES = [
     "kernels/conv_mfma.hip",
+    "kernels/conv_mfma_tiles_a.hip",
+    "kernels/conv_mfma_tiles_b.hip",
+    "kernels/conv_mfma_tiles_c.hip",
+    "kernels/conv_mfma_tiles_d.hip",
+    "kernels/conv_mfma_tiles_e.hip",
     "kernels/conv_wino.hip",
     "kernels/ops.hip",
     "kernels/yolo_decode.hip",
@@ -75,7 +80,7 @@ def _compile(src: str) -> str:
 def build(verbose: bool = False) -> str:
     os.makedirs(OBJ, exist_ok=True)
     os.makedirs(LIBDIR, exist_ok=True)
-    jobs = min(len(SOURCES), max(1, min(8, os.cpu_count() or 1)))
+    jobs = min(len(SOURCES), max(1, min(16, os.cpu_count() or 1)))
     with cf.ThreadPoolExecutor(jobs) as ex:
         objs = list(ex.map(_compile, SOURCES))
     tmp = LIB + ".tmp"

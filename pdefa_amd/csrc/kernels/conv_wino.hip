@@ -29,6 +29,7 @@
 // stores at per-pixel offsets of the output view.
 #include "../kernels.hpp"
 #include "act.hpp"
+#include "jump_fix.hpp"
 
 #include <algorithm>
 #include <mutex>
@@ -388,6 +389,16 @@ __global__ __launch_bounds__(256) void conv_wino_kernel(ConvArgs a, int tiles_h,
             ro[r][3] = r4.w;
         }
     }
+    // compat SiLU: bit 16 r + 4 q + k flags element (r, q, k) for the float64
+    // second pass (pre-activation next to a jump)
+    constexpr bool FIX = ACT == kActSiluWinogradForm;
+    uint32_t bits = 0;
+    auto flag = [&](int r, int q, int k, float pre) {
+        if constexpr (FIX)
+            bits |= static_cast<uint32_t>((yo[r][q] != kWinoNoPixel) & (cob[k] != kWinoNoPixel) &
+                                          silu_winograd_near_jump(pre, a.jump_window))
+                    << (16 * r + 4 * q + k);
+    };
     if (vec_out) {
         floatx4 rv[CB][4];
         if constexpr (RES) {
@@ -405,7 +416,9 @@ __global__ __launch_bounds__(256) void conv_wino_kernel(ConvArgs a, int tiles_h,
                 floatx4 v;
 #pragma unroll
                 for (int k = 0; k < 4; ++k) {
-                    v[k] = act_fixed<ACT>(yv[r][q][k] + bias4[k], a.act, a.slope);
+                    const float pre = yv[r][q][k] + bias4[k];
+                    flag(r, q, k, pre);
+                    v[k] = act_fixed<ACT>(pre, a.act, a.slope);
                     if (RES) v[k] += rv[r][q][k];
                 }
                 __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(uintx4, v), ybuf, yo[r][q] + cob[0], 0, 2);
@@ -428,10 +441,39 @@ __global__ __launch_bounds__(256) void conv_wino_kernel(ConvArgs a, int tiles_h,
             for (int q = 0; q < 4; ++q)
 #pragma unroll
                 for (int k = 0; k < 4; ++k) {
-                    float v = act_fixed<ACT>(yv[r][q][k] + bias4[k], a.act, a.slope);
+                    const float pre = yv[r][q][k] + bias4[k];
+                    flag(r, q, k, pre);
+                    float v = act_fixed<ACT>(pre, a.act, a.slope);
                     if (RES) v += rv[r][q][k];
                     __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v), ybuf, yo[r][q] + cob[k], 0, 2);
                 }
+    }
+    if constexpr (FIX) {
+        if (a.w_raw) {
+            // element (r, q, k): tile tl = tid / G4 + r * (256 / G4), pixel
+            // (row q >> 1, column q & 1), channel n0 + c4 + k; its offsets
+            // are still in s_yo4 / s_ro4
+            fix_near_jumps(
+                a, bits, 0,
+                [&](int e, int& n, int& oh, int& ow, int& co) {
+                    const int tg = t0 + tid / G4 + (e >> 4) * (256 / G4);
+                    n = tg / tiles_img;
+                    const int rr = tg - n * tiles_img;
+                    const int trow = rr / tiles_w;
+                    oh = 2 * trow + ((e >> 3) & 1);
+                    ow = 2 * (rr - trow * tiles_w) + ((e >> 2) & 1);
+                    co = n0 + c4 + (e & 3);
+                },
+                [&](int e, float pre) {
+                    const int tl = tid / G4 + (e >> 4) * (256 / G4);
+                    const int q = (e >> 2) & 3;
+                    const int32_t cb = (n0 + c4 + (e & 3)) * 4;
+                    float v = act_fixed<ACT>(pre, a.act, a.slope);
+                    if constexpr (RES)
+                        v += __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rbuf, s_ro4[tl][q] + cb, 0, 0));
+                    __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v), ybuf, s_yo4[tl][q] + cb, 0, 2);
+                });
+        }
     }
 }
 

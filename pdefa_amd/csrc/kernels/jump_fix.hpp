@@ -1,0 +1,114 @@
+// Float64 recomputation of conv outputs whose fp32 pre-activation lies next
+// to a jump of the reference's Winograd-epilogue SiLU.
+//
+// That SiLU (silu_winograd_form) is discontinuous where -x log2 e crosses a
+// half-integer: its output jumps by ~2% of |x| there.  Two fp32 summation
+// orders of one conv output differ by a few units in the last place of the
+// sum of the magnitudes of its terms, so an output whose -x log2 e lies that
+// close to a half-integer can land on either side of the jump depending on
+// the order -- the reference's AVX2 order, the device's MFMA order and the
+// exactly rounded sum need not agree.  The device takes the side of the
+// exactly rounded sum: every epilogue of a compat-SiLU conv flags the outputs
+// within kJumpWindow of a jump and, after its stores, the wave recomputes each
+// flagged output in float64 from the conv input and the raw OIHW weights and
+// writes it again with the activation applied to that sum rounded to fp32.  Outside the window the fp32 sum is
+// on the exact sum's side: the window exceeds the fp32 summation error of
+// the YOLOv8 layers by a wide margin (the sum of the terms' magnitudes times
+// 2^-24 stays below 5e-7 of max(1, |x log2 e|) on them, the window is 2^-16
+// of it).
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+#include "../kernels.hpp"
+
+namespace pdefa {
+namespace k {
+
+// Default half-width of the flagged band around each jump, relative to
+// max(1, |x log2 e|) (ConvArgs::jump_window).
+constexpr float kJumpWindow = 1.52587890625e-05f;  // 2^-16
+
+// True when -x log2 e (rounded to fp32 as silu_winograd_form rounds it) lies
+// within window * max(1, |x log2 e|) of a half-integer, inside the range
+// where the form's polynomial branch applies.
+__device__ __forceinline__ bool silu_winograd_near_jump(float x, float window) {
+#pragma clang fp contract(off)
+    const float fx = -x * 1.44269504088896341f;
+    const float n = __builtin_truncf(fx + __builtin_copysignf(0.49999997f, fx));
+    const float f = __builtin_fabsf(fx - n);
+    const float ax = __builtin_fabsf(fx);
+    const float w = window * (ax > 1.0f ? ax : 1.0f);
+    return (f >= 0.5f - w) & (ax < 128.0f);
+}
+
+// bias[g*Cout + co] + sum over (kh, kw, ci) of
+// x[n, oh*sh - ph + kh*dh, ow*sw - pw + kw*dw, g*Cin + ci] * w_raw[g*Cout + co][ci][kh][kw]
+// in float64.  The 64 lanes of the wave split the K terms (lane l takes
+// k = l, l + 64, ...) and every lane returns the total.  All 64 lanes must
+// be active; (n, oh, ow, co, g) must name an output element of the conv.
+__device__ __forceinline__ double conv_point_f64(const ConvArgs& a, int n, int oh, int ow, int co, int g) {
+    const int lane = threadIdx.x & 63;
+    const int K = a.KH * a.KW * a.Cin;
+    const int ih0 = oh * a.sh - a.ph, iw0 = ow * a.sw - a.pw;
+    const float* xb = a.x + static_cast<int64_t>(n) * a.x_sn + static_cast<int64_t>(g) * a.Cin;
+    const int64_t co_all = static_cast<int64_t>(g) * a.Cout + co;
+    const float* wb = a.w_raw + co_all * K;
+    double s = 0.0;
+    for (int k = lane; k < K; k += 64) {
+        const int tap = k / a.Cin;
+        const int ci = k - tap * a.Cin;
+        const int kh = tap / a.KW;
+        const int kw = tap - kh * a.KW;
+        const int ih = ih0 + kh * a.dh, iw = iw0 + kw * a.dw;
+        if (static_cast<unsigned>(ih) < static_cast<unsigned>(a.H) &&
+            static_cast<unsigned>(iw) < static_cast<unsigned>(a.W)) {
+            const double xv = xb[static_cast<int64_t>(ih) * a.x_sh + static_cast<int64_t>(iw) * a.x_sw + ci];
+            const double wv = wb[(static_cast<int64_t>(ci) * a.KH + kh) * a.KW + kw];
+            s = __builtin_fma(xv, wv, s);
+        }
+    }
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) s += __shfl_xor(s, off, 64);
+    return s + static_cast<double>(a.bias[co_all]);
+}
+
+// Second pass of a compat-SiLU epilogue, after its stores: for each lane's
+// flagged elements (bit e of `bits`), coord(e, n, oh, ow, co) gives the
+// element's output coordinates and store(e, pre) writes the element again
+// from its float64 pre-activation rounded to fp32 (activation, residual,
+// upsampled copies as the first pass).  The flagged elements of the wave are
+// taken one at a time, lowest lane first, and rewritten by the lane that
+// wrote them first, after that lane's earlier stores have completed.  The
+// branch is uniform: with nothing flagged this costs one ballot.  The
+// residual a store reads must not share elements with the output.
+template <typename Bits, typename Coord, typename Store>
+__device__ __forceinline__ void fix_near_jumps(const ConvArgs& a, Bits bits, int g, Coord&& coord, Store&& store) {
+    if (__builtin_amdgcn_ballot_w64(bits != 0) == 0) return;
+    // vmcnt(0) expcnt(0) lgkmcnt(0): the first pass's stores have landed
+    __builtin_amdgcn_s_waitcnt(0);
+    const int lane = threadIdx.x & 63;
+    while (true) {
+        const uint64_t lanes = __builtin_amdgcn_ballot_w64(bits != 0);
+        if (lanes == 0) break;
+        const int src = __builtin_ctzll(lanes);
+        const unsigned long long lb = __shfl(static_cast<unsigned long long>(bits), src, 64);
+        const int e = __builtin_ctzll(lb);
+        int n, oh, ow, co;
+        coord(e, n, oh, ow, co);
+        n = __shfl(n, src, 64);
+        oh = __shfl(oh, src, 64);
+        ow = __shfl(ow, src, 64);
+        co = __shfl(co, src, 64);
+        const double s = conv_point_f64(a, n, oh, ow, co, g);
+        if (lane == src) {
+            store(e, static_cast<float>(s));
+            bits &= ~(static_cast<Bits>(1) << e);
+        }
+    }
+}
+
+}  // namespace k
+}  // namespace pdefa

@@ -416,6 +416,23 @@ PDEFA_EXPORT EngineStatus pdefa_amd_session_plan(const EngineSession* sess, char
     });
 }
 
+PDEFA_EXPORT EngineStatus pdefa_amd_session_read_conv_input(EngineSession* sess, const char* node, float* dst,
+                                                           size_t cap, int64_t* dims) {
+    if (!sess || sess->magic != kMagicSession) return ENGINE_ERR_INVALID_HANDLE;
+    if (!node || !dims) return ENGINE_ERR_NULL_PTR;
+    return guarded([&] {
+        clear_error();
+        std::vector<float> v;
+        sess->inner->read_conv_input(node, v, dims);
+        if (v.size() > cap || (!dst && !v.empty())) {
+            set_error("read_conv_input: the destination holds fewer floats than the tensor");
+            return ENGINE_ERR_INVALID_ARG;
+        }
+        if (!v.empty()) std::memcpy(dst, v.data(), v.size() * sizeof(float));
+        return ENGINE_OK;
+    });
+}
+
 PDEFA_EXPORT EngineStatus pdefa_amd_plan_model(const EngineModel* m, const int64_t* shape, int32_t ndim, char* buf,
                                                size_t cap, size_t* out_len) {
     if (!m || m->magic != kMagicModel) return ENGINE_ERR_INVALID_HANDLE;

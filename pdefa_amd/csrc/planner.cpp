@@ -1335,8 +1335,10 @@ class Planner {
             }
             // a conv whose output feeds a nearest 2x Resize right after it also
             // writes the upsampled copy (the FPN's upsample into its concat)
+            // (not a compat-SiLU conv: its float64 second pass rewrites only y)
             if (st[i].kind == StepKind::ConvMfma && st[i].vec && !k::is_wino_tile(st[i].tile) && i + 1 < st.size() &&
-                st[i + 1].kind == StepKind::Resize && views_equal(st[i + 1].a, st[i].out)) {
+                st[i].act != k::kActSiluWinogradForm && st[i + 1].kind == StepKind::Resize &&
+                views_equal(st[i + 1].a, st[i].out)) {
                 const VRef& y = st[i].out;
                 const VRef& u = st[i + 1].out;
                 if (u.rank == 4 && y.rank == 4 && u.dims[0] == y.dims[0] && u.dims[1] == y.dims[1] &&
@@ -1442,11 +1444,22 @@ class Planner {
             int tile = -1;
             if (groupable(st[S[0]])) {
                 double cur_ms = 0.0, sep_ms = 0.0;
+                // a conv writing an upsampled copy and a compat-SiLU conv take
+                // different kernel builds, so they never share a launch
+                auto kinds_mix = [&](const std::vector<int>& T) {
+                    bool up = false, compat = false;
+                    for (int t : T) {
+                        up = up || st[t].up.buf != -1;
+                        compat = compat || st[t].act == k::kActSiluWinogradForm;
+                    }
+                    return up && compat;
+                };
                 for (size_t r = 1; r < ready.size() && S.size() < static_cast<size_t>(k::kMaxConvGroup); ++r) {
                     const int c = ready[r];
                     if (!groupable(st[c])) continue;
                     std::vector<int> T = S;
                     T.push_back(c);
+                    if (kinds_mix(T)) continue;
                     std::vector<ConvQuery> qs;
                     std::vector<k::ConvLaunchShape> solo;
                     for (int t : T) {

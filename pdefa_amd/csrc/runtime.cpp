@@ -232,7 +232,8 @@ Session::Session(Model& m) : model_(&m) {
     // false ordering.  Off by default: on YOLOv8 the critical path holds ~80%
     // of the steps and the measured gain was within noise.
     concurrent_ = use_graph_ && env_flag("PDEFA_CONCURRENT", false);
-    opts_.reuse_memory = !concurrent_;
+    keep_tensors_ = env_flag("PDEFA_KEEP_TENSORS", false);
+    opts_.reuse_memory = !concurrent_ && !keep_tensors_;
     opts_.split_k = env_flag("PDEFA_SPLITK", true);
     if (const char* t = std::getenv("PDEFA_CONV_TILE")) {
         for (int i = 0; i < k::kNumConvShapes; ++i)
@@ -570,6 +571,17 @@ void Session::prepare(const std::vector<std::vector<int64_t>>& dims) {
                     c.wpk = pk.wpk;
                 }
                 c.bias = pk.bias;
+                // raw OIHW weights for the compat SiLU's float64 recomputation;
+                // PDEFA_JUMP_WINDOW widens its band (tests: 0.5 recomputes
+                // every output of such a conv)
+                if (s.act == k::kActSiluWinogradForm && s.groups == 1) {
+                    c.w_raw = dev_->wptr.at(-1000 - n.inputs[1]);
+                    if (const char* jw = std::getenv("PDEFA_JUMP_WINDOW")) {
+                        const float w = std::strtof(jw, nullptr);
+                        if (!(w > 0.0f && w <= 0.5f)) throw std::runtime_error("PDEFA_JUMP_WINDOW must be in (0, 0.5]");
+                        c.jump_window = w;
+                    }
+                }
                 c.KH = s.KH;
                 c.KW = s.KW;
                 c.sh = s.sh;
@@ -1013,6 +1025,46 @@ void Session::step_stats(int32_t iters, std::vector<double>& ms, std::vector<int
 }
 
 std::string Session::plan_text() const { return prep_ ? describe_plan(*model_, prep_->plan) : std::string(); }
+
+void Session::read_conv_input(const std::string& node, std::vector<float>& dst, int64_t dims[4]) {
+    if (!keep_tensors_) throw std::runtime_error("tensors are not kept: create the session with PDEFA_KEEP_TENSORS=1");
+    if (!prep_ || runs == 0) throw std::runtime_error("read_conv_input needs a completed run");
+    const Plan& plan = prep_->plan;
+    const Step* st = nullptr;
+    for (const Step& s : plan.steps)
+        if ((s.kind == StepKind::ConvMfma || s.kind == StepKind::ConvDirect) && s.node >= 0 &&
+            model_->nodes.at(s.node).name == node)
+            st = &s;
+    if (!st) throw std::runtime_error("no conv step implements node " + node);
+    const VRef& r = st->a;
+    if (r.rank != 4 || r.buf < 0) throw std::runtime_error("conv input is not a rank-4 arena view");
+    k::View in;
+    in.ptr = prep_->arena + plan.bufs.at(r.buf).offset + r.off;
+    in.rank = 4;
+    k::View out;
+    out.rank = 4;
+    int64_t n = 1;
+    for (int d = 3; d >= 0; --d) {
+        in.dims[d] = out.dims[d] = dims[d] = r.dims[d];
+        in.str[d] = r.str[d];
+        out.str[d] = n;
+        n *= r.dims[d];
+    }
+    float* tmp = nullptr;
+    PDEFA_HIP(hipMalloc(&tmp, static_cast<size_t>(std::max<int64_t>(n, 1)) * sizeof(float)));
+    out.ptr = tmp;
+    try {
+        k::launch_eltwise(k::kEltCopy, out, in, in, 0.0f, stream_);
+        dst.resize(static_cast<size_t>(n));
+        PDEFA_HIP(hipMemcpyAsync(dst.data(), tmp, static_cast<size_t>(n) * sizeof(float), hipMemcpyDeviceToHost,
+                                 stream_));
+        PDEFA_HIP(hipStreamSynchronize(stream_));
+    } catch (...) {
+        (void)hipFree(tmp);
+        throw;
+    }
+    PDEFA_HIP(hipFree(tmp));
+}
 
 // ------------------------------------------------------------- ops_matmul
 

@@ -105,6 +105,13 @@ class Session {
     uint64_t runs = 0;
     std::string plan_text() const;
     const Plan* plan() const { return prep_ ? &prep_->plan : nullptr; }
+    // With PDEFA_KEEP_TENSORS=1 at creation every tensor keeps its own arena
+    // memory (the program and its launch shapes are unchanged): after a run,
+    // the logical [N, C, H, W] input of the conv step implementing graph node
+    // `node` is copied into `dst` (contiguous, N*C*H*W floats); dims receives
+    // N, C, H, W.  Throws when tensors are not kept or no conv step
+    // implements the node.
+    void read_conv_input(const std::string& node, std::vector<float>& dst, int64_t dims[4]);
 
    private:
     struct Launch {
@@ -178,6 +185,7 @@ class Session {
     ProfileFn prof_fn_ = nullptr;
     void* prof_user_ = nullptr;
     bool use_graph_ = true;
+    bool keep_tensors_ = false;  // PDEFA_KEEP_TENSORS=1: no arena reuse (read_conv_input)
     PlanOptions opts_;
     bool autotune_ = true;  // time candidate conv launch shapes while planning
     bool group_convs_ = true;  // grouped launches of independent convs (measured)

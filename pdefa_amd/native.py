@@ -73,6 +73,8 @@ def lib() -> C.CDLL:
             "pdefa_amd_device_name": (C.c_char_p, []),
             "pdefa_amd_tune_stats": (C.c_int, [C.POINTER(i64), C.POINTER(i64)]),
             "pdefa_amd_ops_matmul_noalloc": (C.c_int, [vp, vp, vp]),
+            "pdefa_amd_session_read_conv_input": (C.c_int, [vp, C.c_char_p, C.POINTER(C.c_float), sz,
+                                                            C.POINTER(i64)]),
         }
         for name, (res, args) in sig.items():
             f = getattr(L, name)
@@ -163,6 +165,18 @@ class Engine:
             ts.append((time.perf_counter() - t0) * 1e3)
             check(st, "engine_session_run")
         return ts
+
+    def conv_input(self, node: str, cap: int = 1 << 26) -> np.ndarray:
+        """The [N, C, H, W] input of the conv step implementing `node` after
+        the last run (the session must have been created with
+        PDEFA_KEEP_TENSORS=1)."""
+        buf = np.empty(cap, np.float32)
+        dims = (C.c_int64 * 4)()
+        check(lib().pdefa_amd_session_read_conv_input(self.sess, node.encode(),
+                                                      buf.ctypes.data_as(C.POINTER(C.c_float)), cap, dims),
+              "pdefa_amd_session_read_conv_input")
+        shape = tuple(int(d) for d in dims)
+        return buf[:int(np.prod(shape))].reshape(shape).copy()
 
     def replay(self, iters: int) -> float:
         ms = C.c_double()
