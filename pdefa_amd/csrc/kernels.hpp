@@ -112,12 +112,13 @@ struct ConvArgs {
     int64_t r_sn = 0, r_sh = 0, r_sw = 0;
     const float* wpk = nullptr;
     const float* bias = nullptr;  // >= Cout floats
-    // raw OIHW weights [groups*Cout][Cin][KH][KW]: with act ==
+    // the K-major packed weights (the layout above; the same as wpk on the
+    // implicit-GEMM path, the Winograd path's wpk holds U): with act ==
     // kActSiluWinogradForm the epilogue recomputes outputs next to a jump of
     // that SiLU from them in float64 (kernels/jump_fix.hpp); nullptr skips it.
     // jump_window: the flagged band's half-width relative to
     // max(1, |x log2 e|) (kJumpWindow; 0.5 flags every output)
-    const float* w_raw = nullptr;
+    const float* w_kmaj = nullptr;
     float jump_window = 1.52587890625e-05f;
     int32_t KH = 1, KW = 1, sh = 1, sw = 1, ph = 0, pw = 0, dh = 1, dw = 1;
     int32_t K = 0;        // KH*KW*Cin

@@ -16,7 +16,10 @@ namespace k {
 // as 2^n * P(f) with n = round(-x log2 e), f the remainder in log2 units and P
 // the polynomial below.  The reference applies it on 3x3/s1 layers with
 // 16 < Cin <= 512, and its outputs are matched only with the same function.
-__device__ __forceinline__ float silu_winograd_form(float x) {
+// near (when given): -x log2 e lies within window * max(1, |x log2 e|) of
+// a half-integer, where the form jumps, inside the range where its
+// polynomial branch applies.
+__device__ __forceinline__ float silu_winograd_form(float x, float window = 0.0f, bool* near = nullptr) {
     // The product -x log2 e is rounded before it is used, as in the reference:
     // no contraction into the rounding add or the remainder.
 #pragma clang fp contract(off)
@@ -27,6 +30,10 @@ __device__ __forceinline__ float silu_winograd_form(float x) {
     // check over all such floats agrees); the add is the only rounding step
     const float n = __builtin_truncf(fx + __builtin_copysignf(0.49999997f, fx));
     const float f = fx - n;
+    if (near) {
+        const float ax = __builtin_fabsf(fx);
+        *near = (__builtin_fabsf(f) >= 0.5f - window * (ax > 1.0f ? ax : 1.0f)) & (ax < 128.0f);
+    }
     float p = 1.9875691500e-4f;
     p = __builtin_fmaf(p, f, 1.3981999507e-3f);
     p = __builtin_fmaf(p, f, 8.3334519073e-3f);

@@ -29,7 +29,7 @@ __global__ __launch_bounds__(256) void conv_splitk_reduce(ConvArgs a) {
     const int M = a.N * HoWo;
     const int per_group = M * a.Cout;
     const int total = per_group * a.groups;
-    const bool fix = a.act == kActSiluWinogradForm && a.w_raw != nullptr;  // groups == 1 (launcher)
+    const bool fix = a.act == kActSiluWinogradForm && a.w_kmaj != nullptr;  // groups == 1 (launcher)
     for (int base = blockIdx.x * blockDim.x; base < total; base += gridDim.x * blockDim.x) {
         const bool live = base + static_cast<int>(threadIdx.x) < total;
         const int i = live ? base + static_cast<int>(threadIdx.x) : 0;
@@ -205,7 +205,7 @@ void check_conv(const ConvArgs& a, const ConvTileShape& sh, bool vec) {
         static_cast<int64_t>(a.splits - 1) * a.kt_per_split >= a.ktiles)
         fail("bad split");
     if (a.splits > 1 && !a.ws) fail("split-K without workspace");
-    if (a.w_raw && a.act == kActSiluWinogradForm && a.groups != 1)
+    if (a.w_kmaj && a.act == kActSiluWinogradForm && a.groups != 1)
         fail("the compat SiLU's float64 recomputation takes ungrouped convs");
     if (a.up && (a.u_sn < 0 || a.u_sh < 0 || a.u_sw < 0)) fail("negative upsample strides");
     if (a.x_sh < 0 || a.x_sw < 0 ||

@@ -111,9 +111,11 @@ __device__ __forceinline__ int xcd_tile(int lin, int total) {
 // Epilogue builds of the implicit-GEMM kernels, kept apart so that a larger
 // epilogue does not raise every other build's register count: kEpiPlain
 // (bias, activation, residual), kEpiFix (also the compat SiLU's float64
-// second pass, jump_fix.hpp), kEpiUp (also an upsampled copy of the output).
-// One launch never needs both of the last two (the launchers check).
-constexpr int kEpiPlain = 0, kEpiFix = 1, kEpiUp = 2;
+// second pass, jump_fix.hpp; grouped launches), kEpiFixOnly (the compat
+// SiLU with its second pass alone: one conv's launch), kEpiUp (also an
+// upsampled copy of the output).  One launch never needs both the second
+// pass and an upsampled copy (the launchers check).
+constexpr int kEpiPlain = 0, kEpiFix = 1, kEpiUp = 2, kEpiFixOnly = 3;
 
 // One BM x BN output tile (m block bx, n block by) of K split bz of problem a.
 template <int BM, int BN, int WM, int WN, int KG, int PF, bool VEC, int EPI>
@@ -459,8 +461,9 @@ __device__ __forceinline__ void conv_tile(const ConvArgs& a, const int bx, const
             u[a.u_sh + a.u_sw] = v;
         };
         // compat SiLU: outputs whose pre-activation lies next to one of its
-        // jumps are flagged and written again from a float64 recomputation
-        // after the stores (jump_fix.hpp); the output row offsets stay in LDS
+        // jumps are flagged, left out of the stores and written afterwards
+        // from a float64 recomputation (jump_fix.hpp); the output row offsets
+        // stay in LDS
         constexpr bool FIX = decltype(fix_c)::value && ACT == kActSiluWinogradForm && !PART;
         auto rewrite = [&](int row, int c, float pre) {
             float v = act_fixed<ACT>(pre, a.act, a.slope);
@@ -514,15 +517,19 @@ __device__ __forceinline__ void conv_tile(const ConvArgs& a, const int bx, const
 #pragma unroll
                     for (int tn = 0; tn < TN; ++tn) {
                         float v = acc[tm][tn][e];
+                        bool flagged = false;
                         if (!PART) {
                             const float pre = v + bias_v[tn];
-                            if constexpr (FIX)
-                                bits |= static_cast<Bits>((yo[e] >= 0) & cok[tn] & silu_winograd_near_jump(pre, a.jump_window))
-                                        << ((tm * TN + tn) * NE + e);
-                            v = act_fixed<ACT>(pre, a.act, a.slope);
+                            if constexpr (FIX) {
+                                v = silu_winograd_form(pre, a.jump_window, &flagged);
+                                flagged = flagged & (yo[e] >= 0) & cok[tn];
+                                bits |= static_cast<Bits>(flagged) << ((tm * TN + tn) * NE + e);
+                            } else {
+                                v = act_fixed<ACT>(pre, a.act, a.slope);
+                            }
                         }
                         if (RES) v += rv[e][tn];
-                        if (yo[e] >= 0 && cok[tn]) {
+                        if (yo[e] >= 0 && cok[tn] && !flagged) {
                             __builtin_nontemporal_store(v, &dst[yo[e] + co[tn]]);
                             if (UP) store_up(uo[e], co[tn], v);
                         }
@@ -530,7 +537,7 @@ __device__ __forceinline__ void conv_tile(const ConvArgs& a, const int bx, const
             }
             if constexpr (FIX) {
                 // element (tm * TN + tn) * NE + e
-                if (a.w_raw)
+                if (a.w_kmaj)
                     fix_near_jumps(
                         a, bits, grp,
                         [&](int el, int& n, int& oh, int& ow, int& c) {
@@ -595,21 +602,26 @@ __device__ __forceinline__ void conv_tile(const ConvArgs& a, const int bx, const
 #pragma unroll
             for (int i = 0; i < E; ++i) {
                 float r = v[i];
+                bool flagged = false;
                 if (!PART) {
                     const float pre = r + bias_v;
-                    if constexpr (FIX)
-                        bits |= static_cast<Bits>((yo[i] >= 0) & cok & silu_winograd_near_jump(pre, a.jump_window)) << i;
-                    r = act_fixed<ACT>(pre, a.act, a.slope);
+                    if constexpr (FIX) {
+                        r = silu_winograd_form(pre, a.jump_window, &flagged);
+                        flagged = flagged & (yo[i] >= 0) & cok;
+                        bits |= static_cast<Bits>(flagged) << i;
+                    } else {
+                        r = act_fixed<ACT>(pre, a.act, a.slope);
+                    }
                 }
                 if (RES) r += rv[i];
-                if (yo[i] >= 0 && cok) {
+                if (yo[i] >= 0 && cok && !flagged) {
                     __builtin_nontemporal_store(r, &dst[yo[i] + co]);
                     if (UP) store_up(uo[i], co, r);
                 }
             }
             if constexpr (FIX) {
                 // element i: row tid / BN + i * RSTEP, column co
-                if (a.w_raw)
+                if (a.w_kmaj)
                     fix_near_jumps(
                         a, bits, grp,
                         [&](int i, int& n, int& oh, int& ow, int& c) {
@@ -626,7 +638,10 @@ __device__ __forceinline__ void conv_tile(const ConvArgs& a, const int bx, const
     using COMPAT = std::integral_constant<int, kActSiluWinogradForm>;
     using GENERIC = std::integral_constant<int, kActGeneric>;
     using NONE = std::integral_constant<int, kActNone>;
-    if (a.splits > 1) {
+    if constexpr (EPI == kEpiFixOnly) {  // a compat-SiLU conv with the second pass (checked by the launcher)
+        if (a.res) epilogue(COMPAT{}, YES{}, NO{}, NO{}, YES{});
+        else epilogue(COMPAT{}, NO{}, NO{}, NO{}, YES{});
+    } else if (a.splits > 1) {
         epilogue(NONE{}, NO{}, YES{}, NO{}, NO{});
     } else if (EPI == kEpiUp && a.up) {  // upsampled copy (the FPN's Resize inputs: SiLU, no residual)
         if constexpr (EPI == kEpiUp) {
@@ -638,7 +653,7 @@ __device__ __forceinline__ void conv_tile(const ConvArgs& a, const int bx, const
         if (a.res) epilogue(SILU{}, YES{}, NO{}, NO{}, NO{});
         else epilogue(SILU{}, NO{}, NO{}, NO{}, NO{});
     } else if (a.act == kActSiluWinogradForm) {
-        if (EPI == kEpiFix && a.w_raw) {
+        if (EPI == kEpiFix && a.w_kmaj) {
             if constexpr (EPI == kEpiFix) {
                 if (a.res) epilogue(COMPAT{}, YES{}, NO{}, NO{}, YES{});
                 else epilogue(COMPAT{}, NO{}, NO{}, NO{}, YES{});
@@ -721,7 +736,7 @@ void fail(const std::string& m) { throw std::runtime_error("conv_mfma: " + m); }
 // The build a problem needs: an upsampled copy, the compat SiLU's float64
 // second pass, or neither.
 int epi_of(const ConvArgs& a) {
-    const bool fix = a.act == kActSiluWinogradForm && a.w_raw && a.splits == 1;
+    const bool fix = a.act == kActSiluWinogradForm && a.w_kmaj && a.splits == 1;
     if (a.up && fix) fail("a compat-SiLU conv with the float64 second pass cannot write an upsampled copy");
     return a.up ? kEpiUp : (fix ? kEpiFix : kEpiPlain);
 }
@@ -754,9 +769,9 @@ void launch_tile(const ConvArgs& a, bool vec, dim3 grid, hipStream_t s) {
         launch_one<BM, BN, WM, WN, KG, kPrefetch, true, kEpiUp>(a, grid, s);
     } else if (epi == kEpiFix) {
         if (vec)
-            launch_one<BM, BN, WM, WN, KG, kPrefetch, true, kEpiFix>(a, grid, s);
+            launch_one<BM, BN, WM, WN, KG, kPrefetch, true, kEpiFixOnly>(a, grid, s);
         else
-            launch_one<BM, BN, WM, WN, KG, kPrefetch, false, kEpiFix>(a, grid, s);
+            launch_one<BM, BN, WM, WN, KG, kPrefetch, false, kEpiFixOnly>(a, grid, s);
     } else if (vec) {
         launch_one<BM, BN, WM, WN, KG, kPrefetch, true, kEpiPlain>(a, grid, s);
     } else {

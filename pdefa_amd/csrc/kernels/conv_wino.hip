@@ -389,15 +389,22 @@ __global__ __launch_bounds__(256) void conv_wino_kernel(ConvArgs a, int tiles_h,
             ro[r][3] = r4.w;
         }
     }
-    // compat SiLU: bit 16 r + 4 q + k flags element (r, q, k) for the float64
-    // second pass (pre-activation next to a jump)
+    // compat SiLU with the float64 second pass (a.w_kmaj set): bit
+    // 16 r + 4 q + k flags element (r, q, k), whose pre-activation lies next
+    // to a jump; the stores below leave flagged elements out
     constexpr bool FIX = ACT == kActSiluWinogradForm;
+    const bool fix = FIX && a.w_kmaj != nullptr;
     uint32_t bits = 0;
-    auto flag = [&](int r, int q, int k, float pre) {
-        if constexpr (FIX)
-            bits |= static_cast<uint32_t>((yo[r][q] != kWinoNoPixel) & (cob[k] != kWinoNoPixel) &
-                                          silu_winograd_near_jump(pre, a.jump_window))
+    auto act_flag = [&](int r, int q, int k, float pre) {
+        if constexpr (FIX) {
+            bool near;
+            const float v = silu_winograd_form(pre, a.jump_window, &near);
+            bits |= static_cast<uint32_t>(fix & (yo[r][q] != kWinoNoPixel) & (cob[k] != kWinoNoPixel) & near)
                     << (16 * r + 4 * q + k);
+            return v;
+        } else {
+            return act_fixed<ACT>(pre, a.act, a.slope);
+        }
     };
     if (vec_out) {
         floatx4 rv[CB][4];
@@ -409,20 +416,34 @@ __global__ __launch_bounds__(256) void conv_wino_kernel(ConvArgs a, int tiles_h,
                     rv[r][q] = __builtin_bit_cast(
                         floatx4, __builtin_amdgcn_raw_buffer_load_b128(rbuf, ro[r][q] + cob[0], 0, 0));
         }
+        floatx4 v[CB][4];
 #pragma unroll
         for (int r = 0; r < CB; ++r)
 #pragma unroll
-            for (int q = 0; q < 4; ++q) {
-                floatx4 v;
+            for (int q = 0; q < 4; ++q)
 #pragma unroll
                 for (int k = 0; k < 4; ++k) {
-                    const float pre = yv[r][q][k] + bias4[k];
-                    flag(r, q, k, pre);
-                    v[k] = act_fixed<ACT>(pre, a.act, a.slope);
-                    if (RES) v[k] += rv[r][q][k];
+                    v[r][q][k] = act_flag(r, q, k, yv[r][q][k] + bias4[k]);
+                    if (RES) v[r][q][k] += rv[r][q][k];
                 }
-                __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(uintx4, v), ybuf, yo[r][q] + cob[0], 0, 2);
-            }
+        if (!FIX || __builtin_amdgcn_ballot_w64(bits != 0) == 0) {
+#pragma unroll
+            for (int r = 0; r < CB; ++r)
+#pragma unroll
+                for (int q = 0; q < 4; ++q)
+                    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(uintx4, v[r][q]), ybuf,
+                                                           yo[r][q] + cob[0], 0, 2);
+        } else {  // a flagged element in the wave: single floats, flagged ones left out
+#pragma unroll
+            for (int r = 0; r < CB; ++r)
+#pragma unroll
+                for (int q = 0; q < 4; ++q)
+#pragma unroll
+                    for (int k = 0; k < 4; ++k)
+                        __builtin_amdgcn_raw_buffer_store_b32(
+                            __float_as_uint(v[r][q][k]), ybuf,
+                            (bits >> (16 * r + 4 * q + k)) & 1u ? kWinoNoPixel : yo[r][q] + cob[k], 0, 2);
+        }
     } else {
         float rv[CB][4][4];
         if constexpr (RES) {
@@ -441,15 +462,15 @@ __global__ __launch_bounds__(256) void conv_wino_kernel(ConvArgs a, int tiles_h,
             for (int q = 0; q < 4; ++q)
 #pragma unroll
                 for (int k = 0; k < 4; ++k) {
-                    const float pre = yv[r][q][k] + bias4[k];
-                    flag(r, q, k, pre);
-                    float v = act_fixed<ACT>(pre, a.act, a.slope);
+                    float v = act_flag(r, q, k, yv[r][q][k] + bias4[k]);
                     if (RES) v += rv[r][q][k];
-                    __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v), ybuf, yo[r][q] + cob[k], 0, 2);
+                    __builtin_amdgcn_raw_buffer_store_b32(
+                        __float_as_uint(v), ybuf,
+                        (bits >> (16 * r + 4 * q + k)) & 1u ? kWinoNoPixel : yo[r][q] + cob[k], 0, 2);
                 }
     }
     if constexpr (FIX) {
-        if (a.w_raw) {
+        if (a.w_kmaj) {
             // element (r, q, k): tile tl = tid / G4 + r * (256 / G4), pixel
             // (row q >> 1, column q & 1), channel n0 + c4 + k; its offsets
             // are still in s_yo4 / s_ro4

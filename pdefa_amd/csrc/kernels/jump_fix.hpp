@@ -9,11 +9,12 @@
 // the order -- the reference's AVX2 order, the device's MFMA order and the
 // exactly rounded sum need not agree.  The device takes the side of the
 // exactly rounded sum: every epilogue of a compat-SiLU conv flags the outputs
-// within kJumpWindow of a jump and, after its stores, the wave recomputes each
-// flagged output in float64 from the conv input and the raw OIHW weights and
-// writes it again with the activation applied to that sum rounded to fp32.  Outside the window the fp32 sum is
+// within kJumpWindow of a jump, leaves them out of its stores, and then the
+// wave recomputes each flagged output in float64 from the conv input and the
+// K-major packed weights and writes it with the activation applied to that
+// sum rounded to fp32.  Outside the window the fp32 sum is
 // on the exact sum's side: the window exceeds the fp32 summation error of
-// the YOLOv8 layers by a wide margin (the sum of the terms' magnitudes times
+// the YOLOv8 layers by a margin (the sum of the terms' magnitudes times
 // 2^-24 stays below 5e-7 of max(1, |x log2 e|) on them, the window is 2^-16
 // of it).
 #pragma once
@@ -35,60 +36,75 @@ constexpr float kJumpWindow = 1.52587890625e-05f;  // 2^-16
 // within window * max(1, |x log2 e|) of a half-integer, inside the range
 // where the form's polynomial branch applies.
 __device__ __forceinline__ bool silu_winograd_near_jump(float x, float window) {
-#pragma clang fp contract(off)
-    const float fx = -x * 1.44269504088896341f;
-    const float n = __builtin_truncf(fx + __builtin_copysignf(0.49999997f, fx));
-    const float f = __builtin_fabsf(fx - n);
-    const float ax = __builtin_fabsf(fx);
-    const float w = window * (ax > 1.0f ? ax : 1.0f);
-    return (f >= 0.5f - w) & (ax < 128.0f);
+    bool near;
+    (void)silu_winograd_form(x, window, &near);
+    return near;
 }
 
 // bias[g*Cout + co] + sum over (kh, kw, ci) of
-// x[n, oh*sh - ph + kh*dh, ow*sw - pw + kw*dw, g*Cin + ci] * w_raw[g*Cout + co][ci][kh][kw]
-// in float64.  The 64 lanes of the wave split the K terms (lane l takes
-// k = l, l + 64, ...) and every lane returns the total.  All 64 lanes must
-// be active; (n, oh, ow, co, g) must name an output element of the conv.
+// x[n, oh*sh - ph + kh*dh, ow*sw - pw + kw*dw, g*Cin + ci] * w[co][k] in
+// float64, w the K-major packed weights (k = (kh*KW + kw)*Cin + ci, 32 x 32
+// blocks [co/32][k/32][co%32][k%32], one block set per group).  The 64 lanes
+// of the wave split the channels (lane l takes ci = l, l + 64, ...; its
+// loads are contiguous across lanes; a 3x3 conv's nine taps load together)
+// and every lane returns the total.
+// All 64 lanes must be active; (n, oh, ow, co, g) must name an output
+// element of the conv.
 __device__ __forceinline__ double conv_point_f64(const ConvArgs& a, int n, int oh, int ow, int co, int g) {
     const int lane = threadIdx.x & 63;
-    const int K = a.KH * a.KW * a.Cin;
     const int ih0 = oh * a.sh - a.ph, iw0 = ow * a.sw - a.pw;
     const float* xb = a.x + static_cast<int64_t>(n) * a.x_sn + static_cast<int64_t>(g) * a.Cin;
-    const int64_t co_all = static_cast<int64_t>(g) * a.Cout + co;
-    const float* wb = a.w_raw + co_all * K;
+    const float* wb = a.w_kmaj + static_cast<int64_t>(g) * a.w_group +
+                      static_cast<int64_t>(co >> 5) * a.ktiles * (kConvBN * kConvBK) + (co & 31) * kConvBK;
+    auto w_at = [&](int k) { return wb[static_cast<int64_t>(k >> 5) * (kConvBN * kConvBK) + (k & 31)]; };
     double s = 0.0;
-    for (int k = lane; k < K; k += 64) {
-        const int tap = k / a.Cin;
-        const int ci = k - tap * a.Cin;
-        const int kh = tap / a.KW;
-        const int kw = tap - kh * a.KW;
-        const int ih = ih0 + kh * a.dh, iw = iw0 + kw * a.dw;
-        if (static_cast<unsigned>(ih) < static_cast<unsigned>(a.H) &&
-            static_cast<unsigned>(iw) < static_cast<unsigned>(a.W)) {
-            const double xv = xb[static_cast<int64_t>(ih) * a.x_sh + static_cast<int64_t>(iw) * a.x_sw + ci];
-            const double wv = wb[(static_cast<int64_t>(ci) * a.KH + kh) * a.KW + kw];
-            s = __builtin_fma(xv, wv, s);
+    for (int c0 = 0; c0 < a.Cin; c0 += 64) {
+        const int ci = c0 + lane;
+        const bool cok = ci < a.Cin;
+        if (a.KH == 3 && a.KW == 3) {
+            // the nine taps' loads issued together, then the products
+            float xv[9], wv[9];
+#pragma unroll
+            for (int t = 0; t < 9; ++t) {
+                const int ih = ih0 + (t / 3) * a.dh, iw = iw0 + (t % 3) * a.dw;
+                const bool ok = cok & (static_cast<unsigned>(ih) < static_cast<unsigned>(a.H)) &
+                                (static_cast<unsigned>(iw) < static_cast<unsigned>(a.W));
+                xv[t] = ok ? xb[static_cast<int64_t>(ih) * a.x_sh + static_cast<int64_t>(iw) * a.x_sw + ci] : 0.0f;
+                wv[t] = ok ? w_at(t * a.Cin + ci) : 0.0f;
+            }
+#pragma unroll
+            for (int t = 0; t < 9; ++t) s = __builtin_fma(static_cast<double>(xv[t]), static_cast<double>(wv[t]), s);
+        } else {
+            for (int kh = 0; kh < a.KH; ++kh) {
+                const int ih = ih0 + kh * a.dh;
+                for (int kw = 0; kw < a.KW; ++kw) {
+                    const int iw = iw0 + kw * a.dw;
+                    if (cok && static_cast<unsigned>(ih) < static_cast<unsigned>(a.H) &&
+                        static_cast<unsigned>(iw) < static_cast<unsigned>(a.W))
+                        s = __builtin_fma(
+                            static_cast<double>(xb[static_cast<int64_t>(ih) * a.x_sh +
+                                                   static_cast<int64_t>(iw) * a.x_sw + ci]),
+                            static_cast<double>(w_at((kh * a.KW + kw) * a.Cin + ci)), s);
+                }
+            }
         }
     }
 #pragma unroll
     for (int off = 32; off >= 1; off >>= 1) s += __shfl_xor(s, off, 64);
-    return s + static_cast<double>(a.bias[co_all]);
+    return s + static_cast<double>(a.bias[static_cast<int64_t>(g) * a.Cout + co]);
 }
 
-// Second pass of a compat-SiLU epilogue, after its stores: for each lane's
-// flagged elements (bit e of `bits`), coord(e, n, oh, ow, co) gives the
-// element's output coordinates and store(e, pre) writes the element again
-// from its float64 pre-activation rounded to fp32 (activation, residual,
-// upsampled copies as the first pass).  The flagged elements of the wave are
-// taken one at a time, lowest lane first, and rewritten by the lane that
-// wrote them first, after that lane's earlier stores have completed.  The
-// branch is uniform: with nothing flagged this costs one ballot.  The
-// residual a store reads must not share elements with the output.
+// Second pass of a compat-SiLU epilogue, after its stores, which leave the
+// flagged elements out: for each lane's flagged elements (bit e of `bits`),
+// coord(e, n, oh, ow, co) gives the element's output coordinates and
+// store(e, pre) writes the element from its float64 pre-activation rounded
+// to fp32 (activation, residual as the first pass).  The flagged elements of
+// the wave are taken one at a time, lowest lane first.  The branch is
+// uniform: with nothing flagged this costs one ballot.  The residual a
+// store reads must not share elements with the output.
 template <typename Bits, typename Coord, typename Store>
 __device__ __forceinline__ void fix_near_jumps(const ConvArgs& a, Bits bits, int g, Coord&& coord, Store&& store) {
     if (__builtin_amdgcn_ballot_w64(bits != 0) == 0) return;
-    // vmcnt(0) expcnt(0) lgkmcnt(0): the first pass's stores have landed
-    __builtin_amdgcn_s_waitcnt(0);
     const int lane = threadIdx.x & 63;
     while (true) {
         const uint64_t lanes = __builtin_amdgcn_ballot_w64(bits != 0);

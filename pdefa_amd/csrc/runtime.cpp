@@ -571,11 +571,11 @@ void Session::prepare(const std::vector<std::vector<int64_t>>& dims) {
                     c.wpk = pk.wpk;
                 }
                 c.bias = pk.bias;
-                // raw OIHW weights for the compat SiLU's float64 recomputation;
+                // K-major weights for the compat SiLU's float64 recomputation;
                 // PDEFA_JUMP_WINDOW widens its band (tests: 0.5 recomputes
-                // every output of such a conv)
-                if (s.act == k::kActSiluWinogradForm && s.groups == 1) {
-                    c.w_raw = dev_->wptr.at(-1000 - n.inputs[1]);
+                // every output of such a conv), PDEFA_JUMP_FIX=0 turns it off
+                if (s.act == k::kActSiluWinogradForm && s.groups == 1 && env_flag("PDEFA_JUMP_FIX", true)) {
+                    c.w_kmaj = pk.wpk;
                     if (const char* jw = std::getenv("PDEFA_JUMP_WINDOW")) {
                         const float w = std::strtof(jw, nullptr);
                         if (!(w > 0.0f && w <= 0.5f)) throw std::runtime_error("PDEFA_JUMP_WINDOW must be in (0, 0.5]");
