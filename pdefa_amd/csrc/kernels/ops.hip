@@ -907,9 +907,11 @@ __device__ __forceinline__ int64_t row_offset(const View& v, int axis, int64_t r
     return off;
 }
 
-// Sort key: ascending keys = descending values, then ascending index.
+// Sort key: ascending keys = descending values, then ascending index; -0.0
+// keys as +0.0 (the two compare equal, so they tie and go by index).
 __device__ __forceinline__ unsigned long long topk_key(float v, int32_t i) {
     uint32_t u = __float_as_uint(v);
+    if (u == 0x80000000u) u = 0u;
     u = (u & 0x80000000u) ? ~u : (u | 0x80000000u);  // order-preserving
     return (static_cast<unsigned long long>(~u) << 32) | static_cast<uint32_t>(i);
 }

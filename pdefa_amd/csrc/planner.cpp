@@ -1217,9 +1217,23 @@ class Planner {
             }
             plan_.outputs.push_back(ov);
             plan_.output_dims.push_back(v.dims);
-            plan_.output_int32.push_back(v.producer >= 0 && eops_[v.producer].k == EK::TopK &&
-                                         eops_[v.producer].topk_indices);
+            plan_.output_int32.push_back(holds_indices(r));
         }
+    }
+
+    // True when the value holds TopK indices: produced by an indices TopK,
+    // directly or through Reshape / Slice / Transpose views (the reference
+    // keeps the I32 tensor type through them).
+    bool holds_indices(int32_t ref) {
+        for (int hops = 0; hops < 1024; ++hops) {
+            const Val& v = val(ref);
+            if (v.producer < 0) return false;
+            const EOp& e = eops_[v.producer];
+            if (e.k == EK::TopK) return e.topk_indices;
+            if ((e.k != EK::Reshape && e.k != EK::Slice && e.k != EK::Transpose) || e.in.empty()) return false;
+            ref = e.in[0];
+        }
+        return false;
     }
 
     // ---- 5b. step fusion ---------------------------------------------------
@@ -1763,8 +1777,10 @@ Plan build_plan(const Model& m, const std::vector<std::vector<int64_t>>& input_d
 
 std::string describe_plan(const Model& m, const Plan& p) {
     std::ostringstream os;
+    int int32_outputs = 0;
+    for (bool b : p.output_int32) int32_outputs += b;
     os << "steps=" << p.steps.size() << " bufs=" << p.bufs.size() << " arena_bytes=" << p.arena_elems * 4
-       << " copies=" << p.n_copies << "\n";
+       << " copies=" << p.n_copies << " int32_outputs=" << int32_outputs << "\n";
     for (size_t i = 0; i < p.steps.size(); ++i) {
         const Step& s = p.steps[i];
         os << i << " " << step_kind_name(s.kind);

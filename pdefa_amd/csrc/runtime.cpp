@@ -34,7 +34,10 @@ bool device_available() {
 // blocks go back to a pool (sizes rounded up to 64 KiB) and a later request
 // takes the smallest pooled block that holds it, at most twice its size.  The
 // pool keeps up to 1 GiB; blocks beyond that are released.  Pooled blocks
-// stay allocated until the process ends.
+// stay allocated until the process ends.  Page-locked bytes, live and
+// pooled, stay under PDEFA_PINNED_LIMIT_MB (default 4096): a request beyond
+// it first releases pooled blocks, then falls back to pageable memory.
+// PDEFA_PINNED=0 turns page-locking off (every tensor pageable).
 namespace {
 constexpr size_t kPinnedGrain = 64 * 1024;
 constexpr size_t kPinnedPoolCap = size_t{1} << 30;
@@ -42,11 +45,30 @@ std::mutex g_pinned_mu;
 std::multimap<size_t, void*> g_pinned_pool;          // size -> free block
 std::unordered_map<void*, size_t> g_pinned_size;      // every live or pooled block
 size_t g_pinned_pooled = 0;
+size_t g_pinned_total = 0;  // bytes of every live or pooled block
+
+bool pinning_enabled() {
+    static const bool on = [] {
+        const char* e = std::getenv("PDEFA_PINNED");
+        return !(e && e[0] == '0');
+    }();
+    return on;
+}
+
+size_t pinned_limit() {
+    static const size_t lim = [] {
+        const char* e = std::getenv("PDEFA_PINNED_LIMIT_MB");
+        const long long mb = e ? std::atoll(e) : 4096;
+        return static_cast<size_t>(mb > 0 ? mb : 0) << 20;
+    }();
+    return lim;
+}
 }  // namespace
 
 void* pinned_alloc(size_t bytes) {
-    if (!device_available()) return nullptr;
+    if (!pinning_enabled() || !device_available()) return nullptr;
     const size_t sz = (bytes + kPinnedGrain - 1) / kPinnedGrain * kPinnedGrain;
+    std::vector<void*> release;  // pooled blocks given back to make room
     {
         std::lock_guard<std::mutex> lk(g_pinned_mu);
         auto it = g_pinned_pool.lower_bound(sz);
@@ -56,10 +78,26 @@ void* pinned_alloc(size_t bytes) {
             g_pinned_pool.erase(it);
             return p;
         }
+        while (g_pinned_total + sz > pinned_limit() && !g_pinned_pool.empty()) {
+            auto big = std::prev(g_pinned_pool.end());
+            release.push_back(big->second);
+            g_pinned_pooled -= big->first;
+            g_pinned_total -= big->first;
+            g_pinned_size.erase(big->second);
+            g_pinned_pool.erase(big);
+        }
+        if (g_pinned_total + sz > pinned_limit()) {
+            for (void* q : release) (void)hipHostFree(q);
+            return nullptr;  // pageable fallback
+        }
+        g_pinned_total += sz;  // reserved before the allocation below
     }
+    for (void* q : release) (void)hipHostFree(q);
     void* p = nullptr;
     if (hipHostMalloc(&p, sz, hipHostMallocDefault) != hipSuccess) {
         (void)hipGetLastError();
+        std::lock_guard<std::mutex> lk(g_pinned_mu);
+        g_pinned_total -= sz;
         return nullptr;
     }
     std::lock_guard<std::mutex> lk(g_pinned_mu);
@@ -77,7 +115,10 @@ void pinned_free(void* p) {
         g_pinned_pooled += sz;
         return;
     }
-    if (it != g_pinned_size.end()) g_pinned_size.erase(it);
+    if (it != g_pinned_size.end()) {
+        g_pinned_total -= sz;
+        g_pinned_size.erase(it);
+    }
     lk.unlock();
     (void)hipHostFree(p);
 }

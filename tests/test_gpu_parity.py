@@ -962,6 +962,54 @@ def test_yolov8n_b8_vs_reference(yolov8n, tmp_path):
                                             follow=explained.get(i))
 
 
+def test_sessions_on_threads_batchinference_pattern(yolov8n):
+    """The reference's BatchInference pattern (pdefa/python/src/pdefa/batch.py:
+    45-60): several Sessions of one Model, each driven by its own thread of a
+    pool at the same time (set_input, run, the borrowed per-thread output
+    copied at once, PDEFA1.0/src/api/engine_api.cpp:654-677).  Over several
+    rounds every image's head equals, bit for bit, that image run alone in a
+    session of its own."""
+    import ctypes as C
+    from concurrent.futures import ThreadPoolExecutor
+
+    from pdefa_amd import pdefa
+
+    print("[case] 4 sessions on 4 threads, yolov8n b1 each", flush=True)
+    _, path = yolov8n
+    x, _ = ys.yolo_inputs(8)
+    ctx = pdefa.Context()
+    model = pdefa.Model(ctx, path)
+
+    def tensor(a):
+        t = pdefa.tensor_empty(list(a.shape))
+        a = np.ascontiguousarray(a, np.float32)
+        pdefa._check(pdefa._lib().engine_tensor_copy_from(t.raw, C.c_void_p(a.ctypes.data), a.nbytes), "copy_from")
+        return t
+
+    inputs = [tensor(x[i:i + 1]) for i in range(8)]
+    solo = pdefa.Session(ctx, model)
+    alone = []
+    for t in inputs:
+        solo.set_input(0, t)
+        solo.run()
+        alone.append(solo.output(0).to_numpy().copy())
+    sessions = [pdefa.Session(ctx, model) for _ in range(4)]
+
+    def work(j, img):
+        s = sessions[j]
+        s.set_input(0, inputs[img])
+        s.run()
+        return img, s.output(0).to_numpy().copy()
+
+    with ThreadPoolExecutor(max_workers=4) as ex:
+        for rnd in range(4):
+            futs = [ex.submit(work, j, (2 * rnd + 3 * j) % 8) for j in range(4)]
+            for f in futs:
+                img, out = f.result(timeout=120)
+                assert np.array_equal(out, alone[img]), f"round {rnd}: image {img} differs from its run alone"
+    print("4 rounds x 4 concurrent sessions: every head equal to its image run alone", flush=True)
+
+
 GROUPED_CASES = [
     # cin, cout, k, stride, hw, groups, forced launch shape
     (64, 64, 3, 1, 80, 64, None),      # depthwise
@@ -1404,8 +1452,30 @@ def test_topk_head_vs_reference(tmp_path, anchors, nc, k, k_dtype):
     np.testing.assert_array_equal(got[1].astype(np.float32), ref[1])
 
 
-@pytest.mark.parametrize("shape,axis,k", [((5, 1000), 1, 7), ((1000, 3), 0, 10), ((2, 3, 50), -1, 50),
-                                          ((16384,), 0, 300), ((3, 700, 2), 1, 699)])
+TOPK_CASES = [((5, 1000), 1, 7), ((1000, 3), 0, 10), ((2, 3, 50), -1, 50), ((16384,), 0, 300),
+              ((3, 700, 2), 1, 699)]
+
+
+@pytest.mark.parametrize("shape,axis,k", [((4, 60), 1, 20), ((50, 3), 0, 49)])
+def test_topk_ties(tmp_path, shape, axis, k):
+    """Tied values, +0.0 beside -0.0: the device's TopK equals the oracle's
+    (ties by ascending index, the two zeros equal) in values and indices; the
+    reference's values too (its partial_sort leaves tie order open)."""
+    from test_oracle import tied_rows
+    print(f"[case] topk ties shape={shape} axis={axis} k={k}", flush=True)
+    model, _ = ys.build_topk_gather(shape, axis, k)
+    x = tied_rows(shape)
+    path = str(tmp_path / "t.engine")
+    ys.save(model, path)
+    got = run_engine(path, x)
+    want = graph_ref.run_graph(model, [x])
+    np.testing.assert_array_equal(got[0], want[0])
+    np.testing.assert_array_equal(got[1].astype(np.float32), want[1])
+    ref = reference_runs(path, x, split=False)[0]
+    np.testing.assert_array_equal(got[0], ref[0])
+
+
+@pytest.mark.parametrize("shape,axis,k", TOPK_CASES)
 def test_topk_gather_elements(tmp_path, shape, axis, k):
     """TopK on every axis position up to the 16384-element limit, and
     GatherElements whose constant indices hold negative and out-of-range

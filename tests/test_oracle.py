@@ -558,6 +558,38 @@ def test_oracle_topk_gather_vs_compiled_reference(tmp_path, shape, axis, k):
     np.testing.assert_array_equal(np.moveaxis(oo[2], ax, 0).reshape(shape[ax], -1)[:, 0], want[fixed])
 
 
+def tied_rows(shape, seed=5):
+    """Rows of few distinct values (ties everywhere), +0.0 and -0.0 among them."""
+    rng = np.random.default_rng(seed)
+    vals = np.array([0.5, -0.25, 0.0, -0.0, 1.0, 0.5], np.float32)
+    return vals[rng.integers(0, len(vals), size=shape)]
+
+
+@needs_ref
+@pytest.mark.parametrize("shape,axis,k", [((4, 60), 1, 20), ((50, 3), 0, 49)])
+def test_oracle_topk_ties_vs_compiled_reference(tmp_path, shape, axis, k):
+    """With tied values (and +0.0 beside -0.0) the reference's
+    std::partial_sort leaves the order inside a group of equal values
+    open: its values equal the oracle's exactly, and each of its indices
+    points at a value equal to the oracle's at that position (the indices
+    may differ only inside groups of equal values)."""
+    model, _ = ys.build_topk_gather(shape, axis, k)
+    x = tied_rows(shape)
+    path = str(tmp_path / "t.engine")
+    ys.save(model, path)
+    rv, ri = ref_lib.RefSession(path).run(x)[:2]
+    ov, oi = graph_ref.run_graph(model, [x])[:2]
+    np.testing.assert_array_equal(rv, ov)
+    xa = np.moveaxis(x, axis, -1)
+    take = lambda idx: np.take_along_axis(xa, np.moveaxis(idx, axis, -1).astype(np.int64), axis=-1)
+    np.testing.assert_array_equal(take(ri), np.moveaxis(ov, axis, -1))
+    np.testing.assert_array_equal(take(oi), np.moveaxis(ov, axis, -1))
+    # the oracle's rule: ties by ascending index, +0.0 and -0.0 equal
+    row = xa.reshape(-1, xa.shape[-1])[0]
+    want = sorted(range(len(row)), key=lambda i: (-float(row[i]), i))[:k]
+    assert np.moveaxis(oi, axis, -1).reshape(-1, k)[0].astype(np.int64).tolist() == want
+
+
 def test_engine_format_keeps_int64_constants(tmp_path):
     from pdefa_amd import engine_format as ef
     model, _ = ys.build_topk_head(300, 4, 10)

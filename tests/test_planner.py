@@ -337,6 +337,27 @@ def test_topk_gather_plan(tmp_path):
         native.plan_text(path, list(x.shape))
 
 
+def test_topk_indices_through_views_stay_int32(tmp_path):
+    """TopK indices that reach a graph output through Reshape, Slice and
+    Transpose views are still returned as I32 (the reference keeps the
+    tensor type through them); the values output stays F32."""
+    b = ys.GraphBuilder()
+    vals, idx = b.node("TopK", "/t/TopK", [-1, b.const("/t/k", np.array([6], np.int64))], n_out=2, axis=1)
+    r = b.node("Reshape", "/t/Reshape", [idx, b.const("/t/shape", [1, 2, 3])])
+    t = b.node("Transpose", "/t/Transpose", [r, b.const("/t/Transpose::perm", [0, 2, 1])])
+    model = b.model([1, 40], [None, None], [vals, t])
+    path = str(tmp_path / "topk_view.engine")
+    ys.save(model, path)
+    info, _ = parse(native.plan_text(path, [1, 40]))
+    assert info["int32_outputs"] == 1
+    model = b.model([1, 40], [None, None], [vals, r])
+    ys.save(model, path)
+    assert parse(native.plan_text(path, [1, 40]))[0]["int32_outputs"] == 1
+    model = b.model([1, 40], None, [vals])
+    ys.save(model, path)
+    assert parse(native.plan_text(path, [1, 40]))[0]["int32_outputs"] == 0
+
+
 def test_plan_launches_names_every_3x3_conv(y8n_path, monkeypatch):
     """bench.py's launch list: one entry per launch (the members of a grouped
     launch together), and every conv line names its kernel size and stride,

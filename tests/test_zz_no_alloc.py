@@ -2,6 +2,8 @@
 no allocation) through the C ABI against engine_ops_matmul, whose kernels
 and launch shapes it shares: the same bits, on consecutive calls of
 decreasing size (the second finds the first one's data in the array)."""
+import ctypes as C
+
 import numpy as np
 import pytest
 
@@ -54,3 +56,31 @@ def test_noalloc_matmul_rejects_oversize_and_keeps_ops_rules():
     np.testing.assert_array_equal(native.matmul_into(a, b, sentinel, noalloc=True), sentinel)
     # the array still serves the next call
     _check(*_pair((33, 65), (65, 17), 9), "after the rejected call")
+
+
+def _device_free_bytes():
+    """hipMemGetInfo's free bytes of the current device (the HIP runtime the
+    library is linked against)."""
+    native.lib()
+    hip = C.CDLL("libamdhip64.so")
+    free, total = C.c_size_t(), C.c_size_t()
+    assert hip.hipMemGetInfo(C.byref(free), C.byref(total)) == 0
+    return free.value
+
+
+def test_noalloc_matmul_allocates_no_device_memory():
+    """A call of a shape larger than any earlier one leaves the device's free
+    memory unchanged; engine_ops_matmul on the same shape grows its scratch."""
+    print("[case] ops_matmul_noalloc 1200x1024 @ 1024x1100: device free memory", flush=True)
+    _check(*_pair((64, 64), (64, 64), 11), "warm-up")
+    a, b, out = _pair((1200, 1024), (1024, 1100), 12)
+    before = _device_free_bytes()
+    got = native.matmul_into(a, b, out, noalloc=True)
+    after = _device_free_bytes()
+    assert after == before, f"the no-allocation call changed free device memory by {before - after} bytes"
+    want = native.matmul_into(a, b, out)
+    grown = _device_free_bytes()
+    assert grown < after, "engine_ops_matmul allocated nothing for the larger shape"
+    assert np.array_equal(got, want)
+    print(f"free device memory unchanged by the no-allocation call; engine_ops_matmul took "
+          f"{(after - grown) / 2**20:.1f} MiB", flush=True)
