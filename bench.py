@@ -153,6 +153,12 @@ def conv3x3_layers(eng: native.Engine, iters: int = 20):
     return summary, rows
 
 
+def log_layers(rows):
+    for r in rows:
+        log(f"  3x3 s{r['stride']} {r['kernel']:6s} {r['tile']:10s} {r['us']:8.2f} us {r['gflop']:8.4f} GFLOP "
+            f"{r['tflops']:7.2f} TFLOP/s {r['frac']:6.1%}  {' + '.join(r['names'])}")
+
+
 def roofline_engine(tmp: str):
     model, x = ys.build_single_conv(**CONV_ROOF, seed=7)
     path = os.path.join(tmp, "conv3x3.engine")
@@ -551,10 +557,11 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the reference CPU baseline")
     ap.add_argument("--no-m16", action="store_true", help="skip the YOLOv8m batch-16 line")
     ap.add_argument("--no-pipeline", action="store_true", help="skip the pixels-to-detections pipeline line")
-    ap.add_argument("--only", choices=["all", "roofline", "program"], default="all",
+    ap.add_argument("--only", choices=["all", "roofline", "program", "layers"], default="all",
                     help="program: plan YOLOv8n at --batch, then only warm-up and timed graph replays "
-                         "(a kernel trace's last steps x launches dispatches are the timed forwards)")
-    ap.add_argument("--batch", type=int, default=1, help="with --only program: the batch size")
+                         "(a kernel trace's last steps x launches dispatches are the timed forwards); "
+                         "layers: YOLOv8n's 3x3 conv launches at --batch, one by one")
+    ap.add_argument("--batch", type=int, default=1, help="with --only program / layers: the batch size")
     ap.add_argument("--calib-copy", action="store_true",
                     help="with --only roofline / program: also run the PMC calibration copy")
     ap.add_argument("--ingest-pmc", nargs=3, metavar=("FETCH_CSV", "WRITE_CSV", "TILE"))
@@ -599,6 +606,21 @@ def main():
                                       "ms_per_step": round(ms, 5),
                                       "images_per_s": round(args.batch * 1000.0 / ms, 2)}}), flush=True)
         return
+    if args.only == "layers":
+        with tempfile.TemporaryDirectory() as tmp:
+            path = os.path.join(tmp, "yolov8n.engine")
+            ys.save(ys.build_yolov8("n", seed=0), path)
+            x, _ = ys.yolo_inputs(args.batch)
+            eng = native.Engine(path)
+            try:
+                eng.run(x)
+                c3, rows = conv3x3_layers(eng)
+            finally:
+                eng.close()
+        log(f"yolov8n b{args.batch} 3x3 launches:")
+        log_layers(rows)
+        print(json.dumps({"conv3x3_layers": {f"b{args.batch}": c3}}), flush=True)
+        return
     if args.only == "roofline":
         with tempfile.TemporaryDirectory() as tmp:
             roof = roofline(tmp, 50)
@@ -624,9 +646,7 @@ def main():
                 c3, c3_rows = conv3x3_layers(eng)
             finally:
                 eng.close()
-            for r in c3_rows:
-                log(f"  3x3 s{r['stride']} {r['kernel']:6s} {r['tile']:10s} {r['us']:8.2f} us {r['gflop']:8.4f} GFLOP "
-                    f"{r['tflops']:7.2f} TFLOP/s {r['frac']:6.1%}  {' + '.join(r['names'])}")
+            log_layers(c3_rows)
             res[batch] = dict(ms=ms, wall=wall, first=first, ips=batch * 1000.0 / ms, session_run=sr, conv3x3=c3,
                               **cs)
             log(f"  {res[batch]['ips']:.1f} images/s replayed from HBM, {ms:.4f} ms/step; engine_session_run "

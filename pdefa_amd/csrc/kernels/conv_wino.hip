@@ -13,18 +13,24 @@
 //   G   = [1 0 0; 1/2 1/2 1/2; 1/2 -1/2 1/2; 0 0 1]
 //   A^T = [1 1 1 0; 0 1 -1 -1]
 //
-// A workgroup (4 waves) computes 32 tiles x BN output channels.  Wave i owns
-// the transformed row i (positions (i, 0..3)) for all 32 tiles and BN
-// channels: 4 x BN/32 accumulator blocks of 32x32.  The GEMM operands come
-// straight from global memory (L1/L2), no LDS and no barrier in the K loop:
-// lane (tile l%32, half h) loads the two patch rows that row i of B^T combines
-// (16-byte runs of 4 channels, half h taking channels 4h..4h+3 of each 8-wide
-// K step), forms V_(i,0..3) in registers, and pairs them with U_(i,j) float4s
-// of the same 4 channels; MFMA m of a step uses channel 4h+m on half h, the
-// same k for A and B.  Loads (range-checked buffer loads) run one K step
-// ahead, issued between the step's MFMAs.  At the end each wave applies the
-// column transform (A^T over j) in registers, the 4 waves exchange those rows
-// through LDS, and the row transform (A^T over i), bias, activation and
+// A workgroup (4 waves) computes a block of 32 tiles of one image (a 2-D
+// block, (32 >> b) x (1 << b) tiles, its shape chosen on the host to cover
+// the tile map with the fewest blocks) x BN output channels.  Wave i owns the
+// transformed row i (positions (i, 0..3)) for all 32 tiles and BN channels:
+// 4 x BN/32 accumulator blocks of 32x32.  Each K step (8 input channels) the
+// workgroup copies the block's input patch region -- every pixel once, 16-byte
+// runs of 4 channels, range-checked buffer loads that return zeros outside
+// the image -- into one of three LDS stages; lane (tile l%32, half h) reads
+// the two patch rows that row i of B^T combines from there (half h taking
+// channels 4h..4h+3 of the step), forms V_(i,0..3) in registers, and pairs
+// them with U_(i,j) float4s of the same 4 channels loaded one step ahead;
+// MFMA m of a step uses channel 4h+m on half h, the same k for A and B.  The
+// K loop is software-pipelined over the three stages with one barrier per
+// step: while step s's MFMAs run, step s+1's patch values are read and
+// transformed, step s+2's patch goes from registers to its stage and step
+// s+3's is loaded.  At the end each wave applies the column transform (A^T
+// over j) in registers, the 4 waves exchange those rows through LDS (the
+// stages' memory), and the row transform (A^T over i), bias, activation and
 // residual produce each tile's 2x2 outputs, written with range-checked buffer
 // stores at per-pixel offsets of the output view.
 #include "../kernels.hpp"
@@ -59,6 +65,10 @@ constexpr int32_t kWinoMaxViewBytes = kWinoNoPixel - 4096;
 // buffer resource word 3 for raw 32-bit buffer access
 constexpr int kWinoBufferFlags = 0x00020000;
 
+// Input pixels of the largest tile-block patch region ((2*32+2) x 4 for a
+// 32x1 or 1x32 block): the LDS patch stage holds this many pixels per half.
+constexpr int kWinoMaxPatchPixels = 66 * 4;
+
 int wino_cin_pad(int Cin) { return (Cin + kCK - 1) / kCK * kCK; }
 int wino_cout_pad(int Cout) { return (Cout + 63) / 64 * 64; }
 
@@ -69,6 +79,13 @@ int64_t view_bytes(int N, int H, int W, int C, int64_t sn, int64_t sh, int64_t s
 }
 
 }  // namespace
+
+// A workgroup's 32 output tiles form a block of (32 >> tbw_log2) x
+// (1 << tbw_log2) tiles of one image; block_rows x block_cols blocks cover an
+// image's tiles_h x tiles_w tile map.
+struct WinoGeom {
+    int32_t tiles_h, tiles_w, tbw_log2, block_rows, block_cols;
+};
 
 bool wino_eligible(int KH, int KW, int sh, int sw, int dh, int dw, int Cin) {
     return KH == 3 && KW == 3 && sh == 1 && sw == 1 && dh == 1 && dw == 1 && Cin % 4 == 0 && Cin >= 8 &&
@@ -127,17 +144,21 @@ __global__ void pack_wino_weights_kernel(float* dst, const float* w, int Cout, i
 }
 
 template <int BN, int ACT, bool RES>
-__global__ __launch_bounds__(256) void conv_wino_kernel(ConvArgs a, int tiles_h, int tiles_w, int x_bytes,
-                                                        int u_bytes, int y_bytes, int r_bytes, int vec_out) {
+__global__ __launch_bounds__(256) void conv_wino_kernel(ConvArgs a, WinoGeom geo, int x_bytes, int u_bytes,
+                                                        int y_bytes, int r_bytes, int vec_out) {
     constexpr int CB = BN / 32;  // 32-wide channel blocks per wave
     // Exchange rows [row i][column c][tile] hold BN channels and 8 floats of
     // padding: the two lane halves of a column-transform write (tiles 4
-    // apart) then fall on disjoint LDS banks.
+    // apart) then fall on disjoint LDS banks.  The exchange reuses the
+    // memory of the patch stages (it is written after the K loop).
     constexpr int kXchRow = BN + 8;
-    __shared__ __attribute__((aligned(16))) float xch[4 * 2 * kWT * kXchRow];
+    constexpr int kXchFloats = 4 * 2 * kWT * kXchRow;
+    constexpr int kStageFloats = 3 * 2 * kWinoMaxPatchPixels * 4;  // [stage][half][pixel][4 channels]
+    __shared__ __attribute__((aligned(16))) float smem[kXchFloats > kStageFloats ? kXchFloats : kStageFloats];
+    float* const xch = smem;
     // per tile of the workgroup: byte offsets of its four output (and
     // residual) pixels (r, c) at [2r + c], kWinoNoPixel for pixels outside
-    // the output (or past the last tile)
+    // the output (or outside the tile map)
     __shared__ __attribute__((aligned(16))) int32_t s_yo4[kWT][4];
     __shared__ __attribute__((aligned(16))) int32_t s_ro4[RES ? kWT : 1][4];
 
@@ -146,8 +167,10 @@ __global__ __launch_bounds__(256) void conv_wino_kernel(ConvArgs a, int tiles_h,
     const int wi_row = tid >> 6;  // transformed row i of this wave
     const int half = lane >> 5;
     const int l32 = lane & 31;
-    const int tiles_img = tiles_h * tiles_w;
-    const int T = a.N * tiles_img;
+    const int tiles_h = geo.tiles_h, tiles_w = geo.tiles_w;
+    const int tbw = 1 << geo.tbw_log2, tbh = kWT >> geo.tbw_log2;  // tile block: tbh x tbw tiles
+    const int PW = 2 * tbw + 2;  // its input patch region: (2 tbh + 2) x PW pixels
+    const int PP = (2 * tbh + 2) * PW;
 
     // XCD-aware order: dispatch slot `lin` runs on XCD lin % 8; each XCD takes
     // a contiguous range of (tile block fastest) workgroup indices.
@@ -158,7 +181,13 @@ __global__ __launch_bounds__(256) void conv_wino_kernel(ConvArgs a, int tiles_h,
     const int wid = xcd * q + min(xcd, rmd) + lin / kXcds;
     const int by = wid / gx;
     const int bx = wid - by * gx;
-    const int t0 = bx * kWT;
+    // tile block bx: image bn, block row bbr, block column bbc
+    const int blocks_img = geo.block_rows * geo.block_cols;
+    const int bn = bx / blocks_img;
+    const int brem = bx - bn * blocks_img;
+    const int bbr = brem / geo.block_cols;
+    const int bbc = brem - bbr * geo.block_cols;
+    const int th0 = bbr * tbh, tw0 = bbc * tbw;  // first tile of the block
     const int n0 = by * BN;
     const int cop = (a.Cout + 63) / 64 * 64;
     const int cq = (a.Cin + kCK - 1) / kCK * (kCK / 4);
@@ -178,89 +207,97 @@ __global__ __launch_bounds__(256) void conv_wino_kernel(ConvArgs a, int tiles_h,
     }
 
     if (tid < kWT) {  // read after the barrier that precedes the epilogue
-        const int tg = t0 + tid;
-        const int nn = tg / tiles_img;
-        const int rr = tg - nn * tiles_img;
-        const int oh0 = 2 * (rr / tiles_w);
-        const int ow0 = 2 * (rr - (rr / tiles_w) * tiles_w);
+        const int th = th0 + (tid >> geo.tbw_log2);
+        const int tw = tw0 + (tid & (tbw - 1));
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
-            const int oh = oh0 + (q >> 1), ow = ow0 + (q & 1);
-            const bool ok = tg < T && oh < a.Ho && ow < a.Wo;
-            const int64_t yo = static_cast<int64_t>(nn) * a.y_sn + static_cast<int64_t>(oh) * a.y_sh +
+            const int oh = 2 * th + (q >> 1), ow = 2 * tw + (q & 1);
+            const bool ok = th < tiles_h && tw < tiles_w && oh < a.Ho && ow < a.Wo;
+            const int64_t yo = static_cast<int64_t>(bn) * a.y_sn + static_cast<int64_t>(oh) * a.y_sh +
                                static_cast<int64_t>(ow) * a.y_sw;
             s_yo4[tid][q] = ok ? static_cast<int32_t>(yo * 4) : kWinoNoPixel;
             if constexpr (RES) {
-                const int64_t ro = static_cast<int64_t>(nn) * a.r_sn + static_cast<int64_t>(oh) * a.r_sh +
+                const int64_t ro = static_cast<int64_t>(bn) * a.r_sn + static_cast<int64_t>(oh) * a.r_sh +
                                    static_cast<int64_t>(ow) * a.r_sw;
                 s_ro4[tid][q] = ok ? static_cast<int32_t>(ro * 4) : kWinoNoPixel;
             }
         }
     }
 
-    // this lane's tile and the two patch rows that row i of B^T combines:
-    // s_b = d[ra][b] + sg * d[rb][b]
-    const int t = t0 + l32;
-    const bool t_ok = t < T;
-    const int tt = t_ok ? t : 0;
-    const int n = tt / tiles_img;
-    const int trem = tt - n * tiles_img;
-    const int th = trem / tiles_w;
-    const int tw = trem - th * tiles_w;
-    const int ra = wi_row == 2 ? 2 : (wi_row == 0 ? 0 : 1);
-    const int rb = wi_row == 0 ? 2 : (wi_row == 2 ? 1 : (wi_row == 1 ? 2 : 3));
-    const float sg = wi_row == 1 ? 1.0f : -1.0f;
-    // Patch and weight loads are buffer loads: a per-lane 32-bit byte offset,
-    // the K step's advance in a scalar offset, the channel block in the
-    // immediate.  Patch positions outside the image get kWinoNoPixel, past
-    // the input's buffer range, and load zeros.
+    // Patch stages: each K step (8 input channels) the workgroup copies the
+    // block's patch region -- every input pixel once, 4 channels per 16-byte
+    // load, zeros outside the image and past Cin -- into one of three LDS
+    // stages ([half][pixel][4 channels]); the waves read their tiles' patch
+    // rows from there.  Thread t owns slots t, t + 256, t + 512 (slot =
+    // 2 * pixel + channel half).
     const __amdgpu_buffer_rsrc_t xbuf =
         __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(a.x), 0, x_bytes, kWinoBufferFlags);
     const __amdgpu_buffer_rsrc_t ubuf =
         __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(a.wpk), 0, u_bytes, kWinoBufferFlags);
-    // byte offset of channel 4*half of each patch position
-    int32_t doff[2][4];
+    constexpr int kSlots = 3;
+    constexpr int kStage = 2 * kWinoMaxPatchPixels * 4;  // floats per stage
+    int32_t soff[kSlots];  // byte offset of the slot's 4 channels at step 0 (kWinoNoPixel: zeros)
+    int32_t sdst[kSlots];  // LDS float index of the slot within a stage (-1: no slot)
+    bool shi[kSlots];      // upper channel half
 #pragma unroll
-    for (int r = 0; r < 2; ++r) {
-        const int hi = 2 * th - a.ph + (r == 0 ? ra : rb);
-#pragma unroll
-        for (int b = 0; b < 4; ++b) {
-            const int wi = 2 * tw - a.pw + b;
-            const bool ok = t_ok & (static_cast<unsigned>(hi) < static_cast<unsigned>(a.H)) &
+    for (int j = 0; j < kSlots; ++j) {
+        const int slot = tid + 256 * j;
+        const int p = slot >> 1, h = slot & 1;
+        const int pr = p / PW, pc = p - pr * PW;
+        const int hi = 2 * th0 - a.ph + pr, wi = 2 * tw0 - a.pw + pc;
+        const bool inside = p < PP && (static_cast<unsigned>(hi) < static_cast<unsigned>(a.H)) &&
                             (static_cast<unsigned>(wi) < static_cast<unsigned>(a.W));
-            const int64_t o = static_cast<int64_t>(n) * a.x_sn + static_cast<int64_t>(hi) * a.x_sh +
-                              static_cast<int64_t>(wi) * a.x_sw;
-            doff[r][b] = ok ? static_cast<int32_t>(o * 4) + half * 16 : kWinoNoPixel;
-        }
+        const int64_t o = static_cast<int64_t>(bn) * a.x_sn + static_cast<int64_t>(hi) * a.x_sh +
+                          static_cast<int64_t>(wi) * a.x_sw;
+        soff[j] = inside ? static_cast<int32_t>(o * 4) + h * 16 : kWinoNoPixel;
+        sdst[j] = p < PP ? (h * kWinoMaxPatchPixels + p) * 4 : -1;
+        shi[j] = h != 0;
     }
+    const int32_t d_step = kCK * 4;  // bytes per K step of patch channels
+    const int ns = (a.Cin + kCK - 1) / kCK;  // K steps
+    // the upper half of the last step lies past Cin when Cin % 8 == 4: zeros
+    const bool last_half_past = (a.Cin & 4) != 0;
+    floatx4 sreg[kSlots];
+    auto load_patch = [&](int st) {
+        const bool past = last_half_past && st == ns - 1;
+#pragma unroll
+        for (int j = 0; j < kSlots; ++j)
+            sreg[j] = __builtin_bit_cast(
+                floatx4, __builtin_amdgcn_raw_buffer_load_b128(xbuf, past && shi[j] ? kWinoNoPixel : soff[j],
+                                                               st * d_step, 0));
+    };
+    auto store_patch = [&](int stage) {
+        float* dst = smem + stage * kStage;
+#pragma unroll
+        for (int j = 0; j < kSlots; ++j)
+            if (sdst[j] >= 0) *reinterpret_cast<floatx4*>(dst + sdst[j]) = sreg[j];
+    };
+
+    // this lane's tile within the block and the two patch rows that row i of
+    // B^T combines: s_b = d[ra][b] + sg * d[rb][b]
+    const int tr = l32 >> geo.tbw_log2, tc = l32 & (tbw - 1);
+    const int ra = wi_row == 2 ? 2 : (wi_row == 0 ? 0 : 1);
+    const int rb = wi_row == 0 ? 2 : (wi_row == 2 ? 1 : (wi_row == 1 ? 2 : 3));
+    const float sg = wi_row == 1 ? 1.0f : -1.0f;
+    // LDS float index of patch position (ra / rb, b = 0) of this lane's half
+    const int pa = (half * kWinoMaxPatchPixels + (2 * tr + ra) * PW + 2 * tc) * 4;
+    const int pb = (half * kWinoMaxPatchPixels + (2 * tr + rb) * PW + 2 * tc) * 4;
     // byte offset of the U float4 of (position (i, j), channel group `half`,
     // this lane's output channel of block 0); block cb adds cb * 512 bytes,
     // K step s adds s * 2 * cop float4s
     int32_t uoff[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j) uoff[j] = ((((wi_row * 4 + j) * cq + half) * cop) + n0 + l32) * 16;
-    const int32_t d_step = kCK * 4;      // bytes per K step of patch channels
     const int32_t u_step = 2 * cop * 16;  // bytes per K step of U
 
-    floatx4 dreg[2][2][4];
     floatx4 ureg[2][4][CB];
-    // Channels past Cin (the upper half of the last step when Cin % 8 == 4)
-    // read the last 4 channels again (`back` = 16 bytes on that half of the
-    // last step); their U rows are zero, so they add nothing.
-    const int32_t last_back = (a.Cin & 4) && half ? 16 : 0;
-    auto load = [&](int s, floatx4 (&d)[2][4], floatx4 (&u)[4][CB], int32_t back) {
-#pragma unroll
-        for (int r = 0; r < 2; ++r)
-#pragma unroll
-            for (int b = 0; b < 4; ++b)
-                d[r][b] = __builtin_bit_cast(
-                    floatx4, __builtin_amdgcn_raw_buffer_load_b128(xbuf, doff[r][b] - back, s * d_step, 0));
+    auto load_u = [&](int st, floatx4 (&u)[4][CB]) {
 #pragma unroll
         for (int j = 0; j < 4; ++j)
 #pragma unroll
             for (int cb = 0; cb < CB; ++cb)
                 u[j][cb] = __builtin_bit_cast(
-                    floatx4, __builtin_amdgcn_raw_buffer_load_b128(ubuf, uoff[j] + cb * 512, s * u_step, 0));
+                    floatx4, __builtin_amdgcn_raw_buffer_load_b128(ubuf, uoff[j] + cb * 512, st * u_step, 0));
     };
 
     floatx16 acc[4][CB];
@@ -271,18 +308,28 @@ __global__ __launch_bounds__(256) void conv_wino_kernel(ConvArgs a, int tiles_h,
 #pragma unroll
             for (int e = 0; e < 16; ++e) acc[j][cb][e] = 0.0f;
 
-    // V = (B^T d B) row i for the 4 channels of this lane half (zero outside
-    // the image and past Cin), then the step's MFMAs
-    auto compute = [&](int s, const floatx4 (&d)[2][4], const floatx4 (&u)[4][CB]) {
-        (void)s;
+    // the lane's patch values of one step from an LDS stage, and V = (B^T d B)
+    // row i of them for the 4 channels of this lane half
+    floatx4 dreg[2][4];
+    floatx4 v[4];
+    auto read_d = [&](int stage) {
+        const float* src = smem + stage * kStage;
+#pragma unroll
+        for (int b = 0; b < 4; ++b) {
+            dreg[0][b] = *reinterpret_cast<const floatx4*>(src + pa + 4 * b);
+            dreg[1][b] = *reinterpret_cast<const floatx4*>(src + pb + 4 * b);
+        }
+    };
+    auto transform = [&] {
         floatx4 sv[4];
 #pragma unroll
-        for (int b = 0; b < 4; ++b) sv[b] = d[0][b] + sg * d[1][b];
-        floatx4 v[4];
+        for (int b = 0; b < 4; ++b) sv[b] = dreg[0][b] + sg * dreg[1][b];
         v[0] = sv[0] - sv[2];
         v[1] = sv[1] + sv[2];
         v[2] = sv[2] - sv[1];
         v[3] = sv[1] - sv[3];
+    };
+    auto mfmas = [&](const floatx4 (&u)[4][CB]) {
 #pragma unroll
         for (int m = 0; m < 4; ++m)
 #pragma unroll
@@ -292,46 +339,48 @@ __global__ __launch_bounds__(256) void conv_wino_kernel(ConvArgs a, int tiles_h,
                     acc[j][cb] = __builtin_amdgcn_mfma_f32_32x32x2f32(v[j][m], u[j][cb][m], acc[j][cb], 0, 0, 0);
     };
 
-    // Loads run one K step (8 channels) ahead.  Scheduling barriers keep each
-    // step's loads among the previous step's MFMAs (left alone, the scheduler
-    // sinks them below to save registers, and every step then waits a full L2
-    // round trip).
-    const int ns = (a.Cin + kCK - 1) / kCK;  // K steps
-    auto back_of = [&](int t) { return t == ns - 1 ? last_back : 0; };
-    // A load instruction's issue must not leave the matrix core idle (one
-    // wave per SIMD with BN = 64, two with BN = 32): the next step's loads go
-    // one after each of the step's first MFMAs (after the transform that
-    // feeds them).
-    auto interleave = [&] {
-        {
-            constexpr int kLoads = 8 + 4 * CB, kMfma = 16 * CB;
-            __builtin_amdgcn_sched_group_barrier(0x002, 64, 0);  // vector ALU (the transform)
-#pragma unroll
-            for (int i = 0; i < kLoads; ++i) {
-                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
-                __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // global load
-            }
-            __builtin_amdgcn_sched_group_barrier(0x008, kMfma - kLoads, 0);
-            __builtin_amdgcn_sched_barrier(0);
-        }
-    };
-    load(0, dreg[0], ureg[0], back_of(0));
-    int s = 0;
-    for (; s + 2 < ns; s += 2) {
-        load(s + 1, dreg[1], ureg[1], back_of(s + 1));
-        compute(s, dreg[0], ureg[0]);
-        interleave();
-        load(s + 2, dreg[0], ureg[0], back_of(s + 2));
-        compute(s + 1, dreg[1], ureg[1]);
-        interleave();
+    // Software pipeline over three LDS stages: while step s's MFMAs run, the
+    // patch values of step s + 1 are read from LDS and transformed, step
+    // s + 2's patch (in registers) goes to its stage and step s + 3's is
+    // loaded; U runs one step ahead in registers.  One barrier per step:
+    // the stage written in step s was last read in step s - 2.
+    load_patch(0);
+    load_u(0, ureg[0]);
+    store_patch(0);
+    if (ns > 1) {
+        load_patch(1);
+        store_patch(1);
     }
-    if (s + 1 < ns) {
-        load(s + 1, dreg[1], ureg[1], back_of(s + 1));
-        compute(s, dreg[0], ureg[0]);
-        interleave();
-        compute(s + 1, dreg[1], ureg[1]);
-    } else {
-        compute(s, dreg[0], ureg[0]);
+    if (ns > 2) load_patch(2);
+    __syncthreads();
+    read_d(0);
+    transform();
+    auto step = [&](int st, auto cur_c, auto ub_c) {
+        constexpr int CUR = decltype(cur_c)::value;  // stage of step st
+        constexpr int UB = decltype(ub_c)::value;    // U registers of step st
+        const bool next = st + 1 < ns;
+        if (next) {
+            read_d((CUR + 1) % 3);
+            load_u(st + 1, ureg[UB ^ 1]);
+        }
+        mfmas(ureg[UB]);
+        if (st + 2 < ns) {
+            store_patch((CUR + 2) % 3);
+            if (st + 3 < ns) load_patch(st + 3);
+        }
+        if (next) transform();
+        __syncthreads();
+    };
+    using I0 = std::integral_constant<int, 0>;
+    using I1 = std::integral_constant<int, 1>;
+    using I2 = std::integral_constant<int, 2>;
+    for (int st = 0; st < ns; st += 6) {
+        step(st, I0{}, I0{});
+        if (st + 1 < ns) step(st + 1, I1{}, I1{});
+        if (st + 2 < ns) step(st + 2, I2{}, I0{});
+        if (st + 3 < ns) step(st + 3, I0{}, I1{});
+        if (st + 4 < ns) step(st + 4, I1{}, I0{});
+        if (st + 5 < ns) step(st + 5, I2{}, I1{});
     }
 
     // column transform in registers: P[i][0] = M0 + M1 + M2, P[i][1] = M1 - M2 - M3.
@@ -477,12 +526,10 @@ __global__ __launch_bounds__(256) void conv_wino_kernel(ConvArgs a, int tiles_h,
             fix_near_jumps(
                 a, bits, 0,
                 [&](int e, int& n, int& oh, int& ow, int& co) {
-                    const int tg = t0 + tid / G4 + (e >> 4) * (256 / G4);
-                    n = tg / tiles_img;
-                    const int rr = tg - n * tiles_img;
-                    const int trow = rr / tiles_w;
-                    oh = 2 * trow + ((e >> 3) & 1);
-                    ow = 2 * (rr - trow * tiles_w) + ((e >> 2) & 1);
+                    const int tl = tid / G4 + (e >> 4) * (256 / G4);
+                    n = bn;
+                    oh = 2 * (th0 + (tl >> geo.tbw_log2)) + ((e >> 3) & 1);
+                    ow = 2 * (tw0 + (tl & (tbw - 1))) + ((e >> 2) & 1);
                     co = n0 + c4 + (e & 3);
                 },
                 [&](int e, float pre) {
@@ -507,21 +554,41 @@ struct WinoBytes {
 };
 
 template <int BN, int ACT>
-void launch_act(const ConvArgs& a, dim3 grid, int th, int tw, WinoBytes b, hipStream_t s) {
+void launch_act(const ConvArgs& a, dim3 grid, WinoGeom g, WinoBytes b, hipStream_t s) {
     if (a.res)
-        hipLaunchKernelGGL((conv_wino_kernel<BN, ACT, true>), grid, dim3(256), 0, s, a, th, tw, b.x, b.u, b.y, b.r, b.vec);
+        hipLaunchKernelGGL((conv_wino_kernel<BN, ACT, true>), grid, dim3(256), 0, s, a, g, b.x, b.u, b.y, b.r, b.vec);
     else
-        hipLaunchKernelGGL((conv_wino_kernel<BN, ACT, false>), grid, dim3(256), 0, s, a, th, tw, b.x, b.u, b.y, b.r, b.vec);
+        hipLaunchKernelGGL((conv_wino_kernel<BN, ACT, false>), grid, dim3(256), 0, s, a, g, b.x, b.u, b.y, b.r, b.vec);
 }
 
 template <int BN>
-void launch_bn(const ConvArgs& a, dim3 grid, int th, int tw, WinoBytes b, hipStream_t s) {
+void launch_bn(const ConvArgs& a, dim3 grid, WinoGeom g, WinoBytes b, hipStream_t s) {
     switch (a.act) {
-        case kActSilu: launch_act<BN, kActSilu>(a, grid, th, tw, b, s); break;
-        case kActSiluWinogradForm: launch_act<BN, kActSiluWinogradForm>(a, grid, th, tw, b, s); break;
-        case kActNone: launch_act<BN, kActNone>(a, grid, th, tw, b, s); break;
-        default: launch_act<BN, kActGeneric>(a, grid, th, tw, b, s); break;
+        case kActSilu: launch_act<BN, kActSilu>(a, grid, g, b, s); break;
+        case kActSiluWinogradForm: launch_act<BN, kActSiluWinogradForm>(a, grid, g, b, s); break;
+        case kActNone: launch_act<BN, kActNone>(a, grid, g, b, s); break;
+        default: launch_act<BN, kActGeneric>(a, grid, g, b, s); break;
     }
+}
+
+// The tile block with the fewest blocks over the tile map (ties: the squarer
+// block, whose patch region has the least halo).
+WinoGeom wino_geometry(int64_t tiles_h, int64_t tiles_w) {
+    WinoGeom best{};
+    int64_t best_blocks = -1, best_halo = 0;
+    for (int lg = 0; lg <= 5; ++lg) {
+        const int64_t tbw = int64_t{1} << lg, tbh = kWT / tbw;
+        const int64_t rows = (tiles_h + tbh - 1) / tbh, cols = (tiles_w + tbw - 1) / tbw;
+        const int64_t blocks = rows * cols;
+        const int64_t halo = (2 * tbh + 2) * (2 * tbw + 2);
+        if (best_blocks < 0 || blocks < best_blocks || (blocks == best_blocks && halo < best_halo)) {
+            best_blocks = blocks;
+            best_halo = halo;
+            best = {static_cast<int32_t>(tiles_h), static_cast<int32_t>(tiles_w), lg, static_cast<int32_t>(rows),
+                    static_cast<int32_t>(cols)};
+        }
+    }
+    return best;
 }
 
 
@@ -538,9 +605,11 @@ void launch_conv_wino(const ConvArgs& a, int bn, hipStream_t s) {
     if (a.x_sw % 4 != 0 || a.x_sh % 4 != 0 || a.x_sn % 4 != 0 || reinterpret_cast<uintptr_t>(a.x) % 16 != 0)
         fail("input rows must be 16-byte aligned");
     const int64_t tiles_h = (a.Ho + 1) / 2, tiles_w = (a.Wo + 1) / 2;
-    const int64_t T = a.N * tiles_h * tiles_w;
-    if (T >= (int64_t{1} << 31)) fail("too many tiles");
-    const dim3 grid(static_cast<unsigned>((T + kWT - 1) / kWT), static_cast<unsigned>((a.Cout + bn - 1) / bn));
+    if (tiles_h >= (int64_t{1} << 24) || tiles_w >= (int64_t{1} << 24)) fail("too many tiles");
+    const WinoGeom geo = wino_geometry(tiles_h, tiles_w);
+    const int64_t blocks = static_cast<int64_t>(a.N) * geo.block_rows * geo.block_cols;
+    if (blocks >= (int64_t{1} << 31)) fail("too many tiles");
+    const dim3 grid(static_cast<unsigned>(blocks), static_cast<unsigned>((a.Cout + bn - 1) / bn));
     if (grid.y > 65535) fail("grid");
     if (a.x_sn < 0 || a.x_sh < 0 || a.x_sw < 0 || a.y_sn < 0 || a.y_sh < 0 || a.y_sw < 0 ||
         (a.res && (a.r_sn < 0 || a.r_sh < 0 || a.r_sw < 0)))
@@ -557,9 +626,9 @@ void launch_conv_wino(const ConvArgs& a, int bn, hipStream_t s) {
     b.vec = a.Cout % 4 == 0 && rows16(a.y, a.y_sn, a.y_sh, a.y_sw) &&
             (!a.res || rows16(a.res, a.r_sn, a.r_sh, a.r_sw));
     if (bn == 64)
-        launch_bn<64>(a, grid, static_cast<int>(tiles_h), static_cast<int>(tiles_w), b, s);
+        launch_bn<64>(a, grid, geo, b, s);
     else
-        launch_bn<32>(a, grid, static_cast<int>(tiles_h), static_cast<int>(tiles_w), b, s);
+        launch_bn<32>(a, grid, geo, b, s);
 }
 
 void launch_pack_wino_weights(float* dst, const float* w, int Cout, int Cin, hipStream_t s) {

@@ -46,8 +46,11 @@ __device__ __forceinline__ bool silu_winograd_near_jump(float x, float window) {
 // float64, w the K-major packed weights (k = (kh*KW + kw)*Cin + ci, 32 x 32
 // blocks [co/32][k/32][co%32][k%32], one block set per group).  The 64 lanes
 // of the wave split the channels (lane l takes ci = l, l + 64, ...; its
-// loads are contiguous across lanes; a 3x3 conv's nine taps load together)
-// and every lane returns the total.
+// loads are contiguous across lanes) and every lane returns the total.
+// Every load is unconditional -- taps outside the image and lanes past Cin
+// read a clamped in-range address and zero the product with a select -- so
+// a 3x3 conv's eighteen loads of one channel chunk are in flight together
+// instead of one branch and one wait each.
 // All 64 lanes must be active; (n, oh, ow, co, g) must name an output
 // element of the conv.
 __device__ __forceinline__ double conv_point_f64(const ConvArgs& a, int n, int oh, int ow, int co, int g) {
@@ -57,41 +60,45 @@ __device__ __forceinline__ double conv_point_f64(const ConvArgs& a, int n, int o
     const float* wb = a.w_kmaj + static_cast<int64_t>(g) * a.w_group +
                       static_cast<int64_t>(co >> 5) * a.ktiles * (kConvBN * kConvBK) + (co & 31) * kConvBK;
     auto w_at = [&](int k) { return wb[static_cast<int64_t>(k >> 5) * (kConvBN * kConvBK) + (k & 31)]; };
+    const float bias = a.bias[static_cast<int64_t>(g) * a.Cout + co];
     double s = 0.0;
     for (int c0 = 0; c0 < a.Cin; c0 += 64) {
-        const int ci = c0 + lane;
-        const bool cok = ci < a.Cin;
+        const bool cok = c0 + lane < a.Cin;
+        const int ci = cok ? c0 + lane : a.Cin - 1;
         if (a.KH == 3 && a.KW == 3) {
-            // the nine taps' loads issued together, then the products
             float xv[9], wv[9];
+            bool ok[9];
 #pragma unroll
             for (int t = 0; t < 9; ++t) {
                 const int ih = ih0 + (t / 3) * a.dh, iw = iw0 + (t % 3) * a.dw;
-                const bool ok = cok & (static_cast<unsigned>(ih) < static_cast<unsigned>(a.H)) &
-                                (static_cast<unsigned>(iw) < static_cast<unsigned>(a.W));
-                xv[t] = ok ? xb[static_cast<int64_t>(ih) * a.x_sh + static_cast<int64_t>(iw) * a.x_sw + ci] : 0.0f;
-                wv[t] = ok ? w_at(t * a.Cin + ci) : 0.0f;
+                ok[t] = cok & (static_cast<unsigned>(ih) < static_cast<unsigned>(a.H)) &
+                        (static_cast<unsigned>(iw) < static_cast<unsigned>(a.W));
+                const int ihc = min(max(ih, 0), a.H - 1), iwc = min(max(iw, 0), a.W - 1);
+                xv[t] = xb[static_cast<int64_t>(ihc) * a.x_sh + static_cast<int64_t>(iwc) * a.x_sw + ci];
+                wv[t] = w_at(t * a.Cin + ci);
             }
 #pragma unroll
-            for (int t = 0; t < 9; ++t) s = __builtin_fma(static_cast<double>(xv[t]), static_cast<double>(wv[t]), s);
+            for (int t = 0; t < 9; ++t)
+                s = __builtin_fma(static_cast<double>(ok[t] ? xv[t] : 0.0f), static_cast<double>(wv[t]), s);
         } else {
             for (int kh = 0; kh < a.KH; ++kh) {
                 const int ih = ih0 + kh * a.dh;
+                const int ihc = min(max(ih, 0), a.H - 1);
                 for (int kw = 0; kw < a.KW; ++kw) {
                     const int iw = iw0 + kw * a.dw;
-                    if (cok && static_cast<unsigned>(ih) < static_cast<unsigned>(a.H) &&
-                        static_cast<unsigned>(iw) < static_cast<unsigned>(a.W))
-                        s = __builtin_fma(
-                            static_cast<double>(xb[static_cast<int64_t>(ih) * a.x_sh +
-                                                   static_cast<int64_t>(iw) * a.x_sw + ci]),
-                            static_cast<double>(w_at((kh * a.KW + kw) * a.Cin + ci)), s);
+                    const bool ok = cok & (static_cast<unsigned>(ih) < static_cast<unsigned>(a.H)) &
+                                    (static_cast<unsigned>(iw) < static_cast<unsigned>(a.W));
+                    const int iwc = min(max(iw, 0), a.W - 1);
+                    const float xv = xb[static_cast<int64_t>(ihc) * a.x_sh + static_cast<int64_t>(iwc) * a.x_sw + ci];
+                    const float wv = w_at((kh * a.KW + kw) * a.Cin + ci);
+                    s = __builtin_fma(static_cast<double>(ok ? xv : 0.0f), static_cast<double>(wv), s);
                 }
             }
         }
     }
 #pragma unroll
     for (int off = 32; off >= 1; off >>= 1) s += __shfl_xor(s, off, 64);
-    return s + static_cast<double>(a.bias[static_cast<int64_t>(g) * a.Cout + co]);
+    return s + static_cast<double>(bias);
 }
 
 // Second pass of a compat-SiLU epilogue, after its stores, which leave the
