@@ -557,11 +557,12 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the reference CPU baseline")
     ap.add_argument("--no-m16", action="store_true", help="skip the YOLOv8m batch-16 line")
     ap.add_argument("--no-pipeline", action="store_true", help="skip the pixels-to-detections pipeline line")
-    ap.add_argument("--only", choices=["all", "roofline", "program", "layers"], default="all",
+    ap.add_argument("--only", choices=["all", "roofline", "program", "layers", "session_run"], default="all",
                     help="program: plan YOLOv8n at --batch, then only warm-up and timed graph replays "
                          "(a kernel trace's last steps x launches dispatches are the timed forwards); "
-                         "layers: YOLOv8n's 3x3 conv launches at --batch, one by one")
-    ap.add_argument("--batch", type=int, default=1, help="with --only program / layers: the batch size")
+                         "layers: YOLOv8n's 3x3 conv launches at --batch, one by one; "
+                         "session_run: engine_session_run of YOLOv8n at --batch alone")
+    ap.add_argument("--batch", type=int, default=1, help="with --only program / layers / session_run: the batch size")
     ap.add_argument("--calib-copy", action="store_true",
                     help="with --only roofline / program: also run the PMC calibration copy")
     ap.add_argument("--ingest-pmc", nargs=3, metavar=("FETCH_CSV", "WRITE_CSV", "TILE"))
@@ -605,6 +606,20 @@ def main():
                                       "launches": launches, "steps": args.steps, "warmup": args.warmup,
                                       "ms_per_step": round(ms, 5),
                                       "images_per_s": round(args.batch * 1000.0 / ms, 2)}}), flush=True)
+        return
+    if args.only == "session_run":
+        with tempfile.TemporaryDirectory() as tmp:
+            path = os.path.join(tmp, "yolov8n.engine")
+            ys.save(ys.build_yolov8("n", seed=0), path)
+            x, _ = ys.yolo_inputs(args.batch)
+            eng = native.Engine(path)
+            try:
+                eng.run(x)
+                sr = session_run_stats(eng, args.batch, warmup=args.warmup, runs=args.steps)
+            finally:
+                eng.close()
+        log(f"yolov8n b{args.batch} engine_session_run: median {sr['median_ms']} ms, {sr['images_per_s']} images/s")
+        print(json.dumps({"session_run": {f"b{args.batch}": sr}}), flush=True)
         return
     if args.only == "layers":
         with tempfile.TemporaryDirectory() as tmp:

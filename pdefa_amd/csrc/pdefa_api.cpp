@@ -443,6 +443,9 @@ PDEFA_EXPORT EngineStatus pdefa_amd_plan_model(const EngineModel* m, const int64
                                                std::vector<int64_t>(shape, shape + ndim));
         pdefa::PlanOptions opt;
         if (const char* r = std::getenv("PDEFA_REUSE_MEMORY")) opt.reuse_memory = r[0] != '0';
+        // as a session plans it: the Detect decode split per anchor range
+        const char* so = std::getenv("PDEFA_SPLIT_OUTPUTS");
+        opt.split_outputs = !(so && so[0] == '0');
         if (const char* g = std::getenv("PDEFA_PLAN_GROUP_ALL"); g && g[0] == '1') {
             // Host-only stand-ins for the device measurements: launch shapes
             // from the cost model, and every group the grouping pass offers

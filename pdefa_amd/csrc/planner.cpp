@@ -1,6 +1,7 @@
 #include "planner.hpp"
 
 #include <algorithm>
+#include <climits>
 #include <cmath>
 #include <cstring>
 #include <map>
@@ -344,7 +345,7 @@ bool views_may_overlap(const VRef& a, const VRef& b) {
     int64_t alo, ahi, blo, bhi;
     if (!range(a, 0, alo, ahi) || !range(b, 0, blo, bhi)) return false;  // an empty view touches nothing
     if (ahi < blo || bhi < alo) return false;
-    if (a.rank == b.rank && a.rank > 1 && a.str[0] == b.str[0] && a.str[0] > 0 && range(a, 1, alo, ahi) &&
+    if (a.rank > 1 && b.rank > 1 && a.str[0] == b.str[0] && a.str[0] > 0 && range(a, 1, alo, ahi) &&
         range(b, 1, blo, bhi) && (ahi < blo || bhi < alo) && std::max(ahi, bhi) - std::min(alo, blo) < a.str[0])
         return false;
     if (a.rank != b.rank) return true;
@@ -383,6 +384,7 @@ class Planner {
         assign_storage();
         emit();
         fuse_steps();
+        split_decode();
         group_convs();
         allocate();
         check_bounds();
@@ -1386,6 +1388,74 @@ class Planner {
         st.swap(out);
     }
 
+    // A fused Detect decode over anchors [0, A) whose input rows come from
+    // different producers per anchor range (one conv per scale and branch,
+    // writing its HxW pixels as consecutive anchors) becomes one decode step
+    // per range, in anchor order.  Each part reads and writes only its
+    // anchors, so it depends only on its own range's producers.
+    void split_decode() {
+        if (!opt_.split_outputs) return;
+        auto& st = plan_.steps;
+        std::vector<Step> out;
+        for (size_t i = 0; i < st.size(); ++i) {
+            const Step& d = st[i];
+            out.push_back(d);
+            if (d.kind != StepKind::DetectDecode || d.a.rank != 4 || d.a.buf < 0) continue;
+            const int64_t A = d.a.dims[3], sa = d.a.str[3];
+            if (sa <= 0 || A <= 1) continue;
+            std::vector<int64_t> cuts = {0, A};
+            bool ok = true;
+            for (size_t j = 0; j < i && ok; ++j) {
+                const VRef& v = st[j].out;
+                if (v.buf != d.a.buf) continue;
+                // [N, C, H, W] over anchors (rel / sa) + h * W + w, channels inside the row
+                const int64_t rel = v.off - d.a.off;
+                ok = st[j].kind == StepKind::ConvMfma && v.rank == 4 && v.str[3] == sa && v.str[2] == v.dims[3] * sa &&
+                     v.str[1] == 1 && rel >= 0 && rel % sa + v.dims[1] <= sa;
+                if (!ok) break;
+                const int64_t a0 = rel / sa, a1 = a0 + v.dims[2] * v.dims[3];
+                ok = a1 <= A;
+                cuts.push_back(a0);
+                cuts.push_back(a1);
+            }
+            std::sort(cuts.begin(), cuts.end());
+            cuts.erase(std::unique(cuts.begin(), cuts.end()), cuts.end());
+            if (!ok || cuts.size() < 3) continue;
+            // every producer's range must fall inside one part
+            for (size_t j = 0; j < i && ok; ++j) {
+                const VRef& v = st[j].out;
+                if (v.buf != d.a.buf) continue;
+                const int64_t a0 = (v.off - d.a.off) / sa, a1 = a0 + v.dims[2] * v.dims[3];
+                const auto lo = std::upper_bound(cuts.begin(), cuts.end(), a0);
+                ok = lo != cuts.end() && *lo >= a1;
+            }
+            if (!ok) continue;
+            // the anchor-indexed views: the last dim of every [.., A] view
+            auto cut = [&](VRef v, int64_t a0, int64_t n) {
+                if (v.buf == -1 || v.rank < 1 || v.dims[v.rank - 1] != A) return v;
+                v.off += a0 * v.str[v.rank - 1];
+                v.dims[v.rank - 1] = n;
+                return v;
+            };
+            out.pop_back();
+            for (size_t c = 0; c + 1 < cuts.size(); ++c) {
+                const int64_t a0 = cuts[c], n = cuts[c + 1] - cuts[c];
+                Step p = d;
+                p.a = cut(d.a, a0, n);
+                p.b = cut(d.b, a0, n);
+                p.c = cut(d.c, a0, n);
+                p.res = cut(d.res, a0, n);
+                p.out = cut(d.out, a0, n);
+                if (d.cls_in.buf != -1) {
+                    p.cls_in = cut(d.cls_in, a0, n);
+                    p.cls_out = cut(d.cls_out, a0, n);
+                }
+                out.push_back(p);
+            }
+        }
+        st.swap(out);
+    }
+
     // ---- 6. liveness + arena ----------------------------------------------
     bool groupable(const Step& s) const { return s.kind == StepKind::ConvMfma && s.vec && s.groups == 1; }
 
@@ -1434,6 +1504,29 @@ class Planner {
             sink[i] = any && only_decode;
         }
 
+        // With a split Detect decode, each step takes the first decode part
+        // it feeds as its priority and the list scheduling below runs the
+        // ready steps of the lowest priority first: each anchor range's
+        // producers and decode part before the next range's work.
+        std::vector<int> pri(n, 0);
+        if (opt_.split_outputs) {
+            int parts = 0;
+            for (int i = 0; i < n; ++i) parts += st[i].kind == StepKind::DetectDecode;
+            if (parts > 1) {
+                std::vector<std::vector<int>> users(n);
+                for (int j = 0; j < n; ++j)
+                    for (int i : deps[j]) users[i].push_back(j);
+                int part = parts;
+                std::vector<int> part_of(n, -1);
+                for (int i = n - 1; i >= 0; --i)
+                    if (st[i].kind == StepKind::DetectDecode) part_of[i] = --part;
+                for (int i = n - 1; i >= 0; --i) {
+                    pri[i] = part_of[i] >= 0 ? part_of[i] : parts;
+                    for (int j : users[i]) pri[i] = std::min(pri[i], pri[j]);
+                }
+            }
+        }
+
         std::vector<char> done(n, 0);
         std::vector<Step> out;
         int32_t next_group = 0;
@@ -1449,6 +1542,9 @@ class Planner {
                     }
                 if (ok) ready.push_back(j);
             }
+            int pmin = INT32_MAX;
+            for (int j : ready) pmin = std::min(pmin, pri[j]);
+            ready.erase(std::remove_if(ready.begin(), ready.end(), [&](int j) { return pri[j] != pmin; }), ready.end());
             // waiting sinks go behind every other ready step
             std::stable_partition(ready.begin(), ready.end(), [&](int j) { return !sink[j]; });
             if (!sink[ready.front()])
@@ -1551,6 +1647,42 @@ class Planner {
         for (const VRef& v : plan_.outputs) check(v, -1, "graph output");
     }
 
+    // Length of the leading run of steps that process each image on its own
+    // (conv and elementwise steps whose every view has the batch N as its
+    // outer dimension, or is broadcast over it) on outputs of at least
+    // early_hw pixels, ending at a grouped launch's end.
+    int early_prefix() const {
+        if (opt_.early_hw <= 0 || plan_.input_dims.empty() || plan_.input_dims[0].empty()) return 0;
+        const int64_t N = plan_.input_dims[0][0];
+        if (N < 2) return 0;
+        auto batch_view = [&](const VRef& v, bool broadcast_ok) {
+            if (v.buf == -1 || v.buf == kBufWeight) return true;
+            if (v.rank < 1) return false;
+            if (v.dims[0] == N) return v.str[0] > 0 || N == 1;
+            return broadcast_ok && v.dims[0] == 1;
+        };
+        const auto& st = plan_.steps;
+        int e = 0;
+        for (size_t i = 0; i < st.size(); ++i) {
+            const Step& s = st[i];
+            bool ok = false;
+            if (s.kind == StepKind::ConvMfma || s.kind == StepKind::ConvDirect) {
+                ok = s.out.rank == 4 && s.out.dims[2] * s.out.dims[3] >= opt_.early_hw && batch_view(s.out, false) &&
+                     batch_view(s.a, false) && (!s.has_res || batch_view(s.res, false)) &&
+                     (s.kind != StepKind::ConvMfma || s.up.buf == -1 || batch_view(s.up, false));
+            } else if (s.kind == StepKind::Elt) {
+                int64_t hw = 1;
+                for (int d = 2; d < s.out.rank; ++d) hw *= s.out.dims[d];
+                ok = s.out.rank >= 3 && hw >= opt_.early_hw && batch_view(s.out, false) && batch_view(s.a, true) &&
+                     batch_view(s.b, true);
+            }
+            if (!ok) break;
+            const bool group_continues = s.group >= 0 && i + 1 < st.size() && st[i + 1].group == s.group;
+            if (!group_continues) e = static_cast<int>(i) + 1;
+        }
+        return e;
+    }
+
     void allocate() {
         const int n = static_cast<int>(plan_.steps.size());
         if (!opt_.reuse_memory) {
@@ -1596,6 +1728,17 @@ class Planner {
         for (int b : plan_.input_bufs) {
             plan_.bufs[b].first = -1;
             plan_.bufs[b].last = std::max(plan_.bufs[b].last, -1);
+        }
+        // the early steps run once per batch chunk, chunk after chunk: every
+        // buffer they touch stays live over the whole early segment
+        plan_.early_steps = early_prefix();
+        if (plan_.early_steps > 0) {
+            const int e = plan_.early_steps;
+            for (Buffer& b : plan_.bufs)
+                if (b.first <= b.last && b.first < e) {
+                    b.first = std::min(b.first, 0);
+                    b.last = std::max(b.last, e - 1);
+                }
         }
         for (const VRef& o : plan_.outputs) {
             plan_.bufs[o.buf].first = std::min(plan_.bufs[o.buf].first, n);
@@ -1780,7 +1923,7 @@ std::string describe_plan(const Model& m, const Plan& p) {
     int int32_outputs = 0;
     for (bool b : p.output_int32) int32_outputs += b;
     os << "steps=" << p.steps.size() << " bufs=" << p.bufs.size() << " arena_bytes=" << p.arena_elems * 4
-       << " copies=" << p.n_copies << " int32_outputs=" << int32_outputs << "\n";
+       << " copies=" << p.n_copies << " int32_outputs=" << int32_outputs << " early_steps=" << p.early_steps << "\n";
     for (size_t i = 0; i < p.steps.size(); ++i) {
         const Step& s = p.steps[i];
         os << i << " " << step_kind_name(s.kind);

@@ -96,6 +96,11 @@ struct Plan {
     std::vector<Buffer> bufs;
     int64_t arena_elems = 0;
     int32_t n_copies = 0;                     // materialising copies the planner could not avoid
+    // Leading steps that work image by image (convs and elementwise steps
+    // whose views all have the batch as their outer dimension) on maps of at
+    // least PlanOptions::early_hw pixels: they may run on chunks of the batch
+    // as the input arrives.  Their buffers never share memory with each other.
+    int32_t early_steps = 0;
 };
 
 // Shape of one implicit-GEMM conv (channels-last input and output).
@@ -127,6 +132,15 @@ struct PlanOptions {
     int force_splits = 0;  // > 0 with force_tile: split-K across workgroups into this many splits
     bool reuse_memory = true;  // share arena memory between tensors with disjoint lifetimes
     bool winograd_form_silu = true;  // match the reference's Winograd-layer SiLU
+    // Split a fused Detect decode into one step per anchor range written by
+    // different producers (the scales of a YOLO head) and, where the program
+    // is reordered (tune_group), run each range's producers and its decode
+    // before the next range's: the first ranges' outputs are then final while
+    // the rest of the program still runs, so their download can overlap it.
+    bool split_outputs = false;
+    // > 0: Plan::early_steps covers the leading per-image steps whose outputs
+    // have at least this many pixels (H * W)
+    int64_t early_hw = 0;
 };
 
 // Throws std::runtime_error naming the node for an unsupported op or pattern.

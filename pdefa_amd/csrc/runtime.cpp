@@ -275,6 +275,14 @@ Session::Session(Model& m) : model_(&m) {
     concurrent_ = use_graph_ && env_flag("PDEFA_CONCURRENT", false);
     keep_tensors_ = env_flag("PDEFA_KEEP_TENSORS", false);
     opts_.reuse_memory = !concurrent_ && !keep_tensors_;
+    // PDEFA_SPLIT_OUTPUTS=0: the Detect decode stays one step and every
+    // output is downloaded after the whole program
+    opts_.split_outputs = use_graph_ && !concurrent_ && env_flag("PDEFA_SPLIT_OUTPUTS", true);
+    // PDEFA_INPUT_CHUNKS=c (default 2; 0 or 1: off): batches of two or more
+    // images upload in c slices, and the early steps run on each slice as
+    // it lands; PDEFA_EARLY_HW: the smallest output map (H * W) of an early step
+    if (const char* c = std::getenv("PDEFA_INPUT_CHUNKS")) input_chunks_ = std::atoi(c);
+    if (const char* h = std::getenv("PDEFA_EARLY_HW")) early_hw_ = std::atoll(h);
     opts_.split_k = env_flag("PDEFA_SPLITK", true);
     if (const char* t = std::getenv("PDEFA_CONV_TILE")) {
         for (int i = 0; i < k::kNumConvShapes; ++i)
@@ -303,6 +311,8 @@ Session::~Session() {
     } catch (...) {
     }
     for (hipStream_t s : side_streams_) (void)hipStreamDestroy(s);
+    if (copy_out_) (void)hipStreamDestroy(copy_out_);
+    if (copy_in_) (void)hipStreamDestroy(copy_in_);
     if (stream_) (void)hipStreamDestroy(stream_);
     for (StagedInput& st : staged_) {
         if (st.dev_px) (void)hipFree(st.dev_px);
@@ -467,16 +477,31 @@ const HostTensor* Session::output(int32_t idx) const {
     return &prep_->outputs[idx];
 }
 
+Session::Prepared::~Prepared() {
+    for (InChunk& c : in_chunks) {
+        if (c.exec) (void)hipGraphExecDestroy(c.exec);
+        if (c.graph) (void)hipGraphDestroy(c.graph);
+        if (c.ready) (void)hipEventDestroy(c.ready);
+    }
+    for (Segment& g : segments) {
+        if (g.exec) (void)hipGraphExecDestroy(g.exec);
+        if (g.graph) (void)hipGraphDestroy(g.graph);
+        if (g.done) (void)hipEventDestroy(g.done);
+    }
+    if (exec) (void)hipGraphExecDestroy(exec);
+    if (graph) (void)hipGraphDestroy(graph);
+    for (hipEvent_t e : events)
+        if (e) (void)hipEventDestroy(e);
+    if (arena) (void)hipFree(arena);
+    for (float* h : host_out)
+        if (h) (void)hipHostFree(h);
+}
+
 void Session::release_prepared() {
     if (!prep_) return;
     if (stream_) (void)hipStreamSynchronize(stream_);
-    if (prep_->exec) (void)hipGraphExecDestroy(prep_->exec);
-    if (prep_->graph) (void)hipGraphDestroy(prep_->graph);
-    for (hipEvent_t e : prep_->events)
-        if (e) (void)hipEventDestroy(e);
-    if (prep_->arena) (void)hipFree(prep_->arena);
-    for (float* h : prep_->host_out)
-        if (h) (void)hipHostFree(h);
+    if (copy_out_) (void)hipStreamSynchronize(copy_out_);
+    if (copy_in_) (void)hipStreamSynchronize(copy_in_);
     prep_.reset();
 }
 
@@ -517,6 +542,18 @@ void Session::prepare(const std::vector<std::vector<int64_t>>& dims) {
     release_prepared();
     auto p = std::make_unique<Prepared>();
     PlanOptions opts = opts_;
+    // A single image gains nothing from either: its decode parts would only
+    // split the head's grouped launches, and there is no second slice to
+    // upload behind the first.
+    const int64_t batch = dims.empty() || dims[0].empty() ? 0 : dims[0][0];
+    bool same_batch = true;
+    for (const auto& d : dims) same_batch = same_batch && !d.empty() && d[0] == batch;
+    opts.split_outputs = opts.split_outputs && batch >= 2;
+    const int chunks = input_chunks_;
+    opts.early_hw = (use_graph_ && !concurrent_ && !keep_tensors_ && same_batch && chunks > 1 && batch >= chunks &&
+                     batch % chunks == 0)
+                        ? early_hw_
+                        : 0;
     if (autotune_) {
         opts.tune_conv = [this](const ConvQuery& q) { return tune_conv(q, stream_); };
         // grouped launches change the program order; the concurrent capture
@@ -568,6 +605,7 @@ void Session::prepare(const std::vector<std::vector<int64_t>>& dims) {
         const int si = static_cast<int>(i);
         Launch l;
         l.kind = s.kind;
+        l.step = si;
         l.label = step_label(*model_, s, si);
         switch (s.kind) {
             case StepKind::ConvMfma: {
@@ -788,6 +826,8 @@ void Session::prepare(const std::vector<std::vector<int64_t>>& dims) {
         t.owns = false;
         prep_->outputs.push_back(std::move(t));
     }
+    plan_input_chunks();
+    plan_segments();
 }
 
 void Session::launch_one(const Launch& l, hipStream_t s) {
@@ -849,6 +889,279 @@ void Session::capture_concurrent() {
 
 void Session::launch_all(hipStream_t s) {
     for (const Launch& l : prep_->launches) launch_one(l, s);
+}
+
+void Session::capture_launches(size_t first, size_t last, hipGraph_t* graph, hipGraphExec_t* exec) {
+    PDEFA_HIP(hipStreamBeginCapture(stream_, hipStreamCaptureModeThreadLocal));
+    try {
+        for (size_t i = first; i <= last && i < prep_->launches.size(); ++i) launch_one(prep_->launches[i], stream_);
+    } catch (...) {
+        hipGraph_t g = nullptr;
+        (void)hipStreamEndCapture(stream_, &g);
+        if (g) (void)hipGraphDestroy(g);
+        throw;
+    }
+    PDEFA_HIP(hipStreamEndCapture(stream_, graph));
+    PDEFA_HIP(hipGraphInstantiate(exec, *graph, nullptr, nullptr, 0));
+}
+
+void Session::capture_list(const std::vector<Launch>& ls, hipGraph_t* graph, hipGraphExec_t* exec) {
+    PDEFA_HIP(hipStreamBeginCapture(stream_, hipStreamCaptureModeThreadLocal));
+    try {
+        for (const Launch& l : ls) launch_one(l, stream_);
+    } catch (...) {
+        hipGraph_t g = nullptr;
+        (void)hipStreamEndCapture(stream_, &g);
+        if (g) (void)hipGraphDestroy(g);
+        throw;
+    }
+    PDEFA_HIP(hipStreamEndCapture(stream_, graph));
+    PDEFA_HIP(hipGraphInstantiate(exec, *graph, nullptr, nullptr, 0));
+}
+
+namespace {
+
+// The view restricted to images [first, first + n) of its outer (batch)
+// dimension; a view broadcast over the batch (outer dimension 1) stays.
+k::View batch_slice(k::View v, int64_t N, int64_t first, int64_t n) {
+    if (v.ptr == nullptr || v.rank < 1 || v.dims[0] != N) return v;
+    v.ptr += first * v.str[0];
+    v.dims[0] = n;
+    return v;
+}
+
+void conv_slice(k::ConvArgs& c, int64_t first, int64_t n) {
+    c.x += first * c.x_sn;
+    c.y += first * c.y_sn;
+    if (c.res) c.res += first * c.r_sn;
+    if (c.up) c.up += first * c.u_sn;
+    c.N = static_cast<int32_t>(n);
+}
+
+}  // namespace
+
+// Input chunks: when the plan has early steps (a batch of two or more images
+// that splits evenly into input_chunks_ slices), each slice gets its own copy
+// of the early launches, restricted to its images: convs and elementwise
+// steps index images through the batch stride only, so each image's results
+// are those of the whole-batch launch bit for bit (same launch shapes, same
+// summation order); a split-K workspace is reused slice after slice in stream
+// order.
+void Session::plan_input_chunks() {
+    Prepared& P = *prep_;
+    P.in_chunks.clear();
+    P.early_launches = 0;
+    const Plan& plan = P.plan;
+    if (plan.early_steps <= 0 || input_chunks_ <= 1) return;
+    const int64_t N = plan.input_dims.at(0).at(0);
+    const int64_t c = input_chunks_;
+    if (N % c != 0) return;
+    size_t e = 0;
+    while (e < P.launches.size() && P.launches[e].step >= 0 && P.launches[e].step < plan.early_steps) ++e;
+    if (e == 0 || e == P.launches.size()) return;
+    for (int32_t b : plan.input_bufs) {  // contiguous, batch outermost
+        const Buffer& buf = plan.bufs.at(b);
+        if (buf.elems % N != 0) return;
+    }
+    const int64_t n = N / c;
+    for (int64_t ci = 0; ci < c; ++ci) {
+        Prepared::InChunk ch;
+        ch.first = ci * n;
+        ch.n = n;
+        for (size_t li = 0; li < e; ++li) {
+            Launch l = P.launches[li];
+            switch (l.kind) {
+                case StepKind::ConvMfma:
+                    if (l.group.empty()) {
+                        conv_slice(l.conv, ch.first, n);
+                    } else {
+                        for (k::ConvArgs& g : l.group) conv_slice(g, ch.first, n);
+                        l.conv = l.group.front();
+                    }
+                    break;
+                case StepKind::ConvDirect:
+                    l.direct.x = batch_slice(l.direct.x, N, ch.first, n);
+                    l.direct.y = batch_slice(l.direct.y, N, ch.first, n);
+                    if (l.direct.res.ptr) l.direct.res = batch_slice(l.direct.res, N, ch.first, n);
+                    break;
+                case StepKind::Elt:
+                    l.out = batch_slice(l.out, N, ch.first, n);
+                    l.a = batch_slice(l.a, N, ch.first, n);
+                    l.b = batch_slice(l.b, N, ch.first, n);
+                    break;
+                default:
+                    return;  // the planner's early steps are convs and elementwise steps only
+            }
+            ch.launches.push_back(std::move(l));
+        }
+        P.in_chunks.push_back(std::move(ch));
+    }
+    P.early_launches = e;
+}
+
+// Cuts the program after each decode part but the last (the parts of a
+// Detect decode the planner split by anchor range) when the parts' outputs
+// tile whole graph outputs: a run then downloads each part's rows while the
+// later segments compute.  Each part writes [N, C, A_part] views (the box
+// rows and, right after them, the class rows) of a dense output; a region
+// is one pitched copy of N * C rows where the images' rows follow each other
+// evenly, else one per image.
+void Session::plan_segments() {
+    Prepared& P = *prep_;
+    P.segments.clear();
+    P.out_split.assign(P.outputs.size(), 0);
+    if (!use_graph_ || concurrent_) return;
+    const size_t first0 = P.early_launches;
+    // the program after the input chunks' early launches as one segment
+    auto late_only = [&] {
+        P.segments.clear();
+        std::fill(P.out_split.begin(), P.out_split.end(), 0);
+        if (first0 == 0) return;
+        Segment g;
+        g.first = first0;
+        g.last = P.launches.size() - 1;
+        P.segments.push_back(std::move(g));
+    };
+    if (!opts_.split_outputs) return late_only();
+    const Plan& plan = P.plan;
+    struct Part {
+        size_t launch;
+        std::vector<Region> regions;
+    };
+    std::vector<Part> parts;
+    std::vector<int64_t> covered(P.outputs.size(), 0);
+    for (size_t li = 0; li < P.launches.size(); ++li) {
+        const Launch& l = P.launches[li];
+        if (l.kind != StepKind::DetectDecode || l.step < 0) continue;
+        const Step& s = plan.steps.at(static_cast<size_t>(l.step));
+        size_t o = P.outputs.size();
+        for (size_t i = 0; i < plan.outputs.size(); ++i)
+            if (plan.outputs[i].buf == s.out.buf) o = i;
+        if (o == P.outputs.size()) continue;
+        const VRef& O = plan.outputs[o];
+        // the output view must be dense row-major for host offsets to follow
+        // buffer offsets
+        int64_t numel = 1;
+        bool dense = O.buf >= 0;
+        for (int d = O.rank - 1; d >= 0 && dense; --d) {
+            dense = O.str[d] == numel;
+            numel *= O.dims[d];
+        }
+        if (!dense) return late_only();
+        VRef v = s.out;
+        if (s.cls_in.buf != -1) {
+            const VRef& c = s.cls_out;
+            if (c.buf != v.buf || c.rank != 3 || v.rank != 3 || c.off != v.off + v.dims[1] * v.str[1] ||
+                c.str[0] != v.str[0] || c.str[1] != v.str[1] || c.str[2] != v.str[2] || c.dims[0] != v.dims[0] ||
+                c.dims[2] != v.dims[2])
+                return late_only();
+            v.dims[1] += c.dims[1];
+        }
+        if (v.rank != 3 || v.str[2] != 1 || v.dims[0] <= 0 || v.dims[1] <= 0 || v.dims[2] <= 0) return late_only();
+        const int64_t rel = v.off - O.off;
+        const int64_t span = (v.dims[0] - 1) * v.str[0] + (v.dims[1] - 1) * v.str[1] + v.dims[2];
+        if (rel < 0 || rel + span > numel) return late_only();
+        Part part{li, {}};
+        const bool even = v.dims[0] == 1 || v.str[0] == v.dims[1] * v.str[1];
+        for (int64_t n = 0; n < (even ? 1 : v.dims[0]); ++n) {
+            Region r;
+            r.out = o;
+            r.dev = plan.bufs.at(v.buf).offset + v.off + n * v.str[0];
+            r.host = rel + n * v.str[0];
+            r.width = v.dims[2];
+            r.rows = even ? v.dims[0] * v.dims[1] : v.dims[1];
+            r.pitch = v.str[1];
+            part.regions.push_back(r);
+        }
+        covered[o] += v.dims[0] * v.dims[1] * v.dims[2];
+        parts.push_back(std::move(part));
+    }
+    if (parts.size() < 2) return late_only();
+    for (const Part& p : parts) {
+        const size_t o = p.regions.front().out;
+        int64_t numel = 1;
+        for (auto d : plan.output_dims[o]) numel *= d;
+        if (covered[o] != numel) return late_only();  // the parts leave rows of the output to a full download
+        P.out_split[o] = 1;
+    }
+    const size_t cuts = parts.size() - 1;
+    size_t first = first0;
+    for (size_t k = 0; k <= cuts; ++k) {
+        Segment g;
+        g.first = first;
+        g.last = k < cuts ? parts[k].launch : P.launches.size() - 1;
+        g.regions = parts[k].regions;
+        first = g.last + 1;
+        P.segments.push_back(std::move(g));
+    }
+}
+
+// One run: the inputs (slice by slice on copy_in_ when the early launches
+// run per input chunk: chunk c's early graph waits for its slice only), then
+// the segments on the session stream; after each segment but the last its
+// regions go down on copy_out_ (waiting for that segment only); the last
+// segment's regions and the other outputs follow it on the session stream.
+// Ends with everything finished.
+void Session::run_segments() {
+    Prepared& P = *prep_;
+    const Plan& plan = P.plan;
+    if (!copy_out_) PDEFA_HIP(hipStreamCreateWithFlags(&copy_out_, hipStreamNonBlocking));
+    if (P.in_chunks.empty() || has_staged()) {
+        upload_inputs();
+        for (Prepared::InChunk& c : P.in_chunks) {
+            if (!c.exec) capture_list(c.launches, &c.graph, &c.exec);
+            PDEFA_HIP(hipGraphLaunch(c.exec, stream_));
+        }
+    } else {
+        if (!copy_in_) PDEFA_HIP(hipStreamCreateWithFlags(&copy_in_, hipStreamNonBlocking));
+        const int64_t N = plan.input_dims.at(0).at(0);
+        // the session stream's earlier work (the previous run) is finished:
+        // runs end synchronised
+        for (Prepared::InChunk& c : P.in_chunks) {
+            if (!c.exec) capture_list(c.launches, &c.graph, &c.exec);
+            if (!c.ready) PDEFA_HIP(hipEventCreateWithFlags(&c.ready, hipEventDisableTiming));
+            for (size_t i = 0; i < inputs_.size(); ++i) {
+                const HostTensor* t = inputs_[i];
+                const size_t per_image = t->nbytes / static_cast<size_t>(N);
+                float* dst = P.arena + plan.bufs.at(plan.input_bufs[i]).offset;
+                PDEFA_HIP(hipMemcpyAsync(reinterpret_cast<char*>(dst) + c.first * per_image,
+                                         static_cast<const char*>(t->data) + c.first * per_image,
+                                         static_cast<size_t>(c.n) * per_image, hipMemcpyHostToDevice, copy_in_));
+            }
+            PDEFA_HIP(hipEventRecord(c.ready, copy_in_));
+        }
+        for (Prepared::InChunk& c : P.in_chunks) {
+            PDEFA_HIP(hipStreamWaitEvent(stream_, c.ready, 0));
+            PDEFA_HIP(hipGraphLaunch(c.exec, stream_));
+        }
+    }
+    auto copy = [&](const Region& r, hipStream_t s) {
+        PDEFA_HIP(hipMemcpy2DAsync(P.host_out[r.out] + r.host, static_cast<size_t>(r.pitch) * sizeof(float),
+                                   P.arena + r.dev, static_cast<size_t>(r.pitch) * sizeof(float),
+                                   static_cast<size_t>(r.width) * sizeof(float), static_cast<size_t>(r.rows),
+                                   hipMemcpyDeviceToHost, s));
+    };
+    for (size_t k = 0; k < P.segments.size(); ++k) {
+        Segment& g = P.segments[k];
+        if (!g.exec) capture_launches(g.first, g.last, &g.graph, &g.exec);
+        PDEFA_HIP(hipGraphLaunch(g.exec, stream_));
+        if (k + 1 < P.segments.size()) {
+            if (!g.done) PDEFA_HIP(hipEventCreateWithFlags(&g.done, hipEventDisableTiming));
+            PDEFA_HIP(hipEventRecord(g.done, stream_));
+            PDEFA_HIP(hipStreamWaitEvent(copy_out_, g.done, 0));
+            for (const Region& r : g.regions) copy(r, copy_out_);
+        } else {
+            for (const Region& r : g.regions) copy(r, stream_);
+        }
+    }
+    for (size_t i = 0; i < plan.outputs.size(); ++i) {
+        if (P.out_split[i]) continue;
+        const float* src = P.arena + plan.bufs.at(plan.outputs[i].buf).offset + plan.outputs[i].off;
+        PDEFA_HIP(hipMemcpyAsync(P.host_out[i], src, P.outputs[i].nbytes, hipMemcpyDeviceToHost, stream_));
+    }
+    PDEFA_HIP(hipStreamSynchronize(stream_));
+    PDEFA_HIP(hipStreamSynchronize(copy_out_));
+    if (copy_in_) PDEFA_HIP(hipStreamSynchronize(copy_in_));
 }
 
 void Session::upload_inputs() {
@@ -922,8 +1235,9 @@ void Session::run() {
     if (!dev_) dev_ = device_model(*model_);
     if (!stream_) PDEFA_HIP(hipStreamCreateWithFlags(&stream_, hipStreamNonBlocking));
     if (!prep_ || prep_->plan.input_dims != dims) prepare(dims);
-    upload_inputs();
     const bool per_step = prof_fn_ != nullptr || std::getenv("ENGINE_PROFILE_CSV") != nullptr;
+    const bool segmented = use_graph_ && !per_step && !prep_->segments.empty();
+    if (!segmented) upload_inputs();  // run_segments uploads (by slices) itself
     if (per_step) {
         std::vector<double> ms;
         std::vector<std::string> labels;
@@ -936,30 +1250,35 @@ void Session::run() {
                 std::fclose(f);
             }
         }
+    } else if (segmented) {
+        run_segments();
     } else if (use_graph_) {
         if (!prep_->exec) {
-            PDEFA_HIP(hipStreamBeginCapture(stream_, hipStreamCaptureModeThreadLocal));
-            try {
-                if (concurrent_)
+            if (concurrent_) {
+                PDEFA_HIP(hipStreamBeginCapture(stream_, hipStreamCaptureModeThreadLocal));
+                try {
                     capture_concurrent();
-                else
-                    launch_all(stream_);
-            } catch (...) {
-                hipGraph_t g = nullptr;
-                (void)hipStreamEndCapture(stream_, &g);
-                if (g) (void)hipGraphDestroy(g);
-                throw;
+                } catch (...) {
+                    hipGraph_t g = nullptr;
+                    (void)hipStreamEndCapture(stream_, &g);
+                    if (g) (void)hipGraphDestroy(g);
+                    throw;
+                }
+                PDEFA_HIP(hipStreamEndCapture(stream_, &prep_->graph));
+                PDEFA_HIP(hipGraphInstantiate(&prep_->exec, prep_->graph, nullptr, nullptr, 0));
+            } else {
+                capture_launches(0, prep_->launches.size() - 1, &prep_->graph, &prep_->exec);
             }
-            PDEFA_HIP(hipStreamEndCapture(stream_, &prep_->graph));
-            PDEFA_HIP(hipGraphInstantiate(&prep_->exec, prep_->graph, nullptr, nullptr, 0));
         }
         PDEFA_HIP(hipGraphLaunch(prep_->exec, stream_));
     } else {
         launch_all(stream_);
         PDEFA_HIP(hipGetLastError());
     }
-    download_outputs();
-    PDEFA_HIP(hipStreamSynchronize(stream_));
+    if (per_step || !use_graph_ || prep_->segments.empty()) {
+        download_outputs();
+        PDEFA_HIP(hipStreamSynchronize(stream_));
+    }
     for (size_t i = 0; i < prep_->outputs.size(); ++i) {
         HostTensor& t = prep_->outputs[i];
         if (t.dtype != kI32) continue;
@@ -979,6 +1298,8 @@ double Session::replay(int32_t iters) {
     PDEFA_HIP(hipEventCreate(&a));
     PDEFA_HIP(hipEventCreate(&b));
     PDEFA_HIP(hipEventRecord(a, stream_));
+    if (use_graph_ && !concurrent_ && !prep_->exec)
+        capture_launches(0, prep_->launches.size() - 1, &prep_->graph, &prep_->exec);
     for (int32_t i = 0; i < iters; ++i) {
         if (prep_->exec)
             PDEFA_HIP(hipGraphLaunch(prep_->exec, stream_));

@@ -129,6 +129,24 @@ class Session {
         int64_t topk = 0;
         bool topk_indices = false;
         std::string label;
+        int step = -1;  // the plan step it issues (the first of a grouped launch)
+    };
+    // A rectangle of an output copied to the host: `rows` rows of `width`
+    // floats, `pitch` floats apart, at element offset dev (arena) / host
+    // (the output's pinned buffer).
+    struct Region {
+        size_t out = 0;
+        int64_t dev = 0, host = 0, width = 0, rows = 0, pitch = 0;
+    };
+    // A piece of the program cut after a decode part: its launches run as
+    // one graph, then the outputs that part finished go down on copy_out_
+    // while the next pieces run.
+    struct Segment {
+        size_t first = 0, last = 0;  // launches [first, last]
+        hipGraph_t graph = nullptr;
+        hipGraphExec_t exec = nullptr;
+        hipEvent_t done = nullptr;
+        std::vector<Region> regions;
     };
     struct Prepared {
         Plan plan;
@@ -140,11 +158,35 @@ class Session {
         std::vector<hipEvent_t> events;  // per step (recorded ones only) + per extra stream join
         std::vector<float*> host_out;  // pinned
         std::vector<HostTensor> outputs;
+        // Runs cut after the decode parts of a split Detect head (empty: the
+        // whole program is one graph): out_split[i] marks outputs whose
+        // download is the segments' regions.
+        std::vector<Segment> segments;
+        std::vector<char> out_split;
+        // Batch chunks of the early steps (Plan::early_steps): chunk c runs
+        // launches [0, early_launches) on images [first, first + n) once its
+        // slice of the input has landed, while later slices still upload.
+        struct InChunk {
+            int64_t first = 0, n = 0;
+            std::vector<Launch> launches;
+            hipGraph_t graph = nullptr;
+            hipGraphExec_t exec = nullptr;
+            hipEvent_t ready = nullptr;  // its input slice uploaded
+        };
+        std::vector<InChunk> in_chunks;
+        size_t early_launches = 0;
+        ~Prepared();
     };
 
     void prepare(const std::vector<std::vector<int64_t>>& dims);
     void release_prepared();
     void launch_all(hipStream_t s);
+    // records launches [first, last] as a graph on the session stream
+    void capture_launches(size_t first, size_t last, hipGraph_t* graph, hipGraphExec_t* exec);
+    void capture_list(const std::vector<Launch>& ls, hipGraph_t* graph, hipGraphExec_t* exec);
+    void plan_input_chunks();  // fills prep_->in_chunks (or leaves them empty)
+    void plan_segments();  // fills prep_->segments (or leaves them empty)
+    void run_segments();   // one run through the segments, downloads included
     void capture_concurrent();  // records the program as a multi-stream hipGraph
     void launch_one(const Launch& l, hipStream_t s);
     void upload_inputs();
@@ -169,6 +211,11 @@ class Session {
         size_t dev_cap = 0;
     };
     std::vector<StagedInput> staged_;  // per input; empty images = host tensor input
+    bool has_staged() const {
+        for (const StagedInput& st : staged_)
+            if (!st.images.empty()) return true;
+        return false;
+    }
     // decode workspace (device, grow-only) and its pinned result staging
     void* dec_ws_ = nullptr;
     size_t dec_ws_bytes_ = 0;
@@ -179,6 +226,10 @@ class Session {
     std::shared_ptr<DeviceModel> dev_;
     hipStream_t stream_ = nullptr;
     std::vector<hipStream_t> side_streams_;  // capture-only streams for concurrent branches
+    hipStream_t copy_out_ = nullptr;         // downloads that overlap the program's later segments
+    hipStream_t copy_in_ = nullptr;          // input slices uploaded while earlier chunks compute
+    int input_chunks_ = 2;                   // PDEFA_INPUT_CHUNKS (<= 1: the input goes up whole)
+    int64_t early_hw_ = 80 * 80;             // PDEFA_EARLY_HW: smallest map the early steps produce
     bool concurrent_ = true;
     std::vector<const HostTensor*> inputs_;
     std::unique_ptr<Prepared> prep_;

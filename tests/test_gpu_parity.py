@@ -59,6 +59,19 @@ def errors(got, want, rel_floor=FLT_MIN):
     return float(err.max(initial=0.0)), float(rel.max(initial=0.0)), bad
 
 
+def flip_affected(follow, plain):
+    """Elements that a listed jump flip moves by more than half the bound:
+    the oracle with the flips against the plain oracle.  A reference that
+    took the other side of the jump can differ there by up to the flip's
+    effect plus both sides' rounding, so such elements are not compared
+    with it (the device is still held to the oracle with its flips)."""
+    g = follow.astype(np.float64)
+    w = plain.astype(np.float64)
+    err = np.abs(g - w)
+    rel = np.where(w != 0.0, err / np.where(w != 0.0, np.abs(w), 1.0), 0.0)
+    return (err > 0.5 * ATOL) | (rel > 0.5 * RTOL)
+
+
 def norm_rel(got, want):
     w = want.astype(np.float64)
     return float(np.linalg.norm(got.astype(np.float64) - w) / max(np.linalg.norm(w), 1e-300))
@@ -1010,6 +1023,51 @@ def test_sessions_on_threads_batchinference_pattern(yolov8n):
     print("4 rounds x 4 concurrent sessions: every head equal to its image run alone", flush=True)
 
 
+@pytest.mark.parametrize("batch,chunks", [(8, 2), (8, 4), (6, 3)])
+def test_input_chunks_equal_whole_batch(yolov8n, monkeypatch, batch, chunks):
+    """A batch whose input uploads in slices, the early high-resolution steps
+    running on each slice as it lands, gives the head of the whole-batch
+    launches bit for bit (the slices' launches index images through the
+    batch stride only): on repeated runs, on new inputs and through the
+    device letterbox (set_images, whose slices run one after another)."""
+    from pdefa_amd import pdefa
+    print(f"[case] yolov8n b{batch} input in {chunks} slices", flush=True)
+    _, path = yolov8n
+    x, _ = ys.yolo_inputs(batch)
+    x2 = np.ascontiguousarray(x[::-1])
+    early = lambda e: int(e.plan().splitlines()[0].split("early_steps=")[1].split()[0])
+    monkeypatch.setenv("PDEFA_INPUT_CHUNKS", "1")
+    eng = native.Engine(path)
+    try:
+        whole = eng.run(x)[0].copy()
+        whole2 = eng.run(x2)[0].copy()
+        assert early(eng) == 0
+    finally:
+        eng.close()
+    monkeypatch.setenv("PDEFA_INPUT_CHUNKS", str(chunks))
+    eng = native.Engine(path)
+    try:
+        for rnd in range(2):
+            assert np.array_equal(eng.run(x)[0], whole), f"run {rnd}: sliced-input head differs"
+        assert early(eng) > 0
+        assert np.array_equal(eng.run(x2)[0], whole2), "new inputs: sliced-input head differs"
+    finally:
+        eng.close()
+    rng = np.random.default_rng(batch)
+    imgs = [rng.integers(0, 256, (480 + 16 * i, 640 - 8 * i, 3), dtype=np.uint8) for i in range(batch)]
+    ctx = pdefa.Context()
+    m = pdefa.Model(ctx, path)
+    heads = {}
+    for c in (1, chunks):
+        monkeypatch.setenv("PDEFA_INPUT_CHUNKS", str(c))
+        s = pdefa.Session(ctx, m)
+        s.set_images(0, imgs, 640, 640, 1 / 255, 114 / 255)
+        s.run()
+        heads[c] = s.output(0).to_numpy().copy()
+    assert np.array_equal(heads[chunks], heads[1]), "set_images: sliced-input head differs"
+    print(f"b{batch} in {chunks} slices: heads equal to the whole batch's", flush=True)
+
+
 GROUPED_CASES = [
     # cin, cout, k, stride, hw, groups, forced launch shape
     (64, 64, 3, 1, 80, 64, None),      # depthwise
@@ -1241,6 +1299,9 @@ def _check_golden_samples(arr, g, skip=None, rel_floor=FLT_MIN):
     if skip is not None and skip.any():
         keep = ~skip.reshape(-1)[idx]
         idx, want = idx[keep], want[keep]
+    bad = errors(flat[idx], want, rel_floor)[2]
+    for j in np.flatnonzero(bad)[:8]:
+        print(f"golden sample {int(idx[j])}: device {float(flat[idx[j]])!r}, fixture {float(want[j])!r}", flush=True)
     assert_close(flat[idx], want, "golden samples", rel_floor=rel_floor)
     if skip is None or not skip.any():
         means = arr.reshape(arr.shape[0], arr.shape[1], -1).astype(np.float64).mean(axis=(0, 2))
@@ -1285,7 +1346,7 @@ def test_yolov8n_batch_vs_reference_golden(yolov8n):
     for i in range(3):
         g = _golden(f"yolov8n_640_img{i}")
         plain = graph_ref.run_graph(model, [x[i:i + 1]])[0]
-        differ = errors(follow[i:i + 1], plain)[2]
+        differ = flip_affected(follow[i:i + 1], plain)
         _check_golden_samples(out[i:i + 1], g, skip=differ)
         _check_golden_detections(out[i:i + 1], metas[i], g, f"yolov8n image {i}",
                                  exempt=set(np.unique(np.nonzero(differ)[-1]).tolist()))
@@ -1318,7 +1379,7 @@ def test_yolov8m_b16_vs_reference(tmp_path):
     for i in range(2):
         g = _golden(f"yolov8m_640_img{i}")
         follow = explained.get(i)
-        differ = errors(follow, ref[i:i + 1])[2] if follow is not None else None
+        differ = flip_affected(follow, ref[i:i + 1]) if follow is not None else None
         ex = set(np.unique(np.nonzero(differ)[-1]).tolist()) if differ is not None else set()
         _check_golden_samples(out[i:i + 1], g, skip=differ)
         _check_golden_detections(out[i:i + 1], metas[i], g, f"yolov8m image {i}", exempt=ex)

@@ -64,10 +64,12 @@ def test_yolov8n_plan_is_zero_copy(y8n_path):
     pools = [l for l in lines if " maxpool" in l]
     assert len(pools) == 1 and " maxpool_chain " in pools[0]
     # DFL softmax + 1x1 conv + dist2bbox + stride scale + the class sigmoid
-    # run as one step: no standalone softmax or eltwise step is left
+    # run as one step per scale's anchor range (80x80, 40x40, 20x20 anchors
+    # of the [1, 84, 8400] head): no standalone softmax or eltwise step is left
     dec = [l for l in lines if " detect_decode " in l]
-    assert len(dec) == 1 and "/model.22/dfl/Softmax" in dec[0]
-    assert " cls=b" in dec[0] and " clsout=b0+33600[1,80,8400]" in dec[0]
+    assert len(dec) == 3 and all("/model.22/dfl/Softmax" in l for l in dec)
+    for l, (a0, n) in zip(dec, [(0, 6400), (6400, 1600), (8000, 400)]):
+        assert f" out=b0+{a0}[1,4,{n}]" in l and f" clsout=b0+{33600 + a0}[1,80,{n}]" in l
     assert not any(" softmax" in l for l in lines)
     assert not any("eltwise(" in l for l in lines)
     # Winograd-form SiLU exactly on 3x3/s1 layers with 16 < Cin <= 512
@@ -76,11 +78,37 @@ def test_yolov8n_plan_is_zero_copy(y8n_path):
             assert "/m." in l or "cv2." in l or "cv3." in l
 
 
+def test_decode_split_by_scale_and_scheduled_first(y8n_path, monkeypatch):
+    """The Detect decode splits into one step per scale's anchor range; with
+    the program reordered (host stand-ins for the measurements), each
+    range's producers and its decode part run before the next scale's work:
+    the 80x80 part right after its head convs, ahead of the stride-2 conv
+    that starts the 40x40 branch.  PDEFA_SPLIT_OUTPUTS=0 keeps one step."""
+    monkeypatch.setenv("PDEFA_PLAN_GROUP_ALL", "1")
+    _, lines = parse(native.plan_text(y8n_path, [2, 3, 640, 640]))
+    name = lambda l: l.split("'")[1]
+    order = [name(l) for l in lines]
+    dec = [i for i, l in enumerate(lines) if " detect_decode " in l]
+    assert len(dec) == 3
+    assert dec[0] < order.index("/model.16/conv/Conv")
+    assert dec[1] < order.index("/model.19/conv/Conv") < dec[2]
+    # each part follows its own scale's last head convs
+    for i, tag in zip(dec, ("cv2.0/cv2.0.2", "cv2.1/cv2.1.2", "cv2.2/cv2.2.2")):
+        assert order.index(f"/model.22/{tag}/Conv") < i
+    monkeypatch.setenv("PDEFA_SPLIT_OUTPUTS", "0")
+    _, lines = parse(native.plan_text(y8n_path, [2, 3, 640, 640]))
+    dec = [l for l in lines if " detect_decode " in l]
+    assert len(dec) == 1 and " clsout=b0+33600[2,80,8400]" in dec[0]
+
+
 def test_yolov8n_plan_batch8(y8n_path):
     info, lines = parse(native.plan_text(y8n_path, [8, 3, 640, 640]))
     assert info["copies"] == 0
-    assert lines[-1].split(" out=")[1].startswith("b0+0[8,4,8400]")
-    assert lines[-1].split(" clsout=")[1].startswith("b0+33600[8,80,8400]")
+    dec = [l for l in lines if " detect_decode " in l]
+    assert dec[-1] == lines[-1]
+    for l, (a0, n) in zip(dec, [(0, 6400), (6400, 1600), (8000, 400)]):
+        assert l.split(" out=")[1].startswith(f"b0+{a0}[8,4,{n}]s[705600,8400,1]")
+        assert l.split(" clsout=")[1].startswith(f"b0+{33600 + a0}[8,80,{n}]s[705600,8400,1]")
 
 
 def test_single_conv_plan(tmp_path):
@@ -218,7 +246,9 @@ def test_grouped_plan_keeps_every_hazard_in_order(y8n_path, monkeypatch, shape):
     monkeypatch.setenv("PDEFA_PLAN_GROUP_ALL", "1")
     text = native.plan_text(y8n_path, shape)
     grouped = parse(text)[1]
-    node = lambda l: int(re.search(r" node=(\d+)", l).group(1))
+    # a step's node, and for the parts of the split decode its anchor range
+    node = lambda l: (int(re.search(r" node=(\d+)", l).group(1)),
+                      l.split(" out=")[1].split()[0] if " detect_decode " in l else "")
     assert sorted(map(node, grouped)) == sorted(map(node, base))
     pos = {node(l): i for i, l in enumerate(grouped)}
     acc = touched(base)
@@ -239,13 +269,15 @@ def test_grouped_plan_keeps_every_hazard_in_order(y8n_path, monkeypatch, shape):
         if m:
             groups.setdefault(int(m.group(1)), []).append(i)
     assert len(groups) >= 6  # the Detect head's convs ride along the neck
-    # the head's last 1x1 convs, read only by the decode, wait for the end of
-    # the program (their per-scale slices of the concat buffer are disjoint)
-    # and share the last launch before it
-    last = groups[max(groups)]
-    assert sorted(grouped[i].split("'")[1].split("/")[-2] for i in last) == \
-        sorted(f"cv{b}.{s}.2" for b in (2, 3) for s in range(3))
-    assert " detect_decode " in grouped[last[-1] + 1]
+    # each scale's last two 1x1 convs, read only by that scale's decode part,
+    # wait until nothing else of the scale's work is ready and share the
+    # launch right before the part
+    dec = [i for i, l in enumerate(grouped) if " detect_decode " in l]
+    assert len(dec) == 3
+    for s, d in enumerate(dec):
+        g = [members for members in groups.values() if members[-1] == d - 1]
+        assert len(g) == 1
+        assert sorted(grouped[i].split("'")[1].split("/")[-2] for i in g[0]) == [f"cv2.{s}.2", f"cv3.{s}.2"]
     arena = arena_offsets(text)
     for members in groups.values():
         assert members == list(range(members[0], members[0] + len(members))) and 2 <= len(members) <= 8
