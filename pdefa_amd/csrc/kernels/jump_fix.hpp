@@ -49,8 +49,8 @@ __device__ __forceinline__ bool silu_winograd_near_jump(float x, float window) {
 // loads are contiguous across lanes) and every lane returns the total.
 // Every load is unconditional -- taps outside the image and lanes past Cin
 // read a clamped in-range address and zero the product with a select -- so
-// a 3x3 conv's eighteen loads of one channel chunk are in flight together
-// instead of one branch and one wait each.
+// a 3x3 conv's loads of two channel chunks (36 per lane) are in flight
+// together instead of one branch and one wait each.
 // All 64 lanes must be active; (n, oh, ow, co, g) must name an output
 // element of the conv.
 __device__ __forceinline__ double conv_point_f64(const ConvArgs& a, int n, int oh, int ow, int co, int g) {
@@ -62,25 +62,37 @@ __device__ __forceinline__ double conv_point_f64(const ConvArgs& a, int n, int o
     auto w_at = [&](int k) { return wb[static_cast<int64_t>(k >> 5) * (kConvBN * kConvBK) + (k & 31)]; };
     const float bias = a.bias[static_cast<int64_t>(g) * a.Cout + co];
     double s = 0.0;
-    for (int c0 = 0; c0 < a.Cin; c0 += 64) {
-        const bool cok = c0 + lane < a.Cin;
-        const int ci = cok ? c0 + lane : a.Cin - 1;
-        if (a.KH == 3 && a.KW == 3) {
-            float xv[9], wv[9];
-            bool ok[9];
+    if (a.KH == 3 && a.KW == 3) {
+        // two 64-channel chunks per round: a conv of up to 128 input channels
+        // waits for one round of loads
+        for (int c0 = 0; c0 < a.Cin; c0 += 128) {
+            float xv[2][9], wv[2][9];
+            bool ok[2][9];
 #pragma unroll
-            for (int t = 0; t < 9; ++t) {
-                const int ih = ih0 + (t / 3) * a.dh, iw = iw0 + (t % 3) * a.dw;
-                ok[t] = cok & (static_cast<unsigned>(ih) < static_cast<unsigned>(a.H)) &
-                        (static_cast<unsigned>(iw) < static_cast<unsigned>(a.W));
-                const int ihc = min(max(ih, 0), a.H - 1), iwc = min(max(iw, 0), a.W - 1);
-                xv[t] = xb[static_cast<int64_t>(ihc) * a.x_sh + static_cast<int64_t>(iwc) * a.x_sw + ci];
-                wv[t] = w_at(t * a.Cin + ci);
+            for (int h = 0; h < 2; ++h) {
+                const bool cok = c0 + 64 * h + lane < a.Cin;
+                const int ci = cok ? c0 + 64 * h + lane : a.Cin - 1;
+#pragma unroll
+                for (int t = 0; t < 9; ++t) {
+                    const int ih = ih0 + (t / 3) * a.dh, iw = iw0 + (t % 3) * a.dw;
+                    ok[h][t] = cok & (static_cast<unsigned>(ih) < static_cast<unsigned>(a.H)) &
+                               (static_cast<unsigned>(iw) < static_cast<unsigned>(a.W));
+                    const int ihc = min(max(ih, 0), a.H - 1), iwc = min(max(iw, 0), a.W - 1);
+                    xv[h][t] = xb[static_cast<int64_t>(ihc) * a.x_sh + static_cast<int64_t>(iwc) * a.x_sw + ci];
+                    wv[h][t] = w_at(t * a.Cin + ci);
+                }
             }
 #pragma unroll
-            for (int t = 0; t < 9; ++t)
-                s = __builtin_fma(static_cast<double>(ok[t] ? xv[t] : 0.0f), static_cast<double>(wv[t]), s);
-        } else {
+            for (int h = 0; h < 2; ++h)
+#pragma unroll
+                for (int t = 0; t < 9; ++t)
+                    s = __builtin_fma(static_cast<double>(ok[h][t] ? xv[h][t] : 0.0f), static_cast<double>(wv[h][t]),
+                                      s);
+        }
+    } else {
+        for (int c0 = 0; c0 < a.Cin; c0 += 64) {
+            const bool cok = c0 + lane < a.Cin;
+            const int ci = cok ? c0 + lane : a.Cin - 1;
             for (int kh = 0; kh < a.KH; ++kh) {
                 const int ih = ih0 + kh * a.dh;
                 const int ihc = min(max(ih, 0), a.H - 1);
