@@ -101,6 +101,25 @@ constexpr int kConvBN = 32;
 // NHWC implicit GEMM: M = N*Ho*Wo, Ncol = Cout, K = KH*KW*Cin with k ordered
 // (kh, kw, ci).  Input/output/residual are channels-last views (channel stride
 // 1) described by their n/h/w strides.
+// Division of 0 <= n < 2^31 by a launch-invariant divisor 1 <= d < 2^31 as
+// one 32x32 -> 64-bit multiply and a shift: q = (n * m) >> s with
+// s = 31 + ceil(log2 d) and m = ceil(2^s / d), which is below 2^32.  Exact:
+// with m d = 2^s + e, 0 <= e < d, n m / 2^s = n / d + n e / (d 2^s) and
+// n e / (d 2^s) < 2^(31 - s) <= 1 / d, too little to reach the next integer.
+struct FastDiv {
+    uint32_t m = 0x80000000u;  // d = 1
+    uint32_t s = 31;
+};
+inline FastDiv make_fastdiv(int64_t d) {
+    FastDiv f;
+    if (d < 1 || d >= (int64_t{1} << 31)) return f;  // callers check their divisors' range
+    uint32_t l = 0;
+    while ((int64_t{1} << l) < d) ++l;
+    f.s = 31 + l;
+    f.m = static_cast<uint32_t>(((uint64_t{1} << f.s) + static_cast<uint64_t>(d) - 1) / static_cast<uint64_t>(d));
+    return f;
+}
+
 struct ConvArgs {
     const float* x = nullptr;
     int64_t x_sn = 0, x_sh = 0, x_sw = 0;
@@ -144,6 +163,10 @@ struct ConvArgs {
     // (channels-last, n/h/w strides), e.g. straight into a concat buffer
     float* up = nullptr;
     int64_t u_sn = 0, u_sh = 0, u_sw = 0;
+    // divisors of the implicit-GEMM kernel's index arithmetic, set by its
+    // launchers: Ho*Wo, Wo, Cin, KW, and the grid's m tiles, m*n tiles and
+    // splits
+    FastDiv fd_howo, fd_wo, fd_cin, fd_kw, fd_gx, fd_gxy, fd_splits;
 };
 
 // Tile and split-K choice for an implicit GEMM of this shape on the 256 CUs.

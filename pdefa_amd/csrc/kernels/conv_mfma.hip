@@ -218,6 +218,17 @@ void check_conv(const ConvArgs& a, const ConvTileShape& sh, bool vec) {
     }
 }
 
+// The problem's divisors for the kernel's index arithmetic (every one below
+// 2^31: check_conv bounds the extents).
+ConvArgs with_divisors(const ConvArgs& a) {
+    ConvArgs b = a;
+    b.fd_howo = make_fastdiv(static_cast<int64_t>(a.Ho) * a.Wo);
+    b.fd_wo = make_fastdiv(a.Wo);
+    b.fd_cin = make_fastdiv(a.Cin);
+    b.fd_kw = make_fastdiv(a.KW);
+    return b;
+}
+
 }  // namespace
 
 void launch_conv_mfma(const ConvArgs& a, int tile, bool vec, hipStream_t s) {
@@ -229,9 +240,13 @@ void launch_conv_mfma(const ConvArgs& a, int tile, bool vec, hipStream_t s) {
     const int64_t gz = static_cast<int64_t>(a.splits) * a.groups;
     if (gx * gy * gz >= (int64_t{1} << 31) || gy > 65535 || gz > 65535) fail("grid too large");
     const dim3 grid(static_cast<unsigned>(gx), static_cast<unsigned>(gy), static_cast<unsigned>(gz));
-    if (!(launch_conv_tiles_a(tile, a, vec, grid, s) || launch_conv_tiles_b(tile, a, vec, grid, s) ||
-          launch_conv_tiles_c(tile, a, vec, grid, s) || launch_conv_tiles_d(tile, a, vec, grid, s) ||
-          launch_conv_tiles_e(tile, a, vec, grid, s)))
+    ConvArgs b = with_divisors(a);
+    b.fd_gx = make_fastdiv(gx);
+    b.fd_gxy = make_fastdiv(gx * gy);
+    b.fd_splits = make_fastdiv(a.splits);
+    if (!(launch_conv_tiles_a(tile, b, vec, grid, s) || launch_conv_tiles_b(tile, b, vec, grid, s) ||
+          launch_conv_tiles_c(tile, b, vec, grid, s) || launch_conv_tiles_d(tile, b, vec, grid, s) ||
+          launch_conv_tiles_e(tile, b, vec, grid, s)))
         fail("unknown tile");
     if (a.splits > 1) {
         const int64_t total = M * a.Cout * a.groups;
@@ -256,7 +271,8 @@ void launch_conv_mfma_group(const ConvArgs* probs, int count, int tile, hipStrea
         const int64_t gx = (M + sh.bm - 1) / sh.bm, gy = (a.Cout + sh.bn - 1) / sh.bn;
         g.tile_begin[i] = static_cast<int32_t>(total);
         g.m_tiles[i] = static_cast<int32_t>(gx);
-        g.p[i] = a;
+        g.p[i] = with_divisors(a);
+        g.p[i].fd_gx = make_fastdiv(gx);
         total += gx * gy;
         if (total >= (int64_t{1} << 31)) fail("grid too large");
     }

@@ -101,6 +101,11 @@ constexpr int mfma_block() {
     return (WM % 32 == 0 && WN % 32 == 0) ? 32 : 16;
 }
 
+// n / d for 0 <= n < 2^31 (kernels.hpp FastDiv)
+__device__ __forceinline__ int fdiv(int n, FastDiv f) {
+    return static_cast<int>((static_cast<uint64_t>(static_cast<uint32_t>(n)) * f.m) >> f.s);
+}
+
 // XCD-aware tile order: dispatch slot `lin` (of `total`) runs on XCD lin % 8;
 // give each XCD a contiguous range of tile indices.
 __device__ __forceinline__ int xcd_tile(int lin, int total) {
@@ -209,9 +214,9 @@ __device__ __forceinline__ void conv_tile(const ConvArgs& a, const int bx, const
         const int m = m0 + r0 + ROW_STEP * r;
         row_ok[r] = m < M;
         const int mm = row_ok[r] ? m : 0;
-        const int n = mm / HoWo;
+        const int n = fdiv(mm, a.fd_howo);
         const int rem = mm - n * HoWo;
-        const int ho = rem / a.Wo;
+        const int ho = fdiv(rem, a.fd_wo);
         const int wo = rem - ho * a.Wo;
         row_hi0[r] = ho * a.sh - a.ph;
         row_wi0[r] = wo * a.sw - a.pw;
@@ -222,9 +227,9 @@ __device__ __forceinline__ void conv_tile(const ConvArgs& a, const int bx, const
     int tap = 0, ci = 0, kh = 0, kw = 0;
     if (VEC) {
         const int k0 = kb_begin * BK + chunk * 4;
-        tap = k0 / a.Cin;
+        tap = fdiv(k0, a.fd_cin);
         ci = k0 - tap * a.Cin;
-        kh = tap / a.KW;
+        kh = fdiv(tap, a.fd_kw);
         kw = tap - kh * a.KW;
     }
     // Quotients of small non-negative ints by Cin and KW as (q + 0.5) * (1/d)
@@ -283,9 +288,9 @@ __device__ __forceinline__ void conv_tile(const ConvArgs& a, const int bx, const
                     const int kk = kb0 * BK + chunk * 4 + e;
                     float v = 0.0f;
                     if (row_ok[r] && kk < a.K) {
-                        const int t = kk / a.Cin;
+                        const int t = fdiv(kk, a.fd_cin);
                         const int c = kk - t * a.Cin;
-                        const int yh = t / a.KW;
+                        const int yh = fdiv(t, a.fd_kw);
                         const int xw = t - yh * a.KW;
                         const int hi = row_hi0[r] + yh * a.dh;
                         const int wi = row_wi0[r] + xw * a.dw;
@@ -387,9 +392,9 @@ __device__ __forceinline__ void conv_tile(const ConvArgs& a, const int bx, const
             if (a.splits > 1) {
                 yo = ((static_cast<int64_t>(grp) * a.splits + bz) * M + m) * a.Cout;
             } else {
-                const int n = m / HoWo;
+                const int n = fdiv(m, a.fd_howo);
                 const int rem = m - n * HoWo;
-                const int ho = rem / a.Wo;
+                const int ho = fdiv(rem, a.fd_wo);
                 const int wo = rem - ho * a.Wo;
                 yo = static_cast<int64_t>(n) * a.y_sn + static_cast<int64_t>(ho) * a.y_sh +
                      static_cast<int64_t>(wo) * a.y_sw + g_out;
@@ -473,9 +478,9 @@ __device__ __forceinline__ void conv_tile(const ConvArgs& a, const int bx, const
         };
         auto coord_of_row = [&](int row, int& n, int& oh, int& ow) {
             const int m = m0 + row;
-            n = m / HoWo;
+            n = fdiv(m, a.fd_howo);
             const int rem = m - n * HoWo;
-            oh = rem / a.Wo;
+            oh = fdiv(rem, a.fd_wo);
             ow = rem - oh * a.Wo;
         };
         if constexpr (KG == 1) {
@@ -678,10 +683,10 @@ template <int BM, int BN, int WM, int WN, int KG, int PF, bool VEC, int EPI>
 __global__ __launch_bounds__((tile_threads<BM, BN, WM, WN, KG>())) void conv_mfma_kernel(ConvArgs a) {
     const int gx = gridDim.x, gxy = gridDim.x * gridDim.y;
     const int tile_id = xcd_tile(blockIdx.x + gx * blockIdx.y + gxy * blockIdx.z, gxy * gridDim.z);
-    const int bz = tile_id / gxy;  // group * splits + split
+    const int bz = fdiv(tile_id, a.fd_gxy);  // group * splits + split
     const int bxy = tile_id - bz * gxy;
-    const int by = bxy / gx;
-    const int grp = bz / a.splits;
+    const int by = fdiv(bxy, a.fd_gx);
+    const int grp = fdiv(bz, a.fd_splits);
     conv_tile<BM, BN, WM, WN, KG, PF, VEC, EPI>(a, bxy - by * gx, by, bz - grp * a.splits, grp);
 }
 
@@ -694,7 +699,7 @@ __global__ __launch_bounds__((tile_threads<BM, BN, WM, WN, KG>())) void conv_mfm
     int p = 0;
     while (p + 1 < g.count && tile_id >= g.tile_begin[p + 1]) ++p;
     const int local = tile_id - g.tile_begin[p];
-    const int by = local / g.m_tiles[p];
+    const int by = fdiv(local, g.p[p].fd_gx);
     conv_tile<BM, BN, WM, WN, KG, PF, VEC, EPI>(g.p[p], local - by * g.m_tiles[p], by, 0, 0);
 }
 

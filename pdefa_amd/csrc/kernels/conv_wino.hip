@@ -85,6 +85,9 @@ int64_t view_bytes(int N, int H, int W, int C, int64_t sn, int64_t sh, int64_t s
 // image's tiles_h x tiles_w tile map.
 struct WinoGeom {
     int32_t tiles_h, tiles_w, tbw_log2, block_rows, block_cols;
+    // divisors of the index arithmetic (kernels.hpp FastDiv): the grid's x
+    // extent, blocks per image, block columns, patch row width 2 * tbw + 2
+    FastDiv fd_gx, fd_blocks_img, fd_block_cols, fd_pw;
 };
 
 bool wino_eligible(int KH, int KW, int sh, int sw, int dh, int dw, int Cin) {
@@ -143,6 +146,11 @@ __global__ void pack_wino_weights_kernel(float* dst, const float* w, int Cout, i
     }
 }
 
+// n / d for 0 <= n < 2^31 (kernels.hpp FastDiv)
+__device__ __forceinline__ int wdiv(int n, FastDiv f) {
+    return static_cast<int>((static_cast<uint64_t>(static_cast<uint32_t>(n)) * f.m) >> f.s);
+}
+
 template <int BN, int ACT, bool RES>
 __global__ __launch_bounds__(256) void conv_wino_kernel(ConvArgs a, WinoGeom geo, int x_bytes, int u_bytes,
                                                         int y_bytes, int r_bytes, int vec_out) {
@@ -179,13 +187,13 @@ __global__ __launch_bounds__(256) void conv_wino_kernel(ConvArgs a, WinoGeom geo
     const int lin = blockIdx.x + gx * blockIdx.y;
     const int q = total / kXcds, rmd = total % kXcds, xcd = lin % kXcds;
     const int wid = xcd * q + min(xcd, rmd) + lin / kXcds;
-    const int by = wid / gx;
+    const int by = wdiv(wid, geo.fd_gx);
     const int bx = wid - by * gx;
     // tile block bx: image bn, block row bbr, block column bbc
     const int blocks_img = geo.block_rows * geo.block_cols;
-    const int bn = bx / blocks_img;
+    const int bn = wdiv(bx, geo.fd_blocks_img);
     const int brem = bx - bn * blocks_img;
-    const int bbr = brem / geo.block_cols;
+    const int bbr = wdiv(brem, geo.fd_block_cols);
     const int bbc = brem - bbr * geo.block_cols;
     const int th0 = bbr * tbh, tw0 = bbc * tbw;  // first tile of the block
     const int n0 = by * BN;
@@ -243,7 +251,7 @@ __global__ __launch_bounds__(256) void conv_wino_kernel(ConvArgs a, WinoGeom geo
     for (int j = 0; j < kSlots; ++j) {
         const int slot = tid + 256 * j;
         const int p = slot >> 1, h = slot & 1;
-        const int pr = p / PW, pc = p - pr * PW;
+        const int pr = wdiv(p, geo.fd_pw), pc = p - pr * PW;
         const int hi = 2 * th0 - a.ph + pr, wi = 2 * tw0 - a.pw + pc;
         const bool inside = p < PP && (static_cast<unsigned>(hi) < static_cast<unsigned>(a.H)) &&
                             (static_cast<unsigned>(wi) < static_cast<unsigned>(a.W));
@@ -606,9 +614,13 @@ void launch_conv_wino(const ConvArgs& a, int bn, hipStream_t s) {
         fail("input rows must be 16-byte aligned");
     const int64_t tiles_h = (a.Ho + 1) / 2, tiles_w = (a.Wo + 1) / 2;
     if (tiles_h >= (int64_t{1} << 24) || tiles_w >= (int64_t{1} << 24)) fail("too many tiles");
-    const WinoGeom geo = wino_geometry(tiles_h, tiles_w);
+    WinoGeom geo = wino_geometry(tiles_h, tiles_w);
     const int64_t blocks = static_cast<int64_t>(a.N) * geo.block_rows * geo.block_cols;
     if (blocks >= (int64_t{1} << 31)) fail("too many tiles");
+    geo.fd_gx = make_fastdiv(blocks);
+    geo.fd_blocks_img = make_fastdiv(static_cast<int64_t>(geo.block_rows) * geo.block_cols);
+    geo.fd_block_cols = make_fastdiv(geo.block_cols);
+    geo.fd_pw = make_fastdiv(2 * (int64_t{1} << geo.tbw_log2) + 2);
     const dim3 grid(static_cast<unsigned>(blocks), static_cast<unsigned>((a.Cout + bn - 1) / bn));
     if (grid.y > 65535) fail("grid");
     if (a.x_sn < 0 || a.x_sh < 0 || a.x_sw < 0 || a.y_sn < 0 || a.y_sh < 0 || a.y_sw < 0 ||

@@ -657,6 +657,87 @@ __global__ __launch_bounds__(256) void maxpool_chain_vec_kernel(IView<int32_t> o
     }
 }
 
+// The same three pools over a whole channels-last plane per workgroup, for
+// maps of up to 1024 pixels (SPPF at 20x20 for a 640 input): the workgroup
+// stages all H x W pixels of its 4*G channels once -- no halo re-reads -- and
+// writes each output element once, so the kernel moves the algorithmic bytes
+// (one read of the input, one write of each output).  Windows are clipped at
+// the image edge; the running maximum starts at -FLT_MAX, the floor of the
+// reference's pools (pooling.cpp:53-91).
+constexpr int kPoolPlaneMax = 1024;  // pixels
+template <int r, int G>
+__global__ __launch_bounds__(256) void maxpool_plane_vec_kernel(IView<int32_t> o0, IView<int32_t> o1,
+                                                                IView<int32_t> o2, IView<int32_t> in) {
+    extern __shared__ float4 plane[];  // [H*W][G] input, then [3][H*W][G] row maxima
+    const int H = in.dims[2], W = in.dims[3], HW = H * W;
+    const int c0 = blockIdx.x * 4 * G, n = blockIdx.y;
+    float4* const reg = plane;
+    float4* const hz = plane + HW * G;
+    const float* base = in.ptr + n * in.str[0] + c0;
+    const float4 lowest = make_float4(-3.402823466e+38f, -3.402823466e+38f, -3.402823466e+38f, -3.402823466e+38f);
+    auto vmax = [](float4 a, float4 b) {
+        return make_float4(b.x > a.x ? b.x : a.x, b.y > a.y ? b.y : a.y, b.z > a.z ? b.z : a.z, b.w > a.w ? b.w : a.w);
+    };
+    for (int i = threadIdx.x; i < HW * G; i += 256) {
+        const int g = i % G, p = i / G;
+        const int h = p / W, w = p - h * W;
+        reg[i] = *reinterpret_cast<const float4*>(base + 4 * g + h * in.str[2] + w * in.str[3]);
+    }
+    __syncthreads();
+    // row maxima over radii r, 2r, 3r (one running maximum).  A window
+    // position past the image edge reads the edge pixel instead -- it lies
+    // inside the window too, so the maximum is unchanged -- which keeps the
+    // reads unconditional, all issued before the maxima are taken.
+    for (int i = threadIdx.x; i < HW * G; i += 256) {
+        const int g = i % G, p = i / G;
+        const int h = p / W, w = p - h * W;
+        const float4* row = reg + h * W * G + g;
+        float4 lf[3 * r + 1], rt[3 * r + 1];
+#pragma unroll
+        for (int d = 1; d <= 3 * r; ++d) {
+            lf[d] = row[max(w - d, 0) * G];
+            rt[d] = row[min(w + d, W - 1) * G];
+        }
+        float4 m = vmax(lowest, reg[i]), m1 = m, m2 = m;
+#pragma unroll
+        for (int d = 1; d <= 3 * r; ++d) {
+            m = vmax(vmax(m, lf[d]), rt[d]);
+            if (d == r) m1 = m;
+            if (d == 2 * r) m2 = m;
+        }
+        hz[i] = m1;
+        hz[HW * G + i] = m2;
+        hz[2 * HW * G + i] = m;
+    }
+    __syncthreads();
+    // column maxima of row-maxima plane k over radius (k + 1) r, stored
+    for (int i = threadIdx.x; i < HW * G; i += 256) {
+        const int g = i % G, p = i / G;
+        const int h = p / W, w = p - h * W;
+        auto colmax = [&](int k, auto rad_c) {
+            constexpr int rad = decltype(rad_c)::value;
+            const float4* col = hz + k * HW * G + w * G + g;
+            float4 up[rad + 1], dn[rad + 1];
+#pragma unroll
+            for (int d = 1; d <= rad; ++d) {
+                up[d] = col[max(h - d, 0) * W * G];
+                dn[d] = col[min(h + d, H - 1) * W * G];
+            }
+            float4 m = col[h * W * G];
+#pragma unroll
+            for (int d = 1; d <= rad; ++d) m = vmax(vmax(m, up[d]), dn[d]);
+            return m;
+        };
+        const float4 r0 = colmax(0, std::integral_constant<int, r>{});
+        const float4 r1 = colmax(1, std::integral_constant<int, 2 * r>{});
+        const float4 r2 = colmax(2, std::integral_constant<int, 3 * r>{});
+        const int cc = c0 + 4 * g;
+        *reinterpret_cast<float4*>(o0.ptr + n * o0.str[0] + cc + h * o0.str[2] + w * o0.str[3]) = r0;
+        *reinterpret_cast<float4*>(o1.ptr + n * o1.str[0] + cc + h * o1.str[2] + w * o1.str[3]) = r1;
+        *reinterpret_cast<float4*>(o2.ptr + n * o2.str[0] + cc + h * o2.str[2] + w * o2.str[3]) = r2;
+    }
+}
+
 namespace {
 
 // Channels-last float4 form applies: channel stride 1, C and the pixel
@@ -692,6 +773,32 @@ void launch_maxpool_chain(const View& out0, const View& out1, const View& out2, 
     const auto o0 = iview<int32_t>(out0), o1 = iview<int32_t>(out1), o2 = iview<int32_t>(out2);
     const auto x = iview<int32_t>(in);
     const int tw = static_cast<int>(tiles_w);
+    if (pool_vec_ok(out0) && pool_vec_ok(out1) && pool_vec_ok(out2) && pool_vec_ok(in) && H * W <= kPoolPlaneMax &&
+        N * (C / 4) >= 128) {
+        // whole planes of 4 channels a workgroup (input + three row-maxima
+        // planes: 64 bytes a pixel of LDS); 8 channels where the workgroups
+        // would exceed the CUs
+        const bool g2 = H * W * 2 <= kPoolPlaneMax && C % 8 == 0 && N * (C / 4) > 256;
+        const int64_t per = g2 ? 8 : 4;
+        // (taken where the planes give at least 128 workgroups: with fewer,
+        // the tiled kernel's more workgroups finish sooner)
+        const dim3 pgrid(static_cast<unsigned>(C / per), static_cast<unsigned>(N));
+        const size_t lds = sizeof(float) * 4 * static_cast<size_t>(H * W) * per;
+        auto go = [&](auto r_c) {
+            constexpr int R = decltype(r_c)::value;
+            if (g2)
+                hipLaunchKernelGGL((maxpool_plane_vec_kernel<R, 2>), pgrid, dim3(256), lds, s, o0, o1, o2, x);
+            else
+                hipLaunchKernelGGL((maxpool_plane_vec_kernel<R, 1>), pgrid, dim3(256), lds, s, o0, o1, o2, x);
+        };
+        switch (k / 2) {
+            case 0: go(std::integral_constant<int, 0>{}); break;
+            case 1: go(std::integral_constant<int, 1>{}); break;
+            case 2: go(std::integral_constant<int, 2>{}); break;
+            default: go(std::integral_constant<int, 3>{}); break;
+        }
+        return;
+    }
     if (pool_vec_ok(out0) && pool_vec_ok(out1) && pool_vec_ok(out2) && pool_vec_ok(in)) {
         switch (k / 2) {
             case 0: hipLaunchKernelGGL(maxpool_chain_vec_kernel<0>, grid, dim3(256), 0, s, o0, o1, o2, x, tw); break;
@@ -788,6 +895,13 @@ __global__ __launch_bounds__(256) void detect_decode_kernel(DetectDecodeArgs a, 
     decode_box(a, n, an, d);
 }
 
+// Dispatch slot `lin` (of `total`) runs on XCD lin % 8: the block index that
+// gives each XCD a contiguous range of blocks.
+__device__ __forceinline__ int32_t xcd_block(int32_t lin, int32_t total) {
+    const int32_t q = total / 8, rmd = total % 8, xcd = lin % 8;
+    return xcd * q + min(xcd, rmd) + lin / 8;
+}
+
 // The whole head output of kHeadAnchors consecutive anchors of one image per
 // workgroup, when each anchor's row holds its 4*R box bins followed by its C
 // class scores (row stride S floats, the Detect head's [anchor][144] concat):
@@ -802,8 +916,12 @@ __global__ __launch_bounds__(256) void detect_head_kernel(DetectDecodeArgs a, in
     __shared__ float dist[4][kHeadAnchors];
     const int tid = threadIdx.x;
     const int32_t tiles = (A + kHeadAnchors - 1) / kHeadAnchors;
-    const int32_t n = blockIdx.x / tiles;
-    const int32_t a0 = (blockIdx.x - n * tiles) * kHeadAnchors;
+    // workgroups go round-robin over the 8 XCDs: each XCD takes a contiguous
+    // range of anchor tiles, so the 64-byte runs that neighbouring tiles
+    // write into one class row meet in the same L2
+    const int32_t bid = xcd_block(blockIdx.x, gridDim.x);
+    const int32_t n = bid / tiles;
+    const int32_t a0 = (bid - n * tiles) * kHeadAnchors;
     const int cnt = min(kHeadAnchors, A - a0);
     const int P = S + 1;
     const float4* src = reinterpret_cast<const float4*>(a.x.ptr + n * a.x.str[0] + static_cast<int64_t>(a0) * S);

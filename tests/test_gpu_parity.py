@@ -742,11 +742,15 @@ def test_pool_chain(tmp_path, n, c, h, w, k):
     np.testing.assert_array_equal(got, want)
 
 
-@pytest.mark.parametrize("n,c,h,w,k", [(1, 128, 20, 20, 5), (2, 40, 13, 11, 5), (1, 16, 9, 30, 3), (3, 24, 7, 7, 7)])
+@pytest.mark.parametrize("n,c,h,w,k", [(1, 128, 20, 20, 5), (2, 40, 13, 11, 5), (1, 16, 9, 30, 3), (3, 24, 7, 7, 7),
+                                       (8, 128, 20, 20, 5), (8, 256, 16, 32, 3), (4, 144, 30, 30, 5),
+                                       (2, 16, 40, 40, 5)])
 def test_sppf_channels_last(tmp_path, n, c, h, w, k):
     """The SPPF block (conv, three chained pools, concat, conv): the fused
     pool step reads and writes channels-last conv outputs, which takes the
-    float4 pool kernel, against the oracle."""
+    float4 pool kernels -- whole planes (maps up to 1024 pixels, at least
+    128 planes of 4 channels; 8 channels a workgroup beyond 256 such planes
+    on maps up to 512 pixels), tiles otherwise -- against the oracle."""
     print(f"[case] sppf n={n} c={c} h={h} w={w} k={k}", flush=True)
     model, x = ys.build_sppf(n, c, h, w, k)
     path = str(tmp_path / "sppf.engine")
