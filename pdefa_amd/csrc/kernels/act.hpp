@@ -50,6 +50,52 @@ __device__ __forceinline__ float silu_winograd_form(float x, float window = 0.0f
     return __builtin_unpredictable(neg_x < -88.37626f) ? x : lo;
 }
 
+typedef float act_float4 __attribute__((ext_vector_type(4)));
+typedef int act_int4 __attribute__((ext_vector_type(4)));
+
+// silu_winograd_form of four values, each by the same operations in the same
+// order (bit-identical to four scalar calls), written over 4-wide vectors so
+// that the four dependency chains interleave instruction by instruction
+// instead of running one after another (a wave alone on its SIMD would
+// otherwise wait out every instruction's latency).  dist (when given)
+// receives, per value, (0.5 - window * max(1, |x log2 e|)) - |f| where the
+// polynomial branch applies (|x log2 e| < 128), +inf elsewhere: <= 0 exactly
+// where silu_winograd_form sets near (the difference of two floats is zero
+// only when they are equal), so callers test the minimum of four first.
+__device__ __forceinline__ act_float4 silu_winograd_form4(act_float4 x, float window = 0.0f,
+                                                          act_float4* dist = nullptr) {
+#pragma clang fp contract(off)
+    const act_float4 neg_x = -x;
+    const act_float4 fx = neg_x * 1.44269504088896341f;
+    const act_float4 n = __builtin_elementwise_trunc(fx + __builtin_elementwise_copysign((act_float4)0.49999997f, fx));
+    const act_float4 f = fx - n;
+    if (dist) {
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const float ax = __builtin_fabsf(fx[k]);
+            const float d = (0.5f - window * (ax > 1.0f ? ax : 1.0f)) - __builtin_fabsf(f[k]);
+            (*dist)[k] = __builtin_unpredictable(ax < 128.0f) ? d : __builtin_inff();
+        }
+    }
+    act_float4 p = (act_float4)1.9875691500e-4f;
+    p = __builtin_elementwise_fma(p, f, (act_float4)1.3981999507e-3f);
+    p = __builtin_elementwise_fma(p, f, (act_float4)8.3334519073e-3f);
+    p = __builtin_elementwise_fma(p, f, (act_float4)4.1665795894e-2f);
+    p = __builtin_elementwise_fma(p, f, (act_float4)1.6666665459e-1f);
+    p = __builtin_elementwise_fma(p, f, (act_float4)5.0000001201e-1f);
+    p = __builtin_elementwise_fma(p, f, (act_float4)1.0f);
+    const act_int4 e = (__builtin_convertvector(n, act_int4) + 127) << 23;
+    const act_float4 d = __builtin_elementwise_fma(p, __builtin_bit_cast(act_float4, e), (act_float4)1.0f);
+    act_float4 out;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        const float r = x[k] * __builtin_amdgcn_rcpf(d[k]);
+        const float lo = __builtin_unpredictable(neg_x[k] > 88.37626f) ? 0.0f : r;
+        out[k] = __builtin_unpredictable(neg_x[k] < -88.37626f) ? x[k] : lo;
+    }
+    return out;
+}
+
 // SiLU for the fused conv epilogues: x * 1/(1 + 2^(-x log2 e)) with the
 // hardware exp2 and reciprocal (1 ulp each; the relative error of the result
 // stays below 1e-6 on the fp32 range, far inside the 1e-3 parity tolerance).

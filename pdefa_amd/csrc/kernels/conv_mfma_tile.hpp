@@ -101,6 +101,14 @@ constexpr int mfma_block() {
     return (WM % 32 == 0 && WN % 32 == 0) ? 32 : 16;
 }
 
+// Where the epilogues send the stores of tile elements outside the output
+// (rows past M, channels past Cout, outputs left to the float64 pass): one
+// slot per lane of a workgroup, written and never read.  A store through a
+// selected pointer instead of a branch keeps each element's activation out
+// of a conditional block, so the activations of a lane's elements
+// interleave instead of each waiting out its own chain of latencies.
+__device__ float g_epilogue_discard[512];
+
 // n / d for 0 <= n < 2^31 (kernels.hpp FastDiv)
 __device__ __forceinline__ int fdiv(int n, FastDiv f) {
     return static_cast<int>((static_cast<uint64_t>(static_cast<uint32_t>(n)) * f.m) >> f.s);
@@ -534,9 +542,10 @@ __device__ __forceinline__ void conv_tile(const ConvArgs& a, const int bx, const
                             }
                         }
                         if (RES) v += rv[e][tn];
-                        if (yo[e] >= 0 && cok[tn] && !flagged) {
-                            __builtin_nontemporal_store(v, &dst[yo[e] + co[tn]]);
-                            if (UP) store_up(uo[e], co[tn], v);
+                        const bool ok = yo[e] >= 0 && cok[tn] && !flagged;
+                        __builtin_nontemporal_store(v, ok ? &dst[yo[e] + co[tn]] : &g_epilogue_discard[tid]);
+                        if constexpr (UP) {
+                            if (ok) store_up(uo[e], co[tn], v);
                         }
                     }
             }
@@ -619,9 +628,10 @@ __device__ __forceinline__ void conv_tile(const ConvArgs& a, const int bx, const
                     }
                 }
                 if (RES) r += rv[i];
-                if (yo[i] >= 0 && cok && !flagged) {
-                    __builtin_nontemporal_store(r, &dst[yo[i] + co]);
-                    if (UP) store_up(uo[i], co, r);
+                const bool ok = yo[i] >= 0 && cok && !flagged;
+                __builtin_nontemporal_store(r, ok ? &dst[yo[i] + co] : &g_epilogue_discard[tid]);
+                if constexpr (UP) {
+                    if (ok) store_up(uo[i], co, r);
                 }
             }
             if constexpr (FIX) {

@@ -452,16 +452,27 @@ __global__ __launch_bounds__(256) void conv_wino_kernel(ConvArgs a, WinoGeom geo
     constexpr bool FIX = ACT == kActSiluWinogradForm;
     const bool fix = FIX && a.w_kmaj != nullptr;
     uint32_t bits = 0;
-    auto act_flag = [&](int r, int q, int k, float pre) {
+    // channels of this lane that exist (bit k: channel n0 + c4 + k < Cout)
+    const uint32_t kmask = static_cast<uint32_t>(cob[0] != kWinoNoPixel) | (uint32_t{cob[1] != kWinoNoPixel} << 1) |
+                           (uint32_t{cob[2] != kWinoNoPixel} << 2) | (uint32_t{cob[3] != kWinoNoPixel} << 3);
+    // the activation of the 4 channels of pixel q of tile pass r (the
+    // compat SiLU four at a time, flagging its near-jump elements)
+    auto act4 = [&](int r, int q, floatx4 pre) {
+        floatx4 v;
         if constexpr (FIX) {
-            bool near;
-            const float v = silu_winograd_form(pre, a.jump_window, &near);
-            bits |= static_cast<uint32_t>(fix & (yo[r][q] != kWinoNoPixel) & (cob[k] != kWinoNoPixel) & near)
-                    << (16 * r + 4 * q + k);
-            return v;
+            floatx4 d;
+            v = silu_winograd_form4(pre, a.jump_window, &d);
+            const float dmin = fminf(fminf(d[0], d[1]), fminf(d[2], d[3]));
+            if (fix && yo[r][q] != kWinoNoPixel && dmin <= 0.0f) {  // rare
+                const uint32_t nb = uint32_t{d[0] <= 0.0f} | (uint32_t{d[1] <= 0.0f} << 1) |
+                                    (uint32_t{d[2] <= 0.0f} << 2) | (uint32_t{d[3] <= 0.0f} << 3);
+                bits |= (nb & kmask) << (16 * r + 4 * q);
+            }
         } else {
-            return act_fixed<ACT>(pre, a.act, a.slope);
+#pragma unroll
+            for (int k = 0; k < 4; ++k) v[k] = act_fixed<ACT>(pre[k], a.act, a.slope);
         }
+        return v;
     };
     if (vec_out) {
         floatx4 rv[CB][4];
@@ -477,12 +488,10 @@ __global__ __launch_bounds__(256) void conv_wino_kernel(ConvArgs a, WinoGeom geo
 #pragma unroll
         for (int r = 0; r < CB; ++r)
 #pragma unroll
-            for (int q = 0; q < 4; ++q)
-#pragma unroll
-                for (int k = 0; k < 4; ++k) {
-                    v[r][q][k] = act_flag(r, q, k, yv[r][q][k] + bias4[k]);
-                    if (RES) v[r][q][k] += rv[r][q][k];
-                }
+            for (int q = 0; q < 4; ++q) {
+                v[r][q] = act4(r, q, yv[r][q] + bias4);
+                if constexpr (RES) v[r][q] += rv[r][q];
+            }
         if (!FIX || __builtin_amdgcn_ballot_w64(bits != 0) == 0) {
 #pragma unroll
             for (int r = 0; r < CB; ++r)
@@ -516,15 +525,14 @@ __global__ __launch_bounds__(256) void conv_wino_kernel(ConvArgs a, WinoGeom geo
 #pragma unroll
         for (int r = 0; r < CB; ++r)
 #pragma unroll
-            for (int q = 0; q < 4; ++q)
+            for (int q = 0; q < 4; ++q) {
+                const floatx4 v = act4(r, q, yv[r][q] + bias4);
 #pragma unroll
-                for (int k = 0; k < 4; ++k) {
-                    float v = act_flag(r, q, k, yv[r][q][k] + bias4[k]);
-                    if (RES) v += rv[r][q][k];
+                for (int k = 0; k < 4; ++k)
                     __builtin_amdgcn_raw_buffer_store_b32(
-                        __float_as_uint(v), ybuf,
+                        __float_as_uint(RES ? v[k] + rv[r][q][k] : v[k]), ybuf,
                         (bits >> (16 * r + 4 * q + k)) & 1u ? kWinoNoPixel : yo[r][q] + cob[k], 0, 2);
-                }
+            }
     }
     if constexpr (FIX) {
         if (a.w_kmaj) {
