@@ -484,6 +484,13 @@ void launch_softmax(const View& out, const View& in, int axis, hipStream_t s) {
                            axis, rows);
 }
 
+// Dispatch slot `lin` (of `total`) runs on XCD lin % 8: the block index that
+// gives each XCD a contiguous range of blocks.
+__device__ __forceinline__ int32_t xcd_block(int32_t lin, int32_t total) {
+    const int32_t q = total / 8, rmd = total % 8, xcd = lin % 8;
+    return xcd * q + min(xcd, rmd) + lin / 8;
+}
+
 // SPPF: three chained k x k stride-1 same-padded max pools in one pass.  A
 // workgroup takes a T x T pixel tile of CB channels: it stages the tile plus
 // a 3r halo in LDS (outside the image: -FLT_MAX, so padding never wins), takes
@@ -670,7 +677,12 @@ __global__ __launch_bounds__(256) void maxpool_plane_vec_kernel(IView<int32_t> o
                                                                 IView<int32_t> o2, IView<int32_t> in) {
     extern __shared__ float4 plane[];  // [H*W][G] input, then [3][H*W][G] row maxima
     const int H = in.dims[2], W = in.dims[3], HW = H * W;
-    const int c0 = blockIdx.x * 4 * G, n = blockIdx.y;
+    // each XCD takes a contiguous range of (image, channel group) planes:
+    // neighbouring channel groups share cache lines, which one L2 then
+    // fetches and writes once
+    const int bid = xcd_block(blockIdx.x + gridDim.x * blockIdx.y, gridDim.x * gridDim.y);
+    const int n = bid / gridDim.x;
+    const int c0 = (bid - n * gridDim.x) * 4 * G;
     float4* const reg = plane;
     float4* const hz = plane + HW * G;
     const float* base = in.ptr + n * in.str[0] + c0;
@@ -893,13 +905,6 @@ __global__ __launch_bounds__(256) void detect_decode_kernel(DetectDecodeArgs a, 
         }
     }
     decode_box(a, n, an, d);
-}
-
-// Dispatch slot `lin` (of `total`) runs on XCD lin % 8: the block index that
-// gives each XCD a contiguous range of blocks.
-__device__ __forceinline__ int32_t xcd_block(int32_t lin, int32_t total) {
-    const int32_t q = total / 8, rmd = total % 8, xcd = lin % 8;
-    return xcd * q + min(xcd, rmd) + lin / 8;
 }
 
 // The whole head output of kHeadAnchors consecutive anchors of one image per
