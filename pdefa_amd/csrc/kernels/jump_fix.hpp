@@ -41,6 +41,34 @@ __device__ __forceinline__ bool silu_winograd_near_jump(float x, float window) {
     return near;
 }
 
+// One lane's double moved across the wave by a DPP control (both halves).
+template <int CTRL>
+__device__ __forceinline__ double dpp_f64(double v) {
+    const uint64_t b = __builtin_bit_cast(uint64_t, v);
+    const uint32_t lo = static_cast<uint32_t>(__builtin_amdgcn_mov_dpp(static_cast<int>(b), CTRL, 0xf, 0xf, false));
+    const uint32_t hi =
+        static_cast<uint32_t>(__builtin_amdgcn_mov_dpp(static_cast<int>(b >> 32), CTRL, 0xf, 0xf, false));
+    return __builtin_bit_cast(double, (static_cast<uint64_t>(hi) << 32) | lo);
+}
+
+// The sum of v over the 64 lanes of the wave, in every lane: within each row
+// of 16 lanes by DPP (quad swaps, then rotations by 4 and 8 lanes), then the
+// four row sums read from lanes 0, 16, 32 and 48 -- register moves instead
+// of LDS round trips.
+__device__ __forceinline__ double wave_sum_f64(double v) {
+    v += dpp_f64<0xB1>(v);   // quad_perm [1,0,3,2]
+    v += dpp_f64<0x4E>(v);   // quad_perm [2,3,0,1]: every lane holds its quad's sum
+    v += dpp_f64<0x124>(v);  // row_ror:4
+    v += dpp_f64<0x128>(v);  // row_ror:8: every lane holds its row's sum
+    auto row = [&](int l) {
+        const uint64_t b = __builtin_bit_cast(uint64_t, v);
+        const uint32_t lo = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(b), l));
+        const uint32_t hi = static_cast<uint32_t>(__builtin_amdgcn_readlane(static_cast<int>(b >> 32), l));
+        return __builtin_bit_cast(double, (static_cast<uint64_t>(hi) << 32) | lo);
+    };
+    return (row(0) + row(16)) + (row(32) + row(48));
+}
+
 // bias[g*Cout + co] + sum over (kh, kw, ci) of
 // x[n, oh*sh - ph + kh*dh, ow*sw - pw + kw*dw, g*Cin + ci] * w[co][k] in
 // float64, w the K-major packed weights (k = (kh*KW + kw)*Cin + ci, 32 x 32
@@ -108,9 +136,7 @@ __device__ __forceinline__ double conv_point_f64(const ConvArgs& a, int n, int o
             }
         }
     }
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) s += __shfl_xor(s, off, 64);
-    return s + static_cast<double>(bias);
+    return wave_sum_f64(s) + static_cast<double>(bias);
 }
 
 // Second pass of a compat-SiLU epilogue, after its stores, which leave the
@@ -128,15 +154,20 @@ __device__ __forceinline__ void fix_near_jumps(const ConvArgs& a, Bits bits, int
     while (true) {
         const uint64_t lanes = __builtin_amdgcn_ballot_w64(bits != 0);
         if (lanes == 0) break;
-        const int src = __builtin_ctzll(lanes);
-        const unsigned long long lb = __shfl(static_cast<unsigned long long>(bits), src, 64);
+        const int src = __builtin_ctzll(lanes);  // wave-uniform: lanes come from a ballot
+        const uint64_t b64 = static_cast<uint64_t>(bits);
+        const uint64_t lb = static_cast<uint64_t>(static_cast<uint32_t>(
+                                __builtin_amdgcn_readlane(static_cast<int>(b64), src))) |
+                            (static_cast<uint64_t>(static_cast<uint32_t>(
+                                 __builtin_amdgcn_readlane(static_cast<int>(b64 >> 32), src)))
+                             << 32);
         const int e = __builtin_ctzll(lb);
         int n, oh, ow, co;
         coord(e, n, oh, ow, co);
-        n = __shfl(n, src, 64);
-        oh = __shfl(oh, src, 64);
-        ow = __shfl(ow, src, 64);
-        co = __shfl(co, src, 64);
+        n = __builtin_amdgcn_readlane(n, src);
+        oh = __builtin_amdgcn_readlane(oh, src);
+        ow = __builtin_amdgcn_readlane(ow, src);
+        co = __builtin_amdgcn_readlane(co, src);
         const double s = conv_point_f64(a, n, oh, ow, co, g);
         if (lane == src) {
             store(e, static_cast<float>(s));
