@@ -27,6 +27,7 @@ SOURCES = [
     "kernels/conv_mfma_tiles_d.hip",
     "kernels/conv_mfma_tiles_e.hip",
     "kernels/conv_wino.hip",
+    "kernels/conv_wino_strip.hip",
     "kernels/ops.hip",
     "kernels/yolo_decode.hip",
     "kernels/noalloc.hip",

@@ -33,8 +33,12 @@
 // stages' memory), and the row transform (A^T over i), bias, activation and
 // residual produce each tile's 2x2 outputs, written with range-checked buffer
 // stores at per-pixel offsets of the output view.
+//
+// launch_conv_wino runs this staged form for BN = 32 and the strip form
+// (conv_wino_strip.hip, no LDS staging) for BN = 64; both give the same bits.
 #include "../kernels.hpp"
 #include "act.hpp"
+#include "conv_wino_common.hpp"
 #include "jump_fix.hpp"
 
 #include <algorithm>
@@ -46,37 +50,13 @@
 namespace pdefa {
 namespace k {
 
-typedef float floatx4 __attribute__((ext_vector_type(4)));
-typedef float floatx16 __attribute__((ext_vector_type(16)));
-typedef unsigned int uintx4 __attribute__((ext_vector_type(4)));
+using namespace wino;
 
 namespace {
-
-constexpr int kWT = 32;  // tiles per workgroup (GEMM rows)
-constexpr int kCK = 8;   // input channels per K step (4 per lane half)
-constexpr int kXcds = 8;
-constexpr int kMaxCin = 4096;
-// Input, weights, output and residual are addressed by 32-bit byte offsets
-// from their base.  Their spans stay under kWinoMaxViewBytes, so an offset
-// derived from kWinoNoPixel (less up to 16 bytes, or plus a valid offset, or
-// plus itself) always lands past the buffer range.
-constexpr int32_t kWinoNoPixel = 1 << 30;
-constexpr int32_t kWinoMaxViewBytes = kWinoNoPixel - 4096;
-// buffer resource word 3 for raw 32-bit buffer access
-constexpr int kWinoBufferFlags = 0x00020000;
 
 // Input pixels of the largest tile-block patch region ((2*32+2) x 4 for a
 // 32x1 or 1x32 block): the LDS patch stage holds this many pixels per half.
 constexpr int kWinoMaxPatchPixels = 66 * 4;
-
-int wino_cin_pad(int Cin) { return (Cin + kCK - 1) / kCK * kCK; }
-int wino_cout_pad(int Cout) { return (Cout + 63) / 64 * 64; }
-
-void fail(const std::string& m) { throw std::runtime_error("conv_wino: " + m); }
-// Bytes from a view's base to the end of its last element.
-int64_t view_bytes(int N, int H, int W, int C, int64_t sn, int64_t sh, int64_t sw) {
-    return 4 * ((N - 1) * sn + (H - 1) * sh + (W - 1) * sw + C);
-}
 
 }  // namespace
 
@@ -144,11 +124,6 @@ __global__ void pack_wino_weights_kernel(float* dst, const float* w, int Cout, i
         for (int e = 0; e < 16; ++e)
             dst[((static_cast<int64_t>(e) * cq + ci / 4) * cop + co) * 4 + (ci % 4)] = u[e];
     }
-}
-
-// n / d for 0 <= n < 2^31 (kernels.hpp FastDiv)
-__device__ __forceinline__ int wdiv(int n, FastDiv f) {
-    return static_cast<int>((static_cast<uint64_t>(static_cast<uint32_t>(n)) * f.m) >> f.s);
 }
 
 template <int BN, int ACT, bool RES>
@@ -563,12 +538,6 @@ __global__ __launch_bounds__(256) void conv_wino_kernel(ConvArgs a, WinoGeom geo
 
 namespace {
 
-// Byte extents of the input, transformed weights, output and residual.
-struct WinoBytes {
-    int x, u, y, r;
-    int vec;  // outputs (and residuals) as 16-byte runs
-};
-
 template <int BN, int ACT>
 void launch_act(const ConvArgs& a, dim3 grid, WinoGeom g, WinoBytes b, hipStream_t s) {
     if (a.res)
@@ -622,15 +591,6 @@ void launch_conv_wino(const ConvArgs& a, int bn, hipStream_t s) {
         fail("input rows must be 16-byte aligned");
     const int64_t tiles_h = (a.Ho + 1) / 2, tiles_w = (a.Wo + 1) / 2;
     if (tiles_h >= (int64_t{1} << 24) || tiles_w >= (int64_t{1} << 24)) fail("too many tiles");
-    WinoGeom geo = wino_geometry(tiles_h, tiles_w);
-    const int64_t blocks = static_cast<int64_t>(a.N) * geo.block_rows * geo.block_cols;
-    if (blocks >= (int64_t{1} << 31)) fail("too many tiles");
-    geo.fd_gx = make_fastdiv(blocks);
-    geo.fd_blocks_img = make_fastdiv(static_cast<int64_t>(geo.block_rows) * geo.block_cols);
-    geo.fd_block_cols = make_fastdiv(geo.block_cols);
-    geo.fd_pw = make_fastdiv(2 * (int64_t{1} << geo.tbw_log2) + 2);
-    const dim3 grid(static_cast<unsigned>(blocks), static_cast<unsigned>((a.Cout + bn - 1) / bn));
-    if (grid.y > 65535) fail("grid");
     if (a.x_sn < 0 || a.x_sh < 0 || a.x_sw < 0 || a.y_sn < 0 || a.y_sh < 0 || a.y_sw < 0 ||
         (a.res && (a.r_sn < 0 || a.r_sh < 0 || a.r_sw < 0)))
         fail("negative strides");
@@ -645,10 +605,22 @@ void launch_conv_wino(const ConvArgs& a, int bn, hipStream_t s) {
     };
     b.vec = a.Cout % 4 == 0 && rows16(a.y, a.y_sn, a.y_sh, a.y_sw) &&
             (!a.res || rows16(a.res, a.r_sn, a.r_sh, a.r_sw));
-    if (bn == 64)
-        launch_bn<64>(a, grid, geo, b, s);
-    else
-        launch_bn<32>(a, grid, geo, b, s);
+    // 64 channels a workgroup: the strip form (conv_wino_strip.hip), the
+    // same outputs bit for bit
+    if (bn == 64) {
+        launch_conv_wino_strip(a, 64, static_cast<int>(tiles_h), static_cast<int>(tiles_w), b, s);
+        return;
+    }
+    WinoGeom geo = wino_geometry(tiles_h, tiles_w);
+    const int64_t blocks = static_cast<int64_t>(a.N) * geo.block_rows * geo.block_cols;
+    if (blocks >= (int64_t{1} << 31)) fail("too many tiles");
+    geo.fd_gx = make_fastdiv(blocks);
+    geo.fd_blocks_img = make_fastdiv(static_cast<int64_t>(geo.block_rows) * geo.block_cols);
+    geo.fd_block_cols = make_fastdiv(geo.block_cols);
+    geo.fd_pw = make_fastdiv(2 * (int64_t{1} << geo.tbw_log2) + 2);
+    const dim3 grid(static_cast<unsigned>(blocks), static_cast<unsigned>((a.Cout + 31) / 32));
+    if (grid.y > 65535) fail("grid");
+    launch_bn<32>(a, grid, geo, b, s);
 }
 
 void launch_pack_wino_weights(float* dst, const float* w, int Cout, int Cin, hipStream_t s) {
