@@ -478,6 +478,11 @@ def tune_measured():
     return native.tune_stats()[0]
 
 
+# A run that records launch-shape choices (PDEFA_TUNE_RECORD, usually with the
+# table switched off) times shapes on purpose; the no-timing checks are off.
+TUNE_RECORDING = bool(os.environ.get("PDEFA_TUNE_RECORD"))
+
+
 @pytest.mark.parametrize("cin,cout,k,s,hw", CONV_CASES)
 def test_single_conv(tmp_path, cin, cout, k, s, hw):
     """Conv + bias + SiLU (cfg 2a/2b/2c and edge shapes) against the
@@ -488,7 +493,7 @@ def test_single_conv(tmp_path, cin, cout, k, s, hw):
     ys.save(model, path)
     m0 = tune_measured()
     got = run_engine(path, x)[0]
-    assert tune_measured() == m0, "a launch shape of this conv is not in the launch-shape table"
+    assert TUNE_RECORDING or tune_measured() == m0, "a launch shape of this conv is not in the launch-shape table"
     ref = reference_outputs(path, x)
     _, _, bad = errors(got, ref, REL_FLOOR_CONV)
     jumps = np.flatnonzero(bad).tolist()
@@ -686,7 +691,7 @@ def test_yolov8n_rectangular(tmp_path, hw):
         got = eng.run(x)[0]
     finally:
         eng.close()
-    assert tune_measured() == m0, "a launch shape of this model is not in the launch-shape table"
+    assert TUNE_RECORDING or tune_measured() == m0, "a launch shape of this model is not in the launch-shape table"
     n_anchor = sum((hw[0] // s) * (hw[1] // s) for s in (8, 16, 32))
     assert got.shape == (2, 84, n_anchor)
     follow, _ = assert_network_close(got, model, x, f"yolov8n {hw}")
@@ -715,7 +720,7 @@ def test_yolov8_scales(tmp_path, scale, hw, seed, cls_bias):
         got = eng.run(x)[0]
     finally:
         eng.close()
-    assert tune_measured() == m0, "a launch shape of this model is not in the launch-shape table"
+    assert TUNE_RECORDING or tune_measured() == m0, "a launch shape of this model is not in the launch-shape table"
     assert got.shape == (1, 84, sum((hw // s) ** 2 for s in (8, 16, 32)))
     follow, _ = assert_network_close(got, model, x, f"yolov8{scale} {hw} seed {seed}")
     plain = graph_ref.run_graph(model, [x])[0]
@@ -944,7 +949,7 @@ def test_yolov8n_b1(yolov8n, tmp_path):
         plan = eng.plan()
     finally:
         eng.close()
-    assert tune_measured() == m0, "a launch shape of YOLOv8n b1 is not in the launch-shape table"
+    assert TUNE_RECORDING or tune_measured() == m0, "a launch shape of YOLOv8n b1 is not in the launch-shape table"
     assert np.array_equal(got, again), "two runs differ"
     _save_text("yolov8n_b1_plan", plan)
     ref = reference_outputs(path, x)
@@ -969,7 +974,7 @@ def test_yolov8n_b8_vs_reference(yolov8n, tmp_path):
         got = eng.run(x)[0]
     finally:
         eng.close()
-    assert tune_measured() == m0, "a launch shape of YOLOv8n b8 is not in the launch-shape table"
+    assert TUNE_RECORDING or tune_measured() == m0, "a launch shape of YOLOv8n b8 is not in the launch-shape table"
     assert got.shape == (8, 84, 8400)
     ref = reference_outputs(path, x)
     jumps = read_device_jumps(model, x, got, tmp_path, "yolov8n b8", YOLO_JUMPS["yolov8n_b8"])
@@ -1371,7 +1376,7 @@ def test_yolov8m_b16_vs_reference(tmp_path):
         out = eng.run(x)[0]
     finally:
         eng.close()
-    assert tune_measured() == m0, "a launch shape of YOLOv8m b16 is not in the launch-shape table"
+    assert TUNE_RECORDING or tune_measured() == m0, "a launch shape of YOLOv8m b16 is not in the launch-shape table"
     assert out.shape == (16, 84, 8400)
     pick = [0, 1, 15]
     ref = reference_outputs(path, x[pick])
