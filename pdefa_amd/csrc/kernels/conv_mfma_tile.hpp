@@ -21,10 +21,11 @@
 // k = 8q + 4h + j for step (q, j), with 16x16 blocks lane quarter h supplies
 // k = 16q + 4h + j, the same k for A and B, which covers the 32 k of a slice
 // once.
-// Loads are issued unconditionally (out-of-range A rows read the tensor base,
-// out-of-range K blocks and N rows re-read the last valid block) and the
-// in-range mask is applied when a stage is written to LDS, so the loads of the
-// newest step stay in flight while the previous stage is stored.
+// Loads are issued unconditionally: A chunks outside the input (rows past M,
+// padding pixels, taps past the kernel) read a zero chunk, out-of-range K
+// blocks and N rows re-read the last valid block (such columns are never
+// stored), so a loaded stage goes to LDS as it is and the loads of the newest
+// step stay in flight while the previous stage is stored.
 //
 // Workgroups are dispatched round-robin over the 8 XCDs, each with its own L2;
 // the tile index is remapped so that every XCD works through a contiguous
@@ -109,6 +110,14 @@ constexpr int mfma_block() {
 // interleave instead of each waiting out its own chain of latencies.
 __device__ float g_epilogue_discard[512];
 
+// What the loads of A chunks outside the input (rows past M, taps past the
+// kernel, pixels in the padding) read instead: four zeros, never written.
+// Loading zeros, rather than zeroing a loaded chunk by a select, leaves the
+// loaded registers untouched until their LDS store, so the wait for a load
+// sits at that store, a pipeline step after the load; with the select the
+// compiler placed it, and the wait, right behind the load.
+__device__ __attribute__((aligned(16))) float g_zero_chunk[4];
+
 // n / d for 0 <= n < 2^31 (kernels.hpp FastDiv)
 __device__ __forceinline__ int fdiv(int n, FastDiv f) {
     return static_cast<int>((static_cast<uint64_t>(static_cast<uint32_t>(n)) * f.m) >> f.s);
@@ -152,7 +161,6 @@ __device__ __forceinline__ void conv_tile(const ConvArgs& a, const int bx, const
     constexpr int B_ROWS = BN / ROW_STEP;   // B float4 loads per lane per step
     static_assert(WM % MB == 0 && WN % MB == 0 && BM % ROW_STEP == 0 && BN % ROW_STEP == 0, "tile");
     static_assert(BM * BN >= NT, "one reduced element per lane at least");
-    static_assert(A_ROWS <= 32, "mask bits");
     // One wave per K slice (a single wave tile, KG > 1): each wave loads,
     // stages and multiplies its own slice only, so the pipeline needs no
     // workgroup barrier; LDS operations of one wave complete in issue order,
@@ -261,10 +269,8 @@ __device__ __forceinline__ void conv_tile(const ConvArgs& a, const int bx, const
 
     floatx4 areg[PF][A_ROWS];
     floatx4 breg[PF][B_ROWS];
-    unsigned amask[PF];
 
-    auto load_step = [&](int kb0, floatx4* ar, floatx4* br, unsigned& mask) {
-        unsigned mk = 0;
+    auto load_step = [&](int kb0, floatx4* ar, floatx4* br) {
         if (VEC) {
             const int dy = kh * a.dh, dx = kw * a.dw;
             const int doff = dy * xsh + dx * xsw + ci;
@@ -275,9 +281,8 @@ __device__ __forceinline__ void conv_tile(const ConvArgs& a, const int bx, const
                 const int wi = row_wi0[r] + dx;
                 const bool ok = row_ok[r] & tap_ok & (static_cast<unsigned>(hi) < static_cast<unsigned>(a.H)) &
                                 (static_cast<unsigned>(wi) < static_cast<unsigned>(a.W));
-                const float* p = row_base[r] + (ok ? row_off0[r] + doff : 0);
+                const float* p = ok ? row_base[r] + row_off0[r] + doff : g_zero_chunk;
                 ar[r] = *reinterpret_cast<const floatx4*>(p);
-                mk |= static_cast<unsigned>(ok) << r;
             }
             // advance this lane's chunk to the next step's k
             ci += BKT;
@@ -310,22 +315,18 @@ __device__ __forceinline__ void conv_tile(const ConvArgs& a, const int bx, const
                     ar[r][e] = v;
                 }
             }
-            mk = ~0u;
         }
-        mask = mk;
         const int kb = min(kb0 + cg, a.ktiles - 1);
 #pragma unroll
         for (int i = 0; i < B_ROWS; ++i)
             br[i] = *reinterpret_cast<const floatx4*>(brow[i] + static_cast<int64_t>(kb) * (kConvBN * BK));
     };
-    auto store_step = [&](int st, const floatx4* ar, const floatx4* br, unsigned mask) {
+    auto store_step = [&](int st, const floatx4* ar, const floatx4* br) {
         float* A = As(st, cg);
         float* B = Bs(st, cg);
-        const floatx4 zero = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
         for (int r = 0; r < A_ROWS; ++r)
-            *reinterpret_cast<floatx4*>(&A[(r0 + ROW_STEP * r) * LDS_STRIDE + cc * 4]) =
-                ((mask >> r) & 1u) ? ar[r] : zero;
+            *reinterpret_cast<floatx4*>(&A[(r0 + ROW_STEP * r) * LDS_STRIDE + cc * 4]) = ar[r];
 #pragma unroll
         for (int i = 0; i < B_ROWS; ++i)
             *reinterpret_cast<floatx4*>(&B[(r0 + ROW_STEP * i) * LDS_STRIDE + cc * 4]) = br[i];
@@ -381,10 +382,10 @@ __device__ __forceinline__ void conv_tile(const ConvArgs& a, const int bx, const
     // after it and load only while a step is left, so no load is in flight
     // into the epilogue.
     constexpr int U = PF % 2 == 0 ? PF : 2 * PF;
-    load_step(kb_begin, areg[0], breg[0], amask[0]);
+    load_step(kb_begin, areg[0], breg[0]);
     static_for<PF - 1>([&](auto jc) {
         constexpr int J = decltype(jc)::value + 1;
-        if (J < nk) load_step(kb_begin + J * KG, areg[J], breg[J], amask[J]);
+        if (J < nk) load_step(kb_begin + J * KG, areg[J], breg[J]);
     });
     // Epilogue row table: element offset of each tile row in the output (or in
     // this split's partial slab) and in the residual; -1 past the last row.
@@ -430,7 +431,7 @@ __device__ __forceinline__ void conv_tile(const ConvArgs& a, const int bx, const
             __syncthreads();
         }
     };
-    store_step(0, areg[0], breg[0], amask[0]);
+    store_step(0, areg[0], breg[0]);
     stage_sync();
     // In the main loop both the load and the store happen unconditionally, so
     // each iteration is one basic block and the scheduler can interleave the
@@ -439,9 +440,9 @@ __device__ __forceinline__ void conv_tile(const ConvArgs& a, const int bx, const
         constexpr int J = decltype(jc)::value;
         constexpr int R = J % PF;  // register stage of step it
         constexpr int L = J % 2;   // LDS stage of step it
-        if (load) load_step(kb_begin + (it + PF) * KG, areg[R], breg[R], amask[R]);
+        if (load) load_step(kb_begin + (it + PF) * KG, areg[R], breg[R]);
         compute_step(L);
-        if (store) store_step(L ^ 1, areg[(R + 1) % PF], breg[(R + 1) % PF], amask[(R + 1) % PF]);
+        if (store) store_step(L ^ 1, areg[(R + 1) % PF], breg[(R + 1) % PF]);
         stage_sync();
     };
     int it = 0;
