@@ -831,8 +831,8 @@ void launch_maxpool_chain(const View& out0, const View& out1, const View& out2, 
 // DFL expectation of one side: softmax over the R bins (max, exp(x - max),
 // sum in bin order, * 1/sum, as softmax_kernel) and the weighted sum in bin
 // order (the direct conv's accumulation order) plus the bias.
-template <int R>
-__device__ __forceinline__ float dfl_side(float (&v)[R], const float* w, float bias) {
+template <int R, typename W>
+__device__ __forceinline__ float dfl_side(float (&v)[R], const W& w, float bias) {
     float mx = -1e30f;
 #pragma unroll
     for (int b = 0; b < R; ++b) mx = v[b] > mx ? v[b] : mx;
@@ -849,18 +849,28 @@ __device__ __forceinline__ float dfl_side(float (&v)[R], const float* w, float b
     return acc + bias;
 }
 
-// dist2bbox of one anchor from its four side distances d, then * stride.
-__device__ __forceinline__ void decode_box(const DetectDecodeArgs& a, int32_t n, int32_t an, const float (&d)[4]) {
+// The per-anchor inputs of the box decode: anchor point, divisor, strides.
+struct BoxIn {
+    float ax, ay, tx, ty, st[4];
+};
+
+__device__ __forceinline__ BoxIn load_box_in(const DetectDecodeArgs& a, int32_t n, int32_t an) {
     auto at = [&](const View& v, int c) {
         return v.ptr[n * v.str[0] + c * v.str[1] + static_cast<int64_t>(an) * v.str[2]];
     };
-    const float ax = at(a.anchors, 0), ay = at(a.anchors, 1);
-    const float x1 = ax - d[0], y1 = ay - d[1];
-    const float x2 = ax + d[2], y2 = ay + d[3];
-    const float r[4] = {(x1 + x2) / at(a.two, 0), (y1 + y2) / at(a.two, 1), x2 - x1, y2 - y1};
+    return BoxIn{at(a.anchors, 0), at(a.anchors, 1), at(a.two, 0), at(a.two, 1),
+                 {at(a.strides, 0), at(a.strides, 1), at(a.strides, 2), at(a.strides, 3)}};
+}
+
+// dist2bbox of one anchor from its four side distances d, then * stride.
+__device__ __forceinline__ void decode_box(const DetectDecodeArgs& a, int32_t n, int32_t an, const float (&d)[4],
+                                           const BoxIn& b) {
+    const float x1 = b.ax - d[0], y1 = b.ay - d[1];
+    const float x2 = b.ax + d[2], y2 = b.ay + d[3];
+    const float r[4] = {(x1 + x2) / b.tx, (y1 + y2) / b.ty, x2 - x1, y2 - y1};
 #pragma unroll
     for (int c = 0; c < 4; ++c)
-        a.out.ptr[n * a.out.str[0] + c * a.out.str[1] + static_cast<int64_t>(an) * a.out.str[2]] = r[c] * at(a.strides, c);
+        a.out.ptr[n * a.out.str[0] + c * a.out.str[1] + static_cast<int64_t>(an) * a.out.str[2]] = r[c] * b.st[c];
 }
 
 // One lane per (n, anchor); see kernels.hpp for the arithmetic.  R > 0: the
@@ -904,7 +914,7 @@ __global__ __launch_bounds__(256) void detect_decode_kernel(DetectDecodeArgs a, 
             d[side] = acc + a.dfl_bias;
         }
     }
-    decode_box(a, n, an, d);
+    decode_box(a, n, an, d, load_box_in(a, n, an));
 }
 
 // The whole head output of kHeadAnchors consecutive anchors of one image per
@@ -915,6 +925,8 @@ __global__ __launch_bounds__(256) void detect_decode_kernel(DetectDecodeArgs a, 
 // side's DFL expectation, kHeadAnchors lanes decode the boxes, and the class sigmoids
 // are written class-major with consecutive lanes on consecutive anchors.
 constexpr int kHeadAnchors = 16;
+constexpr int kHeadMaxRow = 252;  // floats per anchor row (S % 4 == 0, S + 1 <= 255)
+constexpr int kHeadLoads = (kHeadAnchors * kHeadMaxRow / 4 + 255) / 256;  // float4 loads per lane
 template <int R>
 __global__ __launch_bounds__(256) void detect_head_kernel(DetectDecodeArgs a, int32_t A, int32_t C, int32_t S) {
     extern __shared__ __attribute__((aligned(16))) float rows[];
@@ -930,16 +942,39 @@ __global__ __launch_bounds__(256) void detect_head_kernel(DetectDecodeArgs a, in
     const int cnt = min(kHeadAnchors, A - a0);
     const int P = S + 1;
     const float4* src = reinterpret_cast<const float4*>(a.x.ptr + n * a.x.str[0] + static_cast<int64_t>(a0) * S);
-    const int q4 = cnt * S / 4;
-    for (int q = tid; q < q4; q += 256) {
-        const float4 v = src[q];
-        const int e = 4 * q;
-        const int r = e / S;
-        float* dst = rows + r * P + (e - r * S);
-        dst[0] = v.x;
-        dst[1] = v.y;
-        dst[2] = v.z;
-        dst[3] = v.w;
+    // the tile's rows as float4s q = (row r, chunk j): every load of this
+    // lane issued before the first LDS store, so their latencies overlap;
+    // r = q / (S/4) as (q + 0.5) * (4/S) in fp32, exact for q < 2^12
+    const int S4 = S / 4;
+    const int q4 = cnt * S4;
+    const float inv_s4 = 1.0f / static_cast<float>(S4);
+    float4 v[kHeadLoads];
+#pragma unroll
+    for (int k = 0; k < kHeadLoads; ++k) {
+        const int q = tid + 256 * k;
+        v[k] = src[q < q4 ? q : 0];
+    }
+    // the DFL weights (lanes of the DFL phase) and the decode inputs of
+    // anchor a0 + tid (lanes of the decode phase), loaded with the rows so
+    // that their latency overlaps the rows'
+    float dw[R];
+    if (tid < 4 * kHeadAnchors) {
+#pragma unroll
+        for (int i = 0; i < R; ++i) dw[i] = a.dfl_w[i];
+    }
+    BoxIn box{};
+    if (tid < kHeadAnchors) box = load_box_in(a, n, a0 + min(tid, cnt - 1));
+#pragma unroll
+    for (int k = 0; k < kHeadLoads; ++k) {
+        const int q = tid + 256 * k;
+        if (q < q4) {
+            const int r = static_cast<int>((static_cast<float>(q) + 0.5f) * inv_s4);
+            float* dst = rows + r * P + 4 * (q - r * S4);
+            dst[0] = v[k].x;
+            dst[1] = v[k].y;
+            dst[2] = v[k].z;
+            dst[3] = v[k].w;
+        }
     }
     __syncthreads();
     if (tid < 4 * kHeadAnchors) {
@@ -950,14 +985,14 @@ __global__ __launch_bounds__(256) void detect_head_kernel(DetectDecodeArgs a, in
             const float* b = rows + an * P + side * R;
 #pragma unroll
             for (int i = 0; i < R; ++i) v[i] = b[i];
-            d = dfl_side<R>(v, a.dfl_w, a.dfl_bias);
+            d = dfl_side<R>(v, dw, a.dfl_bias);
         }
         dist[side][an] = d;
     }
     __syncthreads();
     if (tid < cnt) {
         const float d[4] = {dist[0][tid], dist[1][tid], dist[2][tid], dist[3][tid]};
-        decode_box(a, n, a0 + tid, d);
+        decode_box(a, n, a0 + tid, d, box);
     }
     const View& o = a.cls_out;
     float* ob = o.ptr + n * o.str[0] + static_cast<int64_t>(a0) * o.str[2];
