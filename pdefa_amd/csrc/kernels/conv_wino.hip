@@ -65,9 +65,10 @@ constexpr int kWinoMaxPatchPixels = 66 * 4;
 // image's tiles_h x tiles_w tile map.
 struct WinoGeom {
     int32_t tiles_h, tiles_w, tbw_log2, block_rows, block_cols;
-    // divisors of the index arithmetic (kernels.hpp FastDiv): the grid's x
-    // extent, blocks per image, block columns, patch row width 2 * tbw + 2
-    FastDiv fd_gx, fd_blocks_img, fd_block_cols, fd_pw;
+    // divisors of the index arithmetic (kernels.hpp FastDiv): the grid's y
+    // extent (channel blocks), blocks per image, block columns, patch row
+    // width 2 * tbw + 2
+    FastDiv fd_gy, fd_blocks_img, fd_block_cols, fd_pw;
 };
 
 bool wino_eligible(int KH, int KW, int sh, int sw, int dh, int dw, int Cin) {
@@ -156,14 +157,17 @@ __global__ __launch_bounds__(256) void conv_wino_kernel(ConvArgs a, WinoGeom geo
     const int PP = (2 * tbh + 2) * PW;
 
     // XCD-aware order: dispatch slot `lin` runs on XCD lin % 8; each XCD takes
-    // a contiguous range of (tile block fastest) workgroup indices.
-    const int gx = gridDim.x;
-    const int total = gx * gridDim.y;
+    // a contiguous range of (channel block fastest) workgroup indices, so the
+    // workgroups that read one tile block's input patch for its channel
+    // blocks run one after another on one XCD and all but the first read it
+    // from that XCD's L2.
+    const int gx = gridDim.x, gy = gridDim.y;
+    const int total = gx * gy;
     const int lin = blockIdx.x + gx * blockIdx.y;
     const int q = total / kXcds, rmd = total % kXcds, xcd = lin % kXcds;
     const int wid = xcd * q + min(xcd, rmd) + lin / kXcds;
-    const int by = wdiv(wid, geo.fd_gx);
-    const int bx = wid - by * gx;
+    const int bx = wdiv(wid, geo.fd_gy);
+    const int by = wid - bx * gy;
     // tile block bx: image bn, block row bbr, block column bbc
     const int blocks_img = geo.block_rows * geo.block_cols;
     const int bn = wdiv(bx, geo.fd_blocks_img);
@@ -614,7 +618,7 @@ void launch_conv_wino(const ConvArgs& a, int bn, hipStream_t s) {
     WinoGeom geo = wino_geometry(tiles_h, tiles_w);
     const int64_t blocks = static_cast<int64_t>(a.N) * geo.block_rows * geo.block_cols;
     if (blocks >= (int64_t{1} << 31)) fail("too many tiles");
-    geo.fd_gx = make_fastdiv(blocks);
+    geo.fd_gy = make_fastdiv((a.Cout + 31) / 32);
     geo.fd_blocks_img = make_fastdiv(static_cast<int64_t>(geo.block_rows) * geo.block_cols);
     geo.fd_block_cols = make_fastdiv(geo.block_cols);
     geo.fd_pw = make_fastdiv(2 * (int64_t{1} << geo.tbw_log2) + 2);
