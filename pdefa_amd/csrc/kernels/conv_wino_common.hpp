@@ -54,9 +54,9 @@ struct WinoBytes {
 
 }  // namespace wino
 
-// The strip kernel's launch (conv_wino_strip.hip): BN = 64 or 32 output
-// channels a workgroup, tiles_h x tiles_w tiles per image, the shape checks
-// already made by launch_conv_wino.
+// The strip kernel's launch (conv_wino_strip.hip): bn = 64 output channels
+// a workgroup (the only width it is built for), tiles_h x tiles_w tiles per
+// image, the shape checks already made by launch_conv_wino.
 void launch_conv_wino_strip(const ConvArgs& a, int bn, int tiles_h, int tiles_w, wino::WinoBytes b, hipStream_t s);
 
 }  // namespace k

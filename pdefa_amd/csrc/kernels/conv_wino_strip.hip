@@ -26,7 +26,7 @@ using namespace wino;
 
 template <int BN, int ACT, bool RES>
 __global__ __launch_bounds__(256) void conv_wino_strip_kernel(ConvArgs a, int tiles_h, int tiles_w, FastDiv fd_img, FastDiv fd_tw,
-                                                              FastDiv fd_gx, int x_bytes, int u_bytes, int y_bytes,
+                                                              FastDiv fd_gy, int x_bytes, int u_bytes, int y_bytes,
                                                               int r_bytes, int vec_out) {
     constexpr int CB = BN / 32;  // 32-wide channel blocks per wave
     // Exchange rows [row i][column c][tile] hold BN channels and 8 floats of
@@ -49,14 +49,16 @@ __global__ __launch_bounds__(256) void conv_wino_strip_kernel(ConvArgs a, int ti
     const int T = a.N * tiles_img;
 
     // XCD-aware order: dispatch slot `lin` runs on XCD lin % 8; each XCD takes
-    // a contiguous range of (tile block fastest) workgroup indices.
-    const int gx = gridDim.x;
-    const int total = gx * gridDim.y;
+    // a contiguous range of (channel block fastest) workgroup indices, so the
+    // channel blocks of one strip of tiles read its input patches one after
+    // another from one XCD's L2.
+    const int gx = gridDim.x, gy = gridDim.y;
+    const int total = gx * gy;
     const int lin = blockIdx.x + gx * blockIdx.y;
     const int q = total / kXcds, rmd = total % kXcds, xcd = lin % kXcds;
     const int wid = xcd * q + min(xcd, rmd) + lin / kXcds;
-    const int by = wdiv(wid, fd_gx);
-    const int bx = wid - by * gx;
+    const int bx = wdiv(wid, fd_gy);
+    const int by = wid - bx * gy;
     const int t0 = bx * kWT;
     const int n0 = by * BN;
     const int cop = (a.Cout + 63) / 64 * 64;
@@ -438,11 +440,9 @@ void launch_conv_wino_strip(const ConvArgs& a, int bn, int tiles_h, int tiles_w,
     const dim3 grid(static_cast<unsigned>((T + kWT - 1) / kWT), static_cast<unsigned>((a.Cout + bn - 1) / bn));
     if (grid.y > 65535) fail("grid");
     const FastDiv fi = make_fastdiv(static_cast<int64_t>(tiles_h) * tiles_w), ft = make_fastdiv(tiles_w),
-                  fg = make_fastdiv(grid.x);
-    if (bn == 64)
-        launch_strip_bn<64>(a, grid, tiles_h, tiles_w, fi, ft, fg, b, s);
-    else
-        launch_strip_bn<32>(a, grid, tiles_h, tiles_w, fi, ft, fg, b, s);
+                  fg = make_fastdiv(grid.y);
+    if (bn != 64) fail("the strip form takes 64 channels a workgroup");
+    launch_strip_bn<64>(a, grid, tiles_h, tiles_w, fi, ft, fg, b, s);
 }
 
 }  // namespace k
