@@ -141,6 +141,17 @@ PDEFA_EXPORT EngineStatus pdefa_amd_ops_matmul_noalloc(const EngineTensor* a, co
  * process. */
 PDEFA_EXPORT EngineStatus pdefa_amd_tune_stats(int64_t* measured, int64_t* from_table);
 
+/* Pre-pack cache files read (*read) and written (*written) by this process.
+ * With PDEFA_PACK_CACHE=1 in the environment, a model loaded from an .engine
+ * file keeps its packed conv weight layouts (implicit GEMM, direct and
+ * Winograd) in "<engine path>.<gfx arch>.pack" beside it: the first load on a
+ * device kind packs on the device and writes the file, later loads read it
+ * when its header matches the weights, the layout and the architecture, and
+ * pack again (rewriting it) when it does not.  The persisted counterpart of
+ * the reference's in-memory, pointer-keyed pack caches, which it clears at
+ * every model load (PDEFA1.0/src/loader/custom_loader.cpp:207-211). */
+PDEFA_EXPORT EngineStatus pdefa_amd_pack_cache_stats(int64_t* read, int64_t* written);
+
 #ifdef __cplusplus
 }
 #endif

@@ -215,6 +215,7 @@ bool load_engine_file(const std::string& path, Model& m, std::string* why) {
     }
 
     m.name = path;
+    m.source_path = path;
     m.version = static_cast<int32_t>(version);
     m.weights = std::move(weights);
     m.weight_names = std::move(names);

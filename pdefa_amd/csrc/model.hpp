@@ -56,6 +56,7 @@ struct DeviceModel;  // weights resident in HBM (runtime.hpp)
 
 struct Model {
     std::string name;
+    std::string source_path;  // the .engine file it was read from ("" when built otherwise)
     int32_t version = 0;
     std::vector<HostTensor> weights;
     std::vector<std::string> weight_names;

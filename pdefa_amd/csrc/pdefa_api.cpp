@@ -511,4 +511,10 @@ PDEFA_EXPORT EngineStatus pdefa_amd_tune_stats(int64_t* measured, int64_t* from_
     return ENGINE_OK;
 }
 
+PDEFA_EXPORT EngineStatus pdefa_amd_pack_cache_stats(int64_t* read, int64_t* written) {
+    if (!read || !written) return ENGINE_ERR_NULL_PTR;
+    pdefa::pack_cache_stats(*read, *written);
+    return ENGINE_OK;
+}
+
 }  // extern "C"

@@ -2,7 +2,10 @@
 
 #include "conv_tune.hpp"
 
+#include <unistd.h>
+
 #include <algorithm>
+#include <atomic>
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
@@ -135,7 +138,83 @@ constexpr size_t kAlignFloats = 64;
 constexpr int kMaxCaptureStreams = 8;
 size_t align_up(size_t n) { return (n + kAlignFloats - 1) / kAlignFloats * kAlignFloats; }
 
+// ---- pre-pack cache: the packed conv layouts of a model's device image,
+// persisted next to its .engine file.  File: a header (magic, format
+// version, device architecture, hashes of the raw weight image and of the
+// blob layout, payload length and payload hash) and the payload, the packed
+// part of the blob as floats.  The packed layouts are a deterministic
+// function of the raw weights, the layout and the pack kernels, so a file
+// whose header matches holds exactly what the device would pack; bump
+// kPackFormat whenever a pack kernel or layout changes.
+constexpr char kPackMagic[8] = {'P', 'D', 'F', 'A', 'P', 'A', 'C', 'K'};
+constexpr uint32_t kPackFormat = 1;
+
+struct PackHeader {
+    char magic[8];
+    uint32_t format;
+    uint32_t reserved;
+    char arch[32];
+    uint64_t weights_hash, layout_hash, payload_floats, payload_hash;
+};
+
+std::atomic<int64_t> g_pack_read{0}, g_pack_written{0};
+
+// FNV-1a over 32-bit words
+uint64_t hash_words(const void* p, size_t words, uint64_t h = 1469598103934665603ull) {
+    const uint32_t* w = static_cast<const uint32_t*>(p);
+    for (size_t i = 0; i < words; ++i) h = (h ^ w[i]) * 1099511628211ull;
+    return h;
+}
+
+std::string device_arch(int device) {
+    hipDeviceProp_t prop;
+    if (hipGetDeviceProperties(&prop, device) != hipSuccess) return "";
+    std::string a = prop.gcnArchName;
+    return a.substr(0, a.find(':'));
+}
+
+// Reads the payload when the file's header matches; false otherwise (no
+// file, another model, layout, architecture or format, truncation, or a
+// payload that does not hash to its header's value).
+bool read_pack_cache(const std::string& path, const PackHeader& want, std::vector<float>& payload) {
+    std::FILE* f = std::fopen(path.c_str(), "rb");
+    if (!f) return false;
+    PackHeader h;
+    bool ok = std::fread(&h, sizeof(h), 1, f) == 1 && std::memcmp(h.magic, want.magic, 8) == 0 &&
+              h.format == want.format && std::memcmp(h.arch, want.arch, sizeof(h.arch)) == 0 &&
+              h.weights_hash == want.weights_hash && h.layout_hash == want.layout_hash &&
+              h.payload_floats == want.payload_floats;
+    if (ok) {
+        payload.resize(static_cast<size_t>(h.payload_floats));
+        ok = std::fread(payload.data(), sizeof(float), payload.size(), f) == payload.size() &&
+             hash_words(payload.data(), payload.size()) == h.payload_hash;
+    }
+    std::fclose(f);
+    return ok;
+}
+
+// Writes the file through a temporary name and a rename, so that readers
+// see a whole file or none; a failure leaves no file and is not an error
+// (the cache only saves packing work).
+bool write_pack_cache(const std::string& path, PackHeader h, const std::vector<float>& payload) {
+    h.payload_hash = hash_words(payload.data(), payload.size());
+    const std::string tmp = path + ".tmp" + std::to_string(static_cast<long long>(getpid()));
+    std::FILE* f = std::fopen(tmp.c_str(), "wb");
+    if (!f) return false;
+    bool ok = std::fwrite(&h, sizeof(h), 1, f) == 1 &&
+              std::fwrite(payload.data(), sizeof(float), payload.size(), f) == payload.size();
+    ok = std::fclose(f) == 0 && ok;
+    if (ok) ok = std::rename(tmp.c_str(), path.c_str()) == 0;
+    if (!ok) std::remove(tmp.c_str());
+    return ok;
+}
+
 }  // namespace
+
+void pack_cache_stats(int64_t& read, int64_t& written) {
+    read = g_pack_read.load();
+    written = g_pack_written.load();
+}
 
 DeviceModel::~DeviceModel() {
     if (blob) (void)hipFree(blob);
@@ -222,15 +301,49 @@ std::shared_ptr<DeviceModel> upload_model(const Model& m) {
     dm->wptr.resize(m.weights.size());
     for (size_t i = 0; i < m.weights.size(); ++i) dm->wptr[i] = dm->blob + woff[i];
     dm->packs.resize(m.nodes.size());
+    for (const auto& p : pp) {
+        DeviceModel::Pack& pk = dm->packs[p.node];
+        pk.wpk = dm->blob + p.wpk_off;
+        pk.bias = dm->blob + p.bias_off;
+        pk.dpk = dm->blob + p.dpk_off;
+        pk.groups = p.groups;
+        if (p.wino) pk.wino = dm->blob + p.wino_off;
+    }
+    // the pre-pack cache (PDEFA_PACK_CACHE=1, models read from a file)
+    const size_t packed_floats = total - host_floats;
+    const bool cache = packed_floats > 0 && !m.source_path.empty() && env_flag("PDEFA_PACK_CACHE", false);
+    PackHeader hdr{};
+    std::string cache_path;
+    if (cache) {
+        const std::string arch = device_arch(dm->device);
+        std::memcpy(hdr.magic, kPackMagic, sizeof(hdr.magic));
+        hdr.format = kPackFormat;
+        std::snprintf(hdr.arch, sizeof(hdr.arch), "%s", arch.c_str());
+        hdr.weights_hash = hash_words(host.data(), host.size());
+        std::vector<uint64_t> lay = {total, host_floats};
+        for (const auto& p : pp)
+            for (uint64_t v : {static_cast<uint64_t>(p.node), static_cast<uint64_t>(p.wpk_off),
+                               static_cast<uint64_t>(p.dpk_off), static_cast<uint64_t>(p.wino ? p.wino_off : 0),
+                               static_cast<uint64_t>(p.cout), static_cast<uint64_t>(p.cin), static_cast<uint64_t>(p.kh),
+                               static_cast<uint64_t>(p.kw), static_cast<uint64_t>(p.groups)})
+                lay.push_back(v);
+        hdr.layout_hash = hash_words(lay.data(), lay.size() * 2);
+        hdr.payload_floats = packed_floats;
+        cache_path = m.source_path + "." + arch + ".pack";
+        std::vector<float> payload;
+        if (!arch.empty() && read_pack_cache(cache_path, hdr, payload)) {
+            PDEFA_HIP(hipMemcpy(dm->blob + host_floats, payload.data(), packed_floats * sizeof(float),
+                                hipMemcpyHostToDevice));
+            dm->packs_from_cache = true;
+            g_pack_read.fetch_add(1);
+            return dm;
+        }
+    }
     hipStream_t s;
     PDEFA_HIP(hipStreamCreateWithFlags(&s, hipStreamNonBlocking));
     try {
         for (const auto& p : pp) {
             DeviceModel::Pack& pk = dm->packs[p.node];
-            pk.wpk = dm->blob + p.wpk_off;
-            pk.bias = dm->blob + p.bias_off;
-            pk.dpk = dm->blob + p.dpk_off;
-            pk.groups = p.groups;
             // group g: weight rows [g*Cout/G, (g+1)*Cout/G) packed at g * w_group
             const int cout_g = p.cout / p.groups;
             const int64_t w_group = k::packed_weight_elems(cout_g, p.kh * p.kw * p.cin);
@@ -243,7 +356,6 @@ std::shared_ptr<DeviceModel> upload_model(const Model& m) {
             k::launch_pack_direct_weights(pk.dpk, dm->wptr[p.w], p.cout, p.cin, p.kh, p.kw, p.groups, s);
             PDEFA_HIP(hipGetLastError());
             if (p.wino) {
-                pk.wino = dm->blob + p.wino_off;
                 k::launch_pack_wino_weights(pk.wino, dm->wptr[p.w], p.cout, p.cin, s);
                 PDEFA_HIP(hipGetLastError());
             }
@@ -254,6 +366,12 @@ std::shared_ptr<DeviceModel> upload_model(const Model& m) {
         throw;
     }
     PDEFA_HIP(hipStreamDestroy(s));
+    if (cache && hdr.arch[0]) {
+        std::vector<float> payload(packed_floats);
+        PDEFA_HIP(hipMemcpy(payload.data(), dm->blob + host_floats, packed_floats * sizeof(float),
+                            hipMemcpyDeviceToHost));
+        if (write_pack_cache(cache_path, hdr, payload)) g_pack_written.fetch_add(1);
+    }
     return dm;
 }
 

@@ -45,11 +45,20 @@ struct DeviceModel {
         int groups = 1;         // wpk holds one packed block per group; dpk the grouped layout
     };
     std::vector<Pack> packs;  // by node index (empty for non-conv nodes)
+    bool packs_from_cache = false;  // the packed layouts came from the pre-pack cache file
     ~DeviceModel();
 };
 
-// Uploads and packs on the current device (throws on HIP errors).
+// Uploads and packs on the current device (throws on HIP errors).  With
+// PDEFA_PACK_CACHE=1 in the environment and a model read from a file, the
+// packed layouts are read from the pre-pack cache file next to it
+// ("<engine>.<gfx arch>.pack") when that file matches the weights, the
+// layout and the device architecture, and written there after packing on
+// the device otherwise.
 std::shared_ptr<DeviceModel> upload_model(const Model& m);
+
+// Pre-pack cache files read and written by this process.
+void pack_cache_stats(int64_t& read, int64_t& written);
 std::shared_ptr<DeviceModel> device_model(Model& m);  // lazily, once per model
 
 class Session {

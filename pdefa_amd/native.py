@@ -72,6 +72,7 @@ def lib() -> C.CDLL:
             "pdefa_amd_plan_model": (C.c_int, [vp, C.POINTER(i64), i32, C.c_char_p, sz, C.POINTER(sz)]),
             "pdefa_amd_device_name": (C.c_char_p, []),
             "pdefa_amd_tune_stats": (C.c_int, [C.POINTER(i64), C.POINTER(i64)]),
+            "pdefa_amd_pack_cache_stats": (C.c_int, [C.POINTER(i64), C.POINTER(i64)]),
             "pdefa_amd_ops_matmul_noalloc": (C.c_int, [vp, vp, vp]),
             "pdefa_amd_session_read_conv_input": (C.c_int, [vp, C.c_char_p, C.POINTER(C.c_float), sz,
                                                             C.POINTER(i64)]),
@@ -236,6 +237,14 @@ def tune_stats():
     m, t = C.c_int64(), C.c_int64()
     check(lib().pdefa_amd_tune_stats(C.byref(m), C.byref(t)), "pdefa_amd_tune_stats")
     return m.value, t.value
+
+
+def pack_cache_stats():
+    """(read, written): pre-pack cache files this process read and wrote
+    (PDEFA_PACK_CACHE=1)."""
+    r, w = C.c_int64(), C.c_int64()
+    check(lib().pdefa_amd_pack_cache_stats(C.byref(r), C.byref(w)), "pdefa_amd_pack_cache_stats")
+    return r.value, w.value
 
 
 def plan_text(path: str, shape: Sequence[int]) -> str:

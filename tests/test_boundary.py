@@ -35,7 +35,7 @@ engine_ops_concat engine_ops_stack engine_random_randn engine_random_rand
 EXTENSIONS = ["pdefa_amd_session_replay", "pdefa_amd_session_step_times", "pdefa_amd_session_step_repeat",
               "pdefa_amd_session_plan", "pdefa_amd_session_set_images", "pdefa_amd_image_from_pixels",
               "pdefa_amd_session_decode",
-              "pdefa_amd_plan_model", "pdefa_amd_device_name", "pdefa_amd_tune_stats",
+              "pdefa_amd_plan_model", "pdefa_amd_device_name", "pdefa_amd_tune_stats", "pdefa_amd_pack_cache_stats",
               "pdefa_amd_ops_matmul_noalloc", "pdefa_amd_session_read_conv_input"]
 
 

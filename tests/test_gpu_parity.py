@@ -674,6 +674,48 @@ def test_yolov8n_winograd_everywhere(yolov8n, monkeypatch, tile):
     assert_same_detections(got, [follow], metas[0], "yolov8n b1 winograd")
 
 
+def test_pack_cache_roundtrip(tmp_path, monkeypatch):
+    """The pre-pack cache (PDEFA_PACK_CACHE=1): the first load packs on the
+    device and writes "<engine>.<arch>.pack"; a second load reads it; a file
+    whose payload no longer matches its hash is not used (the load packs
+    again and rewrites it); every run's output is bit for bit that of a load
+    without the cache.  The model's convs take all three packed layouts
+    (implicit GEMM, Winograd, direct for the 3-channel stem)."""
+    print("[case] pack cache yolov8n 160x160", flush=True)
+    model = ys.build_yolov8("n", seed=5, imgsz=160)
+    path = str(tmp_path / "m.engine")
+    ys.save(model, path)
+    x, _ = ys.yolo_inputs(1, imgsz=160)
+
+    def run():
+        eng = native.Engine(path)
+        try:
+            return eng.run(x)[0].copy()
+        finally:
+            eng.close()
+
+    monkeypatch.delenv("PDEFA_PACK_CACHE", raising=False)
+    want = run()
+    monkeypatch.setenv("PDEFA_PACK_CACHE", "1")
+    r0, w0 = native.pack_cache_stats()
+    got1 = run()
+    files = [f for f in os.listdir(tmp_path) if f.endswith(".pack")]
+    assert len(files) == 1 and files[0].startswith("m.engine.gfx"), files
+    assert native.pack_cache_stats() == (r0, w0 + 1)
+    got2 = run()
+    assert native.pack_cache_stats() == (r0 + 1, w0 + 1)
+    cache = tmp_path / files[0]
+    raw = bytearray(cache.read_bytes())
+    raw[len(raw) // 2] ^= 0x40  # a payload byte
+    cache.write_bytes(bytes(raw))
+    got3 = run()
+    assert native.pack_cache_stats() == (r0 + 1, w0 + 2)
+    got4 = run()
+    assert native.pack_cache_stats() == (r0 + 2, w0 + 2)
+    for g in (got1, got2, got3, got4):
+        np.testing.assert_array_equal(g, want)
+
+
 @pytest.mark.parametrize("hw", [(384, 640), (640, 480)])
 def test_yolov8n_rectangular(tmp_path, hw):
     """YOLOv8n built for a rectangular input (h x w, feature maps of unequal
