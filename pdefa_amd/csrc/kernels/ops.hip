@@ -926,9 +926,11 @@ __global__ __launch_bounds__(256) void detect_decode_kernel(DetectDecodeArgs a, 
 // are written class-major with consecutive lanes on consecutive anchors.
 constexpr int kHeadAnchors = 16;
 constexpr int kHeadMaxRow = 252;  // floats per anchor row (S % 4 == 0, S + 1 <= 255)
-constexpr int kHeadLoads = (kHeadAnchors * kHeadMaxRow / 4 + 255) / 256;  // float4 loads per lane
+constexpr int kHeadThreads = 256;  // lanes a workgroup
+constexpr int kHeadLoads = (kHeadAnchors * kHeadMaxRow / 4 + kHeadThreads - 1) / kHeadThreads;  // float4 loads per lane
+static_assert(4 * kHeadAnchors <= kHeadThreads, "one lane per (side, anchor) in the DFL phase");
 template <int R>
-__global__ __launch_bounds__(256) void detect_head_kernel(DetectDecodeArgs a, int32_t A, int32_t C, int32_t S) {
+__global__ __launch_bounds__(kHeadThreads) void detect_head_kernel(DetectDecodeArgs a, int32_t A, int32_t C, int32_t S) {
     extern __shared__ __attribute__((aligned(16))) float rows[];
     __shared__ float dist[4][kHeadAnchors];
     const int tid = threadIdx.x;
@@ -951,7 +953,7 @@ __global__ __launch_bounds__(256) void detect_head_kernel(DetectDecodeArgs a, in
     float4 v[kHeadLoads];
 #pragma unroll
     for (int k = 0; k < kHeadLoads; ++k) {
-        const int q = tid + 256 * k;
+        const int q = tid + kHeadThreads * k;
         v[k] = src[q < q4 ? q : 0];
     }
     // the DFL weights (lanes of the DFL phase) and the decode inputs of
@@ -966,7 +968,7 @@ __global__ __launch_bounds__(256) void detect_head_kernel(DetectDecodeArgs a, in
     if (tid < kHeadAnchors) box = load_box_in(a, n, a0 + min(tid, cnt - 1));
 #pragma unroll
     for (int k = 0; k < kHeadLoads; ++k) {
-        const int q = tid + 256 * k;
+        const int q = tid + kHeadThreads * k;
         if (q < q4) {
             const int r = static_cast<int>((static_cast<float>(q) + 0.5f) * inv_s4);
             float* dst = rows + r * P + 4 * (q - r * S4);
@@ -996,7 +998,7 @@ __global__ __launch_bounds__(256) void detect_head_kernel(DetectDecodeArgs a, in
     }
     const View& o = a.cls_out;
     float* ob = o.ptr + n * o.str[0] + static_cast<int64_t>(a0) * o.str[2];
-    for (int q = tid; q < C * kHeadAnchors; q += 256) {
+    for (int q = tid; q < C * kHeadAnchors; q += kHeadThreads) {
         const int c = q / kHeadAnchors, an = q - c * kHeadAnchors;
         if (an < cnt) ob[c * o.str[1] + an * o.str[2]] = sigmoid_elt(rows[an * P + 4 * R + c]);
     }
@@ -1035,7 +1037,7 @@ void launch_detect_decode(const DetectDecodeArgs& a, hipStream_t s) {
     if (head) {
         const int64_t tiles = (A + kHeadAnchors - 1) / kHeadAnchors;
         const size_t lds = sizeof(float) * kHeadAnchors * static_cast<size_t>(S + 1);
-        hipLaunchKernelGGL(detect_head_kernel<16>, dim3(static_cast<unsigned>(N * tiles)), dim3(256), lds, s, a,
+        hipLaunchKernelGGL(detect_head_kernel<16>, dim3(static_cast<unsigned>(N * tiles)), dim3(kHeadThreads), lds, s, a,
                            static_cast<int32_t>(A), static_cast<int32_t>(C), static_cast<int32_t>(S));
         return;
     }
