@@ -25,9 +25,9 @@ namespace k {
 using namespace wino;
 
 template <int BN, int ACT, bool RES>
-__global__ __launch_bounds__(256) void conv_wino_strip_kernel(ConvArgs a, int tiles_h, int tiles_w, FastDiv fd_img, FastDiv fd_tw,
-                                                              FastDiv fd_gy, int x_bytes, int u_bytes, int y_bytes,
-                                                              int r_bytes, int vec_out) {
+__global__ __launch_bounds__(256) void conv_wino_strip_kernel(ConvArgs a, int tiles_h, int tiles_w, FastDiv fd_img,
+                                                              FastDiv fd_tw, FastDiv fd_gy, int x_bytes, int u_bytes,
+                                                              int y_bytes, int r_bytes, int vec_out) {
     constexpr int CB = BN / 32;  // 32-wide channel blocks per wave
     // Exchange rows [row i][column c][tile] hold BN channels and 8 floats of
     // padding: the two lane halves of a column-transform write (tiles 4
