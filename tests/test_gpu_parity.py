@@ -86,10 +86,55 @@ def reference_runs(path, x, split=True):
     return ref_worker.run(path, x, split)
 
 
+def reference_taps_run(path, x):
+    """The reference engine's outputs of x, each stacked over the images (a
+    `run` for device_jump_flips: the reference's own jump sides)."""
+    runs = reference_runs(path, x)
+    return [np.concatenate([r[k] for r in runs], axis=0) for k in range(len(runs[0]))]
+
+
 def reference_outputs(path, x):
     """The reference engine's first output for each image of x (it has no
     batch path: BatchInference runs one session per image), stacked."""
     return np.concatenate([outs[0] for outs in reference_runs(path, x)], axis=0)
+
+
+def assert_matches_reference_read_sides(got, model, path, x, metas, what, device_flips, tmp, conf=None):
+    """The device head `got` against the compiled reference on every element
+    and the post-NMS lists of every image, with the jump sides of both read
+    from their own activations: the device's (`device_flips`, as
+    assert_network_close returns them) and the reference's (its run with the
+    compat-SiLU tensors as extra outputs).  Where the two take different
+    sides of a jump and that changes the post-NMS list, each engine's list
+    is checked against the oracle with its own sides instead of against the
+    other's."""
+    ref = reference_outputs(path, x)
+    os.makedirs(tmp, exist_ok=True)
+    ref_flips, ref_heads = device_jump_flips(model, x, ref, tmp, f"{what} (reference)", run=reference_taps_run)
+    jumps = {}
+    for n in range(x.shape[0]):
+        sides = {side: sorted((name, i) for name, idxs in f[n].items() for i in idxs)
+                 for side, f in (("device", device_flips), ("reference", ref_flips))}
+        print(f"{what} image {n}: jump sides read: {sides}", flush=True)
+        if sides["device"] or sides["reference"]:
+            jumps[n] = sides
+    explained = assert_matches_reference(got, ref, what, model, x, jumps)
+    for n in range(x.shape[0]):
+        tag = f"{what} image {n}"
+        sides = jumps.get(n)
+        if sides and sides["device"] != sides["reference"]:
+            c = conf if conf is not None else decode_ref.robust_conf(ref[n:n + 1])[0]
+            mine = decode_yolo(got[n:n + 1], metas[n], conf_thres=c, iou_thres=0.45, with_anchor=True)
+            theirs = decode_yolo(ref[n:n + 1], metas[n], conf_thres=c, iou_thres=0.45, with_anchor=True)
+            if [(d["anchor"], d["cls"]) for d in mine] != [(d["anchor"], d["cls"]) for d in theirs]:
+                print(f"{tag}: the post-NMS lists differ with the engines' different jump sides; each is checked "
+                      f"against the oracle with its own", flush=True)
+                assert_same_detections_as_reference(got[n:n + 1], explained[n], metas[n], f"{tag} (device)", conf=c)
+                assert_same_detections_as_reference(ref[n:n + 1], ref_heads[n], metas[n], f"{tag} (reference)",
+                                                    conf=c)
+                continue
+        assert_same_detections_as_reference(got[n:n + 1], ref[n:n + 1], metas[n], tag, conf=conf,
+                                            follow=explained.get(n))
 
 
 def _save(name, arr):
@@ -280,7 +325,7 @@ def with_outputs(model, tids):
     return m
 
 
-def device_jump_flips(model, x, head, tmp, what, band=1e-4, check_inputs=False, images=None):
+def device_jump_flips(model, x, head, tmp, what, band=1e-4, check_inputs=False, images=None, run=None):
     """Per image of the batch x, the compat-SiLU activations (conv node name
     -> flat indices) where the device's activation sits on the other side
     of a jump than the float64 oracle's, read from the device's own
@@ -296,18 +341,25 @@ def device_jump_flips(model, x, head, tmp, what, band=1e-4, check_inputs=False, 
     check_inputs: for every flip, also read the conv's input tensor from the
     device and assert that the float64 conv of the device's own fp32 inputs
     lies on the device's side of the jump: the device's conv is exact there,
-    and the side comes from the rounding of its inputs upstream."""
+    and the side comes from the rounding of its inputs upstream.
+
+    run(path, x) -> outputs: another engine to read the sides of (the
+    compiled reference: reference_taps_run) instead of the device."""
     taps = compat_taps(model)
     written = [t[1] for t in taps]
     silus = [t[2] for t in taps]
     path = os.path.join(tmp, "taps.engine")
     ys.save(with_outputs(model, written), path)
-    eng = native.Engine(path)
-    try:
-        outs = eng.run(x)
-        plan = eng.plan()
-    finally:
-        eng.close()
+    if run is not None:
+        assert not check_inputs, "input checks read the device's tensors"
+        outs, plan = run(path, x), "(not the device)"
+    else:
+        eng = native.Engine(path)
+        try:
+            outs = eng.run(x)
+            plan = eng.plan()
+        finally:
+            eng.close()
     if not np.array_equal(outs[0], head):
         d = np.abs(outs[0].astype(np.float64) - head)
         tag = re.sub(r"[^A-Za-z0-9]+", "_", what)
@@ -721,7 +773,7 @@ def test_yolov8n_rectangular(tmp_path, hw):
     """YOLOv8n built for a rectangular input (h x w, feature maps of unequal
     sides at every scale), batch 2 (a 16:9 and a 4:3 image letterboxed into
     it): every output element and the post-NMS lists of both images match
-    the oracle."""
+    the oracle and the reference engine."""
     print(f"[case] yolov8n {hw[0]}x{hw[1]} b2", flush=True)
     model = ys.build_yolov8("n", seed=0, imgsz=hw)
     path = str(tmp_path / "yolov8n_rect.engine")
@@ -736,9 +788,10 @@ def test_yolov8n_rectangular(tmp_path, hw):
     assert TUNE_RECORDING or tune_measured() == m0, "a launch shape of this model is not in the launch-shape table"
     n_anchor = sum((hw[0] // s) * (hw[1] // s) for s in (8, 16, 32))
     assert got.shape == (2, 84, n_anchor)
-    follow, _ = assert_network_close(got, model, x, f"yolov8n {hw}")
+    follow, flips = assert_network_close(got, model, x, f"yolov8n {hw}")
     for i in range(2):
         assert_same_detections(got[i:i + 1], [follow[i:i + 1]], metas[i], f"yolov8n {hw} image {i}")
+    assert_matches_reference_read_sides(got, model, path, x, metas, f"yolov8n {hw}", flips, str(tmp_path / "ref"))
 
 
 @pytest.mark.parametrize("scale,hw,seed,cls_bias", [("s", 640, 1, None), ("l", 320, 2, -55.0),
@@ -764,11 +817,13 @@ def test_yolov8_scales(tmp_path, scale, hw, seed, cls_bias):
         eng.close()
     assert TUNE_RECORDING or tune_measured() == m0, "a launch shape of this model is not in the launch-shape table"
     assert got.shape == (1, 84, sum((hw // s) ** 2 for s in (8, 16, 32)))
-    follow, _ = assert_network_close(got, model, x, f"yolov8{scale} {hw} seed {seed}")
+    follow, flips = assert_network_close(got, model, x, f"yolov8{scale} {hw} seed {seed}")
     plain = graph_ref.run_graph(model, [x])[0]
     conf, _ = decode_ref.robust_conf(plain)
     assert conf is not None and decode_ref.min_iou_gap(plain.tolist(), metas[0], conf) >= 1e-3
     assert_same_detections(got, [follow], metas[0], f"yolov8{scale} {hw}")
+    assert_matches_reference_read_sides(got, model, path, x, metas, f"yolov8{scale} {hw} seed {seed}", flips,
+                                        str(tmp_path / "ref"), conf=conf)
 
 
 @pytest.mark.parametrize("n,c,h,w,k", [(2, 37, 13, 19, 5), (1, 16, 8, 8, 3), (2, 20, 23, 9, 7), (1, 128, 20, 20, 5)])
